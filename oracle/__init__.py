@@ -1,0 +1,8 @@
+"""ORACLE — test infrastructure, not part of the product.
+
+CPU restatement (plain C, oracle/bs_oracle.c) of the reference BigSmall
+rANS-family codecs. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this package, and only as the checker or the timed
+CPU baseline; the product package bigsmall_amd never imports it.
+"""
+from .oracle import *  # noqa: F401,F403
