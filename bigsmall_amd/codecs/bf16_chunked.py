@@ -1,0 +1,113 @@
+"""`bf16_chunked_v1` / `fp8_chunked_v1`: the engine's GPU-native codec.
+
+A tensor is cut into chunks of 64 x `steps` elements. Each chunk is 64
+interleaved rANS streams (one per wavefront lane) over the tensor's exponent
+(or exact-value) symbols, sharing one 16-bit renormalisation word stream, plus
+a plane of raw sign|mantissa bytes. The blob layout is documented in
+bigsmall_amd/csrc/bsck_decode.hip.
+
+Plugin shape of the reference codec API (bigsmall/codec_registry.py:39-42):
+    encode(raw: bytes, **ctx) -> (blob, extras)
+    decode(blob: bytes, extras: dict, n_weights: int) -> bytes
+plus the device entry points the engine itself uses (`decode_into`).
+Decoding runs only on the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from .. import _native
+from ..device import ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, require_gpu, upload_bytes
+
+CODEC_BF16 = "bf16_chunked_v1"
+CODEC_FP8 = "fp8_chunked_v1"
+DEFAULT_STEPS = 512
+MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT = -1, 0, 1, 2
+
+
+def _threads() -> int:
+    return max(1, min(os.cpu_count() or 1, 16))
+
+
+def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO,
+                 threads: int | None = None) -> bytes:
+    """Encode a uint16 (bf16 words) or uint8 (fp8 bytes) array."""
+    a = np.ascontiguousarray(arr)
+    if a.dtype not in (np.uint16, np.uint8):
+        raise TypeError("encode_array expects uint16 (bf16 bit patterns) or uint8 (fp8 bytes)")
+    eb = a.dtype.itemsize
+    n = a.size
+    if n == 0:
+        return b""
+    L = _native.lib()
+    bound = ctypes.c_uint64()
+    _native.check(L.bs_chunk_encode_bound(n, eb, steps, ctypes.byref(bound)), "bs_chunk_encode_bound")
+    out = np.empty(bound.value, np.uint8)
+    olen = ctypes.c_uint64()
+    _native.check(L.bs_chunk_encode(a.ctypes.data, n, eb, steps, mode, out.ctypes.data, bound.value,
+                                    ctypes.byref(olen), threads or _threads()), "bs_chunk_encode")
+    return out[: olen.value].tobytes()
+
+
+def encode(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:
+    """bf16 raw bytes -> (blob, extras)."""
+    if len(raw) % 2:
+        raise ValueError(f"BF16 byte length must be even, got {len(raw)}")
+    blob = encode_array(np.frombuffer(raw, dtype="<u2"), steps=steps, mode=mode)
+    return blob, {"steps": steps}
+
+
+def encode_fp8(raw: bytes, steps: int = DEFAULT_STEPS, **_) -> tuple[bytes, dict]:
+    blob = encode_array(np.frombuffer(raw, dtype=np.uint8), steps=steps, mode=MODE_EXACT)
+    return blob, {"steps": steps}
+
+
+def info(blob: bytes) -> _native.BsChunkInfo:
+    return inspect_chunk_header(bytes(blob[:32]))
+
+
+def decode_into(d_blob, blob_bytes: int, out, n: int, status: StatusWord | None = None, stream=None) -> StatusWord:
+    """Decode a device-resident blob (uint8 tensor or address) into `out`
+    (a device tensor of n elements of the blob's element size). Asynchronous
+    on `stream`; returns the status word to check after synchronising."""
+    import torch
+    if n == 0:
+        return status or StatusWord(out.device)
+    ptr = d_blob.data_ptr() if isinstance(d_blob, torch.Tensor) else int(d_blob)
+    head = (d_blob[:32].cpu().numpy().tobytes() if isinstance(d_blob, torch.Tensor) else None)
+    if head is None:
+        raise ValueError("decode_into needs the blob tensor (its header sizes the launch)")
+    inf = inspect_chunk_header(head)
+    if inf.n != n:
+        raise ValueError(f"bf16_chunked: weight count mismatch ({inf.n} vs {n})")
+    if out.numel() * out.element_size() < n * inf.elem_bytes:
+        raise ValueError("output tensor too small")
+    st = status or StatusWord(out.device)
+    batch = ChunkBatch([ChunkJob(ptr, blob_bytes, out.data_ptr(), n, inf.n_chunks, inf.plane_mode)], out.device)
+    batch.launch(st, stream)
+    return st
+
+
+def decode(blob: bytes, extras: dict, n_weights: int, elem_bytes: int = 2) -> bytes:
+    """Reference-shaped plugin decode: host bytes in, host bytes out; the
+    decode itself runs on the GPU."""
+    import torch
+    if n_weights == 0 or len(blob) == 0:
+        return b""
+    dev = require_gpu()
+    inf = info(blob)
+    if inf.n != n_weights:
+        raise ValueError(f"bf16_chunked: weight count mismatch ({inf.n} vs {n_weights})")
+    d_blob = upload_bytes(blob, dev)
+    out = torch.empty(n_weights * inf.elem_bytes, dtype=torch.uint8, device=dev)
+    st = decode_into(d_blob, len(blob), out, n_weights)
+    torch.cuda.synchronize(dev)
+    st.check(CODEC_BF16 if inf.elem_bytes == 2 else CODEC_FP8)
+    return out.cpu().numpy().tobytes()
+
+
+def decode_fp8(blob: bytes, extras: dict, n_weights: int) -> bytes:
+    return decode(blob, extras, n_weights, elem_bytes=1)

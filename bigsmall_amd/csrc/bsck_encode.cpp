@@ -1,0 +1,312 @@
+// Host encoder for BSCK, the decode engine's GPU-native chunked rANS format.
+// The byte layout is documented in bsck_decode.hip; this file produces it.
+//
+// Symbol model (per tensor):
+//   bf16, plane_mode 1 (dense):   one symbol per exponent present; every
+//                                 element also stores sign<<7|mantissa in the plane.
+//   bf16, plane_mode 2 (compact): dense's exponent symbols plus up to
+//                                 256-#exponents "exact word" symbols for words
+//                                 frequent enough to beat 8 raw bits (zeros of a
+//                                 sparse tensor, the few values of a norm vector).
+//   bf16/bytes, plane_mode 0:     every distinct value is a symbol (<= 256).
+// The encoder picks the smallest by estimated entropy unless a mode is forced.
+//
+// rANS encoding per chunk: 64 interleaved 32-bit states (L = 2^16, M = 2^12,
+// 16-bit renormalisation, the reference's state machine, bigsmall/codecs/rans.py:115-162),
+// walked from the last step back to the first; the renorm words are laid out
+// so the decoder consumes them step-ascending, lane-ascending.
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <thread>
+#include <vector>
+
+#include "../../include/bigsmall_hip.h"
+
+namespace {
+
+constexpr uint32_t kLanes = 64;
+constexpr uint32_t kL = 1u << 16;
+constexpr uint32_t kM = 4096;
+constexpr uint32_t kBlock = 8;
+
+inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+
+struct Plan {
+  int mode = 1;
+  uint32_t eb = 2;
+  uint32_t nsym = 0;
+  uint32_t value[256];
+  uint32_t consume[256];
+  uint32_t freq[256];
+  uint32_t cum[256];
+  std::vector<uint8_t> sym_of;  // word (or byte) -> symbol
+};
+
+void put16(uint8_t* p, uint32_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
+void put32(uint8_t* p, uint32_t v) { for (int i = 0; i < 4; ++i) p[i] = (uint8_t)(v >> (8 * i)); }
+void put64(uint8_t* p, uint64_t v) { for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i)); }
+
+// counts -> frequencies summing to kM, every present symbol >= 1, chosen by a
+// greedy minimum-codelength correction after proportional rounding.
+void quantise(const std::vector<uint64_t>& counts, uint32_t* freq) {
+  const size_t k = counts.size();
+  uint64_t total = 0;
+  for (uint64_t c : counts) total += c;
+  int64_t sum = 0;
+  std::vector<int64_t> f(k);
+  for (size_t i = 0; i < k; ++i) {
+    double ideal = (double)counts[i] * kM / (double)total;
+    int64_t v = (int64_t)std::llround(ideal);
+    if (v < 1) v = 1;
+    f[i] = v;
+    sum += v;
+  }
+  while (sum != (int64_t)kM) {
+    // pick the symbol whose +/-1 costs the fewest bits: d(bits) = c*log2(f/f')
+    size_t best = k;
+    double best_cost = 1e300;
+    for (size_t i = 0; i < k; ++i) {
+      double cost;
+      if (sum < (int64_t)kM) cost = (double)counts[i] * std::log2((double)f[i] / (double)(f[i] + 1));
+      else {
+        if (f[i] <= 1) continue;
+        cost = (double)counts[i] * std::log2((double)f[i] / (double)(f[i] - 1));
+      }
+      if (cost < best_cost) { best_cost = cost; best = i; }
+    }
+    if (sum < (int64_t)kM) { f[best]++; sum++; }
+    else { f[best]--; sum--; }
+  }
+  for (size_t i = 0; i < k; ++i) freq[i] = (uint32_t)f[i];
+}
+
+double entropy_bits(const std::vector<uint64_t>& counts) {
+  uint64_t total = 0;
+  for (uint64_t c : counts) total += c;
+  double h = 0;
+  for (uint64_t c : counts) if (c) h += (double)c * std::log2((double)total / (double)c);
+  return h;
+}
+
+template <typename Fn>
+void parallel_for(uint64_t n, int threads, Fn fn) {
+  if (threads <= 1 || n <= 1) { for (uint64_t i = 0; i < n; ++i) fn(i); return; }
+  std::atomic<uint64_t> next{0};
+  std::vector<std::thread> pool;
+  for (int t = 0; t < threads; ++t)
+    pool.emplace_back([&] { for (uint64_t i; (i = next.fetch_add(1)) < n;) fn(i); });
+  for (auto& th : pool) th.join();
+}
+
+std::vector<uint64_t> histogram(const void* src, uint64_t n, uint32_t eb, int threads) {
+  const uint32_t bins = eb == 2 ? 65536u : 256u;
+  const uint64_t parts = std::max<uint64_t>(1, std::min<uint64_t>((uint64_t)threads, n / (1u << 20) + 1));
+  std::vector<std::vector<uint64_t>> part(parts, std::vector<uint64_t>(bins, 0));
+  parallel_for(parts, threads, [&](uint64_t p) {
+    uint64_t lo = n * p / parts, hi = n * (p + 1) / parts;
+    auto& h = part[p];
+    if (eb == 2) { const uint16_t* w = (const uint16_t*)src; for (uint64_t i = lo; i < hi; ++i) h[w[i]]++; }
+    else { const uint8_t* w = (const uint8_t*)src; for (uint64_t i = lo; i < hi; ++i) h[w[i]]++; }
+  });
+  std::vector<uint64_t> h(bins, 0);
+  for (auto& q : part) for (uint32_t i = 0; i < bins; ++i) h[i] += q[i];
+  return h;
+}
+
+bool make_plan(const std::vector<uint64_t>& hist, uint32_t eb, int forced, Plan& P) {
+  P.eb = eb;
+  P.sym_of.assign(hist.size(), 0);
+  std::vector<uint64_t> cnt;
+  if (eb == 1) {
+    if (forced != BS_CHUNK_MODE_AUTO && forced != 0) return false;
+    P.mode = 0;
+    for (uint32_t v = 0; v < 256; ++v) if (hist[v]) {
+      P.sym_of[v] = (uint8_t)P.nsym; P.value[P.nsym] = v; P.consume[P.nsym] = 0;
+      cnt.push_back(hist[v]); P.nsym++;
+    }
+    quantise(cnt, P.freq);
+  } else {
+    uint64_t ecnt[256] = {0};
+    uint32_t unique = 0;
+    for (uint32_t w = 0; w < 65536; ++w) if (hist[w]) { ecnt[(w >> 7) & 0xFF] += hist[w]; unique++; }
+    uint32_t nexp = 0;
+    for (int e = 0; e < 256; ++e) nexp += ecnt[e] != 0;
+    uint64_t N = 0; for (uint64_t c : hist) N += c;
+
+    // dense
+    std::vector<uint64_t> dense_c;
+    for (int e = 0; e < 256; ++e) if (ecnt[e]) dense_c.push_back(ecnt[e]);
+    const double cost_dense = entropy_bits(dense_c) + 8.0 * (double)N;
+    // exact-value (mode 0)
+    double cost_exact = 1e300;
+    if (unique <= 256) {
+      std::vector<uint64_t> c; for (uint32_t w = 0; w < 65536; ++w) if (hist[w]) c.push_back(hist[w]);
+      cost_exact = entropy_bits(c);
+    }
+    // compact: exact words worth more than ~1 bit per occurrence
+    std::vector<std::pair<double, uint32_t>> cand;
+    for (uint32_t w = 0; w < 65536; ++w) {
+      if (hist[w] < 2) continue;
+      double save = 8.0 + std::log2((double)hist[w] / (double)ecnt[(w >> 7) & 0xFF]);
+      if (save > 1.0) cand.push_back({save * (double)hist[w], w});
+    }
+    std::sort(cand.begin(), cand.end(), [](auto& a, auto& b) { return a.first > b.first || (a.first == b.first && a.second < b.second); });
+    std::vector<uint8_t> is_exact(65536, 0);
+    uint32_t room = 256 - nexp, taken = 0;
+    for (auto& c : cand) { if (taken == room) break; is_exact[c.second] = 1; taken++; }
+    uint64_t rest[256] = {0};
+    std::vector<uint64_t> comp_c;
+    for (uint32_t w = 0; w < 65536; ++w) if (hist[w]) { if (is_exact[w]) comp_c.push_back(hist[w]); else rest[(w >> 7) & 0xFF] += hist[w]; }
+    uint64_t plane_n = 0;
+    for (int e = 0; e < 256; ++e) if (rest[e]) { comp_c.push_back(rest[e]); plane_n += rest[e]; }
+    const double cost_comp = taken ? entropy_bits(comp_c) + 8.0 * (double)plane_n : 1e300;
+
+    int mode = forced;
+    if (mode == BS_CHUNK_MODE_AUTO) {
+      if (cost_exact <= cost_dense && cost_exact <= cost_comp) mode = 0;
+      else if (cost_comp < cost_dense * 0.995) mode = 2;
+      else mode = 1;
+    }
+    if (mode == 0 && unique > 256) return false;
+    if (mode < 0 || mode > 2) return false;
+    P.mode = mode;
+    if (mode == 0) {
+      for (uint32_t w = 0; w < 65536; ++w) if (hist[w]) {
+        P.sym_of[w] = (uint8_t)P.nsym; P.value[P.nsym] = w; P.consume[P.nsym] = 0;
+        cnt.push_back(hist[w]); P.nsym++;
+      }
+    } else {
+      if (mode == 1) std::fill(is_exact.begin(), is_exact.end(), 0);
+      int sym_of_exp[256];
+      for (int e = 0; e < 256; ++e) sym_of_exp[e] = -1;
+      uint64_t cls[256] = {0};
+      for (uint32_t w = 0; w < 65536; ++w) if (hist[w] && !is_exact[w]) cls[(w >> 7) & 0xFF] += hist[w];
+      for (int e = 0; e < 256; ++e) if (cls[e]) {
+        sym_of_exp[e] = (int)P.nsym; P.value[P.nsym] = (uint32_t)e << 7; P.consume[P.nsym] = 1;
+        cnt.push_back(cls[e]); P.nsym++;
+      }
+      for (uint32_t w = 0; w < 65536; ++w) {
+        if (!hist[w]) continue;
+        if (is_exact[w]) {
+          P.sym_of[w] = (uint8_t)P.nsym; P.value[P.nsym] = w; P.consume[P.nsym] = 0;
+          cnt.push_back(hist[w]); P.nsym++;
+        } else P.sym_of[w] = (uint8_t)sym_of_exp[(w >> 7) & 0xFF];
+      }
+    }
+    quantise(cnt, P.freq);
+  }
+  uint32_t c = 0;
+  for (uint32_t s = 0; s < P.nsym; ++s) { P.cum[s] = c; c += P.freq[s]; }
+  return c == kM && P.nsym >= 1 && P.nsym <= 256;
+}
+
+// Encode one chunk into `out` (states | words | plane, each 16-padded).
+void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, uint32_t& n_words,
+                  uint32_t& n_plane, std::vector<uint8_t>& out) {
+  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+  std::vector<uint16_t> words(nc + 1);
+  size_t pos = words.size();
+  uint32_t x[kLanes];
+  for (uint32_t l = 0; l < kLanes; ++l) x[l] = kL;
+  const uint16_t* w16 = (const uint16_t*)src;
+  const uint8_t* w8 = (const uint8_t*)src;
+  auto sym_at = [&](uint64_t j) -> uint32_t { return P.sym_of[P.eb == 2 ? w16[base + j] : w8[base + j]]; };
+  uint64_t xmax[256];
+  for (uint32_t s = 0; s < P.nsym; ++s) xmax[s] = (uint64_t)P.freq[s] << 20;
+  for (uint32_t t = nsteps; t-- > 0;) {
+    for (uint32_t l = kLanes; l-- > 0;) {
+      const uint64_t j = (uint64_t)t * kLanes + l;
+      if (j >= nc) continue;
+      const uint32_t s = sym_at(j), f = P.freq[s];
+      uint32_t v = x[l];
+      if ((uint64_t)v >= xmax[s]) { words[--pos] = (uint16_t)(v & 0xFFFF); v >>= 16; }
+      const uint32_t q = v / f;
+      x[l] = (q << 12) + (v - q * f) + P.cum[s];
+    }
+  }
+  n_words = (uint32_t)(words.size() - pos);
+  std::vector<uint8_t> plane;
+  if (P.mode == 1) {
+    const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
+    plane.assign((size_t)nblk * kBlock * kLanes, 0);
+    for (uint32_t j = 0; j < nc; ++j) {
+      const uint32_t w = w16[base + j], t = j / kLanes, l = j % kLanes;
+      plane[(size_t)(t / kBlock) * kBlock * kLanes + l * kBlock + (t % kBlock)] = (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
+    }
+  } else if (P.mode == 2) {
+    plane.reserve(nc);
+    for (uint32_t j = 0; j < nc; ++j) {
+      const uint32_t w = w16[base + j];
+      if (P.consume[P.sym_of[w]]) plane.push_back((uint8_t)(((w >> 8) & 0x80) | (w & 0x7F)));
+    }
+  }
+  n_plane = (uint32_t)plane.size();
+  const uint64_t wb = pad16((uint64_t)n_words * 2), pb = pad16(n_plane);
+  out.assign(4 * kLanes + wb + pb, 0);
+  for (uint32_t l = 0; l < kLanes; ++l) put32(out.data() + 4 * l, x[l]);
+  for (uint32_t i = 0; i < n_words; ++i) put16(out.data() + 4 * kLanes + 2 * i, words[pos + i]);
+  if (n_plane) memcpy(out.data() + 4 * kLanes + wb, plane.data(), n_plane);
+}
+
+}  // namespace
+
+extern "C" {
+
+int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t steps, uint64_t* bound) {
+  if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kBlock) return BS_ERR_ARG;
+  const uint64_t per = (uint64_t)kLanes * steps;
+  const uint64_t nch = (n + per - 1) / per;
+  *bound = pad16(32 + 4 * 256) + 16 * nch + nch * (4 * kLanes + pad16(2 * per) + pad16(per) + 32);
+  return BS_OK;
+}
+
+int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t steps, int32_t mode,
+                    uint8_t* dst, uint64_t cap, uint64_t* out_len, int n_threads) {
+  if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kBlock) return BS_ERR_ARG;
+  if (n == 0) { *out_len = 0; return BS_OK; }
+  if (!src || !dst) return BS_ERR_ARG;
+  if (n_threads < 1) n_threads = 1;
+  std::vector<uint64_t> hist = histogram(src, n, elem_bytes, n_threads);
+  Plan P;
+  if (!make_plan(hist, elem_bytes, mode, P)) return BS_ERR_ARG;
+
+  const uint64_t per = (uint64_t)kLanes * steps;
+  const uint64_t nch64 = (n + per - 1) / per;
+  if (nch64 > 0xFFFFFFFFull) return BS_ERR_ARG;
+  const uint32_t nch = (uint32_t)nch64;
+  std::vector<std::vector<uint8_t>> chunks(nch);
+  std::vector<uint32_t> nw(nch), np(nch);
+  parallel_for(nch, n_threads, [&](uint64_t c) {
+    const uint64_t base = c * per;
+    const uint32_t nc = (uint32_t)std::min<uint64_t>(per, n - base);
+    encode_chunk(P, src, base, nc, nw[c], np[c], chunks[c]);
+  });
+
+  const uint64_t ctab = pad16(32 + 4ull * P.nsym);
+  uint64_t total = ctab + 16ull * nch;
+  total = pad16(total);
+  std::vector<uint64_t> offs(nch);
+  for (uint32_t c = 0; c < nch; ++c) { offs[c] = total; total += chunks[c].size(); }
+  if (total > cap) return BS_ERR_CAP;
+  memset(dst, 0, ctab + 16ull * nch + 16);
+  memcpy(dst, "BSCK", 4);
+  dst[4] = 1; dst[5] = (uint8_t)elem_bytes; dst[6] = (uint8_t)P.mode; dst[7] = 12;
+  put64(dst + 8, n); put32(dst + 16, steps); put16(dst + 20, kLanes); put16(dst + 22, P.nsym);
+  put32(dst + 24, nch); put32(dst + 28, 0);
+  for (uint32_t s = 0; s < P.nsym; ++s)
+    put32(dst + 32 + 4 * s, (P.value[s] & 0xFFFF) | (P.freq[s] << 16) | (P.consume[s] << 31));
+  for (uint32_t c = 0; c < nch; ++c) {
+    put64(dst + ctab + 16ull * c, offs[c]);
+    put32(dst + ctab + 16ull * c + 8, nw[c]);
+    put32(dst + ctab + 16ull * c + 12, np[c]);
+  }
+  parallel_for(nch, n_threads, [&](uint64_t c) { memcpy(dst + offs[c], chunks[c].data(), chunks[c].size()); });
+  *out_len = total;
+  return BS_OK;
+}
+
+}  // extern "C"

@@ -82,17 +82,19 @@ int bs_chunk_inspect(const uint8_t *h_blob, uint64_t len, bs_chunk_info *info);
  * ceil(n_chunks / bs_chunk_chunks_per_group())). */
 int bs_chunk_chunks_per_group(void);
 
-/* Decode one BSCK blob into d_out. Device counterpart of the codec plugin's
+/* Decode one BSCK blob into d_out. `plane_mode` is the header's (from
+ * bs_chunk_inspect). Device counterpart of the codec plugin's
  * decode(blob, extras, n_weights) (bigsmall/codec_registry.py:39-42). */
 int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uint64_t n,
-                    uint32_t n_chunks, int32_t *d_status, void *stream);
+                    uint32_t n_chunks, uint32_t plane_mode, int32_t *d_status, void *stream);
 
 /* Decode many BSCK blobs (a transformer layer, a batch of KV blocks) in one
- * launch. Replaces the per-tensor `_decode_blob` loop of decoder.decompress
+ * launch; `max_plane_mode` is the largest plane_mode among the tasks (mode 2
+ * launches reserve extra LDS for the compact-plane rings). Replaces the per-tensor `_decode_blob` loop of decoder.decompress
  * (bigsmall/decoder.py:128-136) and StreamingLoader.load_layer
  * (bigsmall/streaming.py:218-227). */
 int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32_t total_groups,
-                          int32_t *d_status, void *stream);
+                          uint32_t max_plane_mode, int32_t *d_status, void *stream);
 
 /* Host encoder for BSCK. `flags`: BS_CHUNK_MODE_AUTO or a forced plane mode.
  * Replaces the encode half of the codec plugin pair (bigsmall/codec_registry.py:39-47). */

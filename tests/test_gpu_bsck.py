@@ -1,0 +1,129 @@
+"""GPU parity of the BSCK (bf16_chunked_v1 / fp8_chunked_v1) HIP decoder.
+
+Bar: bit-exact. Every case checks GPU output == source words (md5) and ==
+the oracle's CPU decode of the same blob.
+"""
+from __future__ import annotations
+
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_gpu():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    oracle.build()
+    return torch
+
+
+def _check_one(torch_gpu, words, steps=512, mode=-1, label=""):
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    _say(f"[bsck] {label} n={words.size} dtype={words.dtype} steps={steps} mode={mode}")
+    blob = bc.encode_array(words, steps=steps, mode=mode)
+    eb = words.dtype.itemsize
+    gpu = bc.decode(blob, {}, words.size, elem_bytes=eb) if eb == 2 else bc.decode_fp8(blob, {}, words.size)
+    assert hashlib.md5(gpu).hexdigest() == hashlib.md5(words.tobytes()).hexdigest(), label
+    assert gpu == oracle.chunk_decode(blob, words.size, eb), label
+    return blob
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 511, 4097, 32768, 32768 * 3 + 1000, 1 << 20])
+def test_gaussian_sizes(torch_gpu, n):
+    rng = np.random.default_rng(n)
+    _check_one(torch_gpu, _bf16(rng.standard_normal(n) * 0.02), label=f"gauss{n}")
+
+
+@pytest.mark.parametrize("mode", [-1, 1, 2])
+@pytest.mark.parametrize("steps", [8, 64, 512, 1024])
+def test_modes_and_steps(torch_gpu, mode, steps):
+    rng = np.random.default_rng(steps + 7 * mode)
+    w = _bf16(rng.standard_normal(200_003) * 0.02)
+    w[rng.permutation(w.size)[: w.size // 2]] = 0          # 50% exact zeros (compact mode pays off)
+    _check_one(torch_gpu, w, steps=steps, mode=mode, label=f"halfzero s{steps} m{mode}")
+
+
+def test_edge_words_and_heavy_tails(torch_gpu):
+    rng = np.random.default_rng(11)
+    edge = np.array([0x7FC0, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x0080, 0x3F80], np.uint16)
+    w = np.concatenate([edge, _bf16(rng.standard_normal(100_000) * 0.02)])
+    _check_one(torch_gpu, w, label="edge")
+    t = _bf16(rng.standard_t(3, 300_000) * 0.02 / np.sqrt(3))
+    _check_one(torch_gpu, t, label="student-t")
+    allw = rng.integers(0, 65536, 300_000).astype(np.uint16)  # every exponent present
+    _check_one(torch_gpu, allw, label="uniform words")
+
+
+def test_exact_value_modes(torch_gpu):
+    rng = np.random.default_rng(12)
+    _check_one(torch_gpu, np.zeros(100_000, np.uint16), label="zeros")
+    _check_one(torch_gpu, _bf16(1.0 + rng.standard_normal(4096) * 0.01), label="norm")
+    _check_one(torch_gpu, np.full(70_000, 0x3F80, np.uint16), mode=0, label="constant")
+    fp8 = rng.integers(0, 256, 500_000).astype(np.uint8)
+    _check_one(torch_gpu, fp8, label="fp8 uniform")
+    import torch
+    x = torch.randn(300_000, generator=torch.Generator().manual_seed(5)).to(torch.float8_e4m3fn)
+    _check_one(torch_gpu, x.view(torch.uint8).numpy(), label="fp8 e4m3 N(0,1)")
+
+
+def test_batched_launch_matches_single(torch_gpu):
+    import torch
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
+    rng = np.random.default_rng(13)
+    sizes = [5, 64 * 512, 64 * 512 + 3, 1 << 18, 777_777]
+    words = [_bf16(rng.standard_normal(s) * (0.01 + 0.01 * i)) for i, s in enumerate(sizes)]
+    blobs = [bc.encode_array(w) for w in words]
+    _say(f"[bsck] batch of {len(blobs)} blobs")
+    dev = torch.device("cuda")
+    d = [upload_bytes(b, dev) for b in blobs]
+    outs = [torch.empty(w.size, dtype=torch.int16, device=dev) for w in words]
+    jobs = [ChunkJob(db.data_ptr(), len(b), o.data_ptr(), w.size, bc.info(b).n_chunks, bc.info(b).plane_mode)
+            for db, b, o, w in zip(d, blobs, outs, words)]
+    st = StatusWord(dev)
+    batch = ChunkBatch(jobs, dev)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(0)
+        batch.launch(st)
+        torch.cuda.synchronize()
+        st.check()
+        for o, w in zip(outs, words):
+            assert np.array_equal(o.cpu().numpy().view(np.uint16), w), f"rep {rep}"
+
+
+def test_corrupt_stream_is_reported(torch_gpu):
+    import torch
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.exceptions import DecodeError
+    rng = np.random.default_rng(14)
+    w = _bf16(rng.standard_normal(100_000) * 0.02)
+    blob = bytearray(bc.encode_array(w))
+    # flip one renorm word of chunk 0 (inside the blob, so every access stays in bounds)
+    ctab = (32 + 4 * int.from_bytes(blob[22:24], "little") + 15) & ~15
+    off = int.from_bytes(blob[ctab:ctab + 8], "little")
+    blob[off + 256 + 10] ^= 0xFF
+    _say("[bsck] corrupt word -> DecodeError")
+    with pytest.raises(DecodeError):
+        bc.decode(bytes(blob), {}, w.size)
+    # wrong element count is refused on the host before any launch
+    with pytest.raises(ValueError):
+        bc.decode(bytes(blob), {}, w.size + 1)
+    torch.cuda.synchronize()
