@@ -100,6 +100,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--chunk-steps", type=int, default=None)
+    ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -112,11 +113,12 @@ def main():
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
 
     steps = args.chunk_steps or bc.DEFAULT_STEPS
+    lanes = args.lanes or bc.DEFAULT_LANES
     t0 = time.time()
     words = make_layer(0)
     log(f"[bench] layer generated in {time.time() - t0:.1f}s")
     t0 = time.time()
-    blobs = {name: bc.encode_array(w, steps=steps) for name, w in words.items()}
+    blobs = {name: bc.encode_array(w, steps=steps, lanes=lanes) for name, w in words.items()}
     log(f"[bench] encoded in {time.time() - t0:.1f}s")
     n_total = sum(w.size for w in words.values())
     comp_total = sum(len(b) for b in blobs.values())
@@ -184,7 +186,7 @@ def main():
             "workload": "llama3-8b-layer-decode-to-hbm",
             "tensors": len(LAYER), "elements": n_total, "decoded_bytes": out_total,
             "compressed_bytes": comp_total, "ratio_pct": round(100 * comp_total / out_total, 3),
-            "codec": bc.CODEC_BF16, "chunk_steps": steps, "launches_per_step": 1,
+            "codec": bc.CODEC_BF16, "chunk_steps": steps, "chunk_lanes": lanes, "launches_per_step": 1,
         },
         "ms_per_layer": round(ms_per, 5),
         "decoded_output_GBps": round(out_total / (ms_per * 1e-3) / 1e9, 2),

@@ -25,6 +25,7 @@ from ..device import ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, req
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
 DEFAULT_STEPS = 512
+DEFAULT_LANES = 128
 MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT = -1, 0, 1, 2
 
 
@@ -33,7 +34,7 @@ def _threads() -> int:
 
 
 def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO,
-                 threads: int | None = None) -> bytes:
+                 threads: int | None = None, lanes: int = DEFAULT_LANES) -> bytes:
     """Encode a uint16 (bf16 words) or uint8 (fp8 bytes) array."""
     a = np.ascontiguousarray(arr)
     if a.dtype not in (np.uint16, np.uint8):
@@ -44,10 +45,10 @@ def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_A
         return b""
     L = _native.lib()
     bound = ctypes.c_uint64()
-    _native.check(L.bs_chunk_encode_bound(n, eb, steps, ctypes.byref(bound)), "bs_chunk_encode_bound")
+    _native.check(L.bs_chunk_encode_bound(n, eb, lanes, steps, ctypes.byref(bound)), "bs_chunk_encode_bound")
     out = np.empty(bound.value, np.uint8)
     olen = ctypes.c_uint64()
-    _native.check(L.bs_chunk_encode(a.ctypes.data, n, eb, steps, mode, out.ctypes.data, bound.value,
+    _native.check(L.bs_chunk_encode(a.ctypes.data, n, eb, lanes, steps, mode, out.ctypes.data, bound.value,
                                     ctypes.byref(olen), threads or _threads()), "bs_chunk_encode")
     return out[: olen.value].tobytes()
 

@@ -40,27 +40,29 @@ namespace {
 
 #define LDS __attribute__((address_space(3)))
 #define GLB __attribute__((address_space(1)))
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLanes = 64;
+constexpr int kWave = 64;                 // lanes of a wavefront
 constexpr int kWaves = 8;                 // chunks (wavefronts) per workgroup
-constexpr int kThreads = kWaves * kLanes;
-constexpr int kBlock = 8;                 // steps per refill block
+constexpr int kThreads = kWaves * kWave;
+constexpr int kBlock = 8;                 // steps per block (plane block, output flush, refill check)
 constexpr uint32_t kRing = 2048;          // per-wave word ring (u16) and plane ring (bytes)
 constexpr uint32_t kSeg = 256;            // refill segment: words (64 lanes x 8 B) / plane bytes (64 x 4 B)
 constexpr uint32_t kL = 1u << 16;
-// dynamic LDS layout: decode table | word rings | plane rings (compact-capable launches only)
+// dynamic LDS layout (bytes): decode table | word rings | output staging | plane rings (compact launches)
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kWringBytes = kWaves * kRing * 2;
-constexpr uint32_t kPringBytes = kWaves * kRing;
-constexpr uint32_t kLdsLean = kTblBytes + kWringBytes;
-constexpr uint32_t kLdsCompact = kLdsLean + kPringBytes;
+constexpr uint32_t kStageMax = kBlock * 128 * 2;   // per wave: 8 steps x up to 128 states x 2 bytes
+constexpr uint32_t kLdsLean = kTblBytes + kWringBytes + kWaves * kStageMax;
+constexpr uint32_t kLdsCompact = kLdsLean + kWaves * kRing;
 
 __device__ __forceinline__ uint32_t ld_u32(const GLB uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
-__device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+// rank of this lane among the set lanes of m, plus `base`
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m, uint32_t base) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, base));
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -71,19 +73,37 @@ __device__ __forceinline__ void wave_sync() {
 
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
 
-// Combine a bf16 exponent symbol's value with its plane byte (sign<<7 | mant).
-__device__ __forceinline__ uint32_t with_plane(uint32_t v, uint32_t b) {
-  return v | (b & 0x7Fu) | ((b & 0x80u) << 8);
-}
-
 __device__ __forceinline__ void report(int32_t* status, int32_t bits) {
   if (__lane_id() == 0) atomicOr(status, bits);
 }
 
-// ring segment load/store: lane l moves 8 bytes (4 words) / 4 bytes of a 256-entry segment
+// A plane byte b = sign<<7 | mantissa completes an exponent symbol's value v:
+// (b | b<<8) & 0x807F puts the sign at bit 15 and the mantissa at bits 0..6.
+// `sel` picks byte q of the 8 plane bytes {hi:lo} into bytes 0 and 1.
+__device__ __forceinline__ uint32_t plane_merge(uint32_t v, uint64_t bytes8, uint32_t sel) {
+  const uint32_t bb = __builtin_amdgcn_perm((uint32_t)(bytes8 >> 32), (uint32_t)bytes8, sel);
+  return (bb & 0x807Fu) | v;
+}
+__device__ __forceinline__ uint32_t byte_merge(uint32_t v, uint32_t b) { return ((b * 0x101u) & 0x807Fu) | v; }
+
+// ---- ring refills: lane l moves 8 bytes (4 words) / 4 bytes of a 256-entry segment
 __device__ __forceinline__ uint64_t load_wseg(const GLB uint64_t* src, uint32_t pos, uint32_t valid, uint32_t lane) {
   const uint32_t slot = pos / 4u + lane;
   return slot < valid ? src[slot] : 0ull;
+}
+// Unconditional variant for prefetches: out-of-range slots re-read `safe` (the
+// chunk's state words: always inside the blob and in cache) so every block
+// issues the same number of loads; a fixed count lets the compiler's waitcnt
+// placement wait only for the data actually needed.
+__device__ __forceinline__ uint64_t load_wseg_always(const GLB uint64_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
+                                                     const GLB uint64_t* safe) {
+  const uint32_t slot = pos / 4u + lane;
+  return *(slot < valid ? src + slot : safe + (lane & 31u));
+}
+__device__ __forceinline__ uint32_t load_pseg_always(const GLB uint32_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
+                                                     const GLB uint32_t* safe) {
+  const uint32_t slot = pos / 4u + lane;
+  return *(slot < valid ? src + slot : safe + lane);
 }
 __device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, uint64_t v, uint32_t lane) {
   *(LDS uint64_t*)(ring + ((pos + lane * 4u) & (kRing - 1u))) = v;
@@ -96,109 +116,238 @@ __device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, uint
   *(LDS uint32_t*)(ring + ((pos + lane * 4u) & (kRing - 1u))) = v;
 }
 
-// Decode one chunk with one wavefront. MODE = plane mode, EB = element bytes,
-// PARTIAL = chunk may be shorter than 64*steps (the tensor's last chunk).
-template <int MODE, int EB, bool PARTIAL>
-__device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
-                                             LDS uint8_t* __restrict__ pring, const GLB uint8_t* __restrict__ cbase,
-                                             uint32_t n_words, uint32_t n_plane, GLB uint8_t* __restrict__ out8,
-                                             uint64_t base, uint32_t nc, uint32_t nsteps, int32_t* status) {
-  const uint32_t lane = __lane_id();
-  const uint32_t wbytes = pad16(n_words * 2u);
-  const GLB uint64_t* __restrict__ wsrc = (const GLB uint64_t*)(cbase + 4u * kLanes);
-  const GLB uint8_t* psrc8 = cbase + 4u * kLanes + wbytes;
-  const GLB uint32_t* __restrict__ psrc = (const GLB uint32_t*)psrc8;
-  const GLB uint64_t* __restrict__ dplane = (const GLB uint64_t*)psrc8;
-  const uint32_t wvalid = wbytes / 8u;           // readable uint2 slots in the word section
-  const uint32_t pvalid = pad16(n_plane) / 4u;   // readable u32 slots in the plane section
+// Per-wavefront decode state of one chunk.
+template <int K>
+struct ChunkState {
+  uint32_t x[K];
+  uint32_t wptr, wld;    // word ring holds words [wptr, wld)
+  uint32_t pptr, pld;    // plane ring (compact mode) holds bytes [pptr, pld)
+  uint32_t wn, pn;       // segments prefetched for landing at the next block start
+  uint64_t wp0, wp1;
+  uint32_t pp0, pp1;
+};
 
-  uint32_t x = ((const GLB uint32_t*)cbase)[lane];
-  uint32_t wptr = 0, wld = 0;   // word ring holds words [wptr, wld)
-  uint32_t pptr = 0, pld = 0;   // plane ring (compact mode) holds bytes [pptr, pld)
+// Chunk-constant parameters.
+struct ChunkParams {
+  const GLB uint64_t* wsrc;     // renorm words, as 8-byte segments
+  const GLB uint32_t* psrc;     // compact plane, as 4-byte segments
+  const GLB uint64_t* dplane;   // dense plane, 8 bytes per lane per state group per block
+  const GLB uint8_t* cbase;     // chunk start (its state words are a safe dummy address)
+  GLB uint8_t* out8;
+  uint64_t base;                // first element of the chunk
+  uint32_t n_words, n_plane, wvalid, pvalid, nc, nsteps, nblk, lane;
+};
 
-  for (int s = 0; s < 2; ++s) {   // prologue: >= one block of worst-case demand
-    if (wld < n_words) { store_wseg(wring, wld, load_wseg(wsrc, wld, wvalid, lane), lane); wld += kSeg; }
-    if (MODE == 2 && pld < n_plane) { store_pseg(pring, pld, load_pseg(psrc, pld, pvalid, lane), lane); pld += kSeg; }
+// One block of kBlock steps: land prefetched ring segments, top up the rings
+// if they hold less than a block of worst-case demand (rare), prefetch the
+// next segments, decode into the LDS staging area, then store the staged block
+// with one 16-byte store per lane per KiB.
+template <int K, int MODE, int EB, bool PARTIAL>
+__device__ __forceinline__ void decode_block(uint32_t blk, const uint64_t (&pl)[K], ChunkState<K>& S, const ChunkParams& C,
+                                             const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
+                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage) {
+  constexpr uint32_t kStates = kWave * K;
+  constexpr uint32_t kBlkElems = kBlock * kStates;
+  const uint32_t lane = C.lane;
+  if (S.wn >= 1) { store_wseg(wring, S.wld, S.wp0, lane); S.wld += kSeg; }
+  if (S.wn >= 2) { store_wseg(wring, S.wld, S.wp1, lane); S.wld += kSeg; }
+  if (MODE == 2) {
+    if (S.pn >= 1) { store_pseg(pring, S.pld, S.pp0, lane); S.pld += kSeg; }
+    if (S.pn >= 2) { store_pseg(pring, S.pld, S.pp1, lane); S.pld += kSeg; }
+  }
+  {
+    const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
+    while (S.wld - S.wptr < need_w && S.wld < C.n_words) {
+      store_wseg(wring, S.wld, load_wseg(C.wsrc, S.wld, C.wvalid, lane), lane);
+      S.wld += kSeg;
+    }
+    if (MODE == 2) {
+      const uint32_t need_p = min(kBlkElems, C.n_plane - S.pptr);
+      while (S.pld - S.pptr < need_p && S.pld < C.n_plane) {
+        store_pseg(pring, S.pld, load_pseg(C.psrc, S.pld, C.pvalid, lane), lane);
+        S.pld += kSeg;
+      }
+    }
   }
   wave_sync();
-
-  const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
-  uint64_t pnext = 0;
-  if (MODE == 1) pnext = dplane[lane];
-  GLB uint16_t* out16 = (GLB uint16_t*)out8;
-
-  for (uint32_t blk = 0; blk < nblk; ++blk) {
-    // refills issued now, written to the rings after this block (<= 2 segments each)
-    uint64_t wp0 = 0, wp1 = 0;
-    int wn = 0;
-    if (wld < n_words && wld - wptr + kSeg <= kRing) {
-      wp0 = load_wseg(wsrc, wld, wvalid, lane); wn = 1;
-      if (wld + kSeg < n_words && wld - wptr + 2 * kSeg <= kRing) { wp1 = load_wseg(wsrc, wld + kSeg, wvalid, lane); wn = 2; }
+  // prefetch for the next block; always two loads per ring
+  S.wn = 0;
+  if (S.wld < C.n_words && S.wld - S.wptr + kSeg <= kRing) {
+    S.wn = 1;
+    if (S.wld + kSeg < C.n_words && S.wld - S.wptr + 2 * kSeg <= kRing) S.wn = 2;
+  }
+  S.wp0 = load_wseg_always(C.wsrc, S.wn >= 1 ? S.wld : 0u, C.wvalid, lane, (const GLB uint64_t*)C.cbase);
+  S.wp1 = load_wseg_always(C.wsrc, S.wn >= 2 ? S.wld + kSeg : 0u, C.wvalid, lane, (const GLB uint64_t*)C.cbase);
+  if (MODE == 2) {
+    S.pn = 0;
+    if (S.pld < C.n_plane && S.pld - S.pptr + kSeg <= kRing) {
+      S.pn = 1;
+      if (S.pld + kSeg < C.n_plane && S.pld - S.pptr + 2 * kSeg <= kRing) S.pn = 2;
     }
-    uint32_t pp0 = 0, pp1 = 0;
-    int pn = 0;
-    if (MODE == 2 && pld < n_plane && pld - pptr + kSeg <= kRing) {
-      pp0 = load_pseg(psrc, pld, pvalid, lane); pn = 1;
-      if (pld + kSeg < n_plane && pld - pptr + 2 * kSeg <= kRing) { pp1 = load_pseg(psrc, pld + kSeg, pvalid, lane); pn = 2; }
-    }
-    const uint64_t pcur = pnext;
-    if (MODE == 1 && blk + 1 < nblk) pnext = dplane[(blk + 1) * kLanes + lane];
+    S.pp0 = load_pseg_always(C.psrc, S.pn >= 1 ? S.pld : 0u, C.pvalid, lane, (const GLB uint32_t*)C.cbase);
+    S.pp1 = load_pseg_always(C.psrc, S.pn >= 2 ? S.pld + kSeg : 0u, C.pvalid, lane, (const GLB uint32_t*)C.cbase);
+  }
 
 #pragma unroll
-    for (int q = 0; q < kBlock; ++q) {
-      const uint32_t t = blk * kBlock + q;
-      if (PARTIAL && t >= nsteps) break;                 // wave-uniform
-      const uint32_t j = t * kLanes + lane;
-      const bool active = !PARTIAL || j < nc;
-      const uint64_t e = tbl[x & 4095u];
+  for (int q = 0; q < kBlock; ++q) {
+    const uint32_t t = blk * kBlock + q;
+    if (PARTIAL && t >= C.nsteps) break;                 // wave-uniform
+    const uint32_t sel = (uint32_t)q * 0x0101u | 0x0C0C0000u;
+#pragma unroll
+    for (int g = 0; g < K; ++g) {
+      const uint32_t jl = t * kStates + g * kWave + lane;   // element index within the chunk
+      const bool active = !PARTIAL || jl < C.nc;
+      const uint64_t e = tbl[S.x[g] & 4095u];
       const uint32_t elo = (uint32_t)e, ehi = (uint32_t)(e >> 32);
-      uint32_t xn = __umul24(elo & 0x1FFFu, x >> 12) + (elo >> 13);
-      if (PARTIAL && !active) xn = x;
+      uint32_t xn = __umul24(elo & 0x1FFFu, S.x[g] >> 12) + (elo >> 13);
+      if (PARTIAL && !active) xn = S.x[g];
       const bool need = xn < kL;
       const uint64_t m = __ballot(need);
-      const uint32_t w = wring[(wptr + lane_rank(m)) & (kRing - 1u)];
-      x = need ? ((xn << 16) | w) : xn;
-      wptr += (uint32_t)__popcll(m);
+      const uint32_t w = wring[lane_rank(m, S.wptr) & (kRing - 1u)];
+      S.x[g] = need ? ((xn << 16) | w) : xn;
+      S.wptr += (uint32_t)__popcll(m);
       uint32_t v = ehi;
       if (MODE == 1) {
-        v = with_plane(v, (uint32_t)(pcur >> (8 * q)) & 0xFFu);
+        v = plane_merge(v, pl[g], sel);
       } else if (MODE == 2) {
         const bool cons = active && (ehi >> 31);
         const uint64_t bm = __ballot(cons);
-        const uint32_t b = pring[(pptr + lane_rank(bm)) & (kRing - 1u)];
-        pptr += (uint32_t)__popcll(bm);
-        if (cons) v = with_plane(v, b);
+        const uint32_t b = pring[lane_rank(bm, S.pptr) & (kRing - 1u)];
+        S.pptr += (uint32_t)__popcll(bm);
+        if (cons) v = byte_merge(v, b);
       }
-      if (active) {
-        if (EB == 2) out16[base + j] = (uint16_t)v;
-        else out8[base + j] = (uint8_t)v;
-      }
+      const uint32_t si = (uint32_t)q * kStates + g * kWave + lane;   // element index within the block
+      if (EB == 2) ((LDS uint16_t*)stage)[si] = (uint16_t)v;
+      else stage[si] = (uint8_t)v;
     }
+  }
+}
 
-    if (wn >= 1) { store_wseg(wring, wld, wp0, lane); wld += kSeg; }
-    if (wn >= 2) { store_wseg(wring, wld, wp1, lane); wld += kSeg; }
-    if (MODE == 2) {
-      if (pn >= 1) { store_pseg(pring, pld, pp0, lane); pld += kSeg; }
-      if (pn >= 2) { store_pseg(pring, pld, pp1, lane); pld += kSeg; }
+template <int K, int EB, bool PARTIAL>
+__device__ __forceinline__ void flush_block(uint32_t blk, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
+  constexpr uint32_t kBlkElems = kBlock * kWave * K;
+  constexpr uint32_t kBlkBytes = kBlkElems * EB;
+  wave_sync();
+  const uint64_t blk_byte0 = (C.base + (uint64_t)blk * kBlkElems) * EB;
+  const uint32_t valid_bytes = PARTIAL ? min(kBlkBytes, (C.nc - min(C.nc, blk * kBlkElems)) * EB) : kBlkBytes;
+#pragma unroll
+  for (uint32_t i = 0; i < (kBlkBytes + 1023) / 1024; ++i) {
+    const uint32_t o = i * 1024u + C.lane * 16u;
+    if (o + 16u <= valid_bytes) {
+      const u32x4 d = *(const LDS u32x4*)(stage + o);
+      *(GLB u32x4*)(C.out8 + blk_byte0 + o) = d;
+    } else if (PARTIAL && o < valid_bytes) {
+      for (uint32_t k = o; k < min(o + 16u, valid_bytes); ++k) C.out8[blk_byte0 + k] = stage[k];
     }
-    wave_sync();
+  }
+}
+
+// Decode one chunk with one wavefront: K interleaved states per lane (state
+// v = g*64 + lane), MODE = plane mode, EB = element bytes, PARTIAL = chunk may
+// be shorter than 64*K*steps (the tensor's last chunk).
+template <int K, int MODE, int EB, bool PARTIAL>
+__device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
+                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage,
+                                             const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
+                                             uint32_t n_plane, GLB uint8_t* __restrict__ out8, uint64_t base,
+                                             uint32_t nc, uint32_t nsteps, int32_t* status) {
+  constexpr uint32_t kStates = kWave * K;
+  constexpr uint32_t kBlkU64 = kBlock * kStates / 8;   // dense-plane u64s per block
+  ChunkParams C;
+  C.lane = __lane_id();
+  const uint32_t wbytes = pad16(n_words * 2u);
+  C.wsrc = (const GLB uint64_t*)(cbase + 4u * kStates);
+  const GLB uint8_t* psrc8 = cbase + 4u * kStates + wbytes;
+  C.psrc = (const GLB uint32_t*)psrc8;
+  C.dplane = (const GLB uint64_t*)psrc8;
+  C.cbase = cbase;
+  C.out8 = out8;
+  C.base = base;
+  C.n_words = n_words;
+  C.n_plane = n_plane;
+  C.wvalid = wbytes / 8u;
+  C.pvalid = pad16(n_plane) / 4u;
+  C.nc = nc;
+  C.nsteps = nsteps;
+  C.nblk = (nsteps + kBlock - 1) / kBlock;
+
+  ChunkState<K> S;
+#pragma unroll
+  for (int g = 0; g < K; ++g) S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
+  S.wptr = S.wld = S.pptr = S.pld = 0;
+  S.wn = S.pn = 0;
+  S.wp0 = S.wp1 = 0;
+  S.pp0 = S.pp1 = 0;
+
+  // dense plane double buffer (blocks b and b+1), reloaded two blocks ahead
+  uint64_t plA[K], plB[K];
+#pragma unroll
+  for (int g = 0; g < K; ++g) {
+    plA[g] = 0;
+    plB[g] = 0;
+    if (MODE == 1) {
+      plA[g] = C.dplane[C.lane * K + g];
+      plB[g] = C.dplane[min(1u, C.nblk - 1) * kBlkU64 + C.lane * K + g];
+    }
+  }
+  // Consume the prologue loads here, so the loop body never waits on them.
+#pragma unroll
+  for (int g = 0; g < K; ++g) asm volatile("" ::"v"(S.x[g]), "v"(plA[g]), "v"(plB[g]));
+
+  // Two blocks per iteration so the dense-plane registers alternate without
+  // copies. Full chunks have an even block count (steps % 16 == 0), so the
+  // second half is unconditional and every iteration issues the same memory
+  // operations.
+  for (uint32_t blk = 0; blk < C.nblk; blk += 2) {
+    decode_block<K, MODE, EB, PARTIAL>(blk, plA, S, C, tbl, wring, pring, stage);
+    if (MODE == 1) {
+      const uint32_t nb = min(blk + 2, C.nblk - 1);
+#pragma unroll
+      for (int g = 0; g < K; ++g) plA[g] = C.dplane[nb * kBlkU64 + C.lane * K + g];
+    }
+    flush_block<K, EB, PARTIAL>(blk, C, stage);
+    if (PARTIAL && blk + 1 >= C.nblk) break;
+    decode_block<K, MODE, EB, PARTIAL>(blk + 1, plB, S, C, tbl, wring, pring, stage);
+    if (MODE == 1) {
+      const uint32_t nb = min(blk + 3, C.nblk - 1);
+#pragma unroll
+      for (int g = 0; g < K; ++g) plB[g] = C.dplane[nb * kBlkU64 + C.lane * K + g];
+    }
+    flush_block<K, EB, PARTIAL>(blk + 1, C, stage);
   }
 
-  const bool bad_state = x != kL;
-  const bool bad = __ballot(bad_state) != 0 || wptr != n_words || (MODE == 2 && pptr != n_plane);
+  bool bad_state = false;
+#pragma unroll
+  for (int g = 0; g < K; ++g) bad_state |= S.x[g] != kL;
+  const bool bad = __ballot(bad_state) != 0 || S.wptr != n_words || (MODE == 2 && S.pptr != n_plane);
   if (bad) report(status, BS_DEV_ERR_STREAM);
 }
 
-template <int EB, bool PARTIAL, bool COMPACT>
-__device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint64_t* tbl, LDS uint16_t* wring, LDS uint8_t* pring,
-                                                  const GLB uint8_t* cbase, uint32_t nw, uint32_t np, GLB uint8_t* out,
-                                                  uint64_t base, uint32_t nc, uint32_t nsteps, int32_t* status) {
+template <int K, int EB, bool PARTIAL, bool COMPACT>
+__device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint64_t* tbl, LDS uint16_t* wring,
+                                                  LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
+                                                  uint32_t nw, uint32_t np, GLB uint8_t* out, uint64_t base,
+                                                  uint32_t nc, uint32_t nsteps, int32_t* status) {
   if (EB == 1 || mode == 0)
-    decode_chunk<0, EB, PARTIAL>(tbl, wring, pring, cbase, nw, np, out, base, nc, nsteps, status);
+    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
   else if (mode == 1)
-    decode_chunk<1, EB, PARTIAL>(tbl, wring, pring, cbase, nw, np, out, base, nc, nsteps, status);
+    decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
   else if (COMPACT)
-    decode_chunk<2, EB, PARTIAL>(tbl, wring, pring, cbase, nw, np, out, base, nc, nsteps, status);
+    decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+}
+
+template <int K, bool COMPACT>
+__device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32_t mode, const LDS uint64_t* tbl,
+                                               LDS uint16_t* wring, LDS uint8_t* pring, LDS uint8_t* stage,
+                                               const GLB uint8_t* cbase, uint32_t nw, uint32_t np, GLB uint8_t* out,
+                                               uint64_t base, uint32_t nc, uint32_t nsteps, int32_t* status) {
+  if (eb == 2) {
+    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+  } else {
+    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+  }
 }
 
 template <bool COMPACT>
@@ -206,11 +355,14 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
                                                                uint32_t n_tasks, bs_chunk_task single,
                                                                int32_t* __restrict__ status) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ uint32_t s_cum[257];
-  __shared__ uint32_t s_val[256];
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
   LDS uint16_t* s_wring = (LDS uint16_t*)(smem + kTblBytes);
+  LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWringBytes);
   LDS uint8_t* s_pring = (LDS uint8_t*)(smem + kLdsLean);
+  // table-build scratch overlaps the staging area (unused until decoding starts)
+  LDS uint32_t* s_cum = (LDS uint32_t*)s_stage;        // 257 entries
+  LDS uint32_t* s_val = s_cum + 260;                    // 256 entries
+  LDS uint32_t* s_flag = s_val + 256;                   // table-check flag
 
   // ---- which tensor does this workgroup serve (wave-uniform binary search)
   bs_chunk_task T = single;
@@ -237,9 +389,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t lanes = (uint32_t)b[20] | ((uint32_t)b[21] << 8);
   const uint32_t nsym = (uint32_t)b[22] | ((uint32_t)b[23] << 8);
   const uint32_t nch = ld_u32(b + 24);
-  const uint64_t per = (uint64_t)kLanes * steps;
-  if (lanes != kLanes || steps == 0 || (steps % kBlock) != 0 || nsym == 0 || nsym > 256 ||
-      (eb == 1 && mode != 0) || nch != T.n_chunks || per == 0 || nch != (n + per - 1) / per) {
+  const uint64_t per = (uint64_t)lanes * steps;
+  if ((lanes != 64 && lanes != 128) || steps == 0 || (steps % (2 * kBlock)) != 0 || nsym == 0 ||
+      nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per == 0 || nch != (n + per - 1) / per) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
@@ -262,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     s_val[tid] = (ent & 0xFFFFu) | (ent & 0x80000000u);
   }
   if (tid < 256) s_cum[tid + 1] = f_own;
-  if (tid == 0) s_cum[0] = 0;
+  if (tid == 0) { s_cum[0] = 0; *s_flag = 0; }
   __syncthreads();
   for (uint32_t d = 1; d < 256; d <<= 1) {        // inclusive scan of s_cum[1..256]
     uint32_t add = (tid < 256 && tid >= d) ? s_cum[tid + 1 - d] : 0u;
@@ -270,9 +422,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (tid < 256) s_cum[tid + 1] += add;
     __syncthreads();
   }
-  bool bad_tbl = s_cum[256] != 4096u;
-  if (tid < nsym && f_own == 0) bad_tbl = true;
-  if (__syncthreads_or(bad_tbl)) {
+  if ((tid == 0 && s_cum[256] != 4096u) || (tid < nsym && f_own == 0)) *s_flag = 1;
+  __syncthreads();
+  if (*s_flag) {
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
@@ -288,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   __syncthreads();
 
   // ---- one chunk per wavefront
-  const uint32_t wave = tid / kLanes;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform: keeps chunk state scalar
   const uint32_t chunk = group * kWaves + wave;
   if (chunk >= nch) return;
   const GLB uint8_t* ce = b + ctab + 16ull * chunk;
@@ -296,10 +448,10 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t nw = ld_u32(ce + 8), np = ld_u32(ce + 12);
   const uint64_t cbase_idx = (uint64_t)chunk * per;
   const uint32_t nc = (uint32_t)((n - cbase_idx) < per ? (n - cbase_idx) : per);
-  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
-  const uint32_t dense_plane = ((nsteps + kBlock - 1) / kBlock) * kBlock * kLanes;
-  bool ok = (off % 16) == 0 && off + 4ull * kLanes + pad16(nw * 2u) + pad16(np) <= T.blob_bytes &&
-            nw <= nsteps * kLanes;
+  const uint32_t nsteps = (nc + lanes - 1) / lanes;
+  const uint32_t dense_plane = ((nsteps + kBlock - 1) / kBlock) * kBlock * lanes;
+  bool ok = (off % 16) == 0 && off + 4ull * lanes + pad16(nw * 2u) + pad16(np) <= T.blob_bytes &&
+            nw <= nsteps * lanes && T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
   if (mode == 1) ok = ok && np == dense_plane;
   if (mode == 2) ok = ok && np <= nc;
   if (mode == 0) ok = ok && np == 0;
@@ -310,15 +462,13 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const GLB uint8_t* cbase = b + off;
   LDS uint16_t* wring = s_wring + wave * kRing;
   LDS uint8_t* pring = s_pring + wave * kRing;
+  LDS uint8_t* stage = s_stage + wave * kStageMax;
   GLB uint8_t* out = (GLB uint8_t*)T.out;
   const bool partial = nc != per;
-  if (eb == 2) {
-    if (partial) decode_chunk_mode<2, true, COMPACT>(mode, s_tbl, wring, pring, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
-    else decode_chunk_mode<2, false, COMPACT>(mode, s_tbl, wring, pring, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
-  } else {
-    if (partial) decode_chunk_mode<1, true, COMPACT>(0, s_tbl, wring, pring, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
-    else decode_chunk_mode<1, false, COMPACT>(0, s_tbl, wring, pring, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
-  }
+  if (lanes == 64)
+    decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
+  else
+    decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
@@ -362,10 +512,10 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   info->lanes = (uint32_t)h[20] | ((uint32_t)h[21] << 8);
   info->n_syms = (uint32_t)h[22] | ((uint32_t)h[23] << 8);
   info->n_chunks = u32(24);
-  if (h[7] != 12 || info->lanes != kLanes || info->steps == 0 || info->steps % kBlock || info->n_syms == 0 ||
+  if (h[7] != 12 || (info->lanes != 64 && info->lanes != 128) || info->steps == 0 || info->steps % (2 * kBlock) || info->n_syms == 0 ||
       info->n_syms > 256 || (info->elem_bytes != 1 && info->elem_bytes != 2) || info->plane_mode > 2)
     return BS_ERR_FORMAT;
-  const uint64_t per = (uint64_t)kLanes * info->steps;
+  const uint64_t per = (uint64_t)info->lanes * info->steps;
   if (info->n_chunks != (info->n + per - 1) / per) return BS_ERR_FORMAT;
   return BS_OK;
 }
@@ -373,7 +523,7 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
 int bs_chunk_decode(const uint8_t* d_blob, uint64_t blob_bytes, void* d_out, uint64_t n, uint32_t n_chunks,
                     uint32_t plane_mode, int32_t* d_status, void* stream) {
   if (!d_status || (n > 0 && (!d_blob || !d_out))) return BS_ERR_ARG;
-  if (((uintptr_t)d_blob & 15u) != 0 || plane_mode > 2) return BS_ERR_ARG;
+  if (((uintptr_t)d_blob & 15u) != 0 || ((uintptr_t)d_out & 15u) != 0 || plane_mode > 2) return BS_ERR_ARG;
   if (n == 0 || n_chunks == 0) return BS_OK;
   bs_chunk_task t{d_blob, blob_bytes, d_out, n, 0u, n_chunks};
   return launch(nullptr, 0u, t, groups_for(n_chunks), plane_mode, d_status, stream);

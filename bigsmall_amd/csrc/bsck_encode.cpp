@@ -11,10 +11,11 @@
 //   bf16/bytes, plane_mode 0:     every distinct value is a symbol (<= 256).
 // The encoder picks the smallest by estimated entropy unless a mode is forced.
 //
-// rANS encoding per chunk: 64 interleaved 32-bit states (L = 2^16, M = 2^12,
-// 16-bit renormalisation, the reference's state machine, bigsmall/codecs/rans.py:115-162),
-// walked from the last step back to the first; the renorm words are laid out
-// so the decoder consumes them step-ascending, lane-ascending.
+// rANS encoding per chunk: 64*K interleaved 32-bit states (K = 1 or 2 per
+// wavefront lane; L = 2^16, M = 2^12, 16-bit renormalisation: the reference's
+// state machine, bigsmall/codecs/rans.py:115-162), walked from the last step
+// back to the first; the renorm words are laid out so the decoder consumes
+// them step-ascending, state-ascending.
 #include <stdint.h>
 #include <string.h>
 
@@ -28,10 +29,11 @@
 
 namespace {
 
-constexpr uint32_t kLanes = 64;
+constexpr uint32_t kWave = 64;        // lanes of a wavefront
 constexpr uint32_t kL = 1u << 16;
 constexpr uint32_t kM = 4096;
 constexpr uint32_t kBlock = 8;
+constexpr uint32_t kStepAlign = 16;   // steps per chunk: a multiple of two blocks
 
 inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
 
@@ -205,21 +207,23 @@ bool make_plan(const std::vector<uint64_t>& hist, uint32_t eb, int forced, Plan&
 }
 
 // Encode one chunk into `out` (states | words | plane, each 16-padded).
-void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, uint32_t& n_words,
-                  uint32_t& n_plane, std::vector<uint8_t>& out) {
-  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+// `lanes` = 64*K interleaved states; virtual lane v = g*64 + l is state group g
+// of wavefront lane l. Step t covers elements t*lanes .. t*lanes+lanes-1.
+void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, uint32_t lanes,
+                  uint32_t& n_words, uint32_t& n_plane, std::vector<uint8_t>& out) {
+  const uint32_t nsteps = (nc + lanes - 1) / lanes;
+  const uint32_t K = lanes / kWave;
   std::vector<uint16_t> words(nc + 1);
   size_t pos = words.size();
-  uint32_t x[kLanes];
-  for (uint32_t l = 0; l < kLanes; ++l) x[l] = kL;
+  std::vector<uint32_t> x(lanes, kL);
   const uint16_t* w16 = (const uint16_t*)src;
   const uint8_t* w8 = (const uint8_t*)src;
   auto sym_at = [&](uint64_t j) -> uint32_t { return P.sym_of[P.eb == 2 ? w16[base + j] : w8[base + j]]; };
   uint64_t xmax[256];
   for (uint32_t s = 0; s < P.nsym; ++s) xmax[s] = (uint64_t)P.freq[s] << 20;
   for (uint32_t t = nsteps; t-- > 0;) {
-    for (uint32_t l = kLanes; l-- > 0;) {
-      const uint64_t j = (uint64_t)t * kLanes + l;
+    for (uint32_t l = lanes; l-- > 0;) {
+      const uint64_t j = (uint64_t)t * lanes + l;
       if (j >= nc) continue;
       const uint32_t s = sym_at(j), f = P.freq[s];
       uint32_t v = x[l];
@@ -231,11 +235,14 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
   n_words = (uint32_t)(words.size() - pos);
   std::vector<uint8_t> plane;
   if (P.mode == 1) {
+    // dense plane: per 8-step block, wavefront lane l's 8*K bytes are contiguous,
+    // group-major: byte (g, q) of lane l at l*8K + g*8 + q
     const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
-    plane.assign((size_t)nblk * kBlock * kLanes, 0);
+    plane.assign((size_t)nblk * kBlock * lanes, 0);
     for (uint32_t j = 0; j < nc; ++j) {
-      const uint32_t w = w16[base + j], t = j / kLanes, l = j % kLanes;
-      plane[(size_t)(t / kBlock) * kBlock * kLanes + l * kBlock + (t % kBlock)] = (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
+      const uint32_t w = w16[base + j], t = j / lanes, v = j % lanes, g = v / kWave, l = v % kWave;
+      plane[(size_t)(t / kBlock) * kBlock * lanes + l * kBlock * K + g * kBlock + (t % kBlock)] =
+          (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
     }
   } else if (P.mode == 2) {
     plane.reserve(nc);
@@ -246,27 +253,31 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
   }
   n_plane = (uint32_t)plane.size();
   const uint64_t wb = pad16((uint64_t)n_words * 2), pb = pad16(n_plane);
-  out.assign(4 * kLanes + wb + pb, 0);
-  for (uint32_t l = 0; l < kLanes; ++l) put32(out.data() + 4 * l, x[l]);
-  for (uint32_t i = 0; i < n_words; ++i) put16(out.data() + 4 * kLanes + 2 * i, words[pos + i]);
-  if (n_plane) memcpy(out.data() + 4 * kLanes + wb, plane.data(), n_plane);
+  out.assign(4 * lanes + wb + pb, 0);
+  for (uint32_t l = 0; l < lanes; ++l) put32(out.data() + 4 * l, x[l]);
+  for (uint32_t i = 0; i < n_words; ++i) put16(out.data() + 4 * lanes + 2 * i, words[pos + i]);
+  if (n_plane) memcpy(out.data() + 4 * lanes + wb, plane.data(), n_plane);
 }
 
 }  // namespace
 
 extern "C" {
 
-int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t steps, uint64_t* bound) {
-  if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kBlock) return BS_ERR_ARG;
-  const uint64_t per = (uint64_t)kLanes * steps;
+static bool lanes_ok(uint32_t lanes) { return lanes == 64 || lanes == 128; }
+
+int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t* bound) {
+  if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes))
+    return BS_ERR_ARG;
+  const uint64_t per = (uint64_t)lanes * steps;
   const uint64_t nch = (n + per - 1) / per;
-  *bound = pad16(32 + 4 * 256) + 16 * nch + nch * (4 * kLanes + pad16(2 * per) + pad16(per) + 32);
+  *bound = pad16(32 + 4 * 256) + 16 * nch + nch * (4 * lanes + pad16(2 * per) + pad16(per) + 32);
   return BS_OK;
 }
 
-int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t steps, int32_t mode,
+int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t* dst, uint64_t cap, uint64_t* out_len, int n_threads) {
-  if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kBlock) return BS_ERR_ARG;
+  if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes))
+    return BS_ERR_ARG;
   if (n == 0) { *out_len = 0; return BS_OK; }
   if (!src || !dst) return BS_ERR_ARG;
   if (n_threads < 1) n_threads = 1;
@@ -274,7 +285,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t s
   Plan P;
   if (!make_plan(hist, elem_bytes, mode, P)) return BS_ERR_ARG;
 
-  const uint64_t per = (uint64_t)kLanes * steps;
+  const uint64_t per = (uint64_t)lanes * steps;
   const uint64_t nch64 = (n + per - 1) / per;
   if (nch64 > 0xFFFFFFFFull) return BS_ERR_ARG;
   const uint32_t nch = (uint32_t)nch64;
@@ -283,7 +294,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t s
   parallel_for(nch, n_threads, [&](uint64_t c) {
     const uint64_t base = c * per;
     const uint32_t nc = (uint32_t)std::min<uint64_t>(per, n - base);
-    encode_chunk(P, src, base, nc, nw[c], np[c], chunks[c]);
+    encode_chunk(P, src, base, nc, lanes, nw[c], np[c], chunks[c]);
   });
 
   const uint64_t ctab = pad16(32 + 4ull * P.nsym);
@@ -295,7 +306,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t s
   memset(dst, 0, ctab + 16ull * nch + 16);
   memcpy(dst, "BSCK", 4);
   dst[4] = 1; dst[5] = (uint8_t)elem_bytes; dst[6] = (uint8_t)P.mode; dst[7] = 12;
-  put64(dst + 8, n); put32(dst + 16, steps); put16(dst + 20, kLanes); put16(dst + 22, P.nsym);
+  put64(dst + 8, n); put32(dst + 16, steps); put16(dst + 20, lanes); put16(dst + 22, P.nsym);
   put32(dst + 24, nch); put32(dst + 28, 0);
   for (uint32_t s = 0; s < P.nsym; ++s)
     put32(dst + 32 + 4 * s, (P.value[s] & 0xFFFF) | (P.freq[s] << 16) | (P.consume[s] << 31));

@@ -57,7 +57,7 @@ typedef struct {
     uint64_t n;          /* elements */
     uint32_t n_chunks;
     uint32_t steps;      /* rANS steps per lane per full chunk */
-    uint32_t lanes;      /* interleaved rANS states per chunk (64) */
+    uint32_t lanes;      /* interleaved rANS states per chunk (64 or 128) */
     uint32_t n_syms;
     uint32_t elem_bytes; /* 2 = bf16 words, 1 = bytes (fp8) */
     uint32_t plane_mode; /* 0 none, 1 dense, 2 compact */
@@ -82,7 +82,7 @@ int bs_chunk_inspect(const uint8_t *h_blob, uint64_t len, bs_chunk_info *info);
  * ceil(n_chunks / bs_chunk_chunks_per_group())). */
 int bs_chunk_chunks_per_group(void);
 
-/* Decode one BSCK blob into d_out. `plane_mode` is the header's (from
+/* Decode one BSCK blob into d_out (16-byte aligned). `plane_mode` is the header's (from
  * bs_chunk_inspect). Device counterpart of the codec plugin's
  * decode(blob, extras, n_weights) (bigsmall/codec_registry.py:39-42). */
 int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uint64_t n,
@@ -99,8 +99,8 @@ int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32
 /* Host encoder for BSCK. `flags`: BS_CHUNK_MODE_AUTO or a forced plane mode.
  * Replaces the encode half of the codec plugin pair (bigsmall/codec_registry.py:39-47). */
 #define BS_CHUNK_MODE_AUTO (-1)
-int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t steps, uint64_t *bound);
-int bs_chunk_encode(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t steps, int32_t mode,
+int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t *bound);
+int bs_chunk_encode(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t *h_dst, uint64_t cap, uint64_t *out_len, int n_threads);
 
 #ifdef __cplusplus

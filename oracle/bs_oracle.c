@@ -765,25 +765,27 @@ out:
  * counterpart). CPU restatement of the device decoder's semantics, used as a
  * checker of the product encoder. Format:
  *   [0]  "BSCK"  [4] u8 version=1  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
- *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64)
+ *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2)
  *   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
  *   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
  *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16)
- * Element j of chunk c sits at c*lanes*steps + j; lane = j % lanes, step = j / lanes.
- * Decode step order: steps ascending; renorm words consumed lane-ascending
- * among lanes whose state fell below L. plane_mode 1 (dense): every element
- * consumes one byte, stored in blocks of 8 steps, lane-major (lane l's 8 bytes
- * contiguous). plane_mode 2 (compact): consuming elements read bytes in decode
- * order. plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
+ * Element j of chunk c sits at c*lanes*steps + j; state v = j % lanes, step = j / lanes.
+ * Decode step order: steps ascending; renorm words consumed in ascending state
+ * order among states that fell below L. plane_mode 1 (dense): every element
+ * consumes one byte, stored in blocks of 8 steps; state v = g*64 + l (wavefront
+ * lane l, group g) keeps its byte for step 8b+q at b*8*lanes + l*8*(lanes/64) + g*8 + q.
+ * plane_mode 2 (compact): consuming elements read bytes in decode order.
+ * plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
  * ------------------------------------------------------------------------ */
 int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *out_v) {
     if (len < 32 || memcmp(blob, "BSCK", 4) != 0) return ORC_ERR_FORMAT;
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
-    if (ver != 1 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || lanes != 64 || steps == 0 || steps % 8)
+    if (ver != 1 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128) ||
+        steps == 0 || steps % 16)
         return ORC_ERR_FORMAT;
     if (n != n_weights) return ORC_ERR_COUNT;
     if (nsym == 0 || nsym > 256) return ORC_ERR_FORMAT;
@@ -811,7 +813,7 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
         uint64_t base = (uint64_t)ci * per;
         uint64_t nc = n - base < per ? n - base : per;
         uint64_t nsteps = (nc + lanes - 1) / lanes;
-        uint32_t x[64];
+        uint32_t x[256];
         for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
         uint64_t wp = 0, pp = 0;
         for (uint64_t t = 0; t < nsteps; t++) {
@@ -828,8 +830,8 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
                 if (cons[s]) {
                     uint32_t b;
                     if (mode == 1) {
-                        uint64_t blk = t / 8, q = t % 8;
-                        uint64_t idx = blk * 8 * lanes + (uint64_t)l * 8 + q;
+                        uint64_t blk = t / 8, q = t % 8, g = l / 64, wl = l % 64, K = lanes / 64;
+                        uint64_t idx = blk * 8 * lanes + wl * 8 * K + g * 8 + q;
                         if (idx >= np) return ORC_ERR_FORMAT;
                         b = pl[idx];
                     } else if (mode == 2) {

@@ -34,10 +34,10 @@ def torch_gpu():
     return torch
 
 
-def _check_one(torch_gpu, words, steps=512, mode=-1, label=""):
+def _check_one(torch_gpu, words, steps=512, mode=-1, label="", lanes=128):
     from bigsmall_amd.codecs import bf16_chunked as bc
-    _say(f"[bsck] {label} n={words.size} dtype={words.dtype} steps={steps} mode={mode}")
-    blob = bc.encode_array(words, steps=steps, mode=mode)
+    _say(f"[bsck] {label} n={words.size} dtype={words.dtype} steps={steps} mode={mode} lanes={lanes}")
+    blob = bc.encode_array(words, steps=steps, mode=mode, lanes=lanes)
     eb = words.dtype.itemsize
     gpu = bc.decode(blob, {}, words.size, elem_bytes=eb) if eb == 2 else bc.decode_fp8(blob, {}, words.size)
     assert hashlib.md5(gpu).hexdigest() == hashlib.md5(words.tobytes()).hexdigest(), label
@@ -45,19 +45,21 @@ def _check_one(torch_gpu, words, steps=512, mode=-1, label=""):
     return blob
 
 
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 511, 4097, 32768, 32768 * 3 + 1000, 1 << 20])
-def test_gaussian_sizes(torch_gpu, n):
+@pytest.mark.parametrize("lanes", [64, 128])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 127, 129, 511, 4097, 32768, 65536 * 3 + 1000, 1 << 20])
+def test_gaussian_sizes(torch_gpu, n, lanes):
     rng = np.random.default_rng(n)
-    _check_one(torch_gpu, _bf16(rng.standard_normal(n) * 0.02), label=f"gauss{n}")
+    _check_one(torch_gpu, _bf16(rng.standard_normal(n) * 0.02), label=f"gauss{n}", lanes=lanes)
 
 
+@pytest.mark.parametrize("lanes", [64, 128])
 @pytest.mark.parametrize("mode", [-1, 1, 2])
-@pytest.mark.parametrize("steps", [8, 64, 512, 1024])
-def test_modes_and_steps(torch_gpu, mode, steps):
+@pytest.mark.parametrize("steps", [16, 64, 512, 1024])
+def test_modes_and_steps(torch_gpu, mode, steps, lanes):
     rng = np.random.default_rng(steps + 7 * mode)
     w = _bf16(rng.standard_normal(200_003) * 0.02)
     w[rng.permutation(w.size)[: w.size // 2]] = 0          # 50% exact zeros (compact mode pays off)
-    _check_one(torch_gpu, w, steps=steps, mode=mode, label=f"halfzero s{steps} m{mode}")
+    _check_one(torch_gpu, w, steps=steps, mode=mode, label=f"halfzero s{steps} m{mode}", lanes=lanes)
 
 
 def test_edge_words_and_heavy_tails(torch_gpu):
@@ -68,7 +70,8 @@ def test_edge_words_and_heavy_tails(torch_gpu):
     t = _bf16(rng.standard_t(3, 300_000) * 0.02 / np.sqrt(3))
     _check_one(torch_gpu, t, label="student-t")
     allw = rng.integers(0, 65536, 300_000).astype(np.uint16)  # every exponent present
-    _check_one(torch_gpu, allw, label="uniform words")
+    _check_one(torch_gpu, allw, label="uniform words")        # ring refills take the slow path
+    _check_one(torch_gpu, allw, label="uniform words k1", lanes=64)
 
 
 def test_exact_value_modes(torch_gpu):
@@ -78,6 +81,7 @@ def test_exact_value_modes(torch_gpu):
     _check_one(torch_gpu, np.full(70_000, 0x3F80, np.uint16), mode=0, label="constant")
     fp8 = rng.integers(0, 256, 500_000).astype(np.uint8)
     _check_one(torch_gpu, fp8, label="fp8 uniform")
+    _check_one(torch_gpu, fp8[:100_001], label="fp8 uniform k1", lanes=64)
     import torch
     x = torch.randn(300_000, generator=torch.Generator().manual_seed(5)).to(torch.float8_e4m3fn)
     _check_one(torch_gpu, x.view(torch.uint8).numpy(), label="fp8 e4m3 N(0,1)")
@@ -90,7 +94,7 @@ def test_batched_launch_matches_single(torch_gpu):
     rng = np.random.default_rng(13)
     sizes = [5, 64 * 512, 64 * 512 + 3, 1 << 18, 777_777]
     words = [_bf16(rng.standard_normal(s) * (0.01 + 0.01 * i)) for i, s in enumerate(sizes)]
-    blobs = [bc.encode_array(w) for w in words]
+    blobs = [bc.encode_array(w, lanes=64 if i % 2 else 128) for i, w in enumerate(words)]
     _say(f"[bsck] batch of {len(blobs)} blobs")
     dev = torch.device("cuda")
     d = [upload_bytes(b, dev) for b in blobs]
