@@ -2,25 +2,26 @@
 // engine, decoded on CDNA4 (gfx950).
 //
 // Format (little-endian; produced by bsck_encode.cpp):
-//   [0]  "BSCK"  [4] u8 version=1  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
-//   [7]  u8 prec_log2 = 12  [8] u64 n  [16] u32 steps  [20] u16 lanes = 64
+//   [0]  "BSCK"  [4] u8 version=2  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+//   [7]  u8 prec_log2 = 12  [8] u64 n  [16] u32 steps  [20] u16 lanes = 64*K
 //   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
 //   [32] n_syms x u32 symbol entries: bits 0..15 output value (bf16 word with
 //        zero sign/mantissa for exponent symbols, or the exact word/byte),
 //        bits 16..28 quantised frequency (sum 4096), bit 31 = reads one plane byte
 //   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
-//   chunk (16-aligned): 64 x u32 initial states | n_words x u16 renorm words
-//        (pad 16) | n_plane plane bytes (pad 16)
+//   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l) |
+//        n_words x u16 renorm words (pad 16) | n_plane plane bytes (pad 16)
 //
-// Element j of chunk c is element c*64*steps + j of the tensor; lane j%64
-// decodes it at step j/64, so one step of a wavefront produces 64 consecutive
-// outputs (one 128-byte line for bf16). The 64 rANS states of a chunk share one
-// 16-bit word stream: at each step the lanes whose state fell below L=2^16 take
-// the next words in lane order, placed with a wavefront ballot + mbcnt prefix.
+// A chunk is decoded by one wavefront. Lane l owns K interleaved rANS states
+// (g = 0..K-1); at step t state (g, l) decodes element t*64K + l*K + g of the
+// chunk, so a lane's K outputs of a step are adjacent and one step of the
+// wavefront produces 64*K consecutive elements. The 64*K states share one
+// 16-bit renorm word stream, consumed per step group by group (g ascending),
+// lanes ascending among the lanes whose state fell below L = 2^16; the words
+// are placed with a wavefront ballot + mbcnt prefix.
 // Plane bytes (sign<<7 | mantissa) complete bf16 exponent symbols:
 //   plane_mode 1 (dense): every element has one, stored per 8-step block with
-//                         lane l's 8 bytes contiguous (one 8-byte load per lane
-//                         per block, no prefix needed);
+//                         lane l's 8K bytes contiguous, step-major (byte q*K+g);
 //   plane_mode 2 (compact): only elements whose symbol has bit 31 set have one,
 //                         in decode order (ballot + mbcnt again);
 //   plane_mode 0: no plane (every symbol is an exact value).
@@ -29,8 +30,14 @@
 // 32-bit state, L = 2^16, 16-bit renormalisation, M = 2^12):
 //   slot = x & 4095; s = sym(slot); x = f[s]*(x>>12) + slot - cf[s];
 //   if x < L: x = (x << 16) | next_word
-// A valid chunk ends with every lane back at x == L and every word and plane
+// A valid chunk ends with every state back at x == L and every word and plane
 // byte consumed; anything else is reported as BS_DEV_ERR_STREAM.
+//
+// Two decode-table layouts live in LDS (4096 slots x 8 bytes):
+//   dense bf16 (plane_mode 1): {f | exponent << 24, slot - cf}; the update is
+//     one shift and one v_mad_u32_u24 (which ignores bits 24..31 of f's word),
+//     and the exponent byte is placed with v_perm;
+//   generic (plane modes 0/2, bytes): {f | (slot - cf) << 13, value | consume << 31}.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,27 +49,32 @@ namespace {
 #define GLB __attribute__((address_space(1)))
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr uint32_t kVersion = 2;
 constexpr int kWave = 64;                 // lanes of a wavefront
 constexpr int kWaves = 8;                 // chunks (wavefronts) per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kBlock = 8;                 // steps per block (plane block, output flush, refill check)
-constexpr uint32_t kRing = 2048;          // per-wave word ring (u16) and plane ring (bytes)
-constexpr uint32_t kSeg = 256;            // refill segment: words (64 lanes x 8 B) / plane bytes (64 x 4 B)
+constexpr uint32_t kRing = 2048;          // per-wave renorm-word ring (u16 entries), power of two
+constexpr uint32_t kMirror = 64;          // ring words [0, 64) are mirrored after the ring end
+constexpr uint32_t kRingBytes = (kRing + kMirror) * 2;
+constexpr uint32_t kPRing = 4096;         // per-wave compact-plane ring (bytes)
+constexpr uint32_t kWSeg = 512;           // words per word-ring segment (64 lanes x 16 bytes)
+constexpr uint32_t kPSeg = 1024;          // bytes per plane-ring segment
 constexpr uint32_t kL = 1u << 16;
 // dynamic LDS layout (bytes): decode table | word rings | output staging | plane rings (compact launches)
 constexpr uint32_t kTblBytes = 4096 * 8;
-constexpr uint32_t kWringBytes = kWaves * kRing * 2;
-constexpr uint32_t kStageMax = kBlock * 128 * 2;   // per wave: 8 steps x up to 128 states x 2 bytes
-constexpr uint32_t kLdsLean = kTblBytes + kWringBytes + kWaves * kStageMax;
-constexpr uint32_t kLdsCompact = kLdsLean + kWaves * kRing;
+constexpr int kHalf = kBlock / 2;         // steps per output flush (staging holds half a block)
+constexpr uint32_t kStageMax = kHalf * 128 * 2;    // per wave: 4 steps x up to 128 states x 2 bytes
+constexpr uint32_t kLdsLean = kTblBytes + kWaves * (kRingBytes + kStageMax);
+constexpr uint32_t kLdsCompact = kLdsLean + kWaves * kPRing;
 
 __device__ __forceinline__ uint32_t ld_u32(const GLB uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
 
-// rank of this lane among the set lanes of m, plus `base`
-__device__ __forceinline__ uint32_t lane_rank(uint64_t m, uint32_t base) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, base));
+// rank of this lane among the set lanes of m
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -71,49 +83,60 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Makes the values available at this point: every load producing them is
+// issued before it, and nothing can sink them under a later branch.
+template <int K>
+__device__ __forceinline__ void consume(const uint32_t (&v)[K]) {
+  if (K == 1) asm volatile("" ::"v"(v[0]));
+  if (K == 2) asm volatile("" ::"v"(v[0]), "v"(v[K - 1]));
+}
+
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
 
 __device__ __forceinline__ void report(int32_t* status, int32_t bits) {
   if (__lane_id() == 0) atomicOr(status, bits);
 }
 
-// A plane byte b = sign<<7 | mantissa completes an exponent symbol's value v:
-// (b | b<<8) & 0x807F puts the sign at bit 15 and the mantissa at bits 0..6.
-// `sel` picks byte q of the 8 plane bytes {hi:lo} into bytes 0 and 1.
-__device__ __forceinline__ uint32_t plane_merge(uint32_t v, uint64_t bytes8, uint32_t sel) {
-  const uint32_t bb = __builtin_amdgcn_perm((uint32_t)(bytes8 >> 32), (uint32_t)bytes8, sel);
-  return (bb & 0x807Fu) | v;
-}
 __device__ __forceinline__ uint32_t byte_merge(uint32_t v, uint32_t b) { return ((b * 0x101u) & 0x807Fu) | v; }
 
-// ---- ring refills: lane l moves 8 bytes (4 words) / 4 bytes of a 256-entry segment
-__device__ __forceinline__ uint64_t load_wseg(const GLB uint64_t* src, uint32_t pos, uint32_t valid, uint32_t lane) {
-  const uint32_t slot = pos / 4u + lane;
-  return slot < valid ? src[slot] : 0ull;
+// ---- ring refills. A segment is 64 lanes x 16 bytes (512 renorm words or 1024
+// compact-plane bytes); segment positions are multiples of the segment size.
+
+// Load this lane's 16 bytes of the segment at `pos16` (16-byte units);
+// out-of-range lanes read `safe` (the chunk's state words, always in bounds),
+// so every call issues exactly one load per lane.
+__device__ __forceinline__ u32x4 load_seg(const GLB u32x4* src, uint32_t pos16, uint32_t valid16, uint32_t lane,
+                                          const GLB u32x4* safe) {
+  const uint32_t slot = pos16 + lane;
+  return *(slot < valid16 ? src + slot : safe + (lane & 15u));
 }
-// Unconditional variant for prefetches: out-of-range slots re-read `safe` (the
-// chunk's state words: always inside the blob and in cache) so every block
-// issues the same number of loads; a fixed count lets the compiler's waitcnt
-// placement wait only for the data actually needed.
-__device__ __forceinline__ uint64_t load_wseg_always(const GLB uint64_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
-                                                     const GLB uint64_t* safe) {
-  const uint32_t slot = pos / 4u + lane;
-  return *(slot < valid ? src + slot : safe + (lane & 31u));
+// Word ring: words [0, kMirror) also live at [kRing, kRing + kMirror), so a
+// read at (ring position mod kRing) + rank, rank < 64, never wraps.
+__device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, u32x4 v, uint32_t lane) {
+  const uint32_t r = (pos + lane * 8u) & (kRing - 1u);
+  *(LDS u32x4*)(ring + r) = v;
+  if (r < kMirror) *(LDS u32x4*)(ring + kRing + r) = v;
 }
-__device__ __forceinline__ uint32_t load_pseg_always(const GLB uint32_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
-                                                     const GLB uint32_t* safe) {
-  const uint32_t slot = pos / 4u + lane;
-  return *(slot < valid ? src + slot : safe + lane);
+__device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, u32x4 v, uint32_t lane) {
+  *(LDS u32x4*)(ring + ((pos + lane * 16u) & (kPRing - 1u))) = v;
 }
-__device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, uint64_t v, uint32_t lane) {
-  *(LDS uint64_t*)(ring + ((pos + lane * 4u) & (kRing - 1u))) = v;
-}
-__device__ __forceinline__ uint32_t load_pseg(const GLB uint32_t* src, uint32_t pos, uint32_t valid, uint32_t lane) {
-  const uint32_t slot = pos / 4u + lane;
-  return slot < valid ? src[slot] : 0u;
-}
-__device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, uint32_t v, uint32_t lane) {
-  *(LDS uint32_t*)(ring + ((pos + lane * 4u) & (kRing - 1u))) = v;
+
+template <int K>
+struct PlaneRegs {   // dense plane bytes of one block: 8*K per lane
+  uint64_t b[K];
+};
+template <int K>
+__device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, uint32_t blk, uint32_t lane) {
+  PlaneRegs<K> r;
+  const GLB uint8_t* p = dplane + (uint64_t)blk * (kBlock * kWave * K) + lane * 8u * K;
+  if (K == 2) {
+    const u32x4 v = *(const GLB u32x4*)p;
+    r.b[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
+    r.b[K - 1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
+  } else {
+    r.b[0] = *(const GLB uint64_t*)p;
+  }
+  return r;
 }
 
 // Per-wavefront decode state of one chunk.
@@ -122,114 +145,28 @@ struct ChunkState {
   uint32_t x[K];
   uint32_t wptr, wld;    // word ring holds words [wptr, wld)
   uint32_t pptr, pld;    // plane ring (compact mode) holds bytes [pptr, pld)
-  uint32_t wn, pn;       // segments prefetched for landing at the next block start
-  uint64_t wp0, wp1;
-  uint32_t pp0, pp1;
+  bool wn, pn;           // a segment is in flight for landing at the next block start
+  u32x4 wp, pp;
 };
 
 // Chunk-constant parameters.
 struct ChunkParams {
-  const GLB uint64_t* wsrc;     // renorm words, as 8-byte segments
-  const GLB uint32_t* psrc;     // compact plane, as 4-byte segments
-  const GLB uint64_t* dplane;   // dense plane, 8 bytes per lane per state group per block
-  const GLB uint8_t* cbase;     // chunk start (its state words are a safe dummy address)
+  const GLB u32x4* wsrc;        // renorm words, 16-byte units
+  const GLB u32x4* psrc;        // compact plane, 16-byte units
+  const GLB uint8_t* dplane;    // dense plane: 8*K bytes per lane per block
+  const GLB u32x4* safe;        // the chunk's state words: an always-valid dummy address
   GLB uint8_t* out8;
   uint64_t base;                // first element of the chunk
-  uint32_t n_words, n_plane, wvalid, pvalid, nc, nsteps, nblk, lane;
+  uint32_t n_words, n_plane, wvalid16, pvalid16, nc, nsteps, nblk, lane;
 };
 
-// One block of kBlock steps: land prefetched ring segments, top up the rings
-// if they hold less than a block of worst-case demand (rare), prefetch the
-// next segments, decode into the LDS staging area, then store the staged block
-// with one 16-byte store per lane per KiB.
-template <int K, int MODE, int EB, bool PARTIAL>
-__device__ __forceinline__ void decode_block(uint32_t blk, const uint64_t (&pl)[K], ChunkState<K>& S, const ChunkParams& C,
-                                             const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
-                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage) {
-  constexpr uint32_t kStates = kWave * K;
-  constexpr uint32_t kBlkElems = kBlock * kStates;
-  const uint32_t lane = C.lane;
-  if (S.wn >= 1) { store_wseg(wring, S.wld, S.wp0, lane); S.wld += kSeg; }
-  if (S.wn >= 2) { store_wseg(wring, S.wld, S.wp1, lane); S.wld += kSeg; }
-  if (MODE == 2) {
-    if (S.pn >= 1) { store_pseg(pring, S.pld, S.pp0, lane); S.pld += kSeg; }
-    if (S.pn >= 2) { store_pseg(pring, S.pld, S.pp1, lane); S.pld += kSeg; }
-  }
-  {
-    const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
-    while (S.wld - S.wptr < need_w && S.wld < C.n_words) {
-      store_wseg(wring, S.wld, load_wseg(C.wsrc, S.wld, C.wvalid, lane), lane);
-      S.wld += kSeg;
-    }
-    if (MODE == 2) {
-      const uint32_t need_p = min(kBlkElems, C.n_plane - S.pptr);
-      while (S.pld - S.pptr < need_p && S.pld < C.n_plane) {
-        store_pseg(pring, S.pld, load_pseg(C.psrc, S.pld, C.pvalid, lane), lane);
-        S.pld += kSeg;
-      }
-    }
-  }
-  wave_sync();
-  // prefetch for the next block; always two loads per ring
-  S.wn = 0;
-  if (S.wld < C.n_words && S.wld - S.wptr + kSeg <= kRing) {
-    S.wn = 1;
-    if (S.wld + kSeg < C.n_words && S.wld - S.wptr + 2 * kSeg <= kRing) S.wn = 2;
-  }
-  S.wp0 = load_wseg_always(C.wsrc, S.wn >= 1 ? S.wld : 0u, C.wvalid, lane, (const GLB uint64_t*)C.cbase);
-  S.wp1 = load_wseg_always(C.wsrc, S.wn >= 2 ? S.wld + kSeg : 0u, C.wvalid, lane, (const GLB uint64_t*)C.cbase);
-  if (MODE == 2) {
-    S.pn = 0;
-    if (S.pld < C.n_plane && S.pld - S.pptr + kSeg <= kRing) {
-      S.pn = 1;
-      if (S.pld + kSeg < C.n_plane && S.pld - S.pptr + 2 * kSeg <= kRing) S.pn = 2;
-    }
-    S.pp0 = load_pseg_always(C.psrc, S.pn >= 1 ? S.pld : 0u, C.pvalid, lane, (const GLB uint32_t*)C.cbase);
-    S.pp1 = load_pseg_always(C.psrc, S.pn >= 2 ? S.pld + kSeg : 0u, C.pvalid, lane, (const GLB uint32_t*)C.cbase);
-  }
-
-#pragma unroll
-  for (int q = 0; q < kBlock; ++q) {
-    const uint32_t t = blk * kBlock + q;
-    if (PARTIAL && t >= C.nsteps) break;                 // wave-uniform
-    const uint32_t sel = (uint32_t)q * 0x0101u | 0x0C0C0000u;
-#pragma unroll
-    for (int g = 0; g < K; ++g) {
-      const uint32_t jl = t * kStates + g * kWave + lane;   // element index within the chunk
-      const bool active = !PARTIAL || jl < C.nc;
-      const uint64_t e = tbl[S.x[g] & 4095u];
-      const uint32_t elo = (uint32_t)e, ehi = (uint32_t)(e >> 32);
-      uint32_t xn = __umul24(elo & 0x1FFFu, S.x[g] >> 12) + (elo >> 13);
-      if (PARTIAL && !active) xn = S.x[g];
-      const bool need = xn < kL;
-      const uint64_t m = __ballot(need);
-      const uint32_t w = wring[lane_rank(m, S.wptr) & (kRing - 1u)];
-      S.x[g] = need ? ((xn << 16) | w) : xn;
-      S.wptr += (uint32_t)__popcll(m);
-      uint32_t v = ehi;
-      if (MODE == 1) {
-        v = plane_merge(v, pl[g], sel);
-      } else if (MODE == 2) {
-        const bool cons = active && (ehi >> 31);
-        const uint64_t bm = __ballot(cons);
-        const uint32_t b = pring[lane_rank(bm, S.pptr) & (kRing - 1u)];
-        S.pptr += (uint32_t)__popcll(bm);
-        if (cons) v = byte_merge(v, b);
-      }
-      const uint32_t si = (uint32_t)q * kStates + g * kWave + lane;   // element index within the block
-      if (EB == 2) ((LDS uint16_t*)stage)[si] = (uint16_t)v;
-      else stage[si] = (uint8_t)v;
-    }
-  }
-}
-
+// Store the staged outputs of half-block `hb` (kHalf steps) to the output.
 template <int K, int EB, bool PARTIAL>
-__device__ __forceinline__ void flush_block(uint32_t blk, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
-  constexpr uint32_t kBlkElems = kBlock * kWave * K;
+__device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
+  constexpr uint32_t kBlkElems = kHalf * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
-  wave_sync();
-  const uint64_t blk_byte0 = (C.base + (uint64_t)blk * kBlkElems) * EB;
-  const uint32_t valid_bytes = PARTIAL ? min(kBlkBytes, (C.nc - min(C.nc, blk * kBlkElems)) * EB) : kBlkBytes;
+  const uint64_t blk_byte0 = (C.base + (uint64_t)hb * kBlkElems) * EB;
+  const uint32_t valid_bytes = PARTIAL ? min(kBlkBytes, (C.nc - min(C.nc, hb * kBlkElems)) * EB) : kBlkBytes;
 #pragma unroll
   for (uint32_t i = 0; i < (kBlkBytes + 1023) / 1024; ++i) {
     const uint32_t o = i * 1024u + C.lane * 16u;
@@ -242,9 +179,141 @@ __device__ __forceinline__ void flush_block(uint32_t blk, const ChunkParams& C, 
   }
 }
 
-// Decode one chunk with one wavefront: K interleaved states per lane (state
-// v = g*64 + lane), MODE = plane mode, EB = element bytes, PARTIAL = chunk may
-// be shorter than 64*K*steps (the tensor's last chunk).
+// One step of the K states of every lane. Phased so the K dependency chains of
+// a lane overlap: K table reads, then the K state updates with their ballots,
+// then the K ring reads (one wait for all), then the renormalisations.
+// FAST = dense bf16 table layout.
+template <int K, bool FAST, bool PARTIAL>
+__device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C,
+                                          const LDS uint64_t* __restrict__ tbl, const LDS uint16_t* __restrict__ wring,
+                                          uint32_t (&d)[K], uint64_t (&active_m)[K]) {
+  uint64_t e[K];
+#pragma unroll
+  for (int g = 0; g < K; ++g) e[g] = tbl[S.x[g] & 4095u];
+  uint32_t xn[K], w[K];
+  bool need[K];
+  uint32_t pos = S.wptr;
+#pragma unroll
+  for (int g = 0; g < K; ++g) {
+    const uint32_t lo = (uint32_t)e[g], hi = (uint32_t)(e[g] >> 32);
+    if (FAST) {
+      xn[g] = __umul24(lo, S.x[g] >> 12) + hi;             // v_mad_u32_u24: f = bits 0..23 of lo
+      d[g] = lo;                                           // exponent in byte 3
+    } else {
+      xn[g] = __umul24(lo & 0x1FFFu, S.x[g] >> 12) + (lo >> 13);
+      d[g] = hi;                                           // value | consume << 31
+    }
+    bool act = true;
+    if (PARTIAL) {
+      act = t * (kWave * K) + C.lane * K + g < C.nc;
+      if (!act) xn[g] = S.x[g];
+    }
+    active_m[g] = __ballot(act);
+    need[g] = xn[g] < kL;
+    const uint64_t m = __ballot(need[g]);
+    w[g] = wring[(pos & (kRing - 1u)) + lane_rank(m)];   // < kRing + 64: the mirror covers it
+    pos += (uint32_t)__popcll(m);
+  }
+  consume<K>(w);
+  S.wptr = pos;
+#pragma unroll
+  for (int g = 0; g < K; ++g) S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
+}
+
+// One block of kBlock steps. Every global-memory operation of the block is
+// issued at its start, before any decoding: land the ring segments prefetched
+// by the previous block, top the rings up if they hold less than a block of
+// worst-case demand (rare), store the previous block's staged output, prefetch
+// the next block's dense plane and the next ring segments. The 8 steps of
+// decoding that follow cover the latency of all of them, so the wait at the
+// next block start (on gfx9 the vector-memory counter covers loads and
+// stores, in issue order) finds them complete.
+template <int K, int MODE, int EB, bool PARTIAL>
+__device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, PlaneRegs<K>& pl_next,
+                                             ChunkState<K>& S, const ChunkParams& C,
+                                             const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
+                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage) {
+  constexpr uint32_t kStates = kWave * K;
+  constexpr uint32_t kBlkElems = kBlock * kStates;
+  constexpr bool FAST = MODE == 1 && EB == 2;
+  const uint32_t lane = C.lane;
+  if (S.wn) { store_wseg(wring, S.wld, S.wp, lane); S.wld += kWSeg; }
+  if (MODE == 2 && S.pn) { store_pseg(pring, S.pld, S.pp, lane); S.pld += kPSeg; }
+  {
+    const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
+    while (S.wld - S.wptr < need_w) {
+      store_wseg(wring, S.wld, load_seg(C.wsrc, S.wld / 8u, C.wvalid16, lane, C.safe), lane);
+      S.wld += kWSeg;
+    }
+    if (MODE == 2) {
+      const uint32_t need_p = min(kBlkElems, C.n_plane - S.pptr);
+      while (S.pld - S.pptr < need_p) {
+        store_pseg(pring, S.pld, load_seg(C.psrc, S.pld / 16u, C.pvalid16, lane, C.safe), lane);
+        S.pld += kPSeg;
+      }
+    }
+  }
+  wave_sync();
+  if (blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
+  if (MODE == 1) pl_next = load_plane<K>(C.dplane, min(blk + 1, C.nblk - 1), lane);
+  S.wn = S.wld < C.n_words && S.wld - S.wptr + kWSeg <= kRing;
+  S.wp = load_seg(C.wsrc, S.wn ? S.wld / 8u : 0u, C.wvalid16, lane, C.safe);
+  if (MODE == 2) {
+    S.pn = S.pld < C.n_plane && S.pld - S.pptr + kPSeg <= kPRing;
+    S.pp = load_seg(C.psrc, S.pn ? S.pld / 16u : 0u, C.pvalid16, lane, C.safe);
+  }
+  wave_sync();
+
+#pragma unroll
+  for (int q = 0; q < kBlock; ++q) {
+    const uint32_t t = blk * kBlock + q;
+    if (PARTIAL && t >= C.nsteps) break;                 // wave-uniform
+    if (q == kHalf) {                                    // first half of the block is staged: store it
+      wave_sync();
+      flush_half<K, EB, PARTIAL>(2 * blk, C, stage);
+    }
+    const uint32_t qs = q % kHalf;                       // step within the staged half
+    uint32_t d[K];
+    uint64_t am[K];
+    rans_step<K, FAST, PARTIAL>(t, S, C, tbl, wring, d, am);
+    if (FAST) {
+      // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
+      const uint64_t pw = pl.b[(q * K) / 8];
+      const uint32_t o = (q * K) % 8;                    // byte offset in pw
+      const uint32_t phi = (uint32_t)(pw >> 32), plo = (uint32_t)pw;
+      if (K == 2) {
+        // word pair: (p | p<<8) & 0x807F per half, exponents from byte 3 of d
+        const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (o + 1) * 0x01010000u | o * 0x0101u);
+        const uint32_t ex = __builtin_amdgcn_perm(d[K - 1], d[0], 0x070C030Cu) >> 1;
+        const uint32_t v = (dup & 0x807F807Fu) | ex;
+        *(LDS uint32_t*)(stage + qs * (kStates * 2) + lane * 4u) = v;
+      } else {
+        const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
+        const uint32_t v = (dup & 0x807Fu) | (d[0] >> 17);
+        *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)v;
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < K; ++g) {
+        uint32_t v = d[g];
+        if (MODE == 2) {
+          const bool cons = ((am[g] >> lane) & 1ull) && (v >> 31);
+          const uint64_t bm = __ballot(cons);
+          const uint32_t b = ((volatile LDS uint8_t*)pring)[(S.pptr + lane_rank(bm)) & (kPRing - 1u)];
+          S.pptr += (uint32_t)__popcll(bm);
+          if (cons) v = byte_merge(v, b);
+        }
+        const uint32_t si = qs * kStates + lane * K + g;  // element index within the staged half
+        if (EB == 2) ((LDS uint16_t*)stage)[si] = (uint16_t)v;
+        else stage[si] = (uint8_t)v;
+      }
+    }
+  }
+}
+
+// Decode one chunk with one wavefront: K interleaved states per lane, MODE =
+// plane mode, EB = element bytes, PARTIAL = chunk may be shorter than
+// 64*K*steps (the tensor's last chunk).
 template <int K, int MODE, int EB, bool PARTIAL>
 __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
                                              LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage,
@@ -252,21 +321,20 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
                                              uint32_t n_plane, GLB uint8_t* __restrict__ out8, uint64_t base,
                                              uint32_t nc, uint32_t nsteps, int32_t* status) {
   constexpr uint32_t kStates = kWave * K;
-  constexpr uint32_t kBlkU64 = kBlock * kStates / 8;   // dense-plane u64s per block
   ChunkParams C;
   C.lane = __lane_id();
   const uint32_t wbytes = pad16(n_words * 2u);
-  C.wsrc = (const GLB uint64_t*)(cbase + 4u * kStates);
+  C.wsrc = (const GLB u32x4*)(cbase + 4u * kStates);
   const GLB uint8_t* psrc8 = cbase + 4u * kStates + wbytes;
-  C.psrc = (const GLB uint32_t*)psrc8;
-  C.dplane = (const GLB uint64_t*)psrc8;
-  C.cbase = cbase;
+  C.psrc = (const GLB u32x4*)psrc8;
+  C.dplane = psrc8;
+  C.safe = (const GLB u32x4*)cbase;
   C.out8 = out8;
   C.base = base;
   C.n_words = n_words;
   C.n_plane = n_plane;
-  C.wvalid = wbytes / 8u;
-  C.pvalid = pad16(n_plane) / 4u;
+  C.wvalid16 = wbytes / 16u;
+  C.pvalid16 = pad16(n_plane) / 16u;
   C.nc = nc;
   C.nsteps = nsteps;
   C.nblk = (nsteps + kBlock - 1) / kBlock;
@@ -275,46 +343,26 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
 #pragma unroll
   for (int g = 0; g < K; ++g) S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
   S.wptr = S.wld = S.pptr = S.pld = 0;
-  S.wn = S.pn = 0;
-  S.wp0 = S.wp1 = 0;
-  S.pp0 = S.pp1 = 0;
+  S.wn = S.pn = false;
+  S.wp = S.pp = u32x4{0, 0, 0, 0};
 
-  // dense plane double buffer (blocks b and b+1), reloaded two blocks ahead
-  uint64_t plA[K], plB[K];
+  // dense plane double buffer: block b uses one, block b+1's is loaded into the other
+  PlaneRegs<K> plA, plB;
 #pragma unroll
-  for (int g = 0; g < K; ++g) {
-    plA[g] = 0;
-    plB[g] = 0;
-    if (MODE == 1) {
-      plA[g] = C.dplane[C.lane * K + g];
-      plB[g] = C.dplane[min(1u, C.nblk - 1) * kBlkU64 + C.lane * K + g];
-    }
-  }
-  // Consume the prologue loads here, so the loop body never waits on them.
-#pragma unroll
-  for (int g = 0; g < K; ++g) asm volatile("" ::"v"(S.x[g]), "v"(plA[g]), "v"(plB[g]));
+  for (int g = 0; g < K; ++g) plA.b[g] = plB.b[g] = 0;
+  if (MODE == 1) plA = load_plane<K>(C.dplane, 0, C.lane);
 
   // Two blocks per iteration so the dense-plane registers alternate without
-  // copies. Full chunks have an even block count (steps % 16 == 0), so the
-  // second half is unconditional and every iteration issues the same memory
-  // operations.
+  // copies. Full chunks have an even block count (steps % 16 == 0).
   for (uint32_t blk = 0; blk < C.nblk; blk += 2) {
-    decode_block<K, MODE, EB, PARTIAL>(blk, plA, S, C, tbl, wring, pring, stage);
-    if (MODE == 1) {
-      const uint32_t nb = min(blk + 2, C.nblk - 1);
-#pragma unroll
-      for (int g = 0; g < K; ++g) plA[g] = C.dplane[nb * kBlkU64 + C.lane * K + g];
-    }
-    flush_block<K, EB, PARTIAL>(blk, C, stage);
+    decode_block<K, MODE, EB, PARTIAL>(blk, plA, plB, S, C, tbl, wring, pring, stage);
     if (PARTIAL && blk + 1 >= C.nblk) break;
-    decode_block<K, MODE, EB, PARTIAL>(blk + 1, plB, S, C, tbl, wring, pring, stage);
-    if (MODE == 1) {
-      const uint32_t nb = min(blk + 3, C.nblk - 1);
-#pragma unroll
-      for (int g = 0; g < K; ++g) plB[g] = C.dplane[nb * kBlkU64 + C.lane * K + g];
-    }
-    flush_block<K, EB, PARTIAL>(blk + 1, C, stage);
+    decode_block<K, MODE, EB, PARTIAL>(blk + 1, plB, plA, S, C, tbl, wring, pring, stage);
   }
+  // the last staged half: the second half of the last block, or its first if
+  // a partial chunk's last block has at most kHalf steps
+  wave_sync();
+  flush_half<K, EB, PARTIAL>((C.nsteps - 1) / kHalf, C, stage);
 
   bool bad_state = false;
 #pragma unroll
@@ -356,8 +404,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
                                                                int32_t* __restrict__ status) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
-  LDS uint16_t* s_wring = (LDS uint16_t*)(smem + kTblBytes);
-  LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWringBytes);
+  LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
+  LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWaves * kRingBytes);
   LDS uint8_t* s_pring = (LDS uint8_t*)(smem + kLdsLean);
   // table-build scratch overlaps the staging area (unused until decoding starts)
   LDS uint32_t* s_cum = (LDS uint32_t*)s_stage;        // 257 entries
@@ -378,7 +426,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const GLB uint8_t* __restrict__ b = (const GLB uint8_t*)T.blob;
 
   // ---- header checks (uniform across the workgroup)
-  if (T.blob_bytes < 32 || b[0] != 'B' || b[1] != 'S' || b[2] != 'C' || b[3] != 'K' || b[4] != 1 ||
+  if (T.blob_bytes < 32 || b[0] != 'B' || b[1] != 'S' || b[2] != 'C' || b[3] != 'K' || b[4] != kVersion ||
       (b[5] != 1 && b[5] != 2) || b[6] > 2 || b[7] != 12 || (!COMPACT && b[6] == 2)) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
@@ -404,14 +452,18 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_BOUNDS);
     return;
   }
+  const bool fast = eb == 2 && mode == 1;
 
-  // ---- decode table in LDS: slot -> {f | (slot-cf) << 13, value | consume << 31}
+  // ---- decode table in LDS (layouts in the file comment)
   const uint32_t tid = threadIdx.x;
   uint32_t f_own = 0;
+  bool bad_sym = false;
   if (tid < nsym) {
     const uint32_t ent = ld_u32(b + 32 + 4 * tid);
     f_own = (ent >> 16) & 0x1FFFu;
     s_val[tid] = (ent & 0xFFFFu) | (ent & 0x80000000u);
+    // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each
+    bad_sym = f_own == 0 || (fast && ((ent & 0x807Fu) != 0 || (ent >> 31) == 0));
   }
   if (tid < 256) s_cum[tid + 1] = f_own;
   if (tid == 0) { s_cum[0] = 0; *s_flag = 0; }
@@ -422,20 +474,26 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (tid < 256) s_cum[tid + 1] += add;
     __syncthreads();
   }
-  if ((tid == 0 && s_cum[256] != 4096u) || (tid < nsym && f_own == 0)) *s_flag = 1;
+  if ((tid == 0 && s_cum[256] != 4096u) || bad_sym) *s_flag = 1;
   __syncthreads();
   if (*s_flag) {
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
-  for (uint32_t slot = tid; slot < 4096u; slot += kThreads) {
+  // each thread fills 4096/kThreads consecutive slots: one binary search, then a forward walk
+  {
+    uint32_t slot = tid * (4096u / kThreads);
     uint32_t lo = 0, hi = nsym;                      // cum[lo] <= slot < cum[hi]
     while (hi - lo > 1) {
       uint32_t mid = (lo + hi) >> 1;
       if (s_cum[mid] <= slot) lo = mid; else hi = mid;
     }
-    const uint32_t f = s_cum[lo + 1] - s_cum[lo];
-    s_tbl[slot] = (uint64_t)(f | ((slot - s_cum[lo]) << 13)) | ((uint64_t)s_val[lo] << 32);
+    for (uint32_t k = 0; k < 4096u / kThreads; ++k, ++slot) {
+      while (s_cum[lo + 1] <= slot) ++lo;
+      const uint32_t c0 = s_cum[lo], f = s_cum[lo + 1] - c0, val = s_val[lo];
+      s_tbl[slot] = fast ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
+                         : ((uint64_t)(f | ((slot - c0) << 13)) | ((uint64_t)val << 32));
+    }
   }
   __syncthreads();
 
@@ -460,8 +518,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     return;
   }
   const GLB uint8_t* cbase = b + off;
-  LDS uint16_t* wring = s_wring + wave * kRing;
-  LDS uint8_t* pring = s_pring + wave * kRing;
+  LDS uint16_t* wring = (LDS uint16_t*)(s_wring + wave * kRingBytes);
+  LDS uint8_t* pring = s_pring + wave * kPRing;
   LDS uint8_t* stage = s_stage + wave * kStageMax;
   GLB uint8_t* out = (GLB uint8_t*)T.out;
   const bool partial = nc != per;
@@ -497,13 +555,13 @@ int launch(const bs_chunk_task* tasks, uint32_t n_tasks, const bs_chunk_task& si
 
 extern "C" {
 
-int bs_version(void) { return 100; }
+int bs_version(void) { return 200; }
 
 int bs_chunk_chunks_per_group(void) { return kWaves; }
 
 int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   if (!h || !info) return BS_ERR_ARG;
-  if (len < 32 || h[0] != 'B' || h[1] != 'S' || h[2] != 'C' || h[3] != 'K' || h[4] != 1) return BS_ERR_FORMAT;
+  if (len < 32 || h[0] != 'B' || h[1] != 'S' || h[2] != 'C' || h[3] != 'K' || h[4] != kVersion) return BS_ERR_FORMAT;
   auto u32 = [&](int o) { return (uint32_t)h[o] | ((uint32_t)h[o + 1] << 8) | ((uint32_t)h[o + 2] << 16) | ((uint32_t)h[o + 3] << 24); };
   info->elem_bytes = h[5];
   info->plane_mode = h[6];

@@ -13,9 +13,10 @@
 //
 // rANS encoding per chunk: 64*K interleaved 32-bit states (K = 1 or 2 per
 // wavefront lane; L = 2^16, M = 2^12, 16-bit renormalisation: the reference's
-// state machine, bigsmall/codecs/rans.py:115-162), walked from the last step
-// back to the first; the renorm words are laid out so the decoder consumes
-// them step-ascending, state-ascending.
+// state machine, bigsmall/codecs/rans.py:115-162). State v = g*64 + l (lane l,
+// group g) codes element t*64K + l*K + g at step t. States are walked from the
+// last step back to the first, v descending within a step, so the decoder
+// consumes the renorm words step-ascending, v-ascending.
 #include <stdint.h>
 #include <string.h>
 
@@ -29,6 +30,7 @@
 
 namespace {
 
+constexpr uint8_t kVersion = 2;       // BSCK layout version
 constexpr uint32_t kWave = 64;        // lanes of a wavefront
 constexpr uint32_t kL = 1u << 16;
 constexpr uint32_t kM = 4096;
@@ -221,35 +223,40 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
   auto sym_at = [&](uint64_t j) -> uint32_t { return P.sym_of[P.eb == 2 ? w16[base + j] : w8[base + j]]; };
   uint64_t xmax[256];
   for (uint32_t s = 0; s < P.nsym; ++s) xmax[s] = (uint64_t)P.freq[s] << 20;
+  auto elem = [&](uint32_t t, uint32_t v) -> uint64_t { return (uint64_t)t * lanes + (v % kWave) * K + v / kWave; };
   for (uint32_t t = nsteps; t-- > 0;) {
-    for (uint32_t l = lanes; l-- > 0;) {
-      const uint64_t j = (uint64_t)t * lanes + l;
+    for (uint32_t v = lanes; v-- > 0;) {
+      const uint64_t j = elem(t, v);
       if (j >= nc) continue;
       const uint32_t s = sym_at(j), f = P.freq[s];
-      uint32_t v = x[l];
-      if ((uint64_t)v >= xmax[s]) { words[--pos] = (uint16_t)(v & 0xFFFF); v >>= 16; }
-      const uint32_t q = v / f;
-      x[l] = (q << 12) + (v - q * f) + P.cum[s];
+      uint32_t xv = x[v];
+      if ((uint64_t)xv >= xmax[s]) { words[--pos] = (uint16_t)(xv & 0xFFFF); xv >>= 16; }
+      const uint32_t q = xv / f;
+      x[v] = (q << 12) + (xv - q * f) + P.cum[s];
     }
   }
   n_words = (uint32_t)(words.size() - pos);
   std::vector<uint8_t> plane;
   if (P.mode == 1) {
     // dense plane: per 8-step block, wavefront lane l's 8*K bytes are contiguous,
-    // group-major: byte (g, q) of lane l at l*8K + g*8 + q
+    // step-major: byte (q, g) of lane l at l*8K + q*K + g
     const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
     plane.assign((size_t)nblk * kBlock * lanes, 0);
     for (uint32_t j = 0; j < nc; ++j) {
-      const uint32_t w = w16[base + j], t = j / lanes, v = j % lanes, g = v / kWave, l = v % kWave;
-      plane[(size_t)(t / kBlock) * kBlock * lanes + l * kBlock * K + g * kBlock + (t % kBlock)] =
+      const uint32_t w = w16[base + j], t = j / lanes, r = j % lanes, l = r / K, g = r % K;
+      plane[(size_t)(t / kBlock) * kBlock * lanes + l * kBlock * K + (t % kBlock) * K + g] =
           (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
     }
   } else if (P.mode == 2) {
+    // compact plane: bytes of consuming elements in decode order (step, then v)
     plane.reserve(nc);
-    for (uint32_t j = 0; j < nc; ++j) {
-      const uint32_t w = w16[base + j];
-      if (P.consume[P.sym_of[w]]) plane.push_back((uint8_t)(((w >> 8) & 0x80) | (w & 0x7F)));
-    }
+    for (uint32_t t = 0; t < nsteps; ++t)
+      for (uint32_t v = 0; v < lanes; ++v) {
+        const uint64_t j = elem(t, v);
+        if (j >= nc) continue;
+        const uint32_t w = w16[base + j];
+        if (P.consume[P.sym_of[w]]) plane.push_back((uint8_t)(((w >> 8) & 0x80) | (w & 0x7F)));
+      }
   }
   n_plane = (uint32_t)plane.size();
   const uint64_t wb = pad16((uint64_t)n_words * 2), pb = pad16(n_plane);
@@ -305,7 +312,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
   if (total > cap) return BS_ERR_CAP;
   memset(dst, 0, ctab + 16ull * nch + 16);
   memcpy(dst, "BSCK", 4);
-  dst[4] = 1; dst[5] = (uint8_t)elem_bytes; dst[6] = (uint8_t)P.mode; dst[7] = 12;
+  dst[4] = kVersion; dst[5] = (uint8_t)elem_bytes; dst[6] = (uint8_t)P.mode; dst[7] = 12;
   put64(dst + 8, n); put32(dst + 16, steps); put16(dst + 20, lanes); put16(dst + 22, P.nsym);
   put32(dst + 24, nch); put32(dst + 28, 0);
   for (uint32_t s = 0; s < P.nsym; ++s)

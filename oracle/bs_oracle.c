@@ -764,18 +764,19 @@ out:
 /* BSCK — the build's GPU-native chunked rANS container format (no reference
  * counterpart). CPU restatement of the device decoder's semantics, used as a
  * checker of the product encoder. Format:
- *   [0]  "BSCK"  [4] u8 version=1  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+ *   [0]  "BSCK"  [4] u8 version=2  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
  *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2)
  *   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
  *   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
  *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16)
- * Element j of chunk c sits at c*lanes*steps + j; state v = j % lanes, step = j / lanes.
- * Decode step order: steps ascending; renorm words consumed in ascending state
- * order among states that fell below L. plane_mode 1 (dense): every element
- * consumes one byte, stored in blocks of 8 steps; state v = g*64 + l (wavefront
- * lane l, group g) keeps its byte for step 8b+q at b*8*lanes + l*8*(lanes/64) + g*8 + q.
+ * Element j of chunk c sits at c*lanes*steps + j. With K = lanes/64, state
+ * v = g*64 + l (wavefront lane l, group g) decodes element t*lanes + l*K + g at
+ * step t. Decode step order: steps ascending; renorm words consumed in ascending
+ * v order among states that fell below L. plane_mode 1 (dense): every element
+ * consumes one byte, stored in blocks of 8 steps; the byte of state (g, l) for
+ * step 8b+q sits at b*8*lanes + l*8*K + q*K + g.
  * plane_mode 2 (compact): consuming elements read bytes in decode order.
  * plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
  * ------------------------------------------------------------------------ */
@@ -784,7 +785,7 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
-    if (ver != 1 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128) ||
+    if (ver != 2 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128) ||
         steps == 0 || steps % 16)
         return ORC_ERR_FORMAT;
     if (n != n_weights) return ORC_ERR_COUNT;
@@ -816,22 +817,24 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
         uint32_t x[256];
         for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
         uint64_t wp = 0, pp = 0;
+        const uint32_t K = lanes / 64;
         for (uint64_t t = 0; t < nsteps; t++) {
-            for (uint32_t l = 0; l < lanes; l++) {
-                uint64_t j = t * lanes + l;
-                if (j >= nc) break;
-                uint32_t slot = x[l] & 4095, s = slot2sym[slot];
-                x[l] = fr[s] * (x[l] >> 12) + slot - cum[s];
-                if (x[l] < RANS_L) {
+            for (uint32_t sv = 0; sv < lanes; sv++) {
+                uint32_t g = sv / 64, wl = sv % 64;
+                uint64_t j = t * lanes + (uint64_t)wl * K + g;
+                if (j >= nc) continue;
+                uint32_t slot = x[sv] & 4095, s = slot2sym[slot];
+                x[sv] = fr[s] * (x[sv] >> 12) + slot - cum[s];
+                if (x[sv] < RANS_L) {
                     if (wp >= nw) return ORC_ERR_FORMAT;
-                    x[l] = (x[l] << 16) | get16(wd + 2 * wp); wp++;
+                    x[sv] = (x[sv] << 16) | get16(wd + 2 * wp); wp++;
                 }
                 uint32_t v = val[s];
                 if (cons[s]) {
                     uint32_t b;
                     if (mode == 1) {
-                        uint64_t blk = t / 8, q = t % 8, g = l / 64, wl = l % 64, K = lanes / 64;
-                        uint64_t idx = blk * 8 * lanes + wl * 8 * K + g * 8 + q;
+                        uint64_t blk = t / 8, q = t % 8;
+                        uint64_t idx = blk * 8 * lanes + (uint64_t)wl * 8 * K + q * K + g;
                         if (idx >= np) return ORC_ERR_FORMAT;
                         b = pl[idx];
                     } else if (mode == 2) {
