@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+WORKLOAD = "bsck_decode_llama3_8b_layer"
 LAYER = [
     ("model.layers.0.self_attn.q_proj.weight", (4096, 4096)),
     ("model.layers.0.self_attn.k_proj.weight", (1024, 4096)),
@@ -94,6 +95,31 @@ def cpu_baseline(words: dict, budget_s: float = 12.0):
     }
 
 
+def copy_probe(mib: int) -> None:
+    """A plain copy of known size: each launch reads and writes mib MiB. Its
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters for `traffic`."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy),
+    or None when no summary for this workload is committed."""
+    path = os.path.join(ROOT, "profiles", f"{workload}.traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return int(t["fetch_bytes_per_launch"] + t["write_bytes_per_launch"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +128,8 @@ def main():
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
@@ -109,6 +137,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_probe_mb:
+        copy_probe(args.copy_probe_mb)
+        return
     from bigsmall_amd.codecs import bf16_chunked as bc
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
 
@@ -183,7 +214,7 @@ def main():
         "dtype": "u32",
         "data": "synthetic (seeded torch N(0,0.02) weights, 1+N(0,0.01) norms), encoded by the engine",
         "config": {
-            "workload": "llama3-8b-layer-decode-to-hbm",
+            "workload": WORKLOAD,
             "tensors": len(LAYER), "elements": n_total, "decoded_bytes": out_total,
             "compressed_bytes": comp_total, "ratio_pct": round(100 * comp_total / out_total, 3),
             "codec": bc.CODEC_BF16, "chunk_steps": steps, "chunk_lanes": lanes, "launches_per_step": 1,
@@ -191,7 +222,7 @@ def main():
         "ms_per_layer": round(ms_per, 5),
         "decoded_output_GBps": round(out_total / (ms_per * 1e-3) / 1e9, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(WORKLOAD)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
