@@ -45,6 +45,7 @@ SIGNATURES = {
     "bs_chunk_decode_batch": (_INT, [_P, _U32, _U32, _U32, _P, _P]),
     "bs_chunk_encode_bound": (_INT, [_U64, _U32, _U32, _U32, ctypes.POINTER(_U64)]),
     "bs_chunk_encode": (_INT, [_P, _U64, _U32, _U32, _U32, _I32, _P, _U64, ctypes.POINTER(_U64), _INT]),
+    "bs_refcodec_decode": (_INT, [_P, _U32, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _P, _P]),
 }
 
 _lib = None

@@ -1,0 +1,31 @@
+"""`bf16_se_tans`: the reference's format, decoded on the GPU.
+
+Same plugin shape as the reference (bigsmall/codecs/bf16_tans.py:121-167):
+    decode(blob: bytes, extras: dict, n_weights: int) -> bytes
+The blob's framing is parsed on the host (bigsmall_amd/codecs/_refstreams.py);
+every symbol is decoded by the HIP kernels behind bs_refcodec_decode. There is
+no CPU decode path: without a ROCm GPU this raises.
+
+This engine does not encode bf16_se_tans (its own GPU format is bf16_chunked_v1);
+containers in this format come from the reference's encoder.
+"""
+from __future__ import annotations
+
+from . import _refstreams
+
+CODEC = "bf16_se_tans"
+
+
+def parse(blob: bytes, n_weights: int) -> _refstreams.RefPlan:
+    """Host-side framing parse (raises ValueError on malformed blobs)."""
+    return _refstreams.PARSERS[CODEC](bytes(blob), n_weights)
+
+
+def decode(blob: bytes, extras: dict, n_weights: int) -> bytes:
+    """Decode to raw bf16 bytes (little-endian), on the GPU."""
+    return _refstreams.decode_host(CODEC, blob, n_weights)
+
+
+def encode(raw: bytes, **_) -> tuple[bytes, dict]:
+    raise NotImplementedError(f"{CODEC} blobs are produced by the reference encoder; "
+                              "this engine encodes bf16_chunked_v1")

@@ -16,11 +16,11 @@
  *                  plugin API `codec_registry.register_codec(name, enc, dec)`
  *                  (bigsmall/codec_registry.py:45-47) and dispatched from the
  *                  decoder's `_decode_blob` chain (bigsmall/decoder.py:49-97).
- *   bs_par1_*    — `kernels.decode_bf16_parallel(blob, extras, n_weights)`
- *                  (bigsmall/kernels/__init__.py:89-111) and the CPU decode it
- *                  must match, `bf16_parallel.decode` (bigsmall/codecs/bf16_parallel.py:262-352).
- *   bs_tans_*    — `bf16_tans.decode` (bigsmall/codecs/bf16_tans.py:121-167).
- *   bs_sk_*      — `single_kernel.decode` (bigsmall/codecs/single_kernel.py:603-613).
+ *   bs_refcodec_decode — `kernels.decode_bf16_parallel(blob, extras, n_weights)`
+ *                  (bigsmall/kernels/__init__.py:89-111) and the CPU decoders it
+ *                  must match: `bf16_parallel.decode` (bigsmall/codecs/bf16_parallel.py:262-352),
+ *                  `bf16_tans.decode` (bigsmall/codecs/bf16_tans.py:121-167),
+ *                  `single_kernel.decode` (bigsmall/codecs/single_kernel.py:603-613).
  */
 #ifndef BIGSMALL_HIP_H
 #define BIGSMALL_HIP_H
@@ -102,6 +102,55 @@ int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32
 int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t *bound);
 int bs_chunk_encode(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t *h_dst, uint64_t cap, uint64_t *out_len, int n_threads);
+
+/* ------------------------------------------------------------------------ */
+/* The reference's rANS-family bf16 formats, decoded on the GPU:
+ *   bf16_parallel_v1      (bigsmall/codecs/bf16_parallel.py:262-352; the entry
+ *                          kernels.decode_bf16_parallel, bigsmall/kernels/__init__.py:89-111)
+ *   bf16_se_tans          (bigsmall/codecs/bf16_tans.py:121-167)
+ *   bf16_se_single_kernel (bigsmall/codecs/single_kernel.py:603-613)
+ * The host parses the blob header (bigsmall_amd/codecs/_refstreams.py) into
+ * stream descriptors and decode tables; these two kernels do all symbol work. */
+
+/* One rANS stream: initial state x0, then n_words little-endian u16 words at
+ * `words` (device, any alignment). If bit 16 of `tail` is set, one more word
+ * with value (tail & 0xFFFF) follows (an odd trailing byte in the reference's
+ * framing). */
+typedef struct {
+    const uint8_t *words;
+    uint32_t x0;
+    uint32_t n_words;
+    uint32_t tail;
+    uint32_t n;          /* symbols */
+    uint64_t first;      /* element index of the first symbol */
+    uint32_t stride;     /* element index step between symbols */
+    uint32_t reserved;
+} bs_se_stream;
+
+typedef struct {
+    const uint8_t *words;
+    uint32_t x0;
+    uint32_t n_words;
+    uint32_t tail;
+    uint32_t n;          /* mantissas in the bucket */
+    uint64_t perm_begin; /* index in perm of the bucket's first element */
+    uint32_t table;      /* mantissa table index */
+    uint32_t reserved;
+} bs_mant_bucket;
+
+/* Decode one tensor of a reference rANS-family format into d_out (n_out bf16
+ * words). d_se_table: 4096 x {f | (slot-cf) << 13, symbol} u32 pairs.
+ * d_bstart: n_streams x 257 u32, the perm index where the bucket of exponent e
+ * of each stream starts (entry 256 = the stream's end). d_mant_tables:
+ * n_tables x 1024 u32 {f | (slot-cf) << 11 | symbol << 21}. d_perm: n_out u32
+ * of scratch. Asynchronous on `stream`; device integrity failures are OR-ed
+ * into *d_status. Replaces the CPU decode loops of bf16_parallel.decode,
+ * bf16_tans.decode and single_kernel._decode_full_kernel (paths above) and the
+ * SE-only Triton kernel (bigsmall/kernels/ac_triton.py:47-102). */
+int bs_refcodec_decode(const bs_se_stream *d_streams, uint32_t n_streams, const uint32_t *d_se_table,
+                       const uint32_t *d_bstart, const bs_mant_bucket *d_buckets, uint32_t n_buckets,
+                       const uint32_t *d_mant_tables, uint32_t n_tables, uint16_t *d_out, uint64_t n_out,
+                       uint32_t *d_perm, int32_t *d_status, void *stream);
 
 #ifdef __cplusplus
 }

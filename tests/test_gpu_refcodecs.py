@@ -1,0 +1,108 @@
+"""GPU parity of the reference's rANS-family formats (bf16_parallel_v1,
+bf16_se_tans, bf16_se_single_kernel) decoded by bs_refcodec_decode.
+
+Bar: bit-exact. Inputs are (1) the golden blobs written by the reference's own
+encoders (tests/golden/ref_vectors.npz) and (2) larger blobs from the oracle's
+encoders, which are byte-identical to the reference's on every golden vector
+(tests/test_oracle_golden.py). Each GPU output must equal the source words and
+the oracle's CPU decode of the same blob.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+CODECS = {
+    "bf16_parallel_v1": (oracle.par1_encode, oracle.par1_decode, "par1_"),
+    "bf16_se_tans": (oracle.tans_encode, oracle.tans_decode, "tans_"),
+    "bf16_se_single_kernel": (oracle.sk_encode, oracle.sk_decode, "sk_"),
+}
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    oracle.build()
+    return torch
+
+
+def _decode(codec, blob, n):
+    from bigsmall_amd.codecs import _refstreams
+    return _refstreams.decode_host(codec, blob, n)
+
+
+@pytest.mark.parametrize("codec", list(CODECS))
+def test_reference_golden_blobs(gpu, golden, codec):
+    prefix = CODECS[codec][2]
+    seen = 0
+    for k in sorted(golden):
+        if not k.startswith(prefix):
+            continue
+        name = k[len(prefix):].rsplit("_N", 1)[0] if prefix == "par1_" else k[len(prefix):]
+        words = golden[f"in_{name}"].astype("<u2")
+        _say(f"[ref] {codec} golden {k} n={words.size}")
+        assert _decode(codec, golden[k].tobytes(), words.size) == words.tobytes(), k
+        seen += 1
+    assert seen >= 7
+
+
+@pytest.mark.parametrize("codec", list(CODECS))
+@pytest.mark.parametrize("kind", ["gauss", "studentt", "halfzero", "uniform"])
+def test_oracle_encoded_larger(gpu, codec, kind):
+    enc, dec, _ = CODECS[codec]
+    rng = np.random.default_rng(len(kind))
+    n = 300_007 if codec != "bf16_parallel_v1" else 1_000_003
+    if kind == "gauss":
+        w = _bf16(rng.standard_normal(n) * 0.02)
+    elif kind == "studentt":
+        w = _bf16(rng.standard_t(3, n) * 0.02 / np.sqrt(3))
+    elif kind == "halfzero":
+        w = _bf16(rng.standard_normal(n) * 0.02)
+        w[rng.permutation(n)[: n // 2]] = 0
+    else:
+        w = rng.integers(0, 65536, n).astype(np.uint16)
+    blob = enc(w)
+    _say(f"[ref] {codec} {kind} n={n} blob={len(blob)}")
+    got = _decode(codec, blob, n)
+    assert got == w.tobytes()
+    assert got == dec(blob, n)
+
+
+def test_parallel_stream_counts(gpu):
+    rng = np.random.default_rng(5)
+    w = _bf16(rng.standard_normal(70_001) * 0.02)
+    for ns in [1, 3, 64, 128, 257, 1024]:
+        blob = oracle.par1_encode(w, ns)
+        _say(f"[ref] bf16_parallel_v1 N={ns}")
+        assert _decode("bf16_parallel_v1", blob, w.size) == w.tobytes()
+
+
+def test_corrupt_stream_is_reported(gpu):
+    from bigsmall_amd.exceptions import DecodeError
+    rng = np.random.default_rng(6)
+    w = _bf16(rng.standard_normal(50_000) * 0.02)
+    blob2 = bytearray(oracle.tans_encode(w))
+    # flip a byte deep inside the SE renorm words: the stream no longer ends in state L
+    se_n = int.from_bytes(blob2[4:6], "little")
+    se_cw = 4 + 2 + 6 * se_n + 4
+    blob2[se_cw + 200] ^= 0x5A
+    _say("[ref] corrupt tans stream -> DecodeError")
+    with pytest.raises((DecodeError, ValueError)):
+        _decode("bf16_se_tans", bytes(blob2), w.size)

@@ -1,0 +1,115 @@
+"""CPU checks of the host side of the GPU decoders for the reference's formats
+(bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel).
+
+The host parses a blob into stream descriptors, bucket start tables and decode
+tables (bigsmall_amd/codecs/_refstreams.py). Here a plain-Python emulation of
+the two device kernels' semantics (refcodec_decode.hip: se_kernel, mant_kernel)
+runs on those descriptors, for every reference blob in the golden fixtures
+(written by the reference's own encoders), and must give back the original
+words. Malformed framing must raise ValueError.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from bigsmall_amd.codecs import _refstreams as rs
+
+L = 1 << 16
+
+
+def _word(blob: bytes, off: int, i: int) -> int:
+    return blob[off + 2 * i] | (blob[off + 2 * i + 1] << 8)
+
+
+def _run(blob: bytes, s: rs.Stream, n: int, table, precision: int):
+    """Decode n symbols of one stream with the kernels' loop; returns (symbols, end state, words used)."""
+    n_eff = s.n_words + ((s.tail >> 16) & 1)
+    x, pos, out = s.x0, 0, []
+    mask = (1 << precision) - 1
+    for _ in range(n):
+        f, bias, sym = table(x & mask)
+        x = f * (x >> precision) + bias
+        while x < L and pos < n_eff:
+            v = _word(blob, s.words_off, pos) if pos < s.n_words else (s.tail & 0xFFFF)
+            x = ((x << 16) | v) & 0xFFFFFFFF
+            pos += 1
+        out.append(sym)
+    return out, x, pos, n_eff
+
+
+def emulate(plan: rs.RefPlan, blob: bytes) -> np.ndarray:
+    se_t = rs.decode_table_se(plan.se_freqs)
+    mts = [rs.decode_table_mant(f) for f in plan.mant_freqs]
+    out = np.zeros(plan.n, np.uint16)
+    perm = np.full(plan.n, -1, np.int64)
+    for (s, first, stride, n), bs in zip(plan.se_streams, plan.bstart):
+        syms, x, pos, n_eff = _run(blob, s, n, lambda sl: (int(se_t[sl, 0]) & 0x1FFF, int(se_t[sl, 0]) >> 13,
+                                                           int(se_t[sl, 1])), 12)
+        assert x == L and pos == n_eff
+        cur = bs[:256].astype(np.int64).copy()
+        for i, sym in enumerate(syms):
+            e = sym & 0xFF
+            idx = first + i * stride
+            out[idx] = ((sym >> 8) & 1) << 15 | e << 7
+            perm[cur[e]] = idx
+            cur[e] += 1
+        assert np.array_equal(cur, bs[1:].astype(np.int64))
+    for s, pb, n, t in plan.buckets:
+        tbl = mts[t]
+        syms, x, pos, n_eff = _run(blob, s, n, lambda sl: (int(tbl[sl]) & 0x7FF, (int(tbl[sl]) >> 11) & 0x3FF,
+                                                           int(tbl[sl]) >> 21), 10)
+        assert x == L and pos == n_eff
+        for r, m in enumerate(syms):
+            out[perm[pb + r]] |= m
+    return out
+
+
+@pytest.mark.parametrize("codec,prefix", [("bf16_parallel_v1", "par1_"), ("bf16_se_tans", "tans_"),
+                                          ("bf16_se_single_kernel", "sk_")])
+def test_host_plans_decode_reference_blobs(golden, codec, prefix):
+    seen = 0
+    for k in sorted(golden):
+        if not k.startswith(prefix):
+            continue
+        name = k[len(prefix):].rsplit("_N", 1)[0] if prefix == "par1_" else k[len(prefix):]
+        words = golden[f"in_{name}"].astype(np.uint16)
+        if words.size > 40000:
+            continue                       # the pure-Python emulation is slow; GPU tests cover these
+        blob = golden[k].tobytes()
+        plan = rs.PARSERS[codec](blob, words.size)
+        assert np.array_equal(emulate(plan, blob), words), k
+        seen += 1
+    assert seen >= 5
+
+
+def test_tables_are_exact_inverses():
+    rng = np.random.default_rng(0)
+    f = np.zeros(512, np.int64)
+    f[rng.choice(512, 30, replace=False)] = 1
+    f[np.nonzero(f)[0][0]] += 4096 - f.sum()
+    t = rs.decode_table_se(f)
+    cum = np.concatenate([[0], np.cumsum(f)[:-1]])
+    for slot in range(0, 4096, 17):
+        sym = t[slot, 1]
+        assert cum[sym] <= slot < cum[sym] + f[sym]
+        assert t[slot, 0] & 0x1FFF == f[sym] and t[slot, 0] >> 13 == slot - cum[sym]
+
+
+def test_malformed_blobs_raise(golden):
+    blob = golden["par1_gauss_N64"].tobytes()
+    n = golden["in_gauss"].size
+    with pytest.raises(ValueError):
+        rs.parse_parallel(blob, n + 1)              # wrong count
+    with pytest.raises(ValueError):
+        rs.parse_parallel(blob[: len(blob) // 2], n)  # truncated
+    bad = bytearray(blob)
+    bad[0:4] = b"PAR2"
+    with pytest.raises(ValueError):
+        rs.parse_parallel(bytes(bad), n)
+    tb = golden["tans_gauss"].tobytes()
+    with pytest.raises(ValueError):
+        rs.parse_tans(tb[:100], n)
+    sk = golden["sk_gauss"].tobytes()
+    with pytest.raises(ValueError):
+        rs.parse_single_kernel(sk[:-3], n)
