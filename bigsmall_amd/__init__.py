@@ -1,7 +1,33 @@
 """bigsmall_amd — MI355X-native decode engine for BigSmall .bs containers.
 
-Drop-in for the reference's decode path (bigsmall.decoder, codec_registry,
-container readers, StreamingLoader / BigSmallStreamingModel, CompressedKVCache):
-the same entry points, with every decode running as HIP kernels on the GPU.
+Drop-in for the reference's decode path, with every decode running as HIP
+kernels on the GPU:
+    compress(src, dst)                      -> .bs in the GPU format (bf16_chunked_v1)
+    decompress(src, dst=None)               -> dict[str, np.ndarray]
+    load(src, device="cuda")                -> dict[str, torch.Tensor] in HBM
+    info(src), verify(src)
+    StreamingLoader, BigSmallStreamingModel -> layer-at-a-time decode with prefetch
+    CompressedKVCache                       -> KV entries and blocks decoded on the GPU
+    codec_registry.register_codec / get_codec / auto_select_codec
 """
 __version__ = "3.12.0+mi355x"
+
+from .container import info
+from .decoder import decompress, load
+from .encoder import compress
+from .exceptions import BigSmallVersionError, DecodeError
+from .kv_cache_manager import CompressedKVCache
+from .streaming import StreamingLoader
+from .verify import verify
+
+
+def __getattr__(name):
+    # transformers/accelerate are only needed by the streaming model
+    if name == "BigSmallStreamingModel":
+        from .streaming_inference import BigSmallStreamingModel
+        return BigSmallStreamingModel
+    raise AttributeError(name)
+
+
+__all__ = ["compress", "decompress", "load", "info", "verify", "StreamingLoader", "BigSmallStreamingModel",
+           "CompressedKVCache", "BigSmallVersionError", "DecodeError", "__version__"]

@@ -1,0 +1,124 @@
+"""Encoder: tensors -> .bs container in the engine's GPU format.
+
+Mirrors the reference's `compress` (bigsmall/encoder.py:325-496): same header
+fields per tensor (name, shape, dtype, codec, special, compressed_bytes,
+offset, md5, extra) and per container (format, mode, model_type, base_model,
+tensor_count, tensors, safetensors_metadata, codec_stats), the same routing
+before codec selection:
+  * tied: a tensor byte-identical (md5) to an earlier one of the same shape and
+    item size, at least 1024 bytes, becomes `tied_ref` (tensor_analysis.py:97-110);
+  * tiny: fewer than RAW_TINY_THRESHOLD bytes are stored `raw` (encoder.py:57, 386-388);
+  * everything else goes through codec_registry.auto_select_codec.
+The codecs are bf16_chunked_v1 / fp8_chunked_v1 (GPU-decodable); the
+reference's `lowcard` (zstd) route for tensors with <= 16 distinct values is
+covered by bf16_chunked_v1's exact-value mode, which codes up to 256 distinct
+values per tensor and decodes on the GPU.
+Blobs start on 256-byte boundaries of the data section (offsets are explicit
+in the header, so any reader finds them).
+"""
+from __future__ import annotations
+
+import hashlib
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+from . import codec_registry, container, formats
+
+RAW_TINY_THRESHOLD = 512
+TIE_MIN_BYTES = 1024
+
+
+def _tensor_record(name: str, t) -> dict:
+    """name/shape/dtype/raw/fmt/item_bytes of a torch tensor (encoder.py:243-285)."""
+    import torch
+    t = t.detach().contiguous().cpu()
+    dtype_str = str(t.dtype).replace("torch.", "")
+    try:
+        fmt = formats.detect_format_from_dtype(dtype_str)
+    except ValueError:
+        fmt = "raw"
+    raw = t.view(torch.uint8).numpy().tobytes() if t.numel() else b""
+    shape = list(t.shape)
+    return {"name": name, "shape": shape, "dtype": dtype_str, "item_bytes": t.element_size(), "raw": raw,
+            "fmt": fmt}
+
+
+def _gather(src) -> tuple[list[dict], dict]:
+    if isinstance(src, dict):
+        return [_tensor_record(k, v) for k, v in src.items()], {}
+    from safetensors import safe_open
+    recs, meta = [], {}
+    with safe_open(str(src), framework="pt") as f:
+        try:
+            meta = f.metadata() or {}
+        except Exception:
+            meta = {}
+        for k in f.keys():
+            recs.append(_tensor_record(k, f.get_tensor(k)))
+    return recs, meta
+
+
+def _detect_model_type(names: list[str]) -> str:
+    """encoder.py:288-296."""
+    blob = " ".join(names[:200]).lower()
+    markers = ("unet", "vae", "controlnet", "double_block", "transformer_block", "x_embedder", "joint_blocks",
+               "time_embed")
+    return "diffusion" if any(m in blob for m in markers) else "llm"
+
+
+def compress(src, dst: str | Path, mode: str = "balanced", progress: bool = False,
+             exclude_names: Optional[set[str]] = None, steps: Optional[int] = None, **_ignored) -> str:
+    """Compress a safetensors file (or a {name: torch.Tensor} dict) into a .bs container."""
+    tensors, st_meta = _gather(src)
+    if exclude_names:
+        tensors = [t for t in tensors if t["name"] not in exclude_names]
+    counts: dict[str, int] = {}
+    for t in tensors:
+        if t["fmt"] != "raw":
+            counts[t["fmt"]] = counts.get(t["fmt"], 0) + 1
+    dominant = max(counts, key=counts.get) if counts else "bf16"
+
+    data = container.DataSectionBuilder()
+    stats = codec_registry.CodecStats()
+    seen: dict[tuple, int] = {}
+    header_tensors = []
+    for i, t in enumerate(tensors):
+        raw = t["raw"]
+        md5 = hashlib.md5(raw).hexdigest()
+        special = None
+        key = (t["item_bytes"], tuple(t["shape"]), md5)
+        if len(raw) >= TIE_MIN_BYTES and key in seen:
+            blob, codec, extras, special = b"", "tied_ref", {"tied_to": tensors[seen[key]]["name"]}, "tied"
+        elif len(raw) < RAW_TINY_THRESHOLD:
+            blob, codec, extras = raw, "raw", {"n_bytes": len(raw)}
+        else:
+            if len(raw) >= TIE_MIN_BYTES:
+                seen[key] = i
+            if steps is not None and t["fmt"] == "bf16":
+                from .codecs import bf16_chunked
+                blob, extras = bf16_chunked.encode(raw, steps=steps)
+                codec = bf16_chunked.CODEC_BF16
+            else:
+                blob, codec, extras = codec_registry.auto_select_codec(raw, t["fmt"], t["dtype"], t["name"],
+                                                                       tuple(t["shape"]), t["item_bytes"])
+        off = data.add(blob)
+        header_tensors.append({"name": t["name"], "shape": t["shape"], "dtype": t["dtype"], "codec": codec,
+                               "special": special, "compressed_bytes": len(blob), "offset": off, "md5": md5,
+                               "extra": extras or None})
+        stats.record(codec)
+    header = {"format": dominant, "mode": mode, "model_type": _detect_model_type([t["name"] for t in tensors]),
+              "base_model": None, "tensor_count": len(tensors), "tensors": header_tensors,
+              "safetensors_metadata": st_meta or None, "codec_stats": stats.as_dict()}
+    gpu_codecs = {"bf16_chunked_v1", "fp8_chunked_v1", "bf16_parallel_v1"}
+    version = formats.BS_FORMAT_VERSION_V2 if any(h["codec"] in gpu_codecs for h in header_tensors) \
+        else formats.BS_FORMAT_VERSION_V1
+    container.write_container(dst, header, data.getvalue(), format_version=version)
+    return str(dst)
+
+
+def raw_words(t) -> np.ndarray:
+    """bf16 tensor -> uint16 numpy view of its bit patterns (host)."""
+    import torch
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)

@@ -1,0 +1,275 @@
+"""The decode engine: container entries -> device tensors, on one GPU.
+
+Every caller of the drop-in API (decoder.load/decompress, StreamingLoader,
+BigSmallStreamingModel) goes through `GroupDecoder`. A *group* is a set of
+container entries decoded together, normally one transformer layer
+(bigsmall/streaming.py:218-227 decodes a layer tensor by tensor; here it is
+one launch per codec family):
+
+  1. the group's compressed bytes (one contiguous span of the data section)
+     are copied host -> device on a copy stream, from pinned buffers that
+     rotate so the disk read / memcpy of group g+1 overlaps the copy of g;
+  2. the decode stream waits for that copy only, then launches
+       - one batched BSCK launch (bs_chunk_decode_batch) for every
+         bf16_chunked_v1 / fp8_chunked_v1 entry of the group,
+       - bs_refcodec_decode per reference-format entry (bf16_parallel_v1,
+         bf16_se_tans, bf16_se_single_kernel),
+       - device-to-device copies for `raw` entries,
+     writing straight into freshly allocated output tensors;
+  3. tied entries become copies of their master after it is decoded.
+So decoding group g overlaps the host->device copy of group g+1.
+
+Codecs whose bitstream is defined by libraries this engine does not carry
+(constriction's bf16_se_rans / bf16_se_ac / fp8_cat_ac / ..., zstd-based
+`special`/`zstd`) raise BigSmallVersionError naming the codec.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .codecs import _refstreams
+from .codecs import bf16_chunked
+from .container import tensor_numel
+from .device import ChunkBatch, ChunkJob, StatusWord, require_gpu
+from .exceptions import BigSmallVersionError
+from .formats import torch_dtype
+
+BSCK_CODECS = {bf16_chunked.CODEC_BF16: 2, bf16_chunked.CODEC_FP8: 1}
+REF_CODECS = set(_refstreams.PARSERS)
+UNSUPPORTED = {
+    "bf16_se_rans": "constriction ANS (Rust library, not available to this engine)",
+    "bf16_se_ac": "constriction range coder (Rust library, not available to this engine)",
+    "fp8_cat_ac": "constriction range coder", "fp4_cat_ac": "constriction range coder",
+    "fp16_se_ac": "constriction range coder", "fp32_se_ac": "constriction range coder",
+    "bf16_sparsity_v1": "constriction-coded populations", "fp2_residual_v1": "constriction-coded residual",
+    "special": "zstd/blosc2", "zstd": "zstd", "zstd_xor_delta": "zstd",
+}
+
+
+def entry_numel(t: dict) -> int:
+    """Element count the way the reference's _decode_blob computes it (decoder.py:53)."""
+    return tensor_numel(t) if t["shape"] else 1
+
+
+def check_supported(t: dict) -> None:
+    codec = t["codec"]
+    if codec in ("raw", "tied_ref") or codec in BSCK_CODECS or codec in REF_CODECS:
+        return
+    from . import __version__
+    detail = f"file references codec {codec!r}"
+    if codec in UNSUPPORTED:
+        detail += f", whose bitstream is defined by {UNSUPPORTED[codec]}; the MI355X engine decodes " \
+                  f"bf16_chunked_v1, fp8_chunked_v1, bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel and raw"
+    raise BigSmallVersionError(required="newer-than-installed", installed=__version__, detail=detail)
+
+
+@dataclass
+class GroupResult:
+    """Outputs of one decoded group. `tensors` hold valid data once the decode
+    stream has passed `done` (call `wait()` to synchronise and check)."""
+    tensors: dict
+    status: StatusWord
+    done: object = None                   # torch.cuda.Event on the decode stream
+    keep: list = field(default_factory=list)
+
+    def wait(self, what: str = "decode") -> dict:
+        import torch
+        if self.done is not None:
+            self.done.synchronize()
+        else:
+            torch.cuda.synchronize()
+        self.status.check(what)
+        self.keep.clear()
+        return self.tensors
+
+
+class GroupDecoder:
+    """Decodes groups of container entries into device tensors.
+
+    stream: the decode stream (default: torch's current stream).
+    copy_stream: where host->device copies run (default: a new stream).
+    Pinned staging buffers are allocated lazily and reused (n_pinned of them).
+    """
+
+    def __init__(self, device=None, stream=None, copy_stream=None, n_pinned: int = 2):
+        import torch
+        self.device = require_gpu(device)
+        self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
+        self.copy_stream = copy_stream if copy_stream is not None else torch.cuda.Stream(self.device)
+        self._pinned: list = [None] * max(1, n_pinned)
+        self._pinned_busy: list = [None] * len(self._pinned)
+        self._next = 0
+
+    # -- staging ---------------------------------------------------------------
+    def _pinned_buffer(self, nbytes: int):
+        import torch
+        i = self._next
+        self._next = (self._next + 1) % len(self._pinned)
+        ev = self._pinned_busy[i]
+        if ev is not None:
+            ev.synchronize()              # the copy that last read this buffer has finished
+        buf = self._pinned[i]
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True)
+            self._pinned[i] = buf
+        return i, buf
+
+    def upload(self, fill, nbytes: int):
+        """Copy `nbytes` produced by `fill(np_view)` to a new device buffer on the
+        copy stream; returns (device tensor, event recorded after the copy)."""
+        import torch
+        i, buf = self._pinned_buffer(nbytes)
+        view = buf[:nbytes]
+        fill(view.numpy())
+        dev = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        with torch.cuda.stream(self.copy_stream):
+            if nbytes:
+                dev[:nbytes].copy_(view, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.copy_stream)
+        self._pinned_busy[i] = ev
+        return dev, ev
+
+    # -- decoding --------------------------------------------------------------
+    def decode_group(self, entries: list[dict], read_span, span_start: int, span_len: int,
+                     resolve_tied=None, dtype=None) -> GroupResult:
+        """Decode `entries` (container tensor dicts). Their blobs lie in the data
+        section range [span_start, span_start + span_len); `read_span(offset,
+        np_out)` fills np_out with that many bytes of the data section starting
+        at offset. `resolve_tied(name)` returns the decoded master tensor for a
+        tied entry whose master is outside the group."""
+        import torch
+        for t in entries:
+            check_supported(t)
+        host_view = {}
+
+        def fill(dst):
+            if span_len:
+                read_span(span_start, dst)
+            host_view["bytes"] = dst
+
+        d_span, copied = self.upload(fill, span_len)
+        host = host_view["bytes"]
+        with torch.cuda.stream(self.stream):       # allocations and launches on the decode stream
+            status, out, keep = self._launch_group(entries, host, d_span, copied, span_start, span_len,
+                                                   resolve_tied, dtype)
+            done = torch.cuda.Event()
+            done.record(self.stream)
+        return GroupResult(out, status, done, keep)
+
+    def _launch_group(self, entries, host, d_span, copied, span_start, span_len, resolve_tied, dtype):
+        import torch
+        status = StatusWord(self.device)
+        out: dict = {}
+        keep = [d_span]
+        jobs = []
+        refs = []
+        raws = []
+        base = d_span.data_ptr()
+        for t in entries:
+            if t["codec"] == "tied_ref":
+                continue
+            shape = [int(s) for s in t["shape"]]
+            tdt = torch_dtype(t["dtype"])
+            o = torch.empty(shape, dtype=tdt, device=self.device)
+            out[t["name"]] = o
+            off, nb = int(t["offset"]) - span_start, int(t["compressed_bytes"])
+            if not 0 <= off <= off + nb <= span_len:
+                raise ValueError(f"{t['name']}: blob [{t['offset']}, +{nb}) outside its group's span")
+            n = entry_numel(t)
+            codec = t["codec"]
+            if codec == "raw":
+                if nb != o.numel() * o.element_size():
+                    raise ValueError(f"{t['name']}: raw blob has {nb} bytes, tensor needs "
+                                     f"{o.numel() * o.element_size()}")
+                raws.append((o, off, nb))
+            elif codec in BSCK_CODECS:
+                eb = BSCK_CODECS[codec]
+                if o.element_size() != eb:
+                    raise ValueError(f"{t['name']}: {codec} decodes {eb}-byte elements, dtype is {t['dtype']}")
+                if n == 0 or nb == 0:
+                    continue
+                inf = bf16_chunked.info(bytes(host[off:off + 32]))
+                if inf.n != n or inf.elem_bytes != eb:
+                    raise ValueError(f"{t['name']}: {codec} weight count mismatch ({inf.n} vs {n})")
+                ptr = base + off
+                if ptr % 16:
+                    # BSCK needs 16-byte aligned blobs: realign on the decode stream (below)
+                    a = torch.empty(nb + 16, dtype=torch.uint8, device=self.device)
+                    keep.append(a)
+                    jobs.append((ChunkJob(a.data_ptr(), nb, o.data_ptr(), n, inf.n_chunks, inf.plane_mode), (off, nb, a)))
+                else:
+                    jobs.append((ChunkJob(ptr, nb, o.data_ptr(), n, inf.n_chunks, inf.plane_mode), None))
+            elif codec in REF_CODECS:
+                if o.element_size() != 2:
+                    raise ValueError(f"{t['name']}: {codec} decodes bf16, dtype is {t['dtype']}")
+                if n == 0 or nb == 0:
+                    continue
+                plan = _refstreams.PARSERS[codec](bytes(host[off:off + nb]), n)
+                refs.append((_refstreams.RefLaunch(plan, base + off, self.device), o))
+        self.stream.wait_event(copied)
+        d_span.record_stream(self.stream)
+        for o, off, nb in raws:
+            o.view(-1).view(torch.uint8).copy_(d_span[off:off + nb])
+        if jobs:
+            for job, realign in jobs:
+                if realign is not None:
+                    off, nb, a = realign
+                    a[:nb].copy_(d_span[off:off + nb])
+            batch = ChunkBatch([j for j, _ in jobs], self.device)
+            keep.append(batch)
+            batch.launch(status, self.stream)
+        for launch, o in refs:
+            keep.append(launch)
+            launch.launch(o.data_ptr(), status.ptr, int(self.stream.cuda_stream))
+        for t in entries:
+            if t["codec"] != "tied_ref":
+                continue
+            master = (t.get("extra") or {}).get("tied_to")
+            src = out.get(master)
+            if src is None and resolve_tied is not None:
+                src = resolve_tied(master)
+            if src is None:
+                raise KeyError(f"tied_ref master {master!r} of {t['name']!r} not found")
+            out[t["name"]] = src.clone()
+        if dtype is not None:
+            for k, v in out.items():
+                if v.is_floating_point() and v.dtype != dtype:
+                    out[k] = v.to(dtype)
+        return status, out, keep
+
+
+def file_span_reader(path):
+    """read_span(offset, np_out) over the data section of a container file."""
+    from .container import read_header
+    _, data_offset = read_header(path)
+    fd = os.open(str(path), os.O_RDONLY)
+
+    def read_span(offset: int, dst: np.ndarray) -> None:
+        mv = memoryview(dst)
+        got = 0
+        while got < len(mv):
+            k = os.preadv(fd, [mv[got:]], data_offset + offset + got)
+            if k <= 0:
+                raise ValueError(f"{path}: data section truncated at {offset + got}")
+            got += k
+
+    read_span.close = lambda: os.close(fd)
+    return read_span
+
+
+def group_span(entries: list[dict]) -> tuple[int, int]:
+    """[start, end) of the data section holding the entries' blobs."""
+    ents = [t for t in entries if t["codec"] != "tied_ref" and int(t["compressed_bytes"]) > 0]
+    if not ents:
+        return 0, 0
+    lo = min(int(t["offset"]) for t in ents)
+    hi = max(int(t["offset"]) + int(t["compressed_bytes"]) for t in ents)
+    return lo, hi
+
+
+__all__ = ["GroupDecoder", "GroupResult", "check_supported", "entry_numel", "file_span_reader", "group_span",
+           "BSCK_CODECS", "REF_CODECS", "UNSUPPORTED"]

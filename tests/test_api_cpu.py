@@ -1,0 +1,167 @@
+"""CPU checks of the drop-in host API (no GPU needed).
+
+- compress() writes the reference's container layout and header fields, with
+  its routing: tied (md5, >= 1024 B) -> tied_ref, tiny (< 512 B) -> raw, bf16 ->
+  bf16_chunked_v1, fp8 -> fp8_chunked_v1, other dtypes -> raw; every blob's
+  bytes decode (through the oracle's CPU decoder of the GPU format) to the
+  source tensor's bytes, and match the header md5;
+- codec_registry keeps the reference's plugin API and smallest-wins rule;
+- the KV entry framing (versions 1/2 refused, version 3 parsed);
+- StreamingLoader's index (layers, shards, duplicate_map) builds without a GPU;
+- without a GPU, every decode entry point raises instead of decoding on the CPU.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from bigsmall_amd import codec_registry, container, engine, kernels
+from bigsmall_amd.codecs import kv_cache
+from bigsmall_amd.encoder import compress
+from bigsmall_amd.exceptions import BigSmallVersionError
+from bigsmall_amd.streaming import StreamingLoader, layer_index
+from bigsmall_amd.verify import verify_fast
+
+
+def _model(seed=0, layers=2):
+    g = torch.Generator().manual_seed(seed)
+    t = {}
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        t[p + "self_attn.q_proj.weight"] = (torch.randn(256, 128, generator=g) * 0.02).bfloat16()
+        t[p + "mlp.up_proj.weight"] = (torch.randn(300, 128, generator=g) * 0.02).bfloat16()
+        t[p + "input_layernorm.weight"] = (1 + torch.randn(128, generator=g) * 0.01).bfloat16()
+        t[p + "self_attn.q_proj.bias"] = torch.zeros(16, dtype=torch.bfloat16)           # tiny -> raw
+    t["model.embed_tokens.weight"] = (torch.randn(512, 128, generator=g) * 0.02).bfloat16()
+    t["lm_head.weight"] = t["model.embed_tokens.weight"].clone()                         # tied
+    t["model.norm.weight"] = torch.ones(128, dtype=torch.bfloat16)
+    t["fp8.weight"] = torch.randn(4096, generator=g).to(torch.float8_e4m3fn)
+    t["f32.weight"] = torch.randn(300, generator=g)
+    t["position_ids"] = torch.arange(1000, dtype=torch.int64)
+    return t
+
+
+@pytest.fixture(scope="module")
+def container_file(tmp_path_factory):
+    oracle.build()
+    p = tmp_path_factory.mktemp("bs") / "m.bs"
+    src = _model()
+    compress(src, p)
+    return p, src
+
+
+def test_container_fields_and_routing(container_file):
+    p, src = container_file
+    header, data_offset = container.read_header(p)
+    assert header["_format_version"] == 2 and header["tensor_count"] == len(src)
+    for k in ("format", "mode", "model_type", "base_model", "tensors", "codec_stats"):
+        assert k in header
+    by = {t["name"]: t for t in header["tensors"]}
+    assert by["lm_head.weight"]["codec"] == "tied_ref"
+    assert by["lm_head.weight"]["extra"]["tied_to"] == "model.embed_tokens.weight"
+    assert by["model.layers.0.self_attn.q_proj.bias"]["codec"] == "raw"
+    assert by["model.layers.0.self_attn.q_proj.weight"]["codec"] == "bf16_chunked_v1"
+    assert by["fp8.weight"]["codec"] == "fp8_chunked_v1"
+    assert by["f32.weight"]["codec"] == "raw" and by["position_ids"]["codec"] == "raw"
+    for t in header["tensors"]:
+        assert set(t) >= {"name", "shape", "dtype", "codec", "special", "compressed_bytes", "offset", "md5", "extra"}
+        if t["codec"] not in ("tied_ref", "raw"):
+            assert t["offset"] % 256 == 0
+
+
+def test_blobs_decode_to_source_via_oracle(container_file):
+    p, src = container_file
+    header, data_offset = container.read_header(p)
+    for i, t in enumerate(header["tensors"]):
+        want = src[t["name"]].contiguous().view(torch.uint8).numpy().tobytes()
+        assert hashlib.md5(want).hexdigest() == t["md5"]
+        blob = container.read_blob(p, header, data_offset, i)
+        if t["codec"] == "raw":
+            assert blob == want
+        elif t["codec"] in ("bf16_chunked_v1", "fp8_chunked_v1"):
+            eb = 2 if t["codec"] == "bf16_chunked_v1" else 1
+            assert oracle.chunk_decode(blob, len(want) // eb, eb) == want, t["name"]
+
+
+def test_info_and_verify_fast(container_file):
+    p, _ = container_file
+    inf = container.info(p)
+    assert inf["layer_count"] == 2 and inf["tensor_count"] == inf["tensor_count"]
+    ok, problems = verify_fast(p)
+    assert ok, problems
+
+
+def test_unsupported_codec_raises_version_error():
+    for codec in ["bf16_se_rans", "bf16_se_ac", "fp8_cat_ac", "zstd", "something_new"]:
+        with pytest.raises(BigSmallVersionError):
+            engine.check_supported({"codec": codec, "name": "x"})
+    for codec in ["raw", "tied_ref", "bf16_chunked_v1", "bf16_parallel_v1", "bf16_se_tans", "bf16_se_single_kernel"]:
+        engine.check_supported({"codec": codec, "name": "x"})
+
+
+def test_registry_plugin_api_and_smallest_wins(monkeypatch):
+    assert codec_registry.get_codec("bf16_chunked_v1") is not None
+    calls = []
+
+    def fake_enc(raw, **_):
+        calls.append(1)
+        return b"x", {"fake": True}
+
+    codec_registry.register_codec("fake_small", fake_enc, lambda b, e, n: b"")
+    monkeypatch.setitem(codec_registry.CODEC_CANDIDATES, "bf16", ["bf16_chunked_v1", "fake_small"])
+    raw = (torch.randn(10000) * 0.02).bfloat16().view(torch.uint8).numpy().tobytes()
+    blob, name, extras = codec_registry.auto_select_codec(raw, "bf16", "bfloat16")
+    assert name == "fake_small" and blob == b"x" and calls
+    # failing candidates are skipped, never raised
+    codec_registry.register_codec("broken", lambda raw, **_: 1 / 0, lambda *a: b"")
+    monkeypatch.setitem(codec_registry.CODEC_CANDIDATES, "bf16", ["broken"])
+    blob, name, _ = codec_registry.auto_select_codec(raw, "bf16", "bfloat16")
+    assert name == "raw" and blob == raw
+
+
+def test_kv_entry_framing():
+    k = (torch.randn(1, 4, 64, 32) * 2).bfloat16()
+    v = (torch.randn(1, 4, 64, 32) * 0.5).bfloat16()
+    data = kv_cache.compress_kv_entry(k, v)
+    assert data[0] == 3
+    parts = kv_cache.parse_kv_entry(data)
+    for (shape, n, off, blen), t in zip(parts, (k, v)):
+        assert shape == list(t.shape) and n == t.numel()
+        want = t.view(torch.int16).numpy().view(np.uint16).tobytes()
+        assert oracle.chunk_decode(data[off:off + blen], n) == want
+    for ver in (1, 2):
+        with pytest.raises(BigSmallVersionError):
+            kv_cache.parse_kv_entry(bytes([ver]) + data[1:])
+
+
+def test_streaming_index_without_gpu(container_file, tmp_path):
+    p, src = container_file
+    with StreamingLoader(p) as L:
+        assert L.layer_count() == 2
+        assert set(L.layer_tensor_names(0)) == {n for n in src if layer_index(n) == 0}
+        assert "lm_head.weight" in L.non_layer_tensor_names()
+    # directory with an index and a duplicate_map alias
+    d = tmp_path / "sharded"
+    d.mkdir()
+    (d / "a.bs").write_bytes(p.read_bytes())
+    (d / "bigsmall.index.json").write_text(json.dumps(
+        {"metadata": {"shards": ["a.bs"], "duplicate_map": {"alias.weight": {"master": "model.norm.weight"}}}}))
+    with StreamingLoader(d) as L:
+        assert "alias.weight" in L.tensor_names()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU behaviour")
+def test_no_cpu_fallback(container_file):
+    from bigsmall_amd import decoder
+    p, _ = container_file
+    kernels._GPU_BACKEND = None
+    assert not kernels.use_gpu() and kernels.backend_name() == "none"
+    with pytest.raises(RuntimeError):
+        kernels.decode_bf16_parallel(b"PAR1xxxx", {}, 10)
+    with pytest.raises(RuntimeError):
+        decoder.load(p)
