@@ -9,9 +9,10 @@ fallback: every decode entry point raises if it is missing.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libbigsmall_hip.so"
+LIB_PATH = Path(os.environ.get("BIGSMALL_HIP_LIB") or Path(__file__).resolve().parent / "_lib" / "libbigsmall_hip.so")
 
 BS_OK = 0
 BS_ERR_ARG, BS_ERR_FORMAT, BS_ERR_CAP, BS_ERR_HIP, BS_ERR_COUNT = -1, -2, -3, -4, -5

@@ -24,7 +24,12 @@ from ..device import ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, req
 
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
-DEFAULT_STEPS = 512
+# 448 steps x 128 states = 57,344 elements per chunk: a 14336x4096 matrix is
+# 1024 chunks (128 full 8-wave workgroups) and a Llama-3-8B-shaped layer fits
+# in one round of 480 workgroups on 256 CUs (two per CU). Measured on MI355X:
+# 0.175 ms/layer vs 0.184 at 512 steps; the ratio cost of the shorter chunks
+# is +0.05 pp (one 32-bit initial state per 448 elements).
+DEFAULT_STEPS = 448
 DEFAULT_LANES = 128
 MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT = -1, 0, 1, 2
 

@@ -51,7 +51,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kVersion = 2;
 constexpr int kWave = 64;                 // lanes of a wavefront
-constexpr int kWaves = 8;                 // chunks (wavefronts) per workgroup
+#ifndef BSCK_WAVES
+#define BSCK_WAVES 8
+#endif
+constexpr int kWaves = BSCK_WAVES;        // chunks (wavefronts) per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kBlock = 8;                 // steps per block (plane block, output flush, refill check)
 constexpr uint32_t kRing = 2048;          // per-wave renorm-word ring (u16 entries), power of two
@@ -480,15 +483,16 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
-  // each thread fills 4096/kThreads consecutive slots: one binary search, then a forward walk
-  {
-    uint32_t slot = tid * (4096u / kThreads);
+  // each thread fills a run of consecutive slots: one binary search, then a forward walk
+  constexpr uint32_t kRun = (4096u + kThreads - 1) / kThreads;
+  if (tid * kRun < 4096u) {
+    uint32_t slot = tid * kRun;
     uint32_t lo = 0, hi = nsym;                      // cum[lo] <= slot < cum[hi]
     while (hi - lo > 1) {
       uint32_t mid = (lo + hi) >> 1;
       if (s_cum[mid] <= slot) lo = mid; else hi = mid;
     }
-    for (uint32_t k = 0; k < 4096u / kThreads; ++k, ++slot) {
+    for (uint32_t k = 0; k < kRun && slot < 4096u; ++k, ++slot) {
       while (s_cum[lo + 1] <= slot) ++lo;
       const uint32_t c0 = s_cum[lo], f = s_cum[lo + 1] - c0, val = s_val[lo];
       s_tbl[slot] = fast ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
