@@ -1,0 +1,164 @@
+"""GPU parity at the benchmark configurations (bit-exact, md5 per tensor).
+
+C0  4096x4096 bf16 N(0, 0.02): this engine's encoder with auto-selection, and
+    the reference's formats (oracle encoders, byte-identical to the reference's).
+C2  Llama-3-8B-shaped layers at their real shapes (two of the model's 32, plus
+    an embedding slice) through decoder.load's layer pipeline.
+C3  8192x8192 stress: (a) Student-t df=3 at std 0.02, (b) half exact zeros,
+    (c) fp8 e4m3 of N(0, 1) plus its bf16 residual; "forced rANS" = the
+    reference's bf16_parallel_v1 and this engine's bf16_chunked_v1, "forced tANS"
+    = the reference's bf16_se_tans (its Numba rANS codec).
+C4  KV cache blocks of 256 tokens, K and V [8 heads, 32768 tokens, 128] per layer
+    scaled per head by U[0.5, 2], 64 random blocks per layer decoded in one launch
+    (two layers here; bench.py --workload kv runs all 32).
+"""
+from __future__ import annotations
+
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _words(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+
+
+def _gpu_words(t) -> bytes:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).tobytes()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _setup():
+    assert torch.cuda.is_available()
+    oracle.build()
+
+
+def _check_ref(codec, blob, words):
+    from bigsmall_amd.codecs import _refstreams
+    got = _refstreams.decode_host(codec, blob, words.size)
+    assert hashlib.md5(got).hexdigest() == hashlib.md5(words.tobytes()).hexdigest(), codec
+
+
+def _check_bsck(words, **kw):
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    blob = bc.encode_array(words, **kw)
+    eb = words.dtype.itemsize
+    got = bc.decode(blob, {}, words.size, elem_bytes=eb)
+    assert hashlib.md5(got).hexdigest() == hashlib.md5(words.tobytes()).hexdigest(), kw
+    return len(blob) / words.nbytes
+
+
+def test_c0_4096_square(tmp_path):
+    from bigsmall_amd.decoder import load
+    from bigsmall_amd.encoder import compress
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(4096, 4096, generator=g) * 0.02).bfloat16()
+    p = tmp_path / "c0.bs"
+    compress({"w": w}, p)
+    _say("[c0] engine container")
+    assert torch.equal(load(p)["w"].cpu().view(torch.int16), w.view(torch.int16))
+    words = _words(w)
+    for codec, enc in [("bf16_parallel_v1", oracle.par1_encode), ("bf16_se_tans", oracle.tans_encode),
+                       ("bf16_se_single_kernel", oracle.sk_encode)]:
+        _say(f"[c0] {codec}")
+        _check_ref(codec, enc(words), words)
+
+
+def _stress(kind: str) -> np.ndarray:
+    g = torch.Generator().manual_seed(3)
+    n = 8192 * 8192
+    if kind == "studentt":
+        x = torch.distributions.StudentT(3.0).sample((n,)) * (0.02 / np.sqrt(3.0))
+    else:
+        x = torch.randn(n, generator=g) * 0.02
+    w = _words(x.bfloat16())
+    if kind == "halfzero":
+        w = w.copy()
+        w[torch.randperm(n, generator=g).numpy()[: n // 2]] = 0
+    return w
+
+
+@pytest.mark.parametrize("kind", ["studentt", "halfzero"])
+def test_c3_bf16_stress_forced_rans(kind):
+    w = _stress(kind)
+    for mode in (-1, 1, 2):
+        _say(f"[c3] {kind} bf16_chunked_v1 mode={mode}")
+        _check_bsck(w, mode=mode)
+    _say(f"[c3] {kind} bf16_parallel_v1")
+    _check_ref("bf16_parallel_v1", oracle.par1_encode(w), w)
+
+
+@pytest.mark.parametrize("kind", ["studentt", "halfzero"])
+def test_c3_bf16_stress_forced_tans(kind):
+    w = _stress(kind)
+    _say(f"[c3] {kind} bf16_se_tans")
+    _check_ref("bf16_se_tans", oracle.tans_encode(w), w)
+
+
+def test_c3_fp8_and_residual():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(8192 * 8192, generator=g)
+    f8 = x.to(torch.float8_e4m3fn)
+    resid = (x - f8.float()).bfloat16()
+    _say("[c3] fp8 e4m3 fp8_chunked_v1")
+    _check_bsck(f8.view(torch.uint8).numpy())
+    rw = _words(resid)
+    _say("[c3] residual bf16_chunked_v1 / bf16_parallel_v1")
+    _check_bsck(rw)
+    _check_ref("bf16_parallel_v1", oracle.par1_encode(rw), rw)
+
+
+def test_c4_kv_blocks():
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache
+    g = torch.Generator().manual_seed(5)
+    cache = CompressedKVCache(device="cuda")
+    src = {}
+    for layer in range(2):
+        s = torch.empty(8, 1, 1).uniform_(0.5, 2.0, generator=g)
+        k = (torch.randn(8, 32768, 128, generator=g) * s).bfloat16()
+        v = (torch.randn(8, 32768, 128, generator=g) * s).bfloat16()
+        assert cache.set_blocks(layer, k, v, block_tokens=256) == 128
+        src[layer] = (k, v)
+    rng = np.random.default_rng(6)
+    req = [(layer, rng.choice(128, 64, replace=False)) for layer in range(2)]
+    _say("[c4] 2 layers x 64 blocks x (K, V) in one launch")
+    out = cache.get_blocks_multi(req)
+    for (layer, ids), (kb, vb) in zip(req, out):
+        k, v = src[layer]
+        for j, b in enumerate(ids):
+            assert _gpu_words(kb[j]) == _words(k[:, b * 256:(b + 1) * 256]).tobytes()
+            assert _gpu_words(vb[j]) == _words(v[:, b * 256:(b + 1) * 256]).tobytes()
+    assert 0.6 < cache.compression_ratio() < 0.85
+
+
+def test_c2_layers_at_real_shape(tmp_path):
+    from bigsmall_amd.decoder import load
+    from bigsmall_amd.encoder import compress
+    g = torch.Generator().manual_seed(7)
+    shapes = {"self_attn.q_proj": (4096, 4096), "self_attn.k_proj": (1024, 4096), "self_attn.v_proj": (1024, 4096),
+              "self_attn.o_proj": (4096, 4096), "mlp.gate_proj": (14336, 4096), "mlp.up_proj": (14336, 4096),
+              "mlp.down_proj": (4096, 14336)}
+    t = {"model.embed_tokens.weight": (torch.randn(8192, 4096, generator=g) * 0.02).bfloat16()}
+    for i in range(2):
+        for k, s in shapes.items():
+            t[f"model.layers.{i}.{k}.weight"] = (torch.randn(*s, generator=g) * 0.02).bfloat16()
+        for k in ("input_layernorm", "post_attention_layernorm"):
+            t[f"model.layers.{i}.{k}.weight"] = (1 + torch.randn(4096, generator=g) * 0.01).bfloat16()
+    p = tmp_path / "c2.bs"
+    compress(t, p)
+    _say("[c2] load 2 layers + embedding slice")
+    out = load(p)
+    for k, v in t.items():
+        assert torch.equal(out[k].cpu().view(torch.int16), v.view(torch.int16)), k
