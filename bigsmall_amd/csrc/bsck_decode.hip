@@ -56,7 +56,12 @@ constexpr int kWave = 64;                 // lanes of a wavefront
 #endif
 constexpr int kWaves = BSCK_WAVES;        // chunks (wavefronts) per workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kBlock = 8;                 // steps per block (plane block, output flush, refill check)
+// Steps per block (dense-plane block, refill check): 8 for K <= 2 states per
+// lane, 4 for K = 4, so a block is at most 1024 elements (1024 renorm words of
+// worst-case demand) and a lane's plane bytes of a block are 16 bytes.
+template <int K>
+constexpr int block_steps() { return K == 4 ? 4 : 8; }
+constexpr int kBlockMax = 8;
 constexpr uint32_t kRing = 2048;          // per-wave renorm-word ring (u16 entries), power of two
 constexpr uint32_t kMirror = 64;          // ring words [0, 64) are mirrored after the ring end
 constexpr uint32_t kRingBytes = (kRing + kMirror) * 2;
@@ -64,10 +69,12 @@ constexpr uint32_t kPRing = 4096;         // per-wave compact-plane ring (bytes)
 constexpr uint32_t kWSeg = 512;           // words per word-ring segment (64 lanes x 16 bytes)
 constexpr uint32_t kPSeg = 1024;          // bytes per plane-ring segment
 constexpr uint32_t kL = 1u << 16;
+// s_waitcnt immediate for gfx9: vmcnt(2), expcnt and lgkmcnt not waited on
+// (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
+constexpr int kWaitVm2 = 2 | (7 << 4) | (15 << 8);
 // dynamic LDS layout (bytes): decode table | word rings | output staging | plane rings (compact launches)
 constexpr uint32_t kTblBytes = 4096 * 8;
-constexpr int kHalf = kBlock / 2;         // steps per output flush (staging holds half a block)
-constexpr uint32_t kStageMax = kHalf * 128 * 2;    // per wave: 4 steps x up to 128 states x 2 bytes
+constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
 constexpr uint32_t kLdsLean = kTblBytes + kWaves * (kRingBytes + kStageMax);
 constexpr uint32_t kLdsCompact = kLdsLean + kWaves * kPRing;
 
@@ -92,6 +99,7 @@ template <int K>
 __device__ __forceinline__ void consume(const uint32_t (&v)[K]) {
   if (K == 1) asm volatile("" ::"v"(v[0]));
   if (K == 2) asm volatile("" ::"v"(v[0]), "v"(v[K - 1]));
+  if (K == 4) asm volatile("" ::"v"(v[0]), "v"(v[1 % K]), "v"(v[2 % K]), "v"(v[3 % K]));
 }
 
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
@@ -125,21 +133,29 @@ __device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, u32x
 }
 
 template <int K>
-struct PlaneRegs {   // dense plane bytes of one block: 8*K per lane
-  uint64_t b[K];
+struct PlaneRegs {   // dense plane bytes of one block: 8 (K = 1) or 16 (K = 2, 4) per lane
+  static constexpr int kWords = K == 1 ? 1 : 2;
+  uint64_t b[kWords];
 };
 template <int K>
 __device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, uint32_t blk, uint32_t lane) {
   PlaneRegs<K> r;
-  const GLB uint8_t* p = dplane + (uint64_t)blk * (kBlock * kWave * K) + lane * 8u * K;
-  if (K == 2) {
+  constexpr uint32_t kLaneBytes = block_steps<K>() * K;   // 8 (K=1) or 16 (K=2, 4)
+  const GLB uint8_t* p = dplane + (uint64_t)blk * (kLaneBytes * kWave) + lane * kLaneBytes;
+  if (kLaneBytes == 16) {
     const u32x4 v = *(const GLB u32x4*)p;
     r.b[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
-    r.b[K - 1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
+    r.b[PlaneRegs<K>::kWords - 1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
   } else {
     r.b[0] = *(const GLB uint64_t*)p;
   }
   return r;
+}
+
+template <int K>
+__device__ __forceinline__ void consume_plane(const PlaneRegs<K>& p) {
+  if (PlaneRegs<K>::kWords == 1) asm volatile("" ::"v"(p.b[0]));
+  else asm volatile("" ::"v"(p.b[0]), "v"(p.b[PlaneRegs<K>::kWords - 1]));
 }
 
 // Per-wavefront decode state of one chunk.
@@ -163,19 +179,23 @@ struct ChunkParams {
   uint32_t n_words, n_plane, wvalid16, pvalid16, nc, nsteps, nblk, lane;
 };
 
-// Store the staged outputs of half-block `hb` (kHalf steps) to the output.
+// Store the staged outputs of half-block `hb` (half a block of steps) to the output.
 template <int K, int EB, bool PARTIAL>
 __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
-  constexpr uint32_t kBlkElems = kHalf * kWave * K;
+  constexpr uint32_t kBlkElems = block_steps<K>() / 2 * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
   const uint64_t blk_byte0 = (C.base + (uint64_t)hb * kBlkElems) * EB;
   const uint32_t valid_bytes = PARTIAL ? min(kBlkBytes, (C.nc - min(C.nc, hb * kBlkElems)) * EB) : kBlkBytes;
 #pragma unroll
   for (uint32_t i = 0; i < (kBlkBytes + 1023) / 1024; ++i) {
     const uint32_t o = i * 1024u + C.lane * 16u;
-    if (o + 16u <= valid_bytes) {
+    // a full chunk's half block is a multiple of 1024 bytes for bf16 with K >= 2:
+    // the store is then unconditional, which keeps the wait counts exact
+    if ((!PARTIAL && kBlkBytes % 1024u == 0) || o + 16u <= valid_bytes) {
       const u32x4 d = *(const LDS u32x4*)(stage + o);
-      *(GLB u32x4*)(C.out8 + blk_byte0 + o) = d;
+      // streaming store: the decoded tensor is far larger than the L2, and
+      // the hint measured 3-4% faster than a plain store on the 8B layer
+      __builtin_nontemporal_store(d, (GLB u32x4*)(C.out8 + blk_byte0 + o));
     } else if (PARTIAL && o < valid_bytes) {
       for (uint32_t k = o; k < min(o + 16u, valid_bytes); ++k) C.out8[blk_byte0 + k] = stage[k];
     }
@@ -223,23 +243,38 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
   for (int g = 0; g < K; ++g) S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
 }
 
-// One block of kBlock steps. Every global-memory operation of the block is
-// issued at its start, before any decoding: land the ring segments prefetched
-// by the previous block, top the rings up if they hold less than a block of
-// worst-case demand (rare), store the previous block's staged output, prefetch
-// the next block's dense plane and the next ring segments. The 8 steps of
-// decoding that follow cover the latency of all of them, so the wait at the
-// next block start (on gfx9 the vector-memory counter covers loads and
-// stores, in issue order) finds them complete.
+// One block of kBlock steps. Every global load of the block is issued at its
+// start, before any decoding: land the ring segments prefetched by the
+// previous block, top the rings up if they hold less than a block of
+// worst-case demand (rare), prefetch the next block's dense plane and the next
+// ring segments. The block's steps cover their latency. The staged outputs
+// are stored after the loads (mid-block and at the block end), because on
+// gfx9 one vector-memory counter covers loads and stores and retires in issue
+// order: the wait for this block's loads at the next block start must not
+// include a store's write acknowledgement.
 template <int K, int MODE, int EB, bool PARTIAL>
 __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, PlaneRegs<K>& pl_next,
                                              ChunkState<K>& S, const ChunkParams& C,
                                              const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
                                              LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage) {
   constexpr uint32_t kStates = kWave * K;
+  constexpr int kBlock = block_steps<K>();
+  constexpr int kHalf = kBlock / 2;
   constexpr uint32_t kBlkElems = kBlock * kStates;
   constexpr bool FAST = MODE == 1 && EB == 2;
   const uint32_t lane = C.lane;
+  // The previous block's loads were followed by (at most) its two output
+  // stores: vmcnt(2) lands the loads and leaves the stores in flight. Stating
+  // it here gives the compiler's wait-count tracking an exact state at the
+  // block start; its own merge over the conditional paths below is
+  // conservative and would otherwise wait for the stores too.
+  if (!PARTIAL) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm2);
+    // uses of the landed registers at this point keep the compiler's own
+    // waits for them here, before this block's loads are issued
+    if (MODE == 1) consume_plane(pl);
+    asm volatile("" ::"v"(S.wp.x), "v"(S.wp.y), "v"(S.wp.z), "v"(S.wp.w));
+  }
   if (S.wn) { store_wseg(wring, S.wld, S.wp, lane); S.wld += kWSeg; }
   if (MODE == 2 && S.pn) { store_pseg(pring, S.pld, S.pp, lane); S.pld += kPSeg; }
   {
@@ -257,7 +292,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     }
   }
   wave_sync();
-  if (blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
+  if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
   if (MODE == 1) pl_next = load_plane<K>(C.dplane, min(blk + 1, C.nblk - 1), lane);
   S.wn = S.wld < C.n_words && S.wld - S.wptr + kWSeg <= kRing;
   S.wp = load_seg(C.wsrc, S.wn ? S.wld / 8u : 0u, C.wvalid16, lane, C.safe);
@@ -284,12 +319,20 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
       const uint64_t pw = pl.b[(q * K) / 8];
       const uint32_t o = (q * K) % 8;                    // byte offset in pw
       const uint32_t phi = (uint32_t)(pw >> 32), plo = (uint32_t)pw;
-      if (K == 2) {
-        // word pair: (p | p<<8) & 0x807F per half, exponents from byte 3 of d
-        const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (o + 1) * 0x01010000u | o * 0x0101u);
-        const uint32_t ex = __builtin_amdgcn_perm(d[K - 1], d[0], 0x070C030Cu) >> 1;
-        const uint32_t v = (dup & 0x807F807Fu) | ex;
-        *(LDS uint32_t*)(stage + qs * (kStates * 2) + lane * 4u) = v;
+      if (K >= 2) {
+        // word pairs: (p | p<<8) & 0x807F per half, exponents from byte 3 of d
+        constexpr int kPairs = K >= 2 ? K / 2 : 1;
+        uint32_t v[kPairs];
+#pragma unroll
+        for (int h = 0; h < kPairs; ++h) {
+          const uint32_t ob = o + 2 * h;
+          const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (ob + 1) * 0x01010000u | ob * 0x0101u);
+          const uint32_t ex = __builtin_amdgcn_perm(d[(2 * h + 1) % K], d[(2 * h) % K], 0x070C030Cu) >> 1;
+          v[h] = (dup & 0x807F807Fu) | ex;
+        }
+        LDS uint8_t* dst = stage + qs * (kStates * 2) + lane * (2u * K);
+        if (K == 2) *(LDS uint32_t*)dst = v[0];
+        else *(LDS uint64_t*)dst = (uint64_t)v[0] | ((uint64_t)v[kPairs - 1] << 32);
       } else {
         const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
         const uint32_t v = (dup & 0x807Fu) | (d[0] >> 17);
@@ -311,6 +354,14 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         else stage[si] = (uint8_t)v;
       }
     }
+  }
+  // A full chunk stores its second half here, so every store of the block is
+  // issued after the block's loads: the wait for those loads at the next block
+  // start then leaves the stores in flight (the vector-memory counter retires
+  // in issue order). A partial chunk stores it at the next block start.
+  if (!PARTIAL) {
+    wave_sync();
+    flush_half<K, EB, PARTIAL>(2 * blk + 1, C, stage);
   }
 }
 
@@ -340,7 +391,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   C.pvalid16 = pad16(n_plane) / 16u;
   C.nc = nc;
   C.nsteps = nsteps;
-  C.nblk = (nsteps + kBlock - 1) / kBlock;
+  C.nblk = (nsteps + block_steps<K>() - 1) / block_steps<K>();
 
   ChunkState<K> S;
 #pragma unroll
@@ -352,8 +403,14 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   // dense plane double buffer: block b uses one, block b+1's is loaded into the other
   PlaneRegs<K> plA, plB;
 #pragma unroll
-  for (int g = 0; g < K; ++g) plA.b[g] = plB.b[g] = 0;
+  for (int i = 0; i < PlaneRegs<K>::kWords; ++i) plA.b[i] = plB.b[i] = 0;
   if (MODE == 1) plA = load_plane<K>(C.dplane, 0, C.lane);
+  // Land the loads above before the loop. Otherwise the loop header would merge
+  // "initial load pending" into its wait-count state, and the first use of
+  // these registers in every iteration would get a wait that also covers the
+  // stores of the previous block.
+  consume<K>(S.x);
+  if (MODE == 1) consume_plane(plA);
 
   // Two blocks per iteration so the dense-plane registers alternate without
   // copies. Full chunks have an even block count (steps % 16 == 0).
@@ -362,10 +419,12 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     if (PARTIAL && blk + 1 >= C.nblk) break;
     decode_block<K, MODE, EB, PARTIAL>(blk + 1, plB, plA, S, C, tbl, wring, pring, stage);
   }
-  // the last staged half: the second half of the last block, or its first if
-  // a partial chunk's last block has at most kHalf steps
-  wave_sync();
-  flush_half<K, EB, PARTIAL>((C.nsteps - 1) / kHalf, C, stage);
+  // a partial chunk's last staged half: the second half of its last block, or
+  // the first if that block has at most half a block of steps
+  if (PARTIAL) {
+    wave_sync();
+    flush_half<K, EB, PARTIAL>((C.nsteps - 1) / (block_steps<K>() / 2), C, stage);
+  }
 
   bool bad_state = false;
 #pragma unroll
@@ -441,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t nsym = (uint32_t)b[22] | ((uint32_t)b[23] << 8);
   const uint32_t nch = ld_u32(b + 24);
   const uint64_t per = (uint64_t)lanes * steps;
-  if ((lanes != 64 && lanes != 128) || steps == 0 || (steps % (2 * kBlock)) != 0 || nsym == 0 ||
+  if ((lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || (steps % (2 * kBlockMax)) != 0 || nsym == 0 ||
       nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per == 0 || nch != (n + per - 1) / per) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
@@ -511,7 +570,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint64_t cbase_idx = (uint64_t)chunk * per;
   const uint32_t nc = (uint32_t)((n - cbase_idx) < per ? (n - cbase_idx) : per);
   const uint32_t nsteps = (nc + lanes - 1) / lanes;
-  const uint32_t dense_plane = ((nsteps + kBlock - 1) / kBlock) * kBlock * lanes;
+  const uint32_t bsteps = lanes == 256 ? 4u : 8u;     // block_steps<K>()
+  const uint32_t dense_plane = ((nsteps + bsteps - 1) / bsteps) * bsteps * lanes;
   bool ok = (off % 16) == 0 && off + 4ull * lanes + pad16(nw * 2u) + pad16(np) <= T.blob_bytes &&
             nw <= nsteps * lanes && T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
   if (mode == 1) ok = ok && np == dense_plane;
@@ -529,8 +589,10 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const bool partial = nc != per;
   if (lanes == 64)
     decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
-  else
+  else if (lanes == 128)
     decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
+  else
+    decode_chunk_k<4, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
@@ -574,7 +636,8 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   info->lanes = (uint32_t)h[20] | ((uint32_t)h[21] << 8);
   info->n_syms = (uint32_t)h[22] | ((uint32_t)h[23] << 8);
   info->n_chunks = u32(24);
-  if (h[7] != 12 || (info->lanes != 64 && info->lanes != 128) || info->steps == 0 || info->steps % (2 * kBlock) || info->n_syms == 0 ||
+  if (h[7] != 12 || (info->lanes != 64 && info->lanes != 128 && info->lanes != 256) || info->steps == 0 ||
+      info->steps % (2 * kBlockMax) || info->n_syms == 0 ||
       info->n_syms > 256 || (info->elem_bytes != 1 && info->elem_bytes != 2) || info->plane_mode > 2)
     return BS_ERR_FORMAT;
   const uint64_t per = (uint64_t)info->lanes * info->steps;

@@ -34,7 +34,8 @@ constexpr uint8_t kVersion = 2;       // BSCK layout version
 constexpr uint32_t kWave = 64;        // lanes of a wavefront
 constexpr uint32_t kL = 1u << 16;
 constexpr uint32_t kM = 4096;
-constexpr uint32_t kBlock = 8;
+// steps per dense-plane block: 8 for 64 or 128 states per chunk, 4 for 256
+inline uint32_t block_steps(uint32_t lanes) { return lanes == 256 ? 4u : 8u; }
 constexpr uint32_t kStepAlign = 16;   // steps per chunk: a multiple of two blocks
 
 inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
@@ -240,11 +241,12 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
   if (P.mode == 1) {
     // dense plane: per 8-step block, wavefront lane l's 8*K bytes are contiguous,
     // step-major: byte (q, g) of lane l at l*8K + q*K + g
-    const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
-    plane.assign((size_t)nblk * kBlock * lanes, 0);
+    const uint32_t bs = block_steps(lanes);
+    const uint32_t nblk = (nsteps + bs - 1) / bs;
+    plane.assign((size_t)nblk * bs * lanes, 0);
     for (uint32_t j = 0; j < nc; ++j) {
       const uint32_t w = w16[base + j], t = j / lanes, r = j % lanes, l = r / K, g = r % K;
-      plane[(size_t)(t / kBlock) * kBlock * lanes + l * kBlock * K + (t % kBlock) * K + g] =
+      plane[(size_t)(t / bs) * bs * lanes + l * bs * K + (t % bs) * K + g] =
           (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
     }
   } else if (P.mode == 2) {
@@ -270,7 +272,7 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
 
 extern "C" {
 
-static bool lanes_ok(uint32_t lanes) { return lanes == 64 || lanes == 128; }
+static bool lanes_ok(uint32_t lanes) { return lanes == 64 || lanes == 128 || lanes == 256; }
 
 int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t* bound) {
   if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes))

@@ -775,8 +775,8 @@ out:
  * v = g*64 + l (wavefront lane l, group g) decodes element t*lanes + l*K + g at
  * step t. Decode step order: steps ascending; renorm words consumed in ascending
  * v order among states that fell below L. plane_mode 1 (dense): every element
- * consumes one byte, stored in blocks of 8 steps; the byte of state (g, l) for
- * step 8b+q sits at b*8*lanes + l*8*K + q*K + g.
+ * consumes one byte, stored in blocks of B steps (B = 8 for K <= 2, 4 for K = 4);
+ * the byte of state (g, l) for step B*b+q sits at b*B*lanes + l*B*K + q*K + g.
  * plane_mode 2 (compact): consuming elements read bytes in decode order.
  * plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
  * ------------------------------------------------------------------------ */
@@ -785,7 +785,7 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
-    if (ver != 2 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128) ||
+    if (ver != 2 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128 && lanes != 256) ||
         steps == 0 || steps % 16)
         return ORC_ERR_FORMAT;
     if (n != n_weights) return ORC_ERR_COUNT;
@@ -833,8 +833,9 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
                 if (cons[s]) {
                     uint32_t b;
                     if (mode == 1) {
-                        uint64_t blk = t / 8, q = t % 8;
-                        uint64_t idx = blk * 8 * lanes + (uint64_t)wl * 8 * K + q * K + g;
+                        uint64_t bs = lanes == 256 ? 4 : 8;   /* steps per plane block */
+                        uint64_t blk = t / bs, q = t % bs;
+                        uint64_t idx = blk * bs * lanes + (uint64_t)wl * bs * K + q * K + g;
                         if (idx >= np) return ORC_ERR_FORMAT;
                         b = pl[idx];
                     } else if (mode == 2) {

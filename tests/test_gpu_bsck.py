@@ -45,14 +45,14 @@ def _check_one(torch_gpu, words, steps=512, mode=-1, label="", lanes=128):
     return blob
 
 
-@pytest.mark.parametrize("lanes", [64, 128])
+@pytest.mark.parametrize("lanes", [64, 128, 256])
 @pytest.mark.parametrize("n", [1, 63, 64, 65, 127, 129, 511, 4097, 32768, 65536 * 3 + 1000, 1 << 20])
 def test_gaussian_sizes(torch_gpu, n, lanes):
     rng = np.random.default_rng(n)
     _check_one(torch_gpu, _bf16(rng.standard_normal(n) * 0.02), label=f"gauss{n}", lanes=lanes)
 
 
-@pytest.mark.parametrize("lanes", [64, 128])
+@pytest.mark.parametrize("lanes", [64, 128, 256])
 @pytest.mark.parametrize("mode", [-1, 1, 2])
 @pytest.mark.parametrize("steps", [16, 64, 512, 1024])
 def test_modes_and_steps(torch_gpu, mode, steps, lanes):
@@ -94,7 +94,7 @@ def test_batched_launch_matches_single(torch_gpu):
     rng = np.random.default_rng(13)
     sizes = [5, 64 * 512, 64 * 512 + 3, 1 << 18, 777_777]
     words = [_bf16(rng.standard_normal(s) * (0.01 + 0.01 * i)) for i, s in enumerate(sizes)]
-    blobs = [bc.encode_array(w, lanes=64 if i % 2 else 128) for i, w in enumerate(words)]
+    blobs = [bc.encode_array(w, lanes=(64, 128, 256)[i % 3]) for i, w in enumerate(words)]
     _say(f"[bsck] batch of {len(blobs)} blobs")
     dev = torch.device("cuda")
     d = [upload_bytes(b, dev) for b in blobs]

@@ -48,7 +48,7 @@ def _oracle():
     oracle.build()
 
 
-@pytest.mark.parametrize("lanes", [64, 128])
+@pytest.mark.parametrize("lanes", [64, 128, 256])
 @pytest.mark.parametrize("mode", [-1, 1, 2])
 @pytest.mark.parametrize("n", [1, 2, 63, 64, 129, 1000, 65536 + 7, 300_000])
 def test_encoder_roundtrip_via_oracle(n, mode, lanes):
