@@ -69,9 +69,9 @@ constexpr uint32_t kPRing = 4096;         // per-wave compact-plane ring (bytes)
 constexpr uint32_t kWSeg = 512;           // words per word-ring segment (64 lanes x 16 bytes)
 constexpr uint32_t kPSeg = 1024;          // bytes per plane-ring segment
 constexpr uint32_t kL = 1u << 16;
-// s_waitcnt immediate for gfx9: vmcnt(2), expcnt and lgkmcnt not waited on
+// s_waitcnt immediate for gfx9: vmcnt(4), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
-constexpr int kWaitVm2 = 2 | (7 << 4) | (15 << 8);
+constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
 // dynamic LDS layout (bytes): decode table | word rings | output staging | plane rings (compact launches)
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
@@ -164,8 +164,18 @@ struct ChunkState {
   uint32_t x[K];
   uint32_t wptr, wld;    // word ring holds words [wptr, wld)
   uint32_t pptr, pld;    // plane ring (compact mode) holds bytes [pptr, pld)
-  bool wn, pn;           // a segment is in flight for landing at the next block start
-  u32x4 wp, pp;
+};
+
+// Loads issued at a pair start (two blocks) and landed at the next one: up to
+// two word-ring segments, up to two compact-plane segments, and the dense
+// plane of the next pair's two blocks. Every load is issued unconditionally
+// (unneeded ones read an always-valid dummy address) so the wait counts are
+// the same on every path.
+template <int K>
+struct Inflight {
+  u32x4 w[2], p[2];
+  bool wn[2], pn[2];
+  PlaneRegs<K> pl[2];
 };
 
 // Chunk-constant parameters.
@@ -185,18 +195,35 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
   constexpr uint32_t kBlkElems = block_steps<K>() / 2 * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
   const uint64_t blk_byte0 = (C.base + (uint64_t)hb * kBlkElems) * EB;
-  const uint32_t valid_bytes = PARTIAL ? min(kBlkBytes, (C.nc - min(C.nc, hb * kBlkElems)) * EB) : kBlkBytes;
+  // Streaming stores: the decoded tensor is far larger than the L2 (the hint
+  // measured 3-4% faster than plain stores on an 8B layer). A full chunk's
+  // half block is 256, 512 or 1024 bytes: every lane stores its 4, 8 or 16
+  // bytes with one unconditional instruction, which keeps the wait counts of
+  // the pipeline exact.
+  if (!PARTIAL) {
+    static_assert(kBlkBytes == 256 || kBlkBytes == 512 || kBlkBytes == 1024, "half block size");
+    constexpr uint32_t kLB = kBlkBytes / kWave;
+    const uint32_t o = C.lane * kLB;
+    if (kLB == 16) {
+      const u32x4 d = *(const LDS u32x4*)(stage + o);
+      __builtin_nontemporal_store(d, (GLB u32x4*)(C.out8 + blk_byte0 + o));
+    } else if (kLB == 8) {
+      const uint64_t d = *(const LDS uint64_t*)(stage + o);
+      __builtin_nontemporal_store(d, (GLB uint64_t*)(C.out8 + blk_byte0 + o));
+    } else {
+      const uint32_t d = *(const LDS uint32_t*)(stage + o);
+      __builtin_nontemporal_store(d, (GLB uint32_t*)(C.out8 + blk_byte0 + o));
+    }
+    return;
+  }
+  const uint32_t valid_bytes = min(kBlkBytes, (C.nc - min(C.nc, hb * kBlkElems)) * EB);
 #pragma unroll
   for (uint32_t i = 0; i < (kBlkBytes + 1023) / 1024; ++i) {
     const uint32_t o = i * 1024u + C.lane * 16u;
-    // a full chunk's half block is a multiple of 1024 bytes for bf16 with K >= 2:
-    // the store is then unconditional, which keeps the wait counts exact
-    if ((!PARTIAL && kBlkBytes % 1024u == 0) || o + 16u <= valid_bytes) {
+    if (o + 16u <= valid_bytes) {
       const u32x4 d = *(const LDS u32x4*)(stage + o);
-      // streaming store: the decoded tensor is far larger than the L2, and
-      // the hint measured 3-4% faster than a plain store on the 8B layer
-      __builtin_nontemporal_store(d, (GLB u32x4*)(C.out8 + blk_byte0 + o));
-    } else if (PARTIAL && o < valid_bytes) {
+      *(GLB u32x4*)(C.out8 + blk_byte0 + o) = d;
+    } else if (o < valid_bytes) {
       for (uint32_t k = o; k < min(o + 16u, valid_bytes); ++k) C.out8[blk_byte0 + k] = stage[k];
     }
   }
@@ -243,65 +270,88 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
   for (int g = 0; g < K; ++g) S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
 }
 
-// One block of kBlock steps. Every global load of the block is issued at its
-// start, before any decoding: land the ring segments prefetched by the
-// previous block, top the rings up if they hold less than a block of
-// worst-case demand (rare), prefetch the next block's dense plane and the next
-// ring segments. The block's steps cover their latency. The staged outputs
-// are stored after the loads (mid-block and at the block end), because on
-// gfx9 one vector-memory counter covers loads and stores and retires in issue
-// order: the wait for this block's loads at the next block start must not
-// include a store's write acknowledgement.
-template <int K, int MODE, int EB, bool PARTIAL>
-__device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, PlaneRegs<K>& pl_next,
-                                             ChunkState<K>& S, const ChunkParams& C,
-                                             const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
-                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage) {
-  constexpr uint32_t kStates = kWave * K;
-  constexpr int kBlock = block_steps<K>();
-  constexpr int kHalf = kBlock / 2;
-  constexpr uint32_t kBlkElems = kBlock * kStates;
-  constexpr bool FAST = MODE == 1 && EB == 2;
-  const uint32_t lane = C.lane;
-  // The previous block's loads were followed by (at most) its two output
-  // stores: vmcnt(2) lands the loads and leaves the stores in flight. Stating
-  // it here gives the compiler's wait-count tracking an exact state at the
-  // block start; its own merge over the conditional paths below is
-  // conservative and would otherwise wait for the stores too.
-  if (!PARTIAL) {
-    __builtin_amdgcn_s_waitcnt(kWaitVm2);
-    // uses of the landed registers at this point keep the compiler's own
-    // waits for them here, before this block's loads are issued
-    if (MODE == 1) consume_plane(pl);
-    asm volatile("" ::"v"(S.wp.x), "v"(S.wp.y), "v"(S.wp.z), "v"(S.wp.w));
+// Ring upkeep and prefetch, at block granularity.
+//
+// Word-ring and compact-plane segments are requested at a pair start (every
+// other block) when the ring has room, and landed at the next pair start: the
+// two blocks in between cover their latency. So does the dense plane, loaded
+// one pair ahead. The output stores of a block (mid-block and at its end)
+// come after the pair's loads; on gfx9 one vector-memory counter covers loads
+// and stores and retires in issue order, so waiting for the loads at the next
+// pair start leaves the four stores of the pair in flight.
+
+// Land the in-flight ring segments, in request order.
+template <int K, int MODE>
+__device__ __forceinline__ void land_segments(ChunkState<K>& S, Inflight<K>& F, LDS uint16_t* __restrict__ wring,
+                                              LDS uint8_t* __restrict__ pring, uint32_t lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    if (F.wn[i]) { store_wseg(wring, S.wld, F.w[i], lane); S.wld += kWSeg; F.wn[i] = false; }
+  if (MODE == 2) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (F.pn[i]) { store_pseg(pring, S.pld, F.p[i], lane); S.pld += kPSeg; F.pn[i] = false; }
   }
-  if (S.wn) { store_wseg(wring, S.wld, S.wp, lane); S.wld += kWSeg; }
-  if (MODE == 2 && S.pn) { store_pseg(pring, S.pld, S.pp, lane); S.pld += kPSeg; }
-  {
-    const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
+}
+
+// Request up to two segments per ring (as many as fit behind the unconsumed
+// and landed data).
+template <int K, int MODE>
+__device__ __forceinline__ void request_segments(const ChunkState<K>& S, Inflight<K>& F, const ChunkParams& C) {
+  const uint32_t lane = C.lane;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t at = S.wld + i * kWSeg;
+    F.wn[i] = at < C.n_words && at + kWSeg - S.wptr <= kRing;
+    F.w[i] = load_seg(C.wsrc, F.wn[i] ? at / 8u : 0u, C.wvalid16, lane, C.safe);
+  }
+  if (MODE == 2) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t at = S.pld + i * kPSeg;
+      F.pn[i] = at < C.n_plane && at + kPSeg - S.pptr <= kPRing;
+      F.p[i] = load_seg(C.psrc, F.pn[i] ? at / 16u : 0u, C.pvalid16, lane, C.safe);
+    }
+  }
+}
+
+// Make sure the rings hold a block's worst-case demand. Rare: it lands the
+// in-flight segments early (waiting for them) and loads synchronously.
+template <int K, int MODE>
+__device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K>& F, const ChunkParams& C,
+                                       LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring) {
+  constexpr uint32_t kBlkElems = block_steps<K>() * kWave * K;
+  const uint32_t lane = C.lane;
+  const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
+  const uint32_t need_p = MODE == 2 ? min(kBlkElems, C.n_plane - S.pptr) : 0u;
+  if (S.wld - S.wptr < need_w || (MODE == 2 && S.pld - S.pptr < need_p)) {
+    land_segments<K, MODE>(S, F, wring, pring, lane);
     while (S.wld - S.wptr < need_w) {
       store_wseg(wring, S.wld, load_seg(C.wsrc, S.wld / 8u, C.wvalid16, lane, C.safe), lane);
       S.wld += kWSeg;
     }
     if (MODE == 2) {
-      const uint32_t need_p = min(kBlkElems, C.n_plane - S.pptr);
       while (S.pld - S.pptr < need_p) {
         store_pseg(pring, S.pld, load_seg(C.psrc, S.pld / 16u, C.pvalid16, lane, C.safe), lane);
         S.pld += kPSeg;
       }
     }
   }
-  wave_sync();
-  if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
-  if (MODE == 1) pl_next = load_plane<K>(C.dplane, min(blk + 1, C.nblk - 1), lane);
-  S.wn = S.wld < C.n_words && S.wld - S.wptr + kWSeg <= kRing;
-  S.wp = load_seg(C.wsrc, S.wn ? S.wld / 8u : 0u, C.wvalid16, lane, C.safe);
-  if (MODE == 2) {
-    S.pn = S.pld < C.n_plane && S.pld - S.pptr + kPSeg <= kPRing;
-    S.pp = load_seg(C.psrc, S.pn ? S.pld / 16u : 0u, C.pvalid16, lane, C.safe);
-  }
-  wave_sync();
+}
 
+// The steps of one block, staging outputs in LDS and storing each half block
+// once it is complete (a partial chunk stores its second half at the next
+// block start, or after the last block).
+template <int K, int MODE, int EB, bool PARTIAL>
+__device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, ChunkState<K>& S,
+                                             const ChunkParams& C, const LDS uint64_t* __restrict__ tbl,
+                                             const LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring,
+                                             LDS uint8_t* __restrict__ stage) {
+  constexpr uint32_t kStates = kWave * K;
+  constexpr int kBlock = block_steps<K>();
+  constexpr int kHalf = kBlock / 2;
+  constexpr bool FAST = MODE == 1 && EB == 2;
+  const uint32_t lane = C.lane;
 #pragma unroll
   for (int q = 0; q < kBlock; ++q) {
     const uint32_t t = blk * kBlock + q;
@@ -355,10 +405,6 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
       }
     }
   }
-  // A full chunk stores its second half here, so every store of the block is
-  // issued after the block's loads: the wait for those loads at the next block
-  // start then leaves the stores in flight (the vector-memory counter retires
-  // in issue order). A partial chunk stores it at the next block start.
   if (!PARTIAL) {
     wave_sync();
     flush_half<K, EB, PARTIAL>(2 * blk + 1, C, stage);
@@ -397,27 +443,51 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
 #pragma unroll
   for (int g = 0; g < K; ++g) S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
   S.wptr = S.wld = S.pptr = S.pld = 0;
-  S.wn = S.pn = false;
-  S.wp = S.pp = u32x4{0, 0, 0, 0};
 
-  // dense plane double buffer: block b uses one, block b+1's is loaded into the other
-  PlaneRegs<K> plA, plB;
+  // First pair's loads; land all of them before the loop so that the loop
+  // header's wait-count state holds no load issued here.
+  Inflight<K> F;
 #pragma unroll
-  for (int i = 0; i < PlaneRegs<K>::kWords; ++i) plA.b[i] = plB.b[i] = 0;
-  if (MODE == 1) plA = load_plane<K>(C.dplane, 0, C.lane);
-  // Land the loads above before the loop. Otherwise the loop header would merge
-  // "initial load pending" into its wait-count state, and the first use of
-  // these registers in every iteration would get a wait that also covers the
-  // stores of the previous block.
+  for (int i = 0; i < 2; ++i)
+    F.pl[i] = MODE == 1 ? load_plane<K>(C.dplane, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
+  request_segments<K, MODE>(S, F, C);
   consume<K>(S.x);
-  if (MODE == 1) consume_plane(plA);
+  if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
+  asm volatile("" ::"v"(F.w[0].x), "v"(F.w[1].x));
+  if (MODE == 2) asm volatile("" ::"v"(F.p[0].x), "v"(F.p[1].x));
 
-  // Two blocks per iteration so the dense-plane registers alternate without
-  // copies. Full chunks have an even block count (steps % 16 == 0).
-  for (uint32_t blk = 0; blk < C.nblk; blk += 2) {
-    decode_block<K, MODE, EB, PARTIAL>(blk, plA, plB, S, C, tbl, wring, pring, stage);
+  for (uint32_t blk = 0;;) {
+    // ---- pair start: land the previous pair's loads, issue the next pair's
+    const PlaneRegs<K> cur0 = F.pl[0], cur1 = F.pl[1];
+    land_segments<K, MODE>(S, F, wring, pring, C.lane);
+    refill<K, MODE>(S, F, C, wring, pring);
+    wave_sync();
+    if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
+    request_segments<K, MODE>(S, F, C);
+    if (MODE == 1) {
+      F.pl[0] = load_plane<K>(C.dplane, min(blk + 2, C.nblk - 1), C.lane);
+      F.pl[1] = load_plane<K>(C.dplane, min(blk + 3, C.nblk - 1), C.lane);
+    }
+    wave_sync();
+    decode_block<K, MODE, EB, PARTIAL>(blk, cur0, S, C, tbl, wring, pring, stage);
     if (PARTIAL && blk + 1 >= C.nblk) break;
-    decode_block<K, MODE, EB, PARTIAL>(blk + 1, plB, plA, S, C, tbl, wring, pring, stage);
+    // ---- second block of the pair
+    refill<K, MODE>(S, F, C, wring, pring);
+    wave_sync();
+    if (PARTIAL) flush_half<K, EB, PARTIAL>(2 * blk + 1, C, stage);
+    decode_block<K, MODE, EB, PARTIAL>(blk + 1, cur1, S, C, tbl, wring, pring, stage);
+    blk += 2;
+    if (blk >= C.nblk) break;
+    if (!PARTIAL) {
+      // The pair's loads were followed by its four output stores: vmcnt(4)
+      // lands the loads and leaves the stores in flight. Stating it gives the
+      // compiler's wait-count tracking an exact state here; the uses below
+      // keep its own waits for these registers at this point.
+      __builtin_amdgcn_s_waitcnt(kWaitVm4);
+      if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
+      asm volatile("" ::"v"(F.w[0].x), "v"(F.w[1].x));
+      if (MODE == 2) asm volatile("" ::"v"(F.p[0].x), "v"(F.p[1].x));
+    }
   }
   // a partial chunk's last staged half: the second half of its last block, or
   // the first if that block has at most half a block of steps
@@ -425,6 +495,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     wave_sync();
     flush_half<K, EB, PARTIAL>((C.nsteps - 1) / (block_steps<K>() / 2), C, stage);
   }
+  // segments requested but never landed need no wait: nothing reads them
 
   bool bad_state = false;
 #pragma unroll
