@@ -20,8 +20,9 @@
 // lanes ascending among the lanes whose state fell below L = 2^16; the words
 // are placed with a wavefront ballot + mbcnt prefix.
 // Plane bytes (sign<<7 | mantissa) complete bf16 exponent symbols:
-//   plane_mode 1 (dense): every element has one, stored per 8-step block with
-//                         lane l's 8K bytes contiguous, step-major (byte q*K+g);
+//   plane_mode 1 (dense): every element has one, stored per block of B steps
+//                         (B = 8 for K <= 2, 4 for K = 4) with lane l's B*K
+//                         bytes contiguous, step-major (byte q*K+g);
 //   plane_mode 2 (compact): only elements whose symbol has bit 31 set have one,
 //                         in decode order (ballot + mbcnt again);
 //   plane_mode 0: no plane (every symbol is an exact value).
@@ -182,7 +183,7 @@ struct Inflight {
 struct ChunkParams {
   const GLB u32x4* wsrc;        // renorm words, 16-byte units
   const GLB u32x4* psrc;        // compact plane, 16-byte units
-  const GLB uint8_t* dplane;    // dense plane: 8*K bytes per lane per block
+  const GLB uint8_t* dplane;    // dense plane: B*K bytes per lane per block of B steps
   const GLB u32x4* safe;        // the chunk's state words: an always-valid dummy address
   GLB uint8_t* out8;
   uint64_t base;                // first element of the chunk
