@@ -330,13 +330,27 @@ class RefLaunch:
         base = self.dev.data_ptr()
         self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets, self.p_tables = (base + o for o in offs)
         self.n_streams, self.n_buckets, self.n_tables = len(se), len(mb), tables.shape[0]
-        self.perm = torch.empty(max(plan.n, 1), dtype=torch.int32, device=device)
         self.n = plan.n
+        # one SE stream over the whole tensor (bf16_se_tans, bf16_se_single_kernel):
+        # the wave-serial decoder; interleaved streams (bf16_parallel_v1): one lane per stream
+        self.serial = len(plan.se_streams) == 1 and plan.se_streams[0][1:] == (0, 1, plan.n)
+        if self.serial:
+            nbytes = int(_native.lib().bs_refcodec_serial_work_bytes(plan.n))
+            self.work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        else:
+            self.perm = torch.empty(max(plan.n, 1), dtype=torch.int32, device=device)
 
     def launch(self, out_ptr: int, status_ptr: int, stream_ptr: int) -> None:
-        rc = _native.lib().bs_refcodec_decode(self.p_streams, self.n_streams, self.p_se_table, self.p_bstart,
-                                              self.p_buckets, self.n_buckets, self.p_tables, self.n_tables,
-                                              out_ptr, self.n, self.perm.data_ptr(), status_ptr, stream_ptr)
+        L = _native.lib()
+        if self.serial:
+            rc = L.bs_refcodec_decode_serial(self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets,
+                                             self.n_buckets, self.p_tables, self.n_tables, out_ptr, self.n,
+                                             self.work.data_ptr(), self.work.numel(), status_ptr, stream_ptr)
+            _native.check(rc, "bs_refcodec_decode_serial")
+            return
+        rc = L.bs_refcodec_decode(self.p_streams, self.n_streams, self.p_se_table, self.p_bstart,
+                                  self.p_buckets, self.n_buckets, self.p_tables, self.n_tables,
+                                  out_ptr, self.n, self.perm.data_ptr(), status_ptr, stream_ptr)
         _native.check(rc, "bs_refcodec_decode")
 
 

@@ -35,6 +35,7 @@ namespace {
 #define GLB __attribute__((address_space(1)))
 
 constexpr uint32_t kL = 1u << 16;
+constexpr int kWave = 64;
 constexpr int kSeLanes = 64;        // SE streams per workgroup (one wavefront)
 constexpr int kMantThreads = 64;
 
@@ -133,9 +134,287 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
   if (x != kL || pos != n_eff) flag(status, BS_DEV_ERR_STREAM);
 }
 
+// ---- wave-serial path for the single-stream formats (bf16_se_tans,
+// bf16_se_single_kernel): one SE chain over the whole tensor plus one
+// mantissa chain per exponent bucket.
+//
+// Each chain is decoded by one wavefront. The chain itself is uniform (every
+// lane computes the same state; the compiler keeps it in scalar registers),
+// the decode table sits in LDS, and the lanes cooperate on everything around
+// it: they load the word stream 1 KB at a time into an LDS byte ring one
+// segment ahead of use, and they stage 64 consecutive outputs (lane j keeps
+// step j) for one coalesced store. The SE chain writes sign<<15 | exp<<7 of
+// every element; the mantissa chains, which do not depend on it, run at the
+// same time in other workgroups and write their bucket's mantissas in bucket
+// order. Three parallel passes then give every element its position in its
+// bucket (a stable counting sort by exponent: per-tile histograms, a scan over
+// tiles, per-tile ranks by wavefront ballots) and OR in its mantissa.
+
+constexpr uint32_t kRingB = 4096;     // word-stream byte ring per chain
+constexpr uint32_t kSegB = 1024;      // bytes per cooperative load (64 lanes x 16 B)
+constexpr uint32_t kTile = 16384;     // elements per tile of the placement passes
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// This lane's 16 bytes of ring segment q of a stream whose bytes are
+// [s_off, e_off) relative to the 16-byte aligned address A. Bytes outside that
+// range are never read (they come back as zero).
+__device__ __forceinline__ u32x4 seg_block(const GLB uint8_t* A, uint64_t q, uint32_t lane, uint64_t s_off,
+                                           uint64_t e_off) {
+  const uint64_t b0 = q * kSegB + lane * 16u;
+  if (b0 >= s_off && b0 + 16u <= e_off) return *(const GLB u32x4*)(A + b0);
+  u32x4 r = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (uint32_t k = 0; k < 16; ++k) {
+    const uint64_t b = b0 + k;
+    if (b >= s_off && b < e_off) r[k >> 2] |= (uint32_t)A[b] << (8u * (k & 3u));
+  }
+  return r;
+}
+
+__device__ __forceinline__ void seg_land(LDS uint8_t* ring, uint64_t q, uint32_t lane, u32x4 v) {
+  *(LDS u32x4*)(ring + ((q * kSegB + lane * 16u) & (kRingB - 1u))) = v;
+}
+
+// Decode one chain of n symbols. SE: M = 4096, LDS table of u64
+// {f | (slot-cf) << 13, output word sign<<15 | exp<<7}, output u16. Otherwise
+// (mantissa): M = 1024, LDS table of u32 {f | (slot-cf) << 11 | symbol << 21},
+// output one byte per symbol.
+//
+// Renormalisation: the reference loops `while x < L and words remain`. From a
+// state x >= L one decode step leaves x >= 2^4 (SE) or 2^6 (mantissa), so one
+// shifted-in word restores x >= L: a valid stream never takes the loop twice,
+// and an initial state below L, which no encoder writes, is reported as a
+// corrupt stream. A corrupt stream that runs out of words keeps reading (from
+// the ring, in bounds) and fails the end-of-stream check.
+template <bool SE>
+__device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
+                                             uint32_t n, const LDS uint8_t* __restrict__ tbl,
+                                             LDS uint8_t* __restrict__ ring, GLB uint8_t* __restrict__ out,
+                                             int32_t* status) {
+  const uint32_t lane = __lane_id();
+  const uint64_t wa = (uint64_t)words;
+  const GLB uint8_t* A = (const GLB uint8_t*)(wa & ~15ull);
+  const uint32_t s_off = (uint32_t)(wa & 15u);
+  const uint64_t e_off = s_off + 2ull * n_words;
+  const uint32_t n_eff = n_words + ((tail >> 16) & 1u);
+  const uint32_t tail_word = tail & 0xFFFFu;
+  uint64_t landed = 0;        // stream bytes [.., landed) are in the ring (relative to A)
+  bool inflight = false;      // segment `landed / kSegB` is being loaded into `seg`
+  u32x4 seg = {0u, 0u, 0u, 0u};
+  uint32_t x = x0, pos = 0;
+  uint32_t keep = 0;
+  if (x0 < kL) {
+    if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
+    return;
+  }
+  for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
+    // ring upkeep: the next 64 steps read at most 64 words (128 bytes)
+    const uint64_t consumed = s_off + 2ull * pos;
+    if (inflight) {
+      seg_land(ring, landed / kSegB, lane, seg);
+      landed += kSegB;
+      inflight = false;
+    }
+    while (landed < e_off && landed < consumed + 2u * kWave + 2u) {
+      seg_land(ring, landed / kSegB, lane, seg_block(A, landed / kSegB, lane, s_off, e_off));
+      landed += kSegB;
+    }
+    if (landed < e_off && landed + kSegB <= consumed + kRingB) {
+      seg = seg_block(A, landed / kSegB, lane, s_off, e_off);
+      inflight = true;
+    }
+    wave_sync();
+    const uint32_t cnt = min((uint32_t)kWave, n - i0);
+    for (uint32_t j = 0; j < cnt; ++j) {
+      uint32_t v;
+      if (SE) {
+        const uint64_t ent = ((const LDS uint64_t*)tbl)[x & 4095u];
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)ent);
+        v = __builtin_amdgcn_readfirstlane((uint32_t)(ent >> 32));
+        x = (lo & 0x1FFFu) * (x >> 12) + (lo >> 13);
+      } else {
+        const uint32_t ent = __builtin_amdgcn_readfirstlane(((const LDS uint32_t*)tbl)[x & 1023u]);
+        x = (ent & 0x7FFu) * (x >> 10) + ((ent >> 11) & 0x3FFu);
+        v = (ent >> 21) & 0x7Fu;
+      }
+      if (x < kL) {
+        uint32_t w = tail_word;
+        if (pos < n_words) {
+          const uint32_t b = s_off + 2u * pos;
+          w = (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
+          w = __builtin_amdgcn_readfirstlane(w);
+        }
+        x = (x << 16) | w;
+        ++pos;
+      }
+      keep = lane == j ? v : keep;
+    }
+    if (lane < cnt) {
+      if (SE) ((GLB uint16_t*)out)[i0 + lane] = (uint16_t)keep;
+      else out[i0 + lane] = (uint8_t)keep;
+    }
+  }
+  if (x != kL || pos != n_eff) {
+    if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
+  }
+}
+
+// Block 0: the SE stream (element order, stride 1). Block 1 + b: mantissa
+// bucket b, written to mant[perm_begin ...] (bucket order).
+__global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __restrict__ se,
+                                                       const uint32_t* __restrict__ se_table,
+                                                       const bs_mant_bucket* __restrict__ buckets,
+                                                       const uint32_t* __restrict__ mant_tables, uint32_t n_tables,
+                                                       uint16_t* __restrict__ out, uint64_t n_out,
+                                                       uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  LDS uint8_t* ring = (LDS uint8_t*)smem;
+  LDS uint8_t* tbl = (LDS uint8_t*)(smem + kRingB);
+  const uint32_t lane = threadIdx.x;
+  if (blockIdx.x == 0) {
+    const bs_se_stream S = se[0];
+    if (S.first != 0 || S.stride != 1 || S.n != n_out) {
+      if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
+      return;
+    }
+    for (uint32_t i = lane; i < 4096; i += kWave) {
+      const uint32_t sym = se_table[2 * i + 1];
+      const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
+      ((LDS uint64_t*)tbl)[i] = (uint64_t)se_table[2 * i] | ((uint64_t)word << 32);
+    }
+    wave_sync();
+    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring, (GLB uint8_t*)out,
+                       status);
+  } else {
+    const bs_mant_bucket B = buckets[blockIdx.x - 1];
+    if (B.table >= n_tables || B.perm_begin + B.n > n_out) {
+      if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
+      return;
+    }
+    const GLB uint32_t* t = (const GLB uint32_t*)mant_tables + (uint64_t)B.table * 1024u;
+    for (uint32_t i = lane; i < 1024; i += kWave) ((LDS uint32_t*)tbl)[i] = t[i];
+    wave_sync();
+    serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring,
+                        (GLB uint8_t*)(mant + B.perm_begin), status);
+  }
+}
+
+// Exponent histogram of each tile of kTile elements.
+__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out, uint64_t n,
+                                                   uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[256];
+  const uint32_t tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
+  for (uint32_t k = tid; k < kTile; k += 256) {
+    const uint64_t i = t0 + k;
+    if (i < n) atomicAdd(&h[(out[i] >> 7) & 0xFFu], 1u);
+  }
+  __syncthreads();
+  hist[(uint64_t)blockIdx.x * 256 + tid] = h[tid];
+}
+
+// Per exponent: turn tile counts into each tile's first position in the
+// bucket (bstart[e] + counts of the earlier tiles), and check that the
+// decoded exponents fill every bucket exactly.
+__global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, uint32_t n_tiles,
+                                                   const uint32_t* __restrict__ bstart, int32_t* __restrict__ status) {
+  const uint32_t e = threadIdx.x;
+  uint32_t run = bstart[e];
+  for (uint32_t t = 0; t < n_tiles; ++t) {
+    const uint32_t c = hist[(uint64_t)t * 256 + e];
+    hist[(uint64_t)t * 256 + e] = run;
+    run += c;
+  }
+  if (run != bstart[e + 1]) flag(status, BS_DEV_ERR_COUNT);
+}
+
+// Per tile (one wavefront): the position of each element in its bucket, from
+// the tile's first positions plus its rank among the equal exponents before
+// it (64 elements at a time: lanes with the same exponent found with eight
+// ballots); then OR the element's mantissa into it.
+__global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out, uint64_t n,
+                                                      const uint32_t* __restrict__ first,
+                                                      const uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
+  __shared__ uint32_t cnt[256];
+  const uint32_t lane = threadIdx.x;
+  for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)blockIdx.x * 256 + e];
+  wave_sync();
+  const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  bool bad = false;
+  for (uint32_t k0 = 0; k0 < kTile; k0 += kWave) {
+    const uint64_t i = t0 + k0 + lane;
+    if (t0 + k0 >= n) break;
+    const bool valid = i < n;
+    const uint32_t word = valid ? out[i] : 0u;
+    const uint32_t e = (word >> 7) & 0xFFu;
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (e >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
+    }
+    const uint32_t rank = (uint32_t)__popcll(m & lt), total = (uint32_t)__popcll(m);
+    const uint32_t base = cnt[e];
+    wave_sync();
+    if (valid && rank == 0) cnt[e] = base + total;
+    if (valid) {
+      const uint32_t p = base + rank;
+      if (p < n) out[i] = (uint16_t)(word | mant[p]);
+      else bad = true;
+    }
+    wave_sync();
+  }
+  if (__ballot(bad) != 0 && lane == 0) flag(status, BS_DEV_ERR_COUNT);
+}
+
 }  // namespace
 
 extern "C" {
+
+uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out) {
+  const uint64_t tiles = (n_out + kTile - 1) / kTile;
+  return ((n_out + 255) & ~255ull) + tiles * 256 * 4;
+}
+
+int bs_refcodec_decode_serial(const bs_se_stream* d_stream, const uint32_t* d_se_table, const uint32_t* d_bstart,
+                              const bs_mant_bucket* d_buckets, uint32_t n_buckets, const uint32_t* d_mant_tables,
+                              uint32_t n_tables, uint16_t* d_out, uint64_t n_out, void* d_work, uint64_t work_bytes,
+                              int32_t* d_status, void* stream) {
+  if (!d_status || (n_out && (!d_stream || !d_se_table || !d_bstart || !d_out || !d_work)) ||
+      (n_buckets && (!d_buckets || !d_mant_tables)) || n_out > 0xFFFFFFFFull)
+    return BS_ERR_ARG;
+  if (n_out == 0) return BS_OK;
+  if (work_bytes < bs_refcodec_serial_work_bytes(n_out) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* mant = (uint8_t*)d_work;
+  uint32_t* hist = (uint32_t*)(mant + ((n_out + 255) & ~255ull));
+  const uint32_t tiles = (uint32_t)((n_out + kTile - 1) / kTile);
+  constexpr uint32_t kSerLds = kRingB + 4096 * 8;
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)serial_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSerLds);
+    attr = true;
+  }
+  hipLaunchKernelGGL(serial_kernel, dim3(1 + n_buckets), dim3(kWave), kSerLds, s, d_stream, d_se_table, d_buckets,
+                     d_mant_tables, n_tables, d_out, n_out, mant, d_status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, d_out, n_out, hist);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, s, hist, tiles, d_bstart, d_status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(place_kernel, dim3(tiles), dim3(kWave), 0, s, d_out, n_out, hist, mant, d_status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
 
 int bs_refcodec_decode(const bs_se_stream* d_streams, uint32_t n_streams, const uint32_t* d_se_table,
                        const uint32_t* d_bstart, const bs_mant_bucket* d_buckets, uint32_t n_buckets,

@@ -2,9 +2,9 @@
 (bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel).
 
 The host parses a blob into stream descriptors, bucket start tables and decode
-tables (bigsmall_amd/codecs/_refstreams.py). Here a plain-Python emulation of
-the two device kernels' semantics (refcodec_decode.hip: se_kernel, mant_kernel)
-runs on those descriptors, for every reference blob in the golden fixtures
+tables (bigsmall_amd/codecs/_refstreams.py). Here plain-Python emulations of
+the device kernels' semantics (refcodec_decode.hip: se_kernel + mant_kernel,
+and the wave-serial path for one-stream formats) run on those descriptors, for every reference blob in the golden fixtures
 (written by the reference's own encoders), and must give back the original
 words. Malformed framing must raise ValueError.
 """
@@ -63,6 +63,63 @@ def emulate(plan: rs.RefPlan, blob: bytes) -> np.ndarray:
         for r, m in enumerate(syms):
             out[perm[pb + r]] |= m
     return out
+
+
+def emulate_serial(plan: rs.RefPlan, blob: bytes, tile: int = 256) -> np.ndarray:
+    """The wave-serial path (refcodec_decode.hip: serial_kernel, hist_kernel,
+    scan_kernel, place_kernel) for a one-stream plan: the SE chain writes
+    sign<<15 | exp<<7 in element order, each mantissa chain writes its bucket
+    in bucket order, then per-tile exponent histograms, a scan over tiles per
+    exponent and per-64-element ranks place every element's mantissa."""
+    (s, first, stride, n), = plan.se_streams
+    assert (first, stride, n) == (0, 1, plan.n)
+    se_t = rs.decode_table_se(plan.se_freqs)
+    out = np.zeros(n, np.uint16)
+    syms, x, pos, n_eff = _run(blob, s, n, lambda sl: (int(se_t[sl, 0]) & 0x1FFF, int(se_t[sl, 0]) >> 13,
+                                                       int(se_t[sl, 1])), 12)
+    assert x == L and pos == n_eff
+    syms = np.asarray(syms, np.uint32)
+    out[:] = (((syms >> 8) & 1) << 15) | ((syms & 0xFF) << 7)
+    mant = np.zeros(n, np.uint8)
+    for bs_, pb, nb, t in plan.buckets:
+        tbl = rs.decode_table_mant(plan.mant_freqs[t])
+        m, x, pos, n_eff = _run(blob, bs_, nb, lambda sl: (int(tbl[sl]) & 0x7FF, (int(tbl[sl]) >> 11) & 0x3FF,
+                                                           int(tbl[sl]) >> 21), 10)
+        assert x == L and pos == n_eff
+        mant[pb:pb + nb] = m
+    e = (out >> 7) & 0xFF
+    tiles = (n + tile - 1) // tile
+    hist = np.zeros((tiles, 256), np.int64)
+    for t in range(tiles):
+        hist[t] = np.bincount(e[t * tile:(t + 1) * tile], minlength=256)
+    bstart = plan.bstart[0].astype(np.int64)
+    firsts = bstart[:256] + np.concatenate([np.zeros((1, 256), np.int64), np.cumsum(hist, 0)[:-1]])
+    assert np.array_equal(bstart[:256] + hist.sum(0), bstart[1:])
+    for t in range(tiles):
+        cnt = firsts[t].copy()
+        for k0 in range(t * tile, min(n, (t + 1) * tile), 64):
+            ch = e[k0:min(n, k0 + 64)]
+            for lane, ev in enumerate(ch):
+                rank = int(np.count_nonzero(ch[:lane] == ev))
+                out[k0 + lane] |= mant[cnt[ev] + rank]
+            for ev in np.unique(ch):
+                cnt[ev] += int(np.count_nonzero(ch == ev))
+    return out
+
+
+@pytest.mark.parametrize("codec,prefix", [("bf16_se_tans", "tans_"), ("bf16_se_single_kernel", "sk_")])
+def test_serial_path_decodes_reference_blobs(golden, codec, prefix):
+    seen = 0
+    for k in sorted(golden):
+        if not k.startswith(prefix):
+            continue
+        words = golden[f"in_{k[len(prefix):]}"].astype(np.uint16)
+        if words.size > 40000 or words.size == 0:
+            continue
+        blob = golden[k].tobytes()
+        assert np.array_equal(emulate_serial(rs.PARSERS[codec](blob, words.size), blob), words), k
+        seen += 1
+    assert seen >= 5
 
 
 @pytest.mark.parametrize("codec,prefix", [("bf16_parallel_v1", "par1_"), ("bf16_se_tans", "tans_"),
