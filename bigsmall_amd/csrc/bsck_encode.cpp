@@ -55,8 +55,13 @@ void put16(uint8_t* p, uint32_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8)
 void put32(uint8_t* p, uint32_t v) { for (int i = 0; i < 4; ++i) p[i] = (uint8_t)(v >> (8 * i)); }
 void put64(uint8_t* p, uint64_t v) { for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i)); }
 
-// counts -> frequencies summing to kM, every present symbol >= 1, chosen by a
-// greedy minimum-codelength correction after proportional rounding.
+// counts -> frequencies summing to kM, every present symbol >= 1: proportional
+// rounding (half up), then +-1 corrections one at a time, each to the symbol
+// where it costs the fewest bits. The cost of f -> f+1 is c*log2(1 + 1/f) saved,
+// of f -> f-1 c*log2(1 + 1/(f-1)) lost; both are ranked by the integer
+// proxies c/(2f+1) and c/(2f-1) (ln(1 + 1/f) ~ 1/(f + 1/2)), compared by
+// cross-multiplication, ties to the lower index. Integer-only, so the GPU
+// encoder (bsck_encode_gpu.hip) reproduces it exactly.
 void quantise(const std::vector<uint64_t>& counts, uint32_t* freq) {
   const size_t k = counts.size();
   uint64_t total = 0;
@@ -64,26 +69,22 @@ void quantise(const std::vector<uint64_t>& counts, uint32_t* freq) {
   int64_t sum = 0;
   std::vector<int64_t> f(k);
   for (size_t i = 0; i < k; ++i) {
-    double ideal = (double)counts[i] * kM / (double)total;
-    int64_t v = (int64_t)std::llround(ideal);
+    int64_t v = (int64_t)((2 * counts[i] * kM + total) / (2 * total));
     if (v < 1) v = 1;
     f[i] = v;
     sum += v;
   }
   while (sum != (int64_t)kM) {
-    // pick the symbol whose +/-1 costs the fewest bits: d(bits) = c*log2(f/f')
+    const bool up = sum < (int64_t)kM;
     size_t best = k;
-    double best_cost = 1e300;
     for (size_t i = 0; i < k; ++i) {
-      double cost;
-      if (sum < (int64_t)kM) cost = (double)counts[i] * std::log2((double)f[i] / (double)(f[i] + 1));
-      else {
-        if (f[i] <= 1) continue;
-        cost = (double)counts[i] * std::log2((double)f[i] / (double)(f[i] - 1));
-      }
-      if (cost < best_cost) { best_cost = cost; best = i; }
+      if (!up && f[i] <= 1) continue;
+      if (best == k) { best = i; continue; }
+      const uint64_t di = up ? 2 * f[i] + 1 : 2 * f[i] - 1, db = up ? 2 * f[best] + 1 : 2 * f[best] - 1;
+      const unsigned __int128 lhs = (unsigned __int128)counts[i] * db, rhs = (unsigned __int128)counts[best] * di;
+      if (up ? lhs > rhs : lhs < rhs) best = i;     // up: largest c/(2f+1); down: smallest c/(2f-1)
     }
-    if (sum < (int64_t)kM) { f[best]++; sum++; }
+    if (up) { f[best]++; sum++; }
     else { f[best]--; sum--; }
   }
   for (size_t i = 0; i < k; ++i) freq[i] = (uint32_t)f[i];
