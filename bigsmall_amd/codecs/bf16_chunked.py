@@ -20,7 +20,8 @@ import os
 import numpy as np
 
 from .. import _native
-from ..device import ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, require_gpu, upload_bytes
+from ..device import (ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, require_gpu, stream_ptr,
+                      upload_bytes)
 
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
@@ -56,6 +57,77 @@ def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_A
     _native.check(L.bs_chunk_encode(a.ctypes.data, n, eb, lanes, steps, mode, out.ctypes.data, bound.value,
                                     ctypes.byref(olen), threads or _threads()), "bs_chunk_encode")
     return out[: olen.value].tobytes()
+
+
+# bs_encode_task (include/bigsmall_hip.h): 40 bytes
+ENCODE_TASK_DTYPE = np.dtype([("src", "<u8"), ("n", "<u8"), ("dst", "<u8"), ("cap", "<u8"),
+                              ("chunk_begin", "<u4"), ("n_chunks", "<u4")])
+assert ENCODE_TASK_DTYPE.itemsize == 40
+GPU_ENCODE_LANES = 128
+
+
+def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: bool = True):
+    """Encode device-resident bf16 tensors on the GPU (dense plane mode, 128
+    states per chunk); the blobs equal encode_array(words, steps, MODE_DENSE).
+
+    Returns (arena, [(offset, length), ...]): every blob lives in one device
+    uint8 tensor at a 256-byte aligned offset. With compact=False the arena
+    keeps each blob's worst-case slot (no copy after encoding)."""
+    import torch
+    if not tensors:
+        return None, []
+    dev = require_gpu(tensors[0].device)
+    L = _native.lib()
+    per = GPU_ENCODE_LANES * steps
+    srcs, slots, cap_total = [], [], 0
+    for t in tensors:
+        if t.dtype != torch.bfloat16 or t.device != dev:
+            raise ValueError("encode_device expects bf16 tensors on one GPU")
+        t = t.contiguous()
+        if t.data_ptr() % 4:
+            t = t.clone()
+        n = t.numel()
+        bound = ctypes.c_uint64()
+        _native.check(L.bs_chunk_encode_bound(max(n, 1), 2, GPU_ENCODE_LANES, steps, ctypes.byref(bound)),
+                      "bs_chunk_encode_bound")
+        srcs.append(t)
+        slots.append((cap_total, int(bound.value)))
+        cap_total += (int(bound.value) + 255) & ~255
+    arena = torch.empty(max(cap_total, 256), dtype=torch.uint8, device=dev)
+    live = [i for i, t in enumerate(srcs) if t.numel() > 0]
+    tasks = np.zeros(len(live), ENCODE_TASK_DTYPE)
+    chunk = 0
+    for k, i in enumerate(live):
+        n = srcs[i].numel()
+        nch = (n + per - 1) // per
+        tasks[k] = (srcs[i].data_ptr(), n, arena.data_ptr() + slots[i][0], slots[i][1], chunk, nch)
+        chunk += nch
+    lens = [0] * len(srcs)
+    if live:
+        d_tasks = upload_bytes(tasks.view(np.uint8), dev)
+        wb = int(L.bs_chunk_encode_gpu_work_bytes(len(live), chunk, steps))
+        work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
+        out_len = torch.zeros(len(live), dtype=torch.int64, device=dev)
+        st = StatusWord(dev)
+        _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), len(live), chunk, steps, work.data_ptr(), wb,
+                                            out_len.data_ptr(), st.ptr, stream_ptr(stream, dev)),
+                      "bs_chunk_encode_gpu")
+        torch.cuda.synchronize(dev)
+        st.check("bf16_chunked GPU encode")
+        host_lens = out_len.cpu().tolist()
+        for k, i in enumerate(live):
+            lens[i] = int(host_lens[k])
+    if not compact:
+        return arena, [(slots[i][0], lens[i]) for i in range(len(srcs))]
+    offs, pos = [], 0
+    for ln in lens:
+        offs.append(pos)
+        pos += (ln + 255) & ~255
+    tight = torch.empty(max(pos, 256), dtype=torch.uint8, device=dev)
+    for i, ln in enumerate(lens):
+        if ln:
+            tight[offs[i]:offs[i] + ln].copy_(arena[slots[i][0]:slots[i][0] + ln])
+    return tight, list(zip(offs, lens))
 
 
 def encode(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:

@@ -33,14 +33,22 @@ def encode_words(words: np.ndarray, steps: int = KV_STEPS) -> bytes:
 
 
 def compress_kv_entry(keys, values) -> bytes:
-    """Compress one K/V pair into a version-3 entry (host encode, like the reference's D2H + encode)."""
+    """Compress one K/V pair into a version-3 entry. Device tensors are encoded
+    on the GPU and only the compressed bytes come back to the host; host
+    tensors use the host encoder (the reference copies to the host and encodes
+    there, kv_cache.py:28-38)."""
     import torch
     if keys.dtype != torch.bfloat16 or values.dtype != torch.bfloat16:
         raise ValueError("compress_kv_entry requires BF16 keys and values")
+    gpu_blobs = None
+    if keys.is_cuda and values.is_cuda and keys.numel() and values.numel():
+        arena, spans = bf16_chunked.encode_device([keys, values], steps=KV_STEPS, compact=False)
+        host = arena.cpu().numpy()
+        gpu_blobs = [host[o:o + n].tobytes() for o, n in spans]
     out = bytearray(struct.pack("<B", VERSION_GPU))
-    for t in (keys, values):
-        w, shape = _tensor_words(t)
-        blob = encode_words(w)
+    for i, t in enumerate((keys, values)):
+        shape = list(t.shape)
+        blob = gpu_blobs[i] if gpu_blobs is not None else encode_words(_tensor_words(t)[0])
         out += struct.pack("<B", len(shape))
         for s in shape:
             out += struct.pack("<i", int(s))

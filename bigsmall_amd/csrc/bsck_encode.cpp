@@ -81,7 +81,8 @@ void quantise(const std::vector<uint64_t>& counts, uint32_t* freq) {
       if (!up && f[i] <= 1) continue;
       if (best == k) { best = i; continue; }
       const uint64_t di = up ? 2 * f[i] + 1 : 2 * f[i] - 1, db = up ? 2 * f[best] + 1 : 2 * f[best] - 1;
-      const unsigned __int128 lhs = (unsigned __int128)counts[i] * db, rhs = (unsigned __int128)counts[best] * di;
+      // counts < 2^50 and d <= 8193: the products fit in 64 bits
+      const uint64_t lhs = counts[i] * db, rhs = counts[best] * di;
       if (up ? lhs > rhs : lhs < rhs) best = i;     // up: largest c/(2f+1); down: smallest c/(2f-1)
     }
     if (up) { f[best]++; sum++; }

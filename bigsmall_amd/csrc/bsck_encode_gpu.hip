@@ -1,0 +1,434 @@
+// GPU encoder for BSCK (bf16_chunked_v1), dense plane mode, 128 states per
+// chunk: the device-side counterpart of bsck_encode.cpp for tensors that are
+// already in HBM (KV-cache blocks), so compressing them needs no copy to the
+// host. Its blobs are byte-identical to bsck_encode.cpp with plane mode 1
+// forced (same symbol order, integer quantiser, state walk and layout).
+//
+// A batch of tensors ("tasks") is encoded by six launches on one stream:
+//   clear     zero the per-task exponent histograms;
+//   hist      per chunk: exponent histogram (LDS), added into its task's;
+//   plan      per task (one wavefront): symbols = exponents present, in
+//             ascending order; frequencies by the quantiser of bsck_encode.cpp
+//             (rounding, then greedy +-1 corrections, the argmax taken across
+//             the wavefront); writes the blob header and symbol table;
+//   chunk     per chunk (one wavefront, lane l owns states l and 64 + l):
+//             walks the steps backwards, renormalising before each encode as
+//             the decoder renormalises after each decode; renorm words of a
+//             (step, state group) are placed by ballot rank so the decoder
+//             reads them lane-ascending; words go to the chunk's scratch from
+//             its end backwards, final states to its head;
+//   layout    per task: chunk offsets (prefix sum of chunk sizes), chunk table,
+//             blob length (or a capacity error);
+//   assemble  per chunk: states, renorm words and the dense sign|mantissa
+//             plane at the chunk's offset in the blob.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bigsmall_hip.h"
+
+namespace {
+
+#define LDS __attribute__((address_space(3)))
+#define GLB __attribute__((address_space(1)))
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kWave = 64;
+constexpr uint32_t kLanes = 128;       // states per chunk (two per wavefront lane)
+constexpr uint32_t kBlock = 8;         // steps per dense-plane block
+constexpr uint32_t kM = 4096;
+constexpr uint32_t kL = 1u << 16;
+constexpr uint8_t kVersion = 2;
+
+// Per-task plan in the work area.
+struct Plan {
+  uint32_t hist[256];         // elements per exponent
+  uint32_t sym_of_exp[256];   // exponent -> symbol index
+  uint32_t freq[256];         // per symbol
+  uint32_t cum[256];          // per symbol
+  uint32_t nsym, ok, pad0, pad1;
+};
+constexpr uint64_t kPlanBytes = (sizeof(Plan) + 255) & ~uint64_t(255);
+// Per-chunk record in the work area.
+struct ChunkRec {
+  uint64_t off;               // byte offset of the chunk in the blob
+  uint32_t nw, pad;
+};
+
+__host__ __device__ inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+__host__ __device__ inline uint64_t scratch_bytes(uint32_t steps) { return 4ull * kLanes + 2ull * kLanes * steps; }
+
+__device__ __forceinline__ void flag(int32_t* status, int32_t bits) { atomicOr(status, bits); }
+
+// task serving global chunk c (tasks sorted by chunk_begin)
+__device__ __forceinline__ uint32_t task_of(const bs_encode_task* tasks, uint32_t n_tasks, uint32_t c) {
+  uint32_t lo = 0, hi = n_tasks;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (tasks[mid].chunk_begin <= c) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Checks every kernel repeats: the task's fields agree with each other.
+__device__ __forceinline__ bool task_ok(const bs_encode_task& T, uint64_t per) {
+  return T.n > 0 && T.n <= 0xFFFFFFFFull && ((uintptr_t)T.src & 3u) == 0 && ((uintptr_t)T.dst & 15u) == 0 &&
+         (uint64_t)T.n_chunks == (T.n + per - 1) / per;
+}
+
+__global__ __launch_bounds__(256) void enc_clear_kernel(uint8_t* __restrict__ plans) {
+  Plan* P = (Plan*)(plans + blockIdx.x * kPlanBytes);
+  P->hist[threadIdx.x] = 0;
+  if (threadIdx.x == 0) { P->nsym = 0; P->ok = 0; }
+}
+
+__global__ __launch_bounds__(256) void enc_hist_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
+                                                       uint32_t steps, uint8_t* __restrict__ plans) {
+  __shared__ uint32_t h[256];
+  const uint32_t tid = threadIdx.x, c = blockIdx.x;
+  const uint32_t ti = task_of(tasks, n_tasks, c);
+  const bs_encode_task T = tasks[ti];
+  const uint64_t per = (uint64_t)kLanes * steps;
+  if (!task_ok(T, per) || c < T.chunk_begin || c - T.chunk_begin >= T.n_chunks) return;
+  h[tid] = 0;
+  __syncthreads();
+  const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;
+  const uint32_t nc = (uint32_t)min(per, T.n - base);
+  const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
+  for (uint32_t j = tid; j < nc; j += 256) atomicAdd(&h[(src[j] >> 7) & 0xFFu], 1u);
+  __syncthreads();
+  if (h[tid]) atomicAdd(&((Plan*)(plans + ti * kPlanBytes))->hist[tid], h[tid]);
+}
+
+// is candidate (c1, d1, i1) better than (c0, d0, i0)? up: larger c/d; down: smaller c/d; ties: lower index.
+// c < 2^32 (elements of one tensor) and d <= 8193, so the products fit in 64 bits.
+__device__ __forceinline__ bool better(bool up, uint64_t c1, uint64_t d1, uint32_t i1, uint64_t c0, uint64_t d0,
+                                       uint32_t i0) {
+  const uint64_t a = c1 * d0, b = c0 * d1;
+  if (a != b) return up ? a > b : a < b;
+  return i1 < i0;
+}
+
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, uint32_t src_lane) {
+  const uint32_t lo = __shfl((uint32_t)v, src_lane), hi = __shfl((uint32_t)(v >> 32), src_lane);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// One wavefront per task. Lane l holds exponents 4l .. 4l+3, so symbol indices
+// (exponents present, ascending) increase with lane and slot.
+__global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* __restrict__ tasks, uint32_t steps,
+                                                         uint8_t* __restrict__ plans, int32_t* __restrict__ status) {
+  const uint32_t lane = threadIdx.x, ti = blockIdx.x;
+  const bs_encode_task T = tasks[ti];
+  const uint64_t per = (uint64_t)kLanes * steps;
+  Plan* P = (Plan*)(plans + ti * kPlanBytes);
+  if (!task_ok(T, per)) {
+    if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
+    return;
+  }
+  uint64_t c[4];
+  uint32_t present = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    c[r] = P->hist[lane * 4 + r];
+    present += c[r] != 0;
+  }
+  // exclusive scan of `present` across lanes -> first symbol index of this lane
+  uint32_t incl = present;
+  for (uint32_t d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  const uint32_t nsym = __shfl(incl, kWave - 1);
+  uint32_t sidx[4];
+  uint32_t s = incl - present;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    sidx[r] = s;
+    s += c[r] != 0;
+  }
+  uint64_t total = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) total += c[r];
+  for (uint32_t d = 1; d < kWave; d <<= 1) total += shfl64(total, lane ^ d);
+  // proportional rounding, half up, at least 1
+  int64_t f[4];
+  int64_t sum = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    f[r] = 0;
+    if (c[r]) {
+      int64_t v = (int64_t)((2 * c[r] * kM + total) / (2 * total));
+      f[r] = v < 1 ? 1 : v;
+    }
+    sum += f[r];
+  }
+  for (uint32_t d = 1; d < kWave; d <<= 1) sum += (int64_t)shfl64((uint64_t)sum, lane ^ d);
+  // greedy corrections, one symbol per iteration (the same sequence as bsck_encode.cpp)
+  while (sum != (int64_t)kM) {
+    const bool up = sum < (int64_t)kM;
+    uint64_t bc = 0, bd = 1;
+    uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (!c[r] || (!up && f[r] <= 1)) continue;
+      const uint64_t d = up ? 2 * f[r] + 1 : 2 * f[r] - 1;
+      if (bi == 0xFFFFFFFFu || better(up, c[r], d, sidx[r], bc, bd, bi)) { bc = c[r]; bd = d; bi = sidx[r]; }
+    }
+    for (uint32_t d = 1; d < kWave; d <<= 1) {
+      const uint64_t oc = shfl64(bc, lane ^ d), od = shfl64(bd, lane ^ d);
+      const uint32_t oi = __shfl(bi, lane ^ d);
+      if (oi != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || better(up, oc, od, oi, bc, bd, bi))) { bc = oc; bd = od; bi = oi; }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (c[r] && sidx[r] == bi) f[r] += up ? 1 : -1;
+    sum += up ? 1 : -1;
+  }
+  // cumulative frequencies in symbol order
+  int64_t fl = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) fl += f[r];
+  int64_t finc = fl;
+  for (uint32_t d = 1; d < kWave; d <<= 1) {
+    const int64_t o = (int64_t)shfl64((uint64_t)finc, lane - d < kWave ? lane - d : lane);
+    if (lane >= d) finc += o;
+  }
+  int64_t cum = finc - fl;
+  const uint64_t nch = T.n_chunks;
+  const uint64_t ctab = pad16(32 + 4ull * nsym);
+  const bool fits = ctab + 16 * nch + 16 <= T.cap && nsym >= 1;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t e = lane * 4 + r;
+    P->sym_of_exp[e] = c[r] ? sidx[r] : 0u;
+    if (c[r]) {
+      P->freq[sidx[r]] = (uint32_t)f[r];
+      P->cum[sidx[r]] = (uint32_t)cum;
+      if (fits)
+        *(GLB uint32_t*)(T.dst + 32 + 4ull * sidx[r]) = (e << 7) | ((uint32_t)f[r] << 16) | 0x80000000u;
+      cum += f[r];
+    }
+  }
+  if (!fits) {
+    if (lane == 0) flag(status, BS_DEV_ERR_BOUNDS);
+    return;
+  }
+  // header, and zeros from the symbol table's end to the chunk table plus 16
+  // (the chunk table itself is written by the layout pass)
+  for (uint64_t b = 32 + 4ull * nsym + lane; b < ctab; b += kWave) T.dst[b] = 0;
+  for (uint64_t b = ctab + 16 * nch + lane; b < ctab + 16 * nch + 16; b += kWave) T.dst[b] = 0;
+  if (lane == 0) {
+    P->nsym = nsym;
+    uint8_t* d = T.dst;
+    d[0] = 'B'; d[1] = 'S'; d[2] = 'C'; d[3] = 'K';
+    d[4] = kVersion; d[5] = 2; d[6] = 1; d[7] = 12;
+    *(GLB uint32_t*)(d + 8) = (uint32_t)T.n;
+    *(GLB uint32_t*)(d + 12) = (uint32_t)(T.n >> 32);
+    *(GLB uint32_t*)(d + 16) = steps;
+    *(GLB uint32_t*)(d + 20) = kLanes | (nsym << 16);
+    *(GLB uint32_t*)(d + 24) = (uint32_t)nch;
+    *(GLB uint32_t*)(d + 28) = 0;
+    P->ok = 1;
+  }
+}
+
+// One wavefront per chunk: lane l owns states l (group 0) and 64 + l (group 1);
+// state (g, l) codes element t*128 + 2l + g at step t.
+__global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
+                                                          uint32_t steps, const uint8_t* __restrict__ plans,
+                                                          ChunkRec* __restrict__ recs, uint8_t* __restrict__ scratch) {
+  __shared__ uint32_t s_sym[256], s_f[256], s_c[256];
+  const uint32_t lane = threadIdx.x, cg = blockIdx.x;
+  const uint32_t ti = task_of(tasks, n_tasks, cg);
+  const bs_encode_task T = tasks[ti];
+  const uint64_t per = (uint64_t)kLanes * steps;
+  const Plan* P = (const Plan*)(plans + ti * kPlanBytes);
+  if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
+  for (uint32_t i = lane; i < 256; i += kWave) { s_sym[i] = P->sym_of_exp[i]; s_f[i] = P->freq[i]; s_c[i] = P->cum[i]; }
+  __syncthreads();
+  const uint64_t base = (uint64_t)(cg - T.chunk_begin) * per;
+  const uint32_t nc = (uint32_t)min(per, T.n - base);
+  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+  const GLB uint32_t* src2 = (const GLB uint32_t*)((const GLB uint16_t*)T.src + base);   // two words per lane-step
+  const GLB uint16_t* src1 = (const GLB uint16_t*)T.src + base;
+  uint8_t* chunk = scratch + (uint64_t)cg * scratch_bytes(steps);
+  GLB uint16_t* words = (GLB uint16_t*)(chunk + 4u * kLanes);   // capacity per; filled from the end
+  uint32_t x[2] = {kL, kL};
+  uint32_t wpos = (uint32_t)per;
+  const uint64_t above = ~((2ull << lane) - 1ull);               // lanes with a higher index
+  for (uint32_t t = nsteps; t-- > 0;) {
+    const uint32_t j0 = t * kLanes + 2 * lane;
+    uint32_t wv[2];
+    if (j0 + 1 < nc) {
+      const uint32_t p = src2[j0 / 2];
+      wv[0] = p & 0xFFFFu;
+      wv[1] = p >> 16;
+    } else {
+      wv[0] = j0 < nc ? src1[j0] : 0u;
+      wv[1] = 0u;
+    }
+#pragma unroll
+    for (int g = 1; g >= 0; --g) {
+      const bool active = j0 + g < nc;
+      const uint32_t sym = s_sym[(wv[g] >> 7) & 0xFFu];
+      const uint32_t f = s_f[sym], cm = s_c[sym];
+      uint32_t xv = x[g];
+      const bool emit = active && (uint64_t)xv >= ((uint64_t)f << 20);
+      const uint64_t m = __ballot(emit);
+      if (emit) {
+        words[wpos - 1 - (uint32_t)__popcll(m & above)] = (uint16_t)(xv & 0xFFFFu);
+        xv >>= 16;
+      }
+      wpos -= (uint32_t)__popcll(m);
+      if (active) {
+        const uint32_t q = xv / f;
+        xv = (q << 12) + (xv - q * f) + cm;
+      }
+      x[g] = xv;
+    }
+  }
+  GLB uint32_t* st = (GLB uint32_t*)chunk;
+  st[lane] = x[0];
+  st[kWave + lane] = x[1];
+  if (lane == 0) recs[cg].nw = (uint32_t)per - wpos;
+}
+
+__device__ __forceinline__ uint64_t chunk_bytes(uint32_t nc, uint32_t nw) {
+  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+  const uint64_t np = (uint64_t)((nsteps + kBlock - 1) / kBlock) * kBlock * kLanes;
+  return 4ull * kLanes + pad16(2ull * nw) + np;
+}
+
+// One wavefront per task: chunk offsets, chunk table, blob length.
+__global__ __launch_bounds__(kWave) void enc_layout_kernel(const bs_encode_task* __restrict__ tasks, uint32_t steps,
+                                                           uint8_t* __restrict__ plans, ChunkRec* __restrict__ recs,
+                                                           uint64_t* __restrict__ out_len,
+                                                           int32_t* __restrict__ status) {
+  const uint32_t lane = threadIdx.x, ti = blockIdx.x;
+  const bs_encode_task T = tasks[ti];
+  const uint64_t per = (uint64_t)kLanes * steps;
+  Plan* P = (Plan*)(plans + ti * kPlanBytes);
+  if (lane == 0) out_len[ti] = 0;
+  if (!task_ok(T, per) || !P->ok) return;
+  const uint64_t ctab = pad16(32 + 4ull * P->nsym);
+  uint64_t run = pad16(ctab + 16ull * T.n_chunks);
+  for (uint32_t b0 = 0; b0 < T.n_chunks; b0 += kWave) {
+    const uint32_t k = b0 + lane;
+    const bool live = k < T.n_chunks;
+    uint32_t nw = 0, nc = 0;
+    uint64_t sz = 0;
+    if (live) {
+      nw = recs[T.chunk_begin + k].nw;
+      nc = (uint32_t)min(per, T.n - (uint64_t)k * per);
+      sz = chunk_bytes(nc, nw);
+    }
+    uint64_t inc = sz;
+    for (uint32_t d = 1; d < kWave; d <<= 1) {
+      const uint64_t o = shfl64(inc, lane >= d ? lane - d : lane);
+      if (lane >= d) inc += o;
+    }
+    if (live) {
+      const uint64_t off = run + inc - sz;
+      recs[T.chunk_begin + k].off = off;
+      const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+      const uint32_t np = ((nsteps + kBlock - 1) / kBlock) * kBlock * kLanes;
+      GLB uint32_t* e = (GLB uint32_t*)(T.dst + ctab + 16ull * k);
+      e[0] = (uint32_t)off;
+      e[1] = (uint32_t)(off >> 32);
+      e[2] = nw;
+      e[3] = np;
+    }
+    run += shfl64(inc, kWave - 1);
+  }
+  if (lane == 0) {
+    if (run > T.cap) {
+      flag(status, BS_DEV_ERR_BOUNDS);
+      P->ok = 0;
+    } else {
+      out_len[ti] = run;
+    }
+  }
+}
+
+// One wavefront per chunk: states, words (zero-padded to 16), dense plane.
+__global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
+                                                             uint32_t steps, const uint8_t* __restrict__ plans,
+                                                             const ChunkRec* __restrict__ recs,
+                                                             const uint8_t* __restrict__ scratch) {
+  const uint32_t lane = threadIdx.x, cg = blockIdx.x;
+  const uint32_t ti = task_of(tasks, n_tasks, cg);
+  const bs_encode_task T = tasks[ti];
+  const uint64_t per = (uint64_t)kLanes * steps;
+  const Plan* P = (const Plan*)(plans + ti * kPlanBytes);
+  if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
+  const ChunkRec R = recs[cg];
+  const uint64_t base = (uint64_t)(cg - T.chunk_begin) * per;
+  const uint32_t nc = (uint32_t)min(per, T.n - base);
+  const uint8_t* chunk = scratch + (uint64_t)cg * scratch_bytes(steps);
+  GLB uint8_t* out = (GLB uint8_t*)(T.dst + R.off);
+  // states: 512 bytes
+  if (lane < 32) *(GLB u32x4*)(out + 16u * lane) = *(const GLB u32x4*)(chunk + 16u * lane);
+  // words [per - nw, per) of the scratch, then zeros up to a multiple of 8 words
+  const GLB uint16_t* wsrc = (const GLB uint16_t*)(chunk + 4u * kLanes) + (per - R.nw);
+  GLB uint16_t* wdst = (GLB uint16_t*)(out + 4u * kLanes);
+  const uint32_t nw_pad = (uint32_t)(pad16(2ull * R.nw) / 2);
+  for (uint32_t i = lane; i < nw_pad; i += kWave) wdst[i] = i < R.nw ? wsrc[i] : (uint16_t)0;
+  // dense plane: per 8-step block, lane l's 16 bytes hold (q, g) at q*2 + g for
+  // element (blk*8 + q)*128 + 2l + g
+  GLB uint8_t* plane = out + 4u * kLanes + 2ull * nw_pad;
+  const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+  const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
+  const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
+  for (uint32_t blk = 0; blk < nblk; ++blk) {
+    uint32_t b[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (uint32_t q = 0; q < kBlock; ++q) {
+#pragma unroll
+      for (uint32_t g = 0; g < 2; ++g) {
+        const uint32_t j = (blk * kBlock + q) * kLanes + 2 * lane + g;
+        const uint32_t w = j < nc ? src[j] : 0u;
+        const uint32_t byte = ((w >> 8) & 0x80u) | (w & 0x7Fu);
+        const uint32_t k = q * 2 + g;
+        b[k >> 2] |= byte << (8 * (k & 3));
+      }
+    }
+    *(GLB u32x4*)(plane + (uint64_t)blk * kBlock * kLanes + 16u * lane) = u32x4{b[0], b[1], b[2], b[3]};
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t bs_chunk_encode_gpu_work_bytes(uint32_t n_tasks, uint64_t total_chunks, uint32_t steps) {
+  return (uint64_t)n_tasks * kPlanBytes + ((total_chunks * sizeof(ChunkRec) + 255) & ~255ull) +
+         total_chunks * scratch_bytes(steps);
+}
+
+int bs_chunk_encode_gpu(const bs_encode_task* d_tasks, uint32_t n_tasks, uint32_t total_chunks, uint32_t steps,
+                        void* d_work, uint64_t work_bytes, uint64_t* d_out_len, int32_t* d_status, void* stream) {
+  if (!d_status || (n_tasks && (!d_tasks || !d_work || !d_out_len)) || steps == 0 || steps % 16 ||
+      ((uintptr_t)d_work & 255u))
+    return BS_ERR_ARG;
+  if (n_tasks == 0) return BS_OK;
+  if (work_bytes < bs_chunk_encode_gpu_work_bytes(n_tasks, total_chunks, steps)) return BS_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* plans = (uint8_t*)d_work;
+  ChunkRec* recs = (ChunkRec*)(plans + (uint64_t)n_tasks * kPlanBytes);
+  uint8_t* scratch = (uint8_t*)recs + ((total_chunks * sizeof(ChunkRec) + 255) & ~255ull);
+  hipLaunchKernelGGL(enc_clear_kernel, dim3(n_tasks), dim3(256), 0, s, plans);
+  if (total_chunks)
+    hipLaunchKernelGGL(enc_hist_kernel, dim3(total_chunks), dim3(256), 0, s, d_tasks, n_tasks, steps, plans);
+  hipLaunchKernelGGL(enc_plan_kernel, dim3(n_tasks), dim3(kWave), 0, s, d_tasks, steps, plans, d_status);
+  if (total_chunks)
+    hipLaunchKernelGGL(enc_chunk_kernel, dim3(total_chunks), dim3(kWave), 0, s, d_tasks, n_tasks, steps, plans, recs,
+                       scratch);
+  hipLaunchKernelGGL(enc_layout_kernel, dim3(n_tasks), dim3(kWave), 0, s, d_tasks, steps, plans, recs, d_out_len,
+                     d_status);
+  if (total_chunks)
+    hipLaunchKernelGGL(enc_assemble_kernel, dim3(total_chunks), dim3(kWave), 0, s, d_tasks, n_tasks, steps, plans,
+                       recs, scratch);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
+
+}  // extern "C"

@@ -9,8 +9,9 @@ Block API (the reference keys one blob per layer and has no blocks; this adds
 them for on-the-fly attention over a long cache):
     set_blocks(layer_idx, keys, values, block_tokens=256, token_dim=-2)
         splits K and V along the token dimension into blocks, encodes every
-        block (host encoder) and keeps the compressed blocks resident in HBM,
-        one arena per layer;
+        block (on the GPU when K and V are device tensors, else with the host
+        encoder) and keeps the compressed blocks resident in HBM, one arena
+        per layer;
     get_blocks(layer_idx, block_ids) -> (K, V) with shape [len(block_ids), *block_shape]
     get_blocks_multi([(layer_idx, block_ids), ...]) -> [(K, V), ...]
         decode every requested block of every request in ONE batched kernel
@@ -101,6 +102,24 @@ class CompressedKVCache:
         if T % block_tokens:
             raise ValueError(f"set_blocks: {T} tokens is not a multiple of block_tokens={block_tokens}")
         nb = T // block_tokens
+        block_shape = list(keys.shape)
+        block_shape[td] = block_tokens
+        block_elems = int(np.prod(block_shape))
+        if keys.is_cuda and values.is_cuda:
+            # encode on the GPU: the blocks never leave HBM
+            parts = []
+            for t in (keys, values):
+                shape = list(t.shape)
+                blocked = t.detach().reshape(shape[:td] + [nb, block_tokens] + shape[td + 1:])
+                blocked = blocked.movedim(td, 0).contiguous()
+                parts += [blocked[i] for i in range(nb)]
+            arena, spans = bf16_chunked.encode_device(parts, steps=_kv_codec.KV_STEPS)
+            per = bf16_chunked.GPU_ENCODE_LANES * _kv_codec.KV_STEPS
+            nch = (block_elems + per - 1) // per
+            ent = [(off, ln, nch, bf16_chunked.MODE_DENSE) for off, ln in spans]
+            self._blocks[layer_idx] = _LayerBlocks(block_shape, block_elems, arena, ent[:nb], ent[nb:])
+            self._block_raw += 2 * keys.numel() * 2
+            return nb
         blobs = {"k": [], "v": []}
         for which, t in (("k", keys), ("v", values)):
             # [..., T, ...] -> [nb, ..., block_tokens, ...] contiguous blocks
@@ -109,9 +128,6 @@ class CompressedKVCache:
             blocked = blocked.movedim(td, 0).contiguous()
             words = blocked.view(torch.int16).numpy().view(np.uint16).reshape(nb, -1)
             blobs[which] = [_kv_codec.encode_words(words[i]) for i in range(nb)]
-        block_shape = list(keys.shape)
-        block_shape[td] = block_tokens
-        block_elems = int(np.prod(block_shape))
         sizes = [(len(b) + 255) & ~255 for b in blobs["k"] + blobs["v"]]
         arena_host = np.zeros(sum(sizes) + 256, np.uint8)
         entries = {"k": [], "v": []}

@@ -16,6 +16,8 @@
  *                  plugin API `codec_registry.register_codec(name, enc, dec)`
  *                  (bigsmall/codec_registry.py:45-47) and dispatched from the
  *                  decoder's `_decode_blob` chain (bigsmall/decoder.py:49-97).
+ *   bs_chunk_encode_gpu — the host encode of the KV-cache entry codec
+ *                  (bigsmall/codecs/kv_cache.py:41-83) for device-resident tensors.
  *   bs_refcodec_decode — `kernels.decode_bf16_parallel(blob, extras, n_weights)`
  *                  (bigsmall/kernels/__init__.py:89-111) and the CPU decoders it
  *                  must match: `bf16_parallel.decode` (bigsmall/codecs/bf16_parallel.py:262-352),
@@ -102,6 +104,33 @@ int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32
 int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t *bound);
 int bs_chunk_encode(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t *h_dst, uint64_t cap, uint64_t *out_len, int n_threads);
+
+/* GPU encoder for BSCK, for tensors already in HBM (bf16, dense plane mode,
+ * 128 states per chunk). A batch of tasks sorted by chunk_begin; task i owns
+ * global chunks [chunk_begin, chunk_begin + n_chunks), chunks numbered
+ * consecutively from 0 over the batch (total_chunks in all). Blobs are
+ * byte-identical to bs_chunk_encode(..., elem_bytes 2, lanes 128, mode 1).
+ * Replaces the host encode of the KV-cache entry codec
+ * (bigsmall/codecs/kv_cache.py:41-83, which copies the tensor to the host and
+ * encodes there) for device-resident K/V blocks. */
+typedef struct {
+    const void *src;      /* n bf16 words (device, 4-byte aligned), n >= 1, n < 2^32 */
+    uint64_t n;
+    uint8_t *dst;         /* blob output (device, 16-byte aligned) */
+    uint64_t cap;         /* dst capacity, e.g. bs_chunk_encode_bound(n, 2, 128, steps) */
+    uint32_t chunk_begin;
+    uint32_t n_chunks;    /* ceil(n / (128 * steps)) */
+} bs_encode_task;
+
+/* Device scratch bytes bs_chunk_encode_gpu needs. */
+uint64_t bs_chunk_encode_gpu_work_bytes(uint32_t n_tasks, uint64_t total_chunks, uint32_t steps);
+
+/* Encode every task on `stream`. d_out_len[i] receives blob i's length (0 if
+ * the task failed: BS_DEV_ERR_HEADER for inconsistent task fields,
+ * BS_DEV_ERR_BOUNDS for a blob larger than its capacity, OR-ed into
+ * *d_status). d_work: 256-byte aligned scratch of the size above. */
+int bs_chunk_encode_gpu(const bs_encode_task *d_tasks, uint32_t n_tasks, uint32_t total_chunks, uint32_t steps,
+                        void *d_work, uint64_t work_bytes, uint64_t *d_out_len, int32_t *d_status, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* The reference's rANS-family bf16 formats, decoded on the GPU:

@@ -1,0 +1,120 @@
+"""GPU encoder for BSCK (bs_chunk_encode_gpu via bf16_chunked.encode_device).
+
+Bar: every blob is byte-identical to the host encoder's blob for the same
+words with the dense plane mode forced (encode_array(..., mode=MODE_DENSE,
+lanes=128)), and decodes back to the source tensor bit-exactly. Covers chunk
+edges (1 element, a partial step, exactly one chunk, one chunk plus one),
+heavy tails, all-zero and single-exponent tensors, every exponent present,
+several step counts, and batches mixing sizes (with an empty tensor).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _words(rng, kind: str, n: int) -> np.ndarray:
+    if kind == "gauss":
+        x = rng.standard_normal(n) * 0.02
+    elif kind == "studentt":
+        x = rng.standard_t(3, n) * 0.02
+    elif kind == "kv":
+        x = rng.standard_normal(n) * rng.uniform(0.5, 2.0)
+    elif kind == "zeros":
+        return np.zeros(n, np.uint16)
+    elif kind == "one_exp":
+        return (0x3F80 | rng.integers(0, 128, n) | (rng.integers(0, 2, n) << 15)).astype(np.uint16)
+    elif kind == "uniform":
+        return rng.integers(0, 65536, n).astype(np.uint16)
+    else:
+        raise ValueError(kind)
+    return torch.from_numpy(x.astype(np.float32)).bfloat16().view(torch.int16).numpy().view(np.uint16)
+
+
+def _check(words_list, steps):
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    dev = torch.device("cuda", 0)
+    ts = [torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).to(dev) for w in words_list]
+    arena, spans = bc.encode_device(ts, steps=steps)
+    host = arena.cpu().numpy()
+    for w, (off, ln) in zip(words_list, spans):
+        if w.size == 0:
+            assert ln == 0
+            continue
+        want = bc.encode_array(w, steps=steps, mode=bc.MODE_DENSE, lanes=128)
+        got = host[off:off + ln].tobytes()
+        assert len(got) == len(want), (w.size, steps, len(got), len(want))
+        assert got == want, (w.size, steps)
+        out = torch.empty(w.size, dtype=torch.bfloat16, device=dev)
+        st = bc.decode_into(arena[off:off + ln], ln, out, w.size)
+        torch.cuda.synchronize()
+        st.check("round trip")
+        assert out.view(torch.int16).cpu().numpy().view(np.uint16).tobytes() == w.tobytes()
+
+
+@pytest.mark.parametrize("steps", [16, 256, 448])
+@pytest.mark.parametrize("n_rel", ["1", "127", "129", "per-1", "per", "per+1", "3per+17"])
+def test_sizes_match_host_encoder(steps, n_rel):
+    per = 128 * steps
+    n = {"1": 1, "127": 127, "129": 129, "per-1": per - 1, "per": per, "per+1": per + 1,
+         "3per+17": 3 * per + 17}[n_rel]
+    rng = np.random.default_rng(n + steps)
+    _say(f"[enc] gauss n={n} steps={steps}")
+    _check([_words(rng, "gauss", n)], steps)
+
+
+@pytest.mark.parametrize("kind", ["studentt", "kv", "zeros", "one_exp", "uniform"])
+def test_distributions_match_host_encoder(kind):
+    rng = np.random.default_rng(len(kind))
+    _say(f"[enc] {kind} n=1000003")
+    _check([_words(rng, kind, 1_000_003)], 256)
+
+
+def test_batch_of_kv_blocks_and_mixed_sizes():
+    rng = np.random.default_rng(11)
+    ws = [_words(rng, "kv", 262_144) for _ in range(16)] + [np.zeros(0, np.uint16), _words(rng, "gauss", 5)]
+    _say("[enc] batch of 18 tensors")
+    _check(ws, 256)
+
+
+def test_kv_cache_device_tensors_encode_on_gpu():
+    """CompressedKVCache with K/V already in HBM: set_blocks and set encode on
+    the GPU (dense-mode blobs equal to the host encoder's), get/get_blocks
+    give the tensors back bit-exactly."""
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.codecs import kv_cache as kvc
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache
+    g = torch.Generator().manual_seed(21)
+    s = torch.empty(8, 1, 1).uniform_(0.5, 2.0, generator=g)
+    k = (torch.randn(8, 1024, 128, generator=g) * s).bfloat16()
+    v = (torch.randn(8, 1024, 128, generator=g) * s).bfloat16()
+    kd, vd = k.cuda(), v.cuda()
+    c = CompressedKVCache(device="cuda")
+    _say("[enc] kv set_blocks from device tensors")
+    assert c.set_blocks(0, kd, vd, block_tokens=256) == 4
+    L = c._blocks[0]
+    host = L.arena.cpu().numpy()
+    for b in range(4):
+        off, ln, _, mode = L.k_blocks[b]
+        words = k[:, b * 256:(b + 1) * 256].contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+        assert host[off:off + ln].tobytes() == bc.encode_array(words, steps=kvc.KV_STEPS, mode=bc.MODE_DENSE, lanes=128)
+    kb, vb = c.get_blocks(0, [2, 0, 3])
+    for j, b in enumerate([2, 0, 3]):
+        assert torch.equal(kb[j].cpu().view(torch.int16), k[:, b * 256:(b + 1) * 256].view(torch.int16))
+        assert torch.equal(vb[j].cpu().view(torch.int16), v[:, b * 256:(b + 1) * 256].view(torch.int16))
+    _say("[enc] kv set/get from device tensors")
+    c.set(1, kd.unsqueeze(0), vd.unsqueeze(0))
+    k2, v2 = c.get(1)
+    assert torch.equal(k2.cpu().view(torch.int16), k.unsqueeze(0).view(torch.int16))
+    assert torch.equal(v2.cpu().view(torch.int16), v.unsqueeze(0).view(torch.int16))
+    assert 0.6 < c.compression_ratio() < 0.85
