@@ -9,6 +9,7 @@ kernels on the GPU:
     StreamingLoader, BigSmallStreamingModel -> layer-at-a-time decode with prefetch
     CompressedKVCache                       -> KV entries and blocks decoded on the GPU
     codec_registry.register_codec / get_codec / auto_select_codec
+    compress_for_hub(model_dir, out_dir), from_pretrained(path) -> multi-shard .bs models + index
 """
 __version__ = "3.12.0+mi355x"
 
@@ -16,6 +17,7 @@ from .container import info
 from .decoder import decompress, load
 from .encoder import compress
 from .exceptions import BigSmallVersionError, DecodeError
+from .hub import compress_for_hub, from_pretrained
 from .kv_cache_manager import CompressedKVCache
 from .streaming import StreamingLoader
 from .verify import verify
@@ -30,4 +32,5 @@ def __getattr__(name):
 
 
 __all__ = ["compress", "decompress", "load", "info", "verify", "StreamingLoader", "BigSmallStreamingModel",
-           "CompressedKVCache", "BigSmallVersionError", "DecodeError", "__version__"]
+           "CompressedKVCache", "BigSmallVersionError", "DecodeError", "compress_for_hub", "from_pretrained",
+           "__version__"]

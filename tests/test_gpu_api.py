@@ -220,3 +220,32 @@ def test_streaming_model_matches_full_model(tmp_path):
             assert diff <= 1e-5 * max(1.0, want.abs().max().item())
             assert torch.equal(got.argmax(-1), want.argmax(-1))
         m.close()
+
+
+def test_from_pretrained_multi_shard(tmp_path):
+    """compress_for_hub over two safetensors shards with a cross-shard tied
+    tensor, then from_pretrained decodes every shard on the GPU; the alias
+    shares its master's tensor and every tensor is bit-exact."""
+    import json as _json
+    from safetensors.torch import save_file
+    from bigsmall_amd import hub
+    src = tmp_path / "src"
+    src.mkdir()
+    m = _model(seed=4, layers=4)
+    emb = m.pop("model.embed_tokens.weight")
+    m.pop("lm_head.weight")
+    names = sorted(k for k in m if m[k].dtype == torch.bfloat16)
+    a = {k: m[k] for k in names[: len(names) // 2]} | {"model.embed_tokens.weight": emb}
+    b = {k: m[k] for k in names[len(names) // 2:]} | {"lm_head.weight": emb.clone()}
+    save_file(a, str(src / "model-00001-of-00002.safetensors"))
+    save_file(b, str(src / "model-00002-of-00002.safetensors"))
+    wm = {k: "model-00001-of-00002.safetensors" for k in a} | {k: "model-00002-of-00002.safetensors" for k in b}
+    (src / "model.safetensors.index.json").write_text(_json.dumps({"metadata": {}, "weight_map": wm}))
+    out = tmp_path / "bs"
+    hub.compress_for_hub(src, out)
+    _say("[api] from_pretrained over 2 shards")
+    sd = hub.from_pretrained(out, device="cuda")
+    assert set(sd) == set(a) | set(b)
+    for k, v in (a | b).items():
+        assert _bytes(sd[k]) == _bytes(v), k
+    assert sd["lm_head.weight"].data_ptr() == sd["model.embed_tokens.weight"].data_ptr()
