@@ -283,13 +283,26 @@ def run_kv(args) -> dict:
     vw = v0.view(torch.int16).numpy().view(np.uint16).reshape(-1)
     cache = CompressedKVCache(device="cuda")
     src = {}
+    dev_kv = []
     for layer in range(32):
         k = torch.from_numpy(_variants(kw, 2 * layer).view(np.int16)).view(torch.bfloat16).reshape(8, 32768, 128)
         v = torch.from_numpy(_variants(vw, 2 * layer + 1).view(np.int16)).view(torch.bfloat16).reshape(8, 32768, 128)
-        cache.set_blocks(layer, k, v, block_tokens=256)
+        dev_kv.append((k.cuda(), v.cuda()))
         if layer < 2:
             src[layer] = (k, v)
-    log(f"[kv] compressed 32 layers in {time.time() - t0:.1f}s, ratio {cache.compression_ratio():.4f}")
+    log(f"[kv] generated 32 layers in {time.time() - t0:.1f}s")
+    # K/V already in HBM: set_blocks encodes on the GPU (timed, synchronous per layer)
+    cache.set_blocks(0, *dev_kv[0], block_tokens=256)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for layer in range(32):
+        cache.set_blocks(layer, *dev_kv[layer], block_tokens=256)
+    torch.cuda.synchronize()
+    enc_s = time.perf_counter() - t0
+    raw_kv = 32 * 2 * k0.numel() * 2
+    log(f"[kv] GPU-encoded 32 layers in {enc_s * 1e3:.1f} ms ({raw_kv / enc_s / 1e9:.1f} GB/s raw), "
+        f"ratio {cache.compression_ratio():.4f}")
+    del dev_kv
     rng = np.random.default_rng(3)
     req = [(layer, rng.choice(128, 64, replace=False)) for layer in range(32)]
     batch, outs = cache.prepare_blocks_multi(req)
@@ -317,7 +330,69 @@ def run_kv(args) -> dict:
                        "decoded_bytes": int(out_bytes), "ratio_pct": round(100 * cache.compression_ratio(), 3),
                        "launches_per_step": 1},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4)}}
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4)},
+            "gpu_encode": {"seconds_32_layers": round(enc_s, 4), "raw_GBps": round(raw_kv / enc_s / 1e9, 2),
+                           "note": "CompressedKVCache.set_blocks on device K/V, incl. arena compaction"}}
+
+
+def cpu_baseline_refcodecs(words: np.ndarray) -> dict:
+    """The reference's formats on the C0 tensor: blobs written by the oracle's
+    encoders (byte-identical to the reference's, pinned by the golden
+    fixtures) and the oracle's C decoders timed on one host thread."""
+    import oracle
+    oracle.build()
+    out = {}
+    for codec, enc, dec in (("bf16_parallel_v1", oracle.par1_encode, oracle.par1_decode),
+                            ("bf16_se_tans", oracle.tans_encode, oracle.tans_decode),
+                            ("bf16_se_single_kernel", oracle.sk_encode, oracle.sk_decode)):
+        blob = enc(words)
+        t0 = time.perf_counter()
+        got = dec(blob, words.size)
+        dt = time.perf_counter() - t0
+        assert got == words.tobytes(), codec
+        out[codec] = (blob, (len(blob) + words.nbytes) / dt / 1e9)
+    return out
+
+
+def run_refcodecs(args) -> dict:
+    """C0 (4096x4096 N(0, 0.02) bf16, seed 0) in the reference's own formats,
+    decoded on the GPU (bs_refcodec_decode / bs_refcodec_decode_serial) from an
+    HBM-resident blob, beside the oracle's single-thread C decoder."""
+    import torch
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    g = torch.Generator().manual_seed(0)
+    words = (torch.randn(4096 * 4096, generator=g) * 0.02).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    base = cpu_baseline_refcodecs(words)
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for codec, (blob, cpu_gbps) in base.items():
+        d_blob = upload_bytes(blob, dev)
+        out = torch.empty(words.size, dtype=torch.int16, device=dev)
+        st = StatusWord(dev)
+        launch = _refstreams.RefLaunch(_refstreams.PARSERS[codec](blob, words.size), d_blob.data_ptr(), dev)
+        fn = lambda: launch.launch(out.data_ptr(), st.ptr, stream.cuda_stream)
+        fn()
+        torch.cuda.synchronize()
+        st.check(codec)
+        reps = 10 if codec == "bf16_parallel_v1" else 2
+        ms = _timed(fn, reps, stream)
+        st.check(codec)
+        assert out.cpu().numpy().view(np.uint16).tobytes() == words.tobytes(), codec
+        gbps = (len(blob) + words.nbytes) / (ms * 1e-3) / 1e9
+        res[codec] = {"ms": round(ms, 3), "GBps": round(gbps, 3), "ratio_pct": round(100 * len(blob) / words.nbytes, 3),
+                      "cpu_baseline_GBps_1_thread": round(cpu_gbps, 4), "gpu_over_cpu": round(gbps / cpu_gbps, 2)}
+        log(f"[ref] {codec}: {ms:.2f} ms on GPU ({gbps:.3f} GB/s), oracle CPU {cpu_gbps:.3f} GB/s")
+    return {"metric": "decoded GB/s of the reference's bf16 formats on 1 MI355X (C0 tensor)",
+            "value": res["bf16_parallel_v1"]["GBps"], "unit": "GB/s", "n_gpus": 1,
+            "ms_per_step": res["bf16_parallel_v1"]["ms"], "higher_is_better": True, "dtype": "u32",
+            "data": "synthetic: torch seed 0, randn(4096*4096)*0.02 -> bf16; blobs byte-identical to the reference's",
+            "config": {"workload": "refcodecs_c0_4096sq", "elements": int(words.size)},
+            "codecs": res,
+            "roofline": {"bound": "latency (serial rANS chains: 128 streams for bf16_parallel_v1, one for the others)",
+                         "achieved": res["bf16_parallel_v1"]["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(res["bf16_parallel_v1"]["GBps"] / HBM_PEAK_GBPS, 5)}}
 
 
 def main():
@@ -328,8 +403,9 @@ def main():
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["layer", "model", "kv"], default="layer",
-                    help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache blocks)")
+    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs"], default="layer",
+                    help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache "
+                         "blocks), refcodecs (the reference's own formats on the C0 tensor)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -343,7 +419,8 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     if args.workload != "layer":
-        print(json.dumps(run_model(args) if args.workload == "model" else run_kv(args)), flush=True)
+        run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs}[args.workload]
+        print(json.dumps(run(args)), flush=True)
         return
     from bigsmall_amd.codecs import bf16_chunked as bc
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes

@@ -47,10 +47,10 @@ SIGNATURES = {
     "bs_chunk_encode_bound": (_INT, [_U64, _U32, _U32, _U32, ctypes.POINTER(_U64)]),
     "bs_chunk_encode": (_INT, [_P, _U64, _U32, _U32, _U32, _I32, _P, _U64, ctypes.POINTER(_U64), _INT]),
     "bs_refcodec_decode": (_INT, [_P, _U32, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _P, _P]),
-    "bs_refcodec_serial_work_bytes": (_U64, [_U64]),
+    "bs_refcodec_serial_work_bytes": (_U64, [_U64, _U32]),
     "bs_chunk_encode_gpu_work_bytes": (_U64, [_U32, _U64, _U32]),
     "bs_chunk_encode_gpu": (_INT, [_P, _U32, _U32, _U32, _P, _U64, _P, _P, _P]),
-    "bs_refcodec_decode_serial": (_INT, [_P, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _U64, _P, _P]),
+    "bs_refcodec_decode_serial": (_INT, [_P, _U32, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _U64, _P, _P]),
 }
 
 _lib = None

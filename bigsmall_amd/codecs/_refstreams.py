@@ -30,6 +30,7 @@ import numpy as np
 from .. import _native
 
 M_SE, M_MANT = 4096, 1024
+SERIAL_MIN_ELEMENTS = 1 << 16   # from here on a wavefront per chain beats a lane per chain
 SE_ALPHABET, MANT_ALPHABET = 512, 128
 
 SE_STREAM_DTYPE = np.dtype([("words", "<u8"), ("x0", "<u4"), ("n_words", "<u4"), ("tail", "<u4"), ("n", "<u4"),
@@ -331,11 +332,13 @@ class RefLaunch:
         self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets, self.p_tables = (base + o for o in offs)
         self.n_streams, self.n_buckets, self.n_tables = len(se), len(mb), tables.shape[0]
         self.n = plan.n
-        # one SE stream over the whole tensor (bf16_se_tans, bf16_se_single_kernel):
-        # the wave-serial decoder; interleaved streams (bf16_parallel_v1): one lane per stream
-        self.serial = len(plan.se_streams) == 1 and plan.se_streams[0][1:] == (0, 1, plan.n)
+        # one wavefront per chain (bs_refcodec_decode_serial) unless the tensor
+        # is small, where one lane per chain (bs_refcodec_decode) is as fast
+        max_len = max((n for _, _, _, n in plan.se_streams), default=0)
+        self.serial = (plan.n >= SERIAL_MIN_ELEMENTS and len(se) > 0 and
+                       max_len <= -(-plan.n // len(se)))
         if self.serial:
-            nbytes = int(_native.lib().bs_refcodec_serial_work_bytes(plan.n))
+            nbytes = int(_native.lib().bs_refcodec_serial_work_bytes(plan.n, len(se)))
             self.work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         else:
             self.perm = torch.empty(max(plan.n, 1), dtype=torch.int32, device=device)
@@ -343,7 +346,8 @@ class RefLaunch:
     def launch(self, out_ptr: int, status_ptr: int, stream_ptr: int) -> None:
         L = _native.lib()
         if self.serial:
-            rc = L.bs_refcodec_decode_serial(self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets,
+            rc = L.bs_refcodec_decode_serial(self.p_streams, self.n_streams, self.p_se_table, self.p_bstart,
+                                             self.p_buckets,
                                              self.n_buckets, self.p_tables, self.n_tables, out_ptr, self.n,
                                              self.work.data_ptr(), self.work.numel(), status_ptr, stream_ptr)
             _native.check(rc, "bs_refcodec_decode_serial")

@@ -134,9 +134,9 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
   if (x != kL || pos != n_eff) flag(status, BS_DEV_ERR_STREAM);
 }
 
-// ---- wave-serial path for the single-stream formats (bf16_se_tans,
-// bf16_se_single_kernel): one SE chain over the whole tensor plus one
-// mantissa chain per exponent bucket.
+// ---- wave-serial path: every SE stream (one for bf16_se_tans and
+// bf16_se_single_kernel, N interleaved ones for bf16_parallel_v1) and every
+// mantissa bucket is a chain decoded by its own wavefront.
 //
 // Each chain is decoded by one wavefront. The chain itself is uniform (every
 // lane computes the same state; the compiler keeps it in scalar registers),
@@ -147,8 +147,9 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
 // every element; the mantissa chains, which do not depend on it, run at the
 // same time in other workgroups and write their bucket's mantissas in bucket
 // order. Three parallel passes then give every element its position in its
-// bucket (a stable counting sort by exponent: per-tile histograms, a scan over
-// tiles, per-tile ranks by wavefront ballots) and OR in its mantissa.
+// (stream, exponent) bucket (a stable counting sort by exponent within each
+// stream: per-tile histograms, a scan over the stream's tiles, per-tile ranks
+// by wavefront ballots) and OR in its mantissa.
 
 constexpr uint32_t kRingB = 4096;     // word-stream byte ring per chain
 constexpr uint32_t kSegB = 1024;      // bytes per cooperative load (64 lanes x 16 B)
@@ -196,7 +197,7 @@ template <bool SE>
 __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
                                              uint32_t n, const LDS uint8_t* __restrict__ tbl,
                                              LDS uint8_t* __restrict__ ring, GLB uint8_t* __restrict__ out,
-                                             int32_t* status) {
+                                             uint32_t stride, int32_t* status) {
   const uint32_t lane = __lane_id();
   const uint64_t wa = (uint64_t)words;
   const GLB uint8_t* A = (const GLB uint8_t*)(wa & ~15ull);
@@ -256,7 +257,7 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
       keep = lane == j ? v : keep;
     }
     if (lane < cnt) {
-      if (SE) ((GLB uint16_t*)out)[i0 + lane] = (uint16_t)keep;
+      if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)keep;
       else out[i0 + lane] = (uint8_t)keep;
     }
   }
@@ -265,10 +266,11 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   }
 }
 
-// Block 0: the SE stream (element order, stride 1). Block 1 + b: mantissa
-// bucket b, written to mant[perm_begin ...] (bucket order).
-__global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __restrict__ se,
-                                                       const uint32_t* __restrict__ se_table,
+// Block k < n_streams: SE stream k (element first + i*stride for symbol i).
+// Block n_streams + b: mantissa bucket b, written to mant[perm_begin ...]
+// (bucket order). max_len: the longest stream the placement passes hold.
+__global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __restrict__ se, uint32_t n_streams,
+                                                       uint32_t max_len, const uint32_t* __restrict__ se_table,
                                                        const bs_mant_bucket* __restrict__ buckets,
                                                        const uint32_t* __restrict__ mant_tables, uint32_t n_tables,
                                                        uint16_t* __restrict__ out, uint64_t n_out,
@@ -277,9 +279,9 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
   LDS uint8_t* ring = (LDS uint8_t*)smem;
   LDS uint8_t* tbl = (LDS uint8_t*)(smem + kRingB);
   const uint32_t lane = threadIdx.x;
-  if (blockIdx.x == 0) {
-    const bs_se_stream S = se[0];
-    if (S.first != 0 || S.stride != 1 || S.n != n_out) {
+  if (blockIdx.x < n_streams) {
+    const bs_se_stream S = se[blockIdx.x];
+    if (S.n > max_len || S.stride == 0 || (S.n && S.first + (uint64_t)(S.n - 1) * S.stride >= n_out)) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
@@ -289,10 +291,10 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
       ((LDS uint64_t*)tbl)[i] = (uint64_t)se_table[2 * i] | ((uint64_t)word << 32);
     }
     wave_sync();
-    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring, (GLB uint8_t*)out,
-                       status);
+    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring,
+                       (GLB uint8_t*)(out + S.first), S.stride, status);
   } else {
-    const bs_mant_bucket B = buckets[blockIdx.x - 1];
+    const bs_mant_bucket B = buckets[blockIdx.x - n_streams];
     if (B.table >= n_tables || B.perm_begin + B.n > n_out) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
@@ -301,39 +303,41 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
     for (uint32_t i = lane; i < 1024; i += kWave) ((LDS uint32_t*)tbl)[i] = t[i];
     wave_sync();
     serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring,
-                        (GLB uint8_t*)(mant + B.perm_begin), status);
+                        (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
   }
 }
 
-// Exponent histogram of each tile of kTile elements.
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out, uint64_t n,
+// Exponent histogram of each tile: block k * tps + t covers symbols
+// [t*kTile, (t+1)*kTile) of stream k.
+__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out,
+                                                   const bs_se_stream* __restrict__ se, uint32_t tps,
                                                    uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[256];
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x, k = blockIdx.x / tps, t = blockIdx.x % tps;
+  const bs_se_stream S = se[k];
   h[tid] = 0;
   __syncthreads();
-  const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
-  for (uint32_t k = tid; k < kTile; k += 256) {
-    const uint64_t i = t0 + k;
-    if (i < n) atomicAdd(&h[(out[i] >> 7) & 0xFFu], 1u);
-  }
+  const uint32_t lo = t * kTile, hi = min(S.n, lo + kTile);
+  for (uint32_t i = lo + tid; i < hi; i += 256) atomicAdd(&h[(out[S.first + (uint64_t)i * S.stride] >> 7) & 0xFFu], 1u);
   __syncthreads();
   hist[(uint64_t)blockIdx.x * 256 + tid] = h[tid];
 }
 
-// Per exponent: turn tile counts into each tile's first position in the
-// bucket (bstart[e] + counts of the earlier tiles), and check that the
-// decoded exponents fill every bucket exactly.
-__global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, uint32_t n_tiles,
+// Block k, thread e: turn stream k's tile counts of exponent e into each
+// tile's first position in the bucket (bstart[k][e] + counts of the earlier
+// tiles), and check that the decoded exponents fill every bucket exactly.
+__global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, uint32_t tps,
                                                    const uint32_t* __restrict__ bstart, int32_t* __restrict__ status) {
   const uint32_t e = threadIdx.x;
-  uint32_t run = bstart[e];
-  for (uint32_t t = 0; t < n_tiles; ++t) {
-    const uint32_t c = hist[(uint64_t)t * 256 + e];
-    hist[(uint64_t)t * 256 + e] = run;
+  const uint32_t* bs = bstart + (uint64_t)blockIdx.x * 257;
+  uint32_t* hk = hist + (uint64_t)blockIdx.x * tps * 256;
+  uint32_t run = bs[e];
+  for (uint32_t t = 0; t < tps; ++t) {
+    const uint32_t c = hk[(uint64_t)t * 256 + e];
+    hk[(uint64_t)t * 256 + e] = run;
     run += c;
   }
-  if (run != bstart[e + 1]) flag(status, BS_DEV_ERR_COUNT);
+  if (run != bs[e + 1]) flag(status, BS_DEV_ERR_COUNT);
 }
 
 // Per tile (one wavefront): the position of each element in its bucket, from
@@ -341,20 +345,22 @@ __global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, 
 // it (64 elements at a time: lanes with the same exponent found with eight
 // ballots); then OR the element's mantissa into it.
 __global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out, uint64_t n,
+                                                      const bs_se_stream* __restrict__ se, uint32_t tps,
                                                       const uint32_t* __restrict__ first,
                                                       const uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
   __shared__ uint32_t cnt[256];
-  const uint32_t lane = threadIdx.x;
+  const uint32_t lane = threadIdx.x, k = blockIdx.x / tps, t = blockIdx.x % tps;
+  const bs_se_stream S = se[k];
   for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)blockIdx.x * 256 + e];
   wave_sync();
-  const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
+  const uint32_t lo = t * kTile, hi = min(S.n, lo + kTile);
   const uint64_t lt = (1ull << lane) - 1ull;
   bool bad = false;
-  for (uint32_t k0 = 0; k0 < kTile; k0 += kWave) {
-    const uint64_t i = t0 + k0 + lane;
-    if (t0 + k0 >= n) break;
-    const bool valid = i < n;
-    const uint32_t word = valid ? out[i] : 0u;
+  for (uint32_t k0 = lo; k0 < hi; k0 += kWave) {
+    const uint32_t i = k0 + lane;
+    const bool valid = i < hi;
+    const uint64_t el = S.first + (uint64_t)i * S.stride;
+    const uint32_t word = valid ? out[el] : 0u;
     const uint32_t e = (word >> 7) & 0xFFu;
     uint64_t m = __ballot(valid);
 #pragma unroll
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out
     if (valid && rank == 0) cnt[e] = base + total;
     if (valid) {
       const uint32_t p = base + rank;
-      if (p < n) out[i] = (uint16_t)(word | mant[p]);
+      if (p < n) out[el] = (uint16_t)(word | mant[p]);
       else bad = true;
     }
     wave_sync();
@@ -380,41 +386,6 @@ __global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out
 }  // namespace
 
 extern "C" {
-
-uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out) {
-  const uint64_t tiles = (n_out + kTile - 1) / kTile;
-  return ((n_out + 255) & ~255ull) + tiles * 256 * 4;
-}
-
-int bs_refcodec_decode_serial(const bs_se_stream* d_stream, const uint32_t* d_se_table, const uint32_t* d_bstart,
-                              const bs_mant_bucket* d_buckets, uint32_t n_buckets, const uint32_t* d_mant_tables,
-                              uint32_t n_tables, uint16_t* d_out, uint64_t n_out, void* d_work, uint64_t work_bytes,
-                              int32_t* d_status, void* stream) {
-  if (!d_status || (n_out && (!d_stream || !d_se_table || !d_bstart || !d_out || !d_work)) ||
-      (n_buckets && (!d_buckets || !d_mant_tables)) || n_out > 0xFFFFFFFFull)
-    return BS_ERR_ARG;
-  if (n_out == 0) return BS_OK;
-  if (work_bytes < bs_refcodec_serial_work_bytes(n_out) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
-  hipStream_t s = (hipStream_t)stream;
-  uint8_t* mant = (uint8_t*)d_work;
-  uint32_t* hist = (uint32_t*)(mant + ((n_out + 255) & ~255ull));
-  const uint32_t tiles = (uint32_t)((n_out + kTile - 1) / kTile);
-  constexpr uint32_t kSerLds = kRingB + 4096 * 8;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)serial_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSerLds);
-    attr = true;
-  }
-  hipLaunchKernelGGL(serial_kernel, dim3(1 + n_buckets), dim3(kWave), kSerLds, s, d_stream, d_se_table, d_buckets,
-                     d_mant_tables, n_tables, d_out, n_out, mant, d_status);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, d_out, n_out, hist);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, s, hist, tiles, d_bstart, d_status);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(place_kernel, dim3(tiles), dim3(kWave), 0, s, d_out, n_out, hist, mant, d_status);
-  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
-}
 
 int bs_refcodec_decode(const bs_se_stream* d_streams, uint32_t n_streams, const uint32_t* d_se_table,
                        const uint32_t* d_bstart, const bs_mant_bucket* d_buckets, uint32_t n_buckets,
@@ -440,6 +411,45 @@ int bs_refcodec_decode(const bs_se_stream* d_streams, uint32_t n_streams, const 
     if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
   }
   return BS_OK;
+}
+
+uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out, uint32_t n_streams) {
+  if (n_streams == 0) return 0;
+  const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
+  const uint64_t tps = (max_len + kTile - 1) / kTile;
+  return ((n_out + 255) & ~255ull) + (uint64_t)n_streams * tps * 256 * 4;
+}
+
+int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams, const uint32_t* d_se_table,
+                              const uint32_t* d_bstart, const bs_mant_bucket* d_buckets, uint32_t n_buckets,
+                              const uint32_t* d_mant_tables, uint32_t n_tables, uint16_t* d_out, uint64_t n_out,
+                              void* d_work, uint64_t work_bytes, int32_t* d_status, void* stream) {
+  if (!d_status || (n_out && (!d_streams || !d_se_table || !d_bstart || !d_out || !d_work || !n_streams)) ||
+      (n_buckets && (!d_buckets || !d_mant_tables)) || n_out > 0xFFFFFFFFull)
+    return BS_ERR_ARG;
+  if (n_out == 0) return BS_OK;
+  if (work_bytes < bs_refcodec_serial_work_bytes(n_out, n_streams) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* mant = (uint8_t*)d_work;
+  uint32_t* hist = (uint32_t*)(mant + ((n_out + 255) & ~255ull));
+  const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
+  const uint32_t tps = (uint32_t)((max_len + kTile - 1) / kTile);
+  constexpr uint32_t kSerLds = kRingB + 4096 * 8;
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)serial_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSerLds);
+    attr = true;
+  }
+  hipLaunchKernelGGL(serial_kernel, dim3(n_streams + n_buckets), dim3(kWave), kSerLds, s, d_streams, n_streams,
+                     tps * kTile, d_se_table, d_buckets, d_mant_tables, n_tables, d_out, n_out, mant, d_status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(hist_kernel, dim3(n_streams * tps), dim3(256), 0, s, d_out, d_streams, tps, hist);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(scan_kernel, dim3(n_streams), dim3(256), 0, s, hist, tps, d_bstart, d_status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(place_kernel, dim3(n_streams * tps), dim3(kWave), 0, s, d_out, n_out, d_streams, tps, hist, mant,
+                     d_status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 
 }  // extern "C"

@@ -102,6 +102,9 @@ class CompressedKVCache:
         if T % block_tokens:
             raise ValueError(f"set_blocks: {T} tokens is not a multiple of block_tokens={block_tokens}")
         nb = T // block_tokens
+        if layer_idx in self._blocks:          # replacing a layer: drop its raw size from the totals
+            old = self._blocks.pop(layer_idx)
+            self._block_raw -= 2 * 2 * old.block_elems * len(old.k_blocks)
         block_shape = list(keys.shape)
         block_shape[td] = block_tokens
         block_elems = int(np.prod(block_shape))

@@ -181,24 +181,26 @@ int bs_refcodec_decode(const bs_se_stream *d_streams, uint32_t n_streams, const 
                        const uint32_t *d_mant_tables, uint32_t n_tables, uint16_t *d_out, uint64_t n_out,
                        uint32_t *d_perm, int32_t *d_status, void *stream);
 
-/* Workspace bytes bs_refcodec_decode_serial needs for n_out elements. */
-uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out);
+/* Workspace bytes bs_refcodec_decode_serial needs for n_out elements in n_streams SE streams. */
+uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out, uint32_t n_streams);
 
-/* The single-stream formats (bf16_se_tans, bigsmall/codecs/bf16_tans.py:121-167;
- * bf16_se_single_kernel, bigsmall/codecs/single_kernel.py:431-580): one SE
- * stream over all n_out elements (first 0, stride 1) plus one mantissa bucket
- * per exponent. Same tables and descriptors as bs_refcodec_decode (one
- * stream, d_bstart of 257 entries); d_work: bs_refcodec_serial_work_bytes(n_out)
- * bytes of device scratch, 256-byte aligned. Each chain is decoded by one
- * wavefront (SE and mantissa chains at the same time), then the elements are
- * placed by a parallel stable counting sort. Replaces the serial decode loops
- * of numba_rans._decode_kernel (bigsmall/codecs/numba_rans.py:168-192) and
- * single_kernel._decode_full_kernel (bigsmall/codecs/single_kernel.py:431-580).
- * n_out < 2^32. Asynchronous on `stream`; integrity failures OR-ed into *d_status. */
-int bs_refcodec_decode_serial(const bs_se_stream *d_stream, const uint32_t *d_se_table, const uint32_t *d_bstart,
-                              const bs_mant_bucket *d_buckets, uint32_t n_buckets, const uint32_t *d_mant_tables,
-                              uint32_t n_tables, uint16_t *d_out, uint64_t n_out, void *d_work, uint64_t work_bytes,
-                              int32_t *d_status, void *stream);
+/* The same formats and descriptors as bs_refcodec_decode, decoded with one
+ * wavefront per chain: every SE stream (N for bf16_parallel_v1,
+ * bigsmall/codecs/bf16_parallel.py:262-352; one for bf16_se_tans,
+ * bigsmall/codecs/bf16_tans.py:121-167, and bf16_se_single_kernel,
+ * bigsmall/codecs/single_kernel.py:431-580) and every mantissa bucket, SE and
+ * mantissa chains at the same time, then a parallel stable counting sort by
+ * exponent within each stream places the mantissas. Streams must each hold at
+ * most ceil(n_out / n_streams) symbols. d_work: bs_refcodec_serial_work_bytes
+ * bytes of device scratch, 256-byte aligned. Replaces the serial decode loops
+ * of rans.decode_stream (bigsmall/codecs/rans.py:165-207),
+ * numba_rans._decode_kernel (bigsmall/codecs/numba_rans.py:168-192) and
+ * single_kernel._decode_full_kernel. n_out < 2^32. Asynchronous on `stream`;
+ * integrity failures OR-ed into *d_status. */
+int bs_refcodec_decode_serial(const bs_se_stream *d_streams, uint32_t n_streams, const uint32_t *d_se_table,
+                              const uint32_t *d_bstart, const bs_mant_bucket *d_buckets, uint32_t n_buckets,
+                              const uint32_t *d_mant_tables, uint32_t n_tables, uint16_t *d_out, uint64_t n_out,
+                              void *d_work, uint64_t work_bytes, int32_t *d_status, void *stream);
 
 #ifdef __cplusplus
 }

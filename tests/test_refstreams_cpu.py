@@ -67,19 +67,20 @@ def emulate(plan: rs.RefPlan, blob: bytes) -> np.ndarray:
 
 def emulate_serial(plan: rs.RefPlan, blob: bytes, tile: int = 256) -> np.ndarray:
     """The wave-serial path (refcodec_decode.hip: serial_kernel, hist_kernel,
-    scan_kernel, place_kernel) for a one-stream plan: the SE chain writes
-    sign<<15 | exp<<7 in element order, each mantissa chain writes its bucket
-    in bucket order, then per-tile exponent histograms, a scan over tiles per
-    exponent and per-64-element ranks place every element's mantissa."""
-    (s, first, stride, n), = plan.se_streams
-    assert (first, stride, n) == (0, 1, plan.n)
+    scan_kernel, place_kernel): each SE chain writes sign<<15 | exp<<7 at its
+    elements first + i*stride, each mantissa chain writes its bucket in bucket
+    order, then per stream: tile exponent histograms over the stream's symbol
+    index, a scan over its tiles per exponent from bstart, and per-64-symbol
+    ranks place every element's mantissa."""
     se_t = rs.decode_table_se(plan.se_freqs)
+    n = plan.n
     out = np.zeros(n, np.uint16)
-    syms, x, pos, n_eff = _run(blob, s, n, lambda sl: (int(se_t[sl, 0]) & 0x1FFF, int(se_t[sl, 0]) >> 13,
-                                                       int(se_t[sl, 1])), 12)
-    assert x == L and pos == n_eff
-    syms = np.asarray(syms, np.uint32)
-    out[:] = (((syms >> 8) & 1) << 15) | ((syms & 0xFF) << 7)
+    for s, first, stride, ns in plan.se_streams:
+        syms, x, pos, n_eff = _run(blob, s, ns, lambda sl: (int(se_t[sl, 0]) & 0x1FFF, int(se_t[sl, 0]) >> 13,
+                                                            int(se_t[sl, 1])), 12)
+        assert x == L and pos == n_eff
+        syms = np.asarray(syms, np.uint32)
+        out[first + stride * np.arange(ns)] = (((syms >> 8) & 1) << 15) | ((syms & 0xFF) << 7)
     mant = np.zeros(n, np.uint8)
     for bs_, pb, nb, t in plan.buckets:
         tbl = rs.decode_table_mant(plan.mant_freqs[t])
@@ -87,33 +88,37 @@ def emulate_serial(plan: rs.RefPlan, blob: bytes, tile: int = 256) -> np.ndarray
                                                            int(tbl[sl]) >> 21), 10)
         assert x == L and pos == n_eff
         mant[pb:pb + nb] = m
-    e = (out >> 7) & 0xFF
-    tiles = (n + tile - 1) // tile
-    hist = np.zeros((tiles, 256), np.int64)
-    for t in range(tiles):
-        hist[t] = np.bincount(e[t * tile:(t + 1) * tile], minlength=256)
-    bstart = plan.bstart[0].astype(np.int64)
-    firsts = bstart[:256] + np.concatenate([np.zeros((1, 256), np.int64), np.cumsum(hist, 0)[:-1]])
-    assert np.array_equal(bstart[:256] + hist.sum(0), bstart[1:])
-    for t in range(tiles):
-        cnt = firsts[t].copy()
-        for k0 in range(t * tile, min(n, (t + 1) * tile), 64):
-            ch = e[k0:min(n, k0 + 64)]
-            for lane, ev in enumerate(ch):
-                rank = int(np.count_nonzero(ch[:lane] == ev))
-                out[k0 + lane] |= mant[cnt[ev] + rank]
-            for ev in np.unique(ch):
-                cnt[ev] += int(np.count_nonzero(ch == ev))
+    for (s, first, stride, ns), bstart in zip(plan.se_streams, plan.bstart):
+        elems = first + stride * np.arange(ns)
+        e = (out[elems] >> 7) & 0xFF
+        tiles = (ns + tile - 1) // tile
+        hist = np.zeros((tiles, 256), np.int64)
+        for t in range(tiles):
+            hist[t] = np.bincount(e[t * tile:(t + 1) * tile], minlength=256)
+        bstart = bstart.astype(np.int64)
+        firsts = bstart[:256] + np.concatenate([np.zeros((1, 256), np.int64), np.cumsum(hist, 0)[:-1]])
+        assert np.array_equal(bstart[:256] + hist.sum(0), bstart[1:])
+        for t in range(tiles):
+            cnt = firsts[t].copy()
+            for k0 in range(t * tile, min(ns, (t + 1) * tile), 64):
+                ch = e[k0:min(ns, k0 + 64)]
+                for lane, ev in enumerate(ch):
+                    rank = int(np.count_nonzero(ch[:lane] == ev))
+                    out[elems[k0 + lane]] |= mant[cnt[ev] + rank]
+                for ev in np.unique(ch):
+                    cnt[ev] += int(np.count_nonzero(ch == ev))
     return out
 
 
-@pytest.mark.parametrize("codec,prefix", [("bf16_se_tans", "tans_"), ("bf16_se_single_kernel", "sk_")])
+@pytest.mark.parametrize("codec,prefix", [("bf16_parallel_v1", "par1_"), ("bf16_se_tans", "tans_"),
+                                          ("bf16_se_single_kernel", "sk_")])
 def test_serial_path_decodes_reference_blobs(golden, codec, prefix):
     seen = 0
     for k in sorted(golden):
         if not k.startswith(prefix):
             continue
-        words = golden[f"in_{k[len(prefix):]}"].astype(np.uint16)
+        name = k[len(prefix):].rsplit("_N", 1)[0] if prefix == "par1_" else k[len(prefix):]
+        words = golden[f"in_{name}"].astype(np.uint16)
         if words.size > 40000 or words.size == 0:
             continue
         blob = golden[k].tobytes()
