@@ -3,9 +3,10 @@
  *
  * Plain-C restatement of the reference BigSmall CPU encode/decode algorithms
  * for the rANS-family bf16 codecs. Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * or as the timed CPU baseline. The product decode path (bigsmall_amd) never
- * links or calls it.
+ * cpu_baseline legs of bench.py may load this library: to check results
+ * against, as the timed CPU baseline, and to write the reference-format blobs
+ * that baseline decodes. The product decode path (bigsmall_amd) never links
+ * or calls it.
  *
  * Every function cites the reference file:line it restates (paths relative to
  * the reference repository root). Pinning (see tests/test_oracle_*.py):
