@@ -395,6 +395,99 @@ def run_refcodecs(args) -> dict:
                          "frac": round(res["bf16_parallel_v1"]["GBps"] / HBM_PEAK_GBPS, 5)}}
 
 
+def _c3_tensors():
+    """8192x8192 stress tensors: (a) Student-t df=3 at std 0.02, (b) N(0, 0.02)
+    with exactly half the positions (randperm) +0.0, (c) fp8 e4m3 of N(0, 1)
+    and its bf16 residual."""
+    import torch
+    n = 8192 * 8192
+    g = torch.Generator().manual_seed(3)
+    torch.manual_seed(3)
+    st = (torch.distributions.StudentT(3.0).sample((n,)) * (0.02 / np.sqrt(3.0))).bfloat16()
+    hz = (torch.randn(n, generator=g) * 0.02).bfloat16()
+    hz[torch.randperm(n, generator=g)[: n // 2]] = 0
+    x = torch.randn(n, generator=torch.Generator().manual_seed(4))
+    f8 = x.to(torch.float8_e4m3fn)
+    resid = (x - f8.float()).bfloat16()
+    w = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    return [("studentt", w(st)), ("halfzero", w(hz)), ("fp8_e4m3", f8.view(torch.uint8).numpy()),
+            ("fp8_residual", w(resid))]
+
+
+def cpu_baseline_c3(tensors) -> dict:
+    """bf16_se_tans (the reference's forced-tANS codec) blobs from the oracle's
+    encoder, and its C decoder timed on one host thread."""
+    import oracle
+    oracle.build()
+    out = {}
+    for name, w in tensors:
+        if w.dtype != np.uint16:
+            continue
+        blob = oracle.tans_encode(w)
+        t0 = time.perf_counter()
+        assert oracle.tans_decode(blob, w.size) == w.tobytes(), name
+        out[name] = (blob, (len(blob) + w.nbytes) / (time.perf_counter() - t0) / 1e9)
+    return out
+
+
+def run_c3(args) -> dict:
+    """The 8192x8192 stress tensors decoded on the GPU: forced rANS = this
+    engine's bf16_chunked_v1 / fp8_chunked_v1 (one launch per tensor), forced
+    tANS = the reference's bf16_se_tans (wave-serial path), the latter beside
+    the oracle's C decoder on one host thread."""
+    import torch
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
+    tensors = _c3_tensors()
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    # the format's default chunk (448 steps: sized for layer batches) gives one
+    # 67M-element tensor 1,171 chunks, fewer than the 4,096 wavefront slots of
+    # the GPU; 128 steps fill them (4,096 chunks) at a small ratio cost
+    steps = args.chunk_steps or 128
+    for name, w in tensors:
+        blob = bc.encode_array(w, steps=steps)
+        inf = bc.info(blob)
+        d_blob = upload_bytes(blob, dev)
+        out = torch.empty(w.nbytes, dtype=torch.uint8, device=dev)
+        st = StatusWord(dev)
+        batch = ChunkBatch([ChunkJob(d_blob.data_ptr(), len(blob), out.data_ptr(), w.size, inf.n_chunks,
+                                     inf.plane_mode)], dev)
+        batch.launch(st, stream)
+        ms = _timed(lambda: batch.launch(st, stream), args.steps, stream)
+        st.check(name)
+        assert out.cpu().numpy().tobytes() == w.tobytes(), name
+        gbps = (len(blob) + w.nbytes) / (ms * 1e-3) / 1e9
+        res[name] = {"rans_bsck": {"ms": round(ms, 4), "GBps": round(gbps, 2), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                   "ratio_pct": round(100 * len(blob) / w.nbytes, 3), "plane_mode": inf.plane_mode,
+                                   "elem_bytes": inf.elem_bytes, "chunk_steps": steps}}
+        log(f"[c3] {name}: bf16/fp8_chunked {ms:.3f} ms, {gbps:.0f} GB/s, ratio {100 * len(blob) / w.nbytes:.2f} %")
+    for name, (blob, cpu_gbps) in cpu_baseline_c3(tensors).items():
+        w = dict(tensors)[name]
+        d_blob = upload_bytes(blob, dev)
+        out = torch.empty(w.size, dtype=torch.int16, device=dev)
+        st = StatusWord(dev)
+        launch = _refstreams.RefLaunch(_refstreams.PARSERS["bf16_se_tans"](blob, w.size), d_blob.data_ptr(), dev)
+        ms = _timed(lambda: launch.launch(out.data_ptr(), st.ptr, stream.cuda_stream), 1, stream)
+        st.check(name)
+        assert out.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), name
+        gbps = (len(blob) + w.nbytes) / (ms * 1e-3) / 1e9
+        res[name]["tans_reference_format"] = {"ms": round(ms, 1), "GBps": round(gbps, 4),
+                                              "ratio_pct": round(100 * len(blob) / w.nbytes, 3),
+                                              "cpu_baseline_GBps_1_thread": round(cpu_gbps, 4)}
+        log(f"[c3] {name}: bf16_se_tans {ms:.0f} ms on GPU, oracle CPU {cpu_gbps:.3f} GB/s")
+    head = res["studentt"]["rans_bsck"]
+    return {"metric": "decoded GB/s, 8192x8192 stress tensors (forced rANS on this engine's format; forced tANS "
+                      "on the reference's bf16_se_tans)",
+            "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "ms_per_step": head["ms"], "higher_is_better": True,
+            "dtype": "u32", "data": "synthetic: Student-t df=3, half zeros, fp8 e4m3 + bf16 residual (seeded)",
+            "config": {"workload": "c3_stress_8192sq", "elements_per_tensor": 8192 * 8192}, "tensors": res,
+            "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": head["frac"]}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,9 +496,10 @@ def main():
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3"], default="layer",
                     help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache "
-                         "blocks), refcodecs (the reference's own formats on the C0 tensor)")
+                         "blocks), refcodecs (the reference's own formats on the C0 tensor), c3 (stress "
+                         "tensors)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -419,7 +513,7 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     if args.workload != "layer":
-        run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs}[args.workload]
+        run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs, "c3": run_c3}[args.workload]
         print(json.dumps(run(args)), flush=True)
         return
     from bigsmall_amd.codecs import bf16_chunked as bc
