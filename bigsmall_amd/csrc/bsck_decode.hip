@@ -49,6 +49,7 @@ namespace {
 #define LDS __attribute__((address_space(3)))
 #define GLB __attribute__((address_space(1)))
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kVersion = 2;
 constexpr int kWave = 64;                 // lanes of a wavefront
@@ -63,21 +64,43 @@ constexpr int kThreads = kWaves * kWave;
 template <int K>
 constexpr int block_steps() { return K == 4 ? 4 : 8; }
 constexpr int kBlockMax = 8;
-constexpr uint32_t kRing = 2048;          // per-wave renorm-word ring (u16 entries), power of two
-constexpr uint32_t kMirror = 64;          // ring words [0, 64) are mirrored after the ring end
-constexpr uint32_t kRingBytes = (kRing + kMirror) * 2;
-constexpr uint32_t kPRing = 4096;         // per-wave compact-plane ring (bytes)
-constexpr uint32_t kWSeg = 512;           // words per word-ring segment (64 lanes x 16 bytes)
-constexpr uint32_t kPSeg = 1024;          // bytes per plane-ring segment
+constexpr uint32_t kMirror = 64;          // word-ring entries [0, 64) are mirrored after the ring end
+constexpr uint32_t kRingBytes = (2048 + kMirror) * 2;   // per-wave ring area
 constexpr uint32_t kL = 1u << 16;
 // s_waitcnt immediate for gfx9: vmcnt(4), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
 constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
-// dynamic LDS layout (bytes): decode table | word rings | output staging | plane rings (compact launches)
+// dynamic LDS layout (bytes): decode table | per-wave ring areas | per-wave output staging
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
-constexpr uint32_t kLdsLean = kTblBytes + kWaves * (kRingBytes + kStageMax);
-constexpr uint32_t kLdsCompact = kLdsLean + kWaves * kPRing;
+constexpr uint32_t kLds = kTblBytes + kWaves * (kRingBytes + kStageMax);   // 74752: two workgroups per CU
+
+template <bool HALF> struct SegVec { typedef u32x4 T; };
+template <> struct SegVec<true> { typedef u32x2 T; };
+
+// Ring geometry of a chunk. Plane modes 0 and 1 use the whole ring area as a
+// 2048-word renorm ring, refilled in 512-word segments (64 lanes x 16 bytes),
+// with blocks of block_steps<K>() steps (up to 1024 elements). Compact-plane
+// chunks (mode 2) run at half scale: blocks of 512 elements, a 1024-word renorm
+// ring and a 2048-byte plane ring sharing the same area, segments of 64 lanes x
+// 8 bytes. Every ring then holds the same multiple of a block's worst-case
+// demand, and a compact launch needs no more LDS than any other (two
+// workgroups per CU).
+template <int K, int MODE>
+struct Geo {
+  static constexpr bool kHalf = MODE == 2;
+  static constexpr int kBlock = kHalf ? 8 / K : block_steps<K>();
+  static constexpr uint32_t kBlkElems = (uint32_t)kBlock * kWave * K;   // worst-case words/plane bytes per block
+  static constexpr uint32_t kRing = kHalf ? 1024 : 2048;                 // renorm-word ring entries
+  static constexpr uint32_t kLaneSeg = kHalf ? 8 : 16;                   // bytes per lane per segment
+  static constexpr uint32_t kWSeg = kLaneSeg * kWave / 2;                // words per segment
+  static constexpr uint32_t kPRing = 2048;                               // plane ring bytes (mode 2)
+  static constexpr uint32_t kPSeg = kLaneSeg * kWave;                    // plane bytes per segment
+  static constexpr uint32_t kPRingOff = (kRing + kMirror) * 2;           // plane ring offset in the ring area
+  typedef typename SegVec<kHalf>::T Seg;
+  static_assert(!kHalf || kPRingOff + kPRing <= kRingBytes, "compact rings exceed the ring area");
+  static_assert(kHalf || (kRing + kMirror) * 2 <= kRingBytes, "word ring exceeds the ring area");
+};
 
 __device__ __forceinline__ uint32_t ld_u32(const GLB uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -111,26 +134,29 @@ __device__ __forceinline__ void report(int32_t* status, int32_t bits) {
 
 __device__ __forceinline__ uint32_t byte_merge(uint32_t v, uint32_t b) { return ((b * 0x101u) & 0x807Fu) | v; }
 
-// ---- ring refills. A segment is 64 lanes x 16 bytes (512 renorm words or 1024
-// compact-plane bytes); segment positions are multiples of the segment size.
+// ---- ring refills. A segment is 64 lanes x Geo::kLaneSeg bytes; segment
+// positions are multiples of the segment size.
 
-// Load this lane's 16 bytes of the segment at `pos16` (16-byte units);
-// out-of-range lanes read `safe` (the chunk's state words, always in bounds),
-// so every call issues exactly one load per lane.
-__device__ __forceinline__ u32x4 load_seg(const GLB u32x4* src, uint32_t pos16, uint32_t valid16, uint32_t lane,
-                                          const GLB u32x4* safe) {
-  const uint32_t slot = pos16 + lane;
-  return *(slot < valid16 ? src + slot : safe + (lane & 15u));
+// Load this lane's part of the segment at `pos` (in units of V); out-of-range
+// lanes read `safe` (the chunk's state words, 256 bytes or more, always in
+// bounds), so every call issues exactly one load per lane.
+template <typename V>
+__device__ __forceinline__ V load_seg(const GLB uint8_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
+                                      const GLB uint8_t* safe) {
+  const uint32_t slot = pos + lane;
+  return *(slot < valid ? (const GLB V*)src + slot : (const GLB V*)safe + (lane & (256u / sizeof(V) - 1u)));
 }
 // Word ring: words [0, kMirror) also live at [kRing, kRing + kMirror), so a
 // read at (ring position mod kRing) + rank, rank < 64, never wraps.
-__device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, u32x4 v, uint32_t lane) {
-  const uint32_t r = (pos + lane * 8u) & (kRing - 1u);
-  *(LDS u32x4*)(ring + r) = v;
-  if (r < kMirror) *(LDS u32x4*)(ring + kRing + r) = v;
+template <class G>
+__device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, typename G::Seg v, uint32_t lane) {
+  const uint32_t r = (pos + lane * (G::kLaneSeg / 2u)) & (G::kRing - 1u);
+  *(LDS typename G::Seg*)(ring + r) = v;
+  if (r < kMirror) *(LDS typename G::Seg*)(ring + G::kRing + r) = v;
 }
-__device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, u32x4 v, uint32_t lane) {
-  *(LDS u32x4*)(ring + ((pos + lane * 16u) & (kPRing - 1u))) = v;
+template <class G>
+__device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, typename G::Seg v, uint32_t lane) {
+  *(LDS typename G::Seg*)(ring + ((pos + lane * G::kLaneSeg) & (G::kPRing - 1u))) = v;
 }
 
 template <int K>
@@ -172,28 +198,30 @@ struct ChunkState {
 // plane of the next pair's two blocks. Every load is issued unconditionally
 // (unneeded ones read an always-valid dummy address) so the wait counts are
 // the same on every path.
-template <int K>
+template <int K, int MODE>
 struct Inflight {
-  u32x4 w[2], p[2];
+  typename Geo<K, MODE>::Seg w[2], p[2];
   bool wn[2], pn[2];
   PlaneRegs<K> pl[2];
 };
 
 // Chunk-constant parameters.
 struct ChunkParams {
-  const GLB u32x4* wsrc;        // renorm words, 16-byte units
-  const GLB u32x4* psrc;        // compact plane, 16-byte units
+  const GLB uint8_t* wsrc;      // renorm words
+  const GLB uint8_t* psrc;      // compact plane
   const GLB uint8_t* dplane;    // dense plane: B*K bytes per lane per block of B steps
-  const GLB u32x4* safe;        // the chunk's state words: an always-valid dummy address
+  const GLB uint8_t* safe;      // the chunk's state words: an always-valid dummy address
   GLB uint8_t* out8;
   uint64_t base;                // first element of the chunk
-  uint32_t n_words, n_plane, wvalid16, pvalid16, nc, nsteps, nblk, lane;
+  uint32_t n_words, n_plane;
+  uint32_t wvalid, pvalid;      // readable words / plane bytes, in segment-lane units
+  uint32_t nc, nsteps, nblk, lane;
 };
 
-// Store the staged outputs of half-block `hb` (half a block of steps) to the output.
-template <int K, int EB, bool PARTIAL>
+// Store the staged outputs of half-block `hb` (HS steps) to the output.
+template <int K, int EB, bool PARTIAL, int HS>
 __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
-  constexpr uint32_t kBlkElems = block_steps<K>() / 2 * kWave * K;
+  constexpr uint32_t kBlkElems = (uint32_t)HS * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
   const uint64_t blk_byte0 = (C.base + (uint64_t)hb * kBlkElems) * EB;
   // Streaming stores: the decoded tensor is far larger than the L2 (the hint
@@ -233,17 +261,21 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
 // One step of the K states of every lane. Phased so the K dependency chains of
 // a lane overlap: K table reads, then the K state updates with their ballots,
 // then the K ring reads (one wait for all), then the renormalisations.
-// FAST = dense bf16 table layout.
-template <int K, bool FAST, bool PARTIAL>
+// FAST = dense bf16 table layout (d = the table word holding the exponent);
+// otherwise d = value | consume << 31, and for MODE 2 the compact-plane byte
+// of each consuming element is read beside the renorm words (same wait) and
+// merged into d.
+template <int K, int MODE, bool FAST, bool PARTIAL>
 __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C,
                                           const LDS uint64_t* __restrict__ tbl, const LDS uint16_t* __restrict__ wring,
-                                          uint32_t (&d)[K], uint64_t (&active_m)[K]) {
+                                          const LDS uint8_t* __restrict__ pring, uint32_t (&d)[K]) {
+  typedef Geo<K, MODE> G;
   uint64_t e[K];
 #pragma unroll
   for (int g = 0; g < K; ++g) e[g] = tbl[S.x[g] & 4095u];
-  uint32_t xn[K], w[K];
-  bool need[K];
-  uint32_t pos = S.wptr;
+  uint32_t xn[K], w[K], pb[K];
+  bool need[K], cons[K];
+  uint32_t pos = S.wptr, ppos = S.pptr;
 #pragma unroll
   for (int g = 0; g < K; ++g) {
     const uint32_t lo = (uint32_t)e[g], hi = (uint32_t)(e[g] >> 32);
@@ -259,16 +291,27 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
       act = t * (kWave * K) + C.lane * K + g < C.nc;
       if (!act) xn[g] = S.x[g];
     }
-    active_m[g] = __ballot(act);
     need[g] = xn[g] < kL;
     const uint64_t m = __ballot(need[g]);
-    w[g] = wring[(pos & (kRing - 1u)) + lane_rank(m)];   // < kRing + 64: the mirror covers it
+    w[g] = wring[(pos & (G::kRing - 1u)) + lane_rank(m)];   // < kRing + 64: the mirror covers it
     pos += (uint32_t)__popcll(m);
+    if (MODE == 2) {
+      // plane bytes follow decode order: groups ascending, then lanes ascending
+      cons[g] = act && (int32_t)hi < 0;
+      const uint64_t cm = __ballot(cons[g]);
+      pb[g] = pring[(ppos + lane_rank(cm)) & (G::kPRing - 1u)];
+      ppos += (uint32_t)__popcll(cm);
+    }
   }
   consume<K>(w);
+  if (MODE == 2) consume<K>(pb);
   S.wptr = pos;
+  if (MODE == 2) S.pptr = ppos;
 #pragma unroll
-  for (int g = 0; g < K; ++g) S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
+  for (int g = 0; g < K; ++g) {
+    S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
+    if (MODE == 2 && cons[g]) d[g] = byte_merge(d[g], pb[g]);
+  }
 }
 
 // Ring upkeep and prefetch, at block granularity.
@@ -283,35 +326,38 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 
 // Land the in-flight ring segments, in request order.
 template <int K, int MODE>
-__device__ __forceinline__ void land_segments(ChunkState<K>& S, Inflight<K>& F, LDS uint16_t* __restrict__ wring,
+__device__ __forceinline__ void land_segments(ChunkState<K>& S, Inflight<K, MODE>& F, LDS uint16_t* __restrict__ wring,
                                               LDS uint8_t* __restrict__ pring, uint32_t lane) {
+  typedef Geo<K, MODE> G;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
-    if (F.wn[i]) { store_wseg(wring, S.wld, F.w[i], lane); S.wld += kWSeg; F.wn[i] = false; }
+    if (F.wn[i]) { store_wseg<G>(wring, S.wld, F.w[i], lane); S.wld += G::kWSeg; F.wn[i] = false; }
   if (MODE == 2) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      if (F.pn[i]) { store_pseg(pring, S.pld, F.p[i], lane); S.pld += kPSeg; F.pn[i] = false; }
+      if (F.pn[i]) { store_pseg<G>(pring, S.pld, F.p[i], lane); S.pld += G::kPSeg; F.pn[i] = false; }
   }
 }
 
 // Request up to two segments per ring (as many as fit behind the unconsumed
 // and landed data).
 template <int K, int MODE>
-__device__ __forceinline__ void request_segments(const ChunkState<K>& S, Inflight<K>& F, const ChunkParams& C) {
+__device__ __forceinline__ void request_segments(const ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C) {
+  typedef Geo<K, MODE> G;
+  typedef typename G::Seg V;
   const uint32_t lane = C.lane;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const uint32_t at = S.wld + i * kWSeg;
-    F.wn[i] = at < C.n_words && at + kWSeg - S.wptr <= kRing;
-    F.w[i] = load_seg(C.wsrc, F.wn[i] ? at / 8u : 0u, C.wvalid16, lane, C.safe);
+    const uint32_t at = S.wld + i * G::kWSeg;
+    F.wn[i] = at < C.n_words && at + G::kWSeg - S.wptr <= G::kRing;
+    F.w[i] = load_seg<V>(C.wsrc, F.wn[i] ? at / (G::kLaneSeg / 2u) : 0u, C.wvalid, lane, C.safe);
   }
   if (MODE == 2) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t at = S.pld + i * kPSeg;
-      F.pn[i] = at < C.n_plane && at + kPSeg - S.pptr <= kPRing;
-      F.p[i] = load_seg(C.psrc, F.pn[i] ? at / 16u : 0u, C.pvalid16, lane, C.safe);
+      const uint32_t at = S.pld + i * G::kPSeg;
+      F.pn[i] = at < C.n_plane && at + G::kPSeg - S.pptr <= G::kPRing;
+      F.p[i] = load_seg<V>(C.psrc, F.pn[i] ? at / G::kLaneSeg : 0u, C.pvalid, lane, C.safe);
     }
   }
 }
@@ -319,22 +365,24 @@ __device__ __forceinline__ void request_segments(const ChunkState<K>& S, Infligh
 // Make sure the rings hold a block's worst-case demand. Rare: it lands the
 // in-flight segments early (waiting for them) and loads synchronously.
 template <int K, int MODE>
-__device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K>& F, const ChunkParams& C,
+__device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C,
                                        LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring) {
-  constexpr uint32_t kBlkElems = block_steps<K>() * kWave * K;
+  typedef Geo<K, MODE> G;
+  typedef typename G::Seg V;
+  constexpr uint32_t kBlkElems = G::kBlkElems;
   const uint32_t lane = C.lane;
   const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
   const uint32_t need_p = MODE == 2 ? min(kBlkElems, C.n_plane - S.pptr) : 0u;
   if (S.wld - S.wptr < need_w || (MODE == 2 && S.pld - S.pptr < need_p)) {
     land_segments<K, MODE>(S, F, wring, pring, lane);
     while (S.wld - S.wptr < need_w) {
-      store_wseg(wring, S.wld, load_seg(C.wsrc, S.wld / 8u, C.wvalid16, lane, C.safe), lane);
-      S.wld += kWSeg;
+      store_wseg<G>(wring, S.wld, load_seg<V>(C.wsrc, S.wld / (G::kLaneSeg / 2u), C.wvalid, lane, C.safe), lane);
+      S.wld += G::kWSeg;
     }
     if (MODE == 2) {
       while (S.pld - S.pptr < need_p) {
-        store_pseg(pring, S.pld, load_seg(C.psrc, S.pld / 16u, C.pvalid16, lane, C.safe), lane);
-        S.pld += kPSeg;
+        store_pseg<G>(pring, S.pld, load_seg<V>(C.psrc, S.pld / G::kLaneSeg, C.pvalid, lane, C.safe), lane);
+        S.pld += G::kPSeg;
       }
     }
   }
@@ -349,7 +397,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
                                              const LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring,
                                              LDS uint8_t* __restrict__ stage) {
   constexpr uint32_t kStates = kWave * K;
-  constexpr int kBlock = block_steps<K>();
+  constexpr int kBlock = Geo<K, MODE>::kBlock;
   constexpr int kHalf = kBlock / 2;
   constexpr bool FAST = MODE == 1 && EB == 2;
   const uint32_t lane = C.lane;
@@ -359,12 +407,11 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     if (PARTIAL && t >= C.nsteps) break;                 // wave-uniform
     if (q == kHalf) {                                    // first half of the block is staged: store it
       wave_sync();
-      flush_half<K, EB, PARTIAL>(2 * blk, C, stage);
+      flush_half<K, EB, PARTIAL, kHalf>(2 * blk, C, stage);
     }
     const uint32_t qs = q % kHalf;                       // step within the staged half
     uint32_t d[K];
-    uint64_t am[K];
-    rans_step<K, FAST, PARTIAL>(t, S, C, tbl, wring, d, am);
+    rans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
     if (FAST) {
       // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
       const uint64_t pw = pl.b[(q * K) / 8];
@@ -390,25 +437,24 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)v;
       }
     } else {
-#pragma unroll
-      for (int g = 0; g < K; ++g) {
-        uint32_t v = d[g];
-        if (MODE == 2) {
-          const bool cons = ((am[g] >> lane) & 1ull) && (v >> 31);
-          const uint64_t bm = __ballot(cons);
-          const uint32_t b = ((volatile LDS uint8_t*)pring)[(S.pptr + lane_rank(bm)) & (kPRing - 1u)];
-          S.pptr += (uint32_t)__popcll(bm);
-          if (cons) v = byte_merge(v, b);
-        }
-        const uint32_t si = qs * kStates + lane * K + g;  // element index within the staged half
-        if (EB == 2) ((LDS uint16_t*)stage)[si] = (uint16_t)v;
-        else stage[si] = (uint8_t)v;
+      // the lane's K outputs of this step are adjacent: one LDS store
+      LDS uint8_t* dst = stage + (qs * kStates + lane * K) * EB;
+      if (EB == 2) {
+        if (K == 1) *(LDS uint16_t*)dst = (uint16_t)d[0];
+        else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], 0x05040100u);
+        else *(LDS uint64_t*)dst = (uint64_t)__builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u) |
+                                   ((uint64_t)__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u) << 32);
+      } else {
+        if (K == 1) *dst = (uint8_t)d[0];
+        else if (K == 2) *(LDS uint16_t*)dst = (uint16_t)__builtin_amdgcn_perm(d[K - 1], d[0], 0x0C0C0400u);
+        else *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[1 % K], d[0], 0x0C0C0400u) |
+                                   (__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x0C0C0400u) << 16);
       }
     }
   }
   if (!PARTIAL) {
     wave_sync();
-    flush_half<K, EB, PARTIAL>(2 * blk + 1, C, stage);
+    flush_half<K, EB, PARTIAL, kHalf>(2 * blk + 1, C, stage);
   }
 }
 
@@ -421,24 +467,24 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
                                              uint32_t n_plane, GLB uint8_t* __restrict__ out8, uint64_t base,
                                              uint32_t nc, uint32_t nsteps, int32_t* status) {
+  typedef Geo<K, MODE> G;
   constexpr uint32_t kStates = kWave * K;
   ChunkParams C;
   C.lane = __lane_id();
   const uint32_t wbytes = pad16(n_words * 2u);
-  C.wsrc = (const GLB u32x4*)(cbase + 4u * kStates);
-  const GLB uint8_t* psrc8 = cbase + 4u * kStates + wbytes;
-  C.psrc = (const GLB u32x4*)psrc8;
-  C.dplane = psrc8;
-  C.safe = (const GLB u32x4*)cbase;
+  C.wsrc = cbase + 4u * kStates;
+  C.psrc = cbase + 4u * kStates + wbytes;
+  C.dplane = C.psrc;
+  C.safe = cbase;
   C.out8 = out8;
   C.base = base;
   C.n_words = n_words;
   C.n_plane = n_plane;
-  C.wvalid16 = wbytes / 16u;
-  C.pvalid16 = pad16(n_plane) / 16u;
+  C.wvalid = wbytes / G::kLaneSeg;
+  C.pvalid = pad16(n_plane) / G::kLaneSeg;
   C.nc = nc;
   C.nsteps = nsteps;
-  C.nblk = (nsteps + block_steps<K>() - 1) / block_steps<K>();
+  C.nblk = (nsteps + G::kBlock - 1) / G::kBlock;
 
   ChunkState<K> S;
 #pragma unroll
@@ -447,7 +493,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
 
   // First pair's loads; land all of them before the loop so that the loop
   // header's wait-count state holds no load issued here.
-  Inflight<K> F;
+  Inflight<K, MODE> F;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
     F.pl[i] = MODE == 1 ? load_plane<K>(C.dplane, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
@@ -463,7 +509,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     land_segments<K, MODE>(S, F, wring, pring, C.lane);
     refill<K, MODE>(S, F, C, wring, pring);
     wave_sync();
-    if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL>(2 * blk - 1, C, stage);
+    if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk - 1, C, stage);
     request_segments<K, MODE>(S, F, C);
     if (MODE == 1) {
       F.pl[0] = load_plane<K>(C.dplane, min(blk + 2, C.nblk - 1), C.lane);
@@ -475,7 +521,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     // ---- second block of the pair
     refill<K, MODE>(S, F, C, wring, pring);
     wave_sync();
-    if (PARTIAL) flush_half<K, EB, PARTIAL>(2 * blk + 1, C, stage);
+    if (PARTIAL) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk + 1, C, stage);
     decode_block<K, MODE, EB, PARTIAL>(blk + 1, cur1, S, C, tbl, wring, pring, stage);
     blk += 2;
     if (blk >= C.nblk) break;
@@ -494,7 +540,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   // the first if that block has at most half a block of steps
   if (PARTIAL) {
     wave_sync();
-    flush_half<K, EB, PARTIAL>((C.nsteps - 1) / (block_steps<K>() / 2), C, stage);
+    flush_half<K, EB, PARTIAL, G::kBlock / 2>((C.nsteps - 1) / (G::kBlock / 2), C, stage);
   }
   // segments requested but never landed need no wait: nothing reads them
 
@@ -510,12 +556,18 @@ __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint6
                                                   LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
                                                   uint32_t nw, uint32_t np, GLB uint8_t* out, uint64_t base,
                                                   uint32_t nc, uint32_t nsteps, int32_t* status) {
-  if (EB == 1 || mode == 0)
+  if constexpr (EB == 1) {   // byte elements have no plane
     decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
-  else if (mode == 1)
-    decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
-  else if (COMPACT)
-    decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+  } else {
+    if (mode == 0) {
+      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    } else if (mode == 1) {
+      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    } else {
+      if constexpr (COMPACT)
+        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    }
+  }
 }
 
 template <int K, bool COMPACT>
@@ -540,7 +592,6 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
   LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
   LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWaves * kRingBytes);
-  LDS uint8_t* s_pring = (LDS uint8_t*)(smem + kLdsLean);
   // table-build scratch overlaps the staging area (unused until decoding starts)
   LDS uint32_t* s_cum = (LDS uint32_t*)s_stage;        // 257 entries
   LDS uint32_t* s_val = s_cum + 260;                    // 256 entries
@@ -655,7 +706,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   }
   const GLB uint8_t* cbase = b + off;
   LDS uint16_t* wring = (LDS uint16_t*)(s_wring + wave * kRingBytes);
-  LDS uint8_t* pring = s_pring + wave * kPRing;
+  LDS uint8_t* pring = s_wring + wave * kRingBytes + Geo<1, 2>::kPRingOff;   // compact chunks only
   LDS uint8_t* stage = s_stage + wave * kStageMax;
   GLB uint8_t* out = (GLB uint8_t*)T.out;
   const bool partial = nc != per;
@@ -672,8 +723,8 @@ inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) /
 bool g_attr_set = false;
 void ensure_lds_attr() {
   if (g_attr_set) return;
-  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLean);
-  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCompact);
+  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   g_attr_set = true;
 }
 
@@ -681,10 +732,10 @@ int launch(const bs_chunk_task* tasks, uint32_t n_tasks, const bs_chunk_task& si
            uint32_t max_mode, int32_t* status, void* stream) {
   ensure_lds_attr();
   if (max_mode >= 2)
-    hipLaunchKernelGGL(bsck_decode_kernel<true>, dim3(groups), dim3(kThreads), kLdsCompact, (hipStream_t)stream,
+    hipLaunchKernelGGL(bsck_decode_kernel<true>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
                        tasks, n_tasks, single, status);
   else
-    hipLaunchKernelGGL(bsck_decode_kernel<false>, dim3(groups), dim3(kThreads), kLdsLean, (hipStream_t)stream,
+    hipLaunchKernelGGL(bsck_decode_kernel<false>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
                        tasks, n_tasks, single, status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }

@@ -113,6 +113,42 @@ def test_batched_launch_matches_single(torch_gpu):
             assert np.array_equal(o.cpu().numpy().view(np.uint16), w), f"rep {rep}"
 
 
+def test_batched_launch_mixing_every_plane_mode(torch_gpu):
+    """One launch holding compact (mode 2), dense (1) and exact (0) bf16 blobs
+    and an fp8 blob, at every lane count, with partial last chunks: the
+    compact launch decodes every mode with its own ring geometry."""
+    import torch
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
+    rng = np.random.default_rng(15)
+    cases = []
+    for i, lanes in enumerate((64, 128, 256)):
+        half = _bf16(rng.standard_normal(300_001 + 77 * i) * 0.02)
+        half[rng.permutation(half.size)[: half.size // 2]] = 0
+        cases.append((half, 2, lanes))
+        cases.append((_bf16(rng.standard_normal(200_003) * 0.02), 1, lanes))
+        cases.append((_bf16(1.0 + rng.standard_normal(70_001) * 0.01), 0, lanes))
+        cases.append((rng.integers(0, 256, 150_007).astype(np.uint8), 0, lanes))
+    blobs = [bc.encode_array(w, steps=64, mode=m, lanes=ln) for w, m, ln in cases]
+    assert [bc.info(b).plane_mode for b in blobs] == [m for _, m, _ in cases]
+    _say(f"[bsck] mixed-mode batch of {len(blobs)} blobs")
+    dev = torch.device("cuda")
+    d = [upload_bytes(b, dev) for b in blobs]
+    outs = [torch.empty(w.nbytes, dtype=torch.uint8, device=dev) for w, _, _ in cases]
+    jobs = [ChunkJob(db.data_ptr(), len(b), o.data_ptr(), w.size, bc.info(b).n_chunks, bc.info(b).plane_mode)
+            for db, b, o, (w, _, _) in zip(d, blobs, outs, cases)]
+    st = StatusWord(dev)
+    batch = ChunkBatch(jobs, dev)
+    for rep in range(2):
+        for o in outs:
+            o.fill_(0)
+        batch.launch(st)
+        torch.cuda.synchronize()
+        st.check()
+        for o, (w, m, ln) in zip(outs, cases):
+            assert o.cpu().numpy().tobytes() == w.tobytes(), f"rep {rep} mode {m} lanes {ln} n {w.size}"
+
+
 def test_corrupt_stream_is_reported(torch_gpu):
     import torch
     from bigsmall_amd.codecs import bf16_chunked as bc
