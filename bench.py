@@ -67,6 +67,19 @@ def make_layer(seed: int = 0):
     return out
 
 
+def zero_layer(words: dict, fraction: float, seed: int = 1) -> dict:
+    """The layer with a seeded Bernoulli(fraction) share of every matrix's
+    elements set to +0.0 (a pruned model's layer); norms untouched."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, w in words.items():
+        if "norm" not in name:
+            w = w.copy()
+            w[rng.random(w.size) < fraction] = 0
+        out[name] = w
+    return out
+
+
 def cpu_baseline(words: dict, budget_s: float = 12.0):
     """Oracle port of bf16_se_single_kernel decode (bigsmall/codecs/single_kernel.py:431-580)
     on the layer's seven matrices: all of them at once, one host thread per tensor
@@ -497,6 +510,9 @@ def main():
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--zero-fraction", type=float, default=0.0,
+                    help="layer workload only: set this seeded share of every matrix's elements to +0.0 "
+                         "(a pruned layer; such tensors take the compact plane mode)")
     ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3"], default="layer",
                     help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache "
                          "blocks), refcodecs (the reference's own formats on the C0 tensor), c3 (stress "
@@ -524,6 +540,10 @@ def main():
     lanes = args.lanes or bc.DEFAULT_LANES
     t0 = time.time()
     words = make_layer(0)
+    workload = WORKLOAD
+    if args.zero_fraction:
+        words = zero_layer(words, args.zero_fraction)
+        workload = f"{WORKLOAD}_{round(100 * args.zero_fraction)}pct_zeros"
     log(f"[bench] layer generated in {time.time() - t0:.1f}s")
     t0 = time.time()
     blobs = {name: bc.encode_array(w, steps=steps, lanes=lanes) for name, w in words.items()}
@@ -591,9 +611,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u32",
-        "data": "synthetic (seeded torch N(0,0.02) weights, 1+N(0,0.01) norms), encoded by the engine",
+        "data": "synthetic (seeded torch N(0,0.02) weights, 1+N(0,0.01) norms"
+                + (f", {args.zero_fraction:g} of matrix elements zeroed" if args.zero_fraction else "")
+                + "), encoded by the engine",
         "config": {
-            "workload": WORKLOAD,
+            "workload": workload,
             "tensors": len(LAYER), "elements": n_total, "decoded_bytes": out_total,
             "compressed_bytes": comp_total, "ratio_pct": round(100 * comp_total / out_total, 3),
             "codec": bc.CODEC_BF16, "chunk_steps": steps, "chunk_lanes": lanes, "launches_per_step": 1,
@@ -601,7 +623,7 @@ def main():
         "ms_per_layer": round(ms_per, 5),
         "decoded_output_GBps": round(out_total / (ms_per * 1e-3) / 1e9, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(WORKLOAD),
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(workload),
                      "device_copy_GBps": round(copy_gbps, 1), "frac_of_device_copy": round(gbps / copy_gbps, 4)},
         "cpu_baseline": cpu,
     }
