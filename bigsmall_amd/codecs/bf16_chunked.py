@@ -14,6 +14,7 @@ Decoding runs only on the GPU.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -71,8 +72,10 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
     states per chunk); the blobs equal encode_array(words, steps, MODE_DENSE).
 
     Returns (arena, [(offset, length), ...]): every blob lives in one device
-    uint8 tensor at a 256-byte aligned offset. With compact=False the arena
-    keeps each blob's worst-case slot (no copy after encoding)."""
+    uint8 tensor. With compact=True the blobs are packed back to back (every
+    blob length is a multiple of 16, so each stays 16-byte aligned); with
+    compact=False each keeps its worst-case slot at a 256-byte aligned offset
+    (no copy after encoding)."""
     import torch
     if not tensors:
         return None, []
@@ -80,6 +83,7 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
     L = _native.lib()
     per = GPU_ENCODE_LANES * steps
     srcs, slots, cap_total = [], [], 0
+    bounds: dict[int, int] = {}
     for t in tensors:
         if t.dtype != torch.bfloat16 or t.device != dev:
             raise ValueError("encode_device expects bf16 tensors on one GPU")
@@ -87,12 +91,14 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
         if t.data_ptr() % 4:
             t = t.clone()
         n = t.numel()
-        bound = ctypes.c_uint64()
-        _native.check(L.bs_chunk_encode_bound(max(n, 1), 2, GPU_ENCODE_LANES, steps, ctypes.byref(bound)),
-                      "bs_chunk_encode_bound")
+        if n not in bounds:
+            bound = ctypes.c_uint64()
+            _native.check(L.bs_chunk_encode_bound(max(n, 1), 2, GPU_ENCODE_LANES, steps, ctypes.byref(bound)),
+                          "bs_chunk_encode_bound")
+            bounds[n] = int(bound.value)
         srcs.append(t)
-        slots.append((cap_total, int(bound.value)))
-        cap_total += (int(bound.value) + 255) & ~255
+        slots.append((cap_total, bounds[n]))
+        cap_total += (bounds[n] + 255) & ~255
     arena = torch.empty(max(cap_total, 256), dtype=torch.uint8, device=dev)
     live = [i for i, t in enumerate(srcs) if t.numel() > 0]
     tasks = np.zeros(len(live), ENCODE_TASK_DTYPE)
@@ -121,12 +127,15 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
         return arena, [(slots[i][0], lens[i]) for i in range(len(srcs))]
     offs, pos = [], 0
     for ln in lens:
+        if ln % 16:
+            raise RuntimeError(f"GPU encoder returned a blob length {ln} that is not a multiple of 16")
         offs.append(pos)
-        pos += (ln + 255) & ~255
-    tight = torch.empty(max(pos, 256), dtype=torch.uint8, device=dev)
-    for i, ln in enumerate(lens):
-        if ln:
-            tight[offs[i]:offs[i] + ln].copy_(arena[slots[i][0]:slots[i][0] + ln])
+        pos += ln
+    parts = [arena[slots[i][0]:slots[i][0] + ln] for i, ln in enumerate(lens) if ln]
+    if not parts:
+        return torch.empty(256, dtype=torch.uint8, device=dev), list(zip(offs, lens))
+    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+        tight = torch.cat(parts)          # one batched copy kernel, not one copy per blob
     return tight, list(zip(offs, lens))
 
 
