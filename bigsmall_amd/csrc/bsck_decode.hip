@@ -34,11 +34,13 @@
 // A valid chunk ends with every state back at x == L and every word and plane
 // byte consumed; anything else is reported as BS_DEV_ERR_STREAM.
 //
-// Two decode-table layouts live in LDS (4096 slots x 8 bytes):
+// Three decode-table layouts live in LDS (4096 slots x 8 bytes):
 //   dense bf16 (plane_mode 1): {f | exponent << 24, slot - cf}; the update is
 //     one shift and one v_mad_u32_u24 (which ignores bits 24..31 of f's word),
 //     and the exponent byte is placed with v_perm;
-//   generic (plane modes 0/2, bytes): {f | (slot - cf) << 13, value | consume << 31}.
+//   bytes (elem_bytes 1): {f | value << 24, slot - cf}, the same update, the
+//     output byte taken from bits 24..31 with v_perm;
+//   generic (bf16 plane modes 0/2): {f | (slot - cf) << 13, value | consume << 31}.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -261,8 +263,9 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
 // One step of the K states of every lane. Phased so the K dependency chains of
 // a lane overlap: K table reads, then the K state updates with their ballots,
 // then the K ring reads (one wait for all), then the renormalisations.
-// FAST = dense bf16 table layout (d = the table word holding the exponent);
-// otherwise d = value | consume << 31, and for MODE 2 the compact-plane byte
+// FAST = dense bf16 or byte table layout (d = the table word holding the
+// exponent or byte in bits 24..31); otherwise d = value | consume << 31, and
+// for MODE 2 the compact-plane byte
 // of each consuming element is read beside the renorm words (same wait) and
 // merged into d.
 template <int K, int MODE, bool FAST, bool PARTIAL>
@@ -281,7 +284,7 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
     const uint32_t lo = (uint32_t)e[g], hi = (uint32_t)(e[g] >> 32);
     if (FAST) {
       xn[g] = __umul24(lo, S.x[g] >> 12) + hi;             // v_mad_u32_u24: f = bits 0..23 of lo
-      d[g] = lo;                                           // exponent in byte 3
+      d[g] = lo;                                           // exponent or byte value in byte 3
     } else {
       xn[g] = __umul24(lo & 0x1FFFu, S.x[g] >> 12) + (lo >> 13);
       d[g] = hi;                                           // value | consume << 31
@@ -399,7 +402,8 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
   constexpr uint32_t kStates = kWave * K;
   constexpr int kBlock = Geo<K, MODE>::kBlock;
   constexpr int kHalf = kBlock / 2;
-  constexpr bool FAST = MODE == 1 && EB == 2;
+  constexpr bool DENSE = MODE == 1 && EB == 2;
+  constexpr bool FAST = DENSE || EB == 1;               // mad24 table layouts
   const uint32_t lane = C.lane;
 #pragma unroll
   for (int q = 0; q < kBlock; ++q) {
@@ -412,7 +416,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     const uint32_t qs = q % kHalf;                       // step within the staged half
     uint32_t d[K];
     rans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
-    if (FAST) {
+    if (DENSE) {
       // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
       const uint64_t pw = pl.b[(q * K) / 8];
       const uint32_t o = (q * K) % 8;                    // byte offset in pw
@@ -444,11 +448,11 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], 0x05040100u);
         else *(LDS uint64_t*)dst = (uint64_t)__builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u) |
                                    ((uint64_t)__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u) << 32);
-      } else {
-        if (K == 1) *dst = (uint8_t)d[0];
-        else if (K == 2) *(LDS uint16_t*)dst = (uint16_t)__builtin_amdgcn_perm(d[K - 1], d[0], 0x0C0C0400u);
-        else *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[1 % K], d[0], 0x0C0C0400u) |
-                                   (__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x0C0C0400u) << 16);
+      } else {                                           // byte values in bits 24..31 of d
+        if (K == 1) *dst = (uint8_t)(d[0] >> 24);
+        else if (K == 2) *(LDS uint16_t*)dst = (uint16_t)__builtin_amdgcn_perm(d[K - 1], d[0], 0x0C0C0703u);
+        else *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[1 % K], d[0], 0x0C0C0703u) |
+                                   (__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x0C0C0703u) << 16);
       }
     }
   }
@@ -677,8 +681,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     for (uint32_t k = 0; k < kRun && slot < 4096u; ++k, ++slot) {
       while (s_cum[lo + 1] <= slot) ++lo;
       const uint32_t c0 = s_cum[lo], f = s_cum[lo + 1] - c0, val = s_val[lo];
-      s_tbl[slot] = fast ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
-                         : ((uint64_t)(f | ((slot - c0) << 13)) | ((uint64_t)val << 32));
+      s_tbl[slot] = fast    ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
+                    : eb == 1 ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
+                              : ((uint64_t)(f | ((slot - c0) << 13)) | ((uint64_t)val << 32));
     }
   }
   __syncthreads();
