@@ -316,7 +316,19 @@ def run_kv(args) -> dict:
     raw_kv = 32 * 2 * k0.numel() * 2
     log(f"[kv] GPU-encoded 32 layers in {enc_s * 1e3:.1f} ms ({raw_kv / enc_s / 1e9:.1f} GB/s raw), "
         f"ratio {cache.compression_ratio():.4f}")
-    del dev_kv
+    # the path without the GPU encoder, for comparison: device K/V copied to the
+    # host and encoded by the multithreaded C++ encoder (two layers)
+    from bigsmall_amd.codecs.bf16_chunked import _threads as bc_threads
+    host_cache = CompressedKVCache(device="cuda")
+    t0 = time.perf_counter()
+    for layer in range(2):
+        host_cache.set_blocks(layer, dev_kv[layer][0].cpu(), dev_kv[layer][1].cpu(), block_tokens=256)
+    torch.cuda.synchronize()
+    host_s = (time.perf_counter() - t0) / 2
+    raw_layer = 2 * k0.numel() * 2
+    log(f"[kv] host path (D2H + C++ encode + upload): {host_s * 1e3:.1f} ms per layer "
+        f"({raw_layer / host_s / 1e9:.2f} GB/s raw)")
+    del dev_kv, host_cache
     rng = np.random.default_rng(3)
     req = [(layer, rng.choice(128, 64, replace=False)) for layer in range(32)]
     batch, outs = cache.prepare_blocks_multi(req)
@@ -346,7 +358,11 @@ def run_kv(args) -> dict:
             "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4)},
             "gpu_encode": {"seconds_32_layers": round(enc_s, 4), "raw_GBps": round(raw_kv / enc_s / 1e9, 2),
-                           "note": "CompressedKVCache.set_blocks on device K/V, incl. arena compaction"}}
+                           "note": "CompressedKVCache.set_blocks on device K/V, incl. block-major copies and "
+                                   "blob packing"},
+            "host_path_encode": {"seconds_per_layer": round(host_s, 4), "raw_GBps": round(raw_layer / host_s / 1e9, 3),
+                                 "threads": bc_threads(),
+                                 "note": "set_blocks on host copies of the device K/V (D2H + C++ encoder + upload)"}}
 
 
 def cpu_baseline_refcodecs(words: np.ndarray) -> dict:
