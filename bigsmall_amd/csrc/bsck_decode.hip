@@ -45,6 +45,7 @@
 #include <stdint.h>
 
 #include "../../include/bigsmall_hip.h"
+#include "lds_limit.h"
 
 namespace {
 
@@ -725,23 +726,19 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
 
-bool g_attr_set = false;
-void ensure_lds_attr() {
-  if (g_attr_set) return;
-  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  (void)hipFuncSetAttribute((const void*)bsck_decode_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  g_attr_set = true;
-}
+std::atomic<uint64_t> g_lds_plain{0}, g_lds_compact{0};   // devices configured, one bit each
 
 int launch(const bs_chunk_task* tasks, uint32_t n_tasks, const bs_chunk_task& single, uint32_t groups,
            uint32_t max_mode, int32_t* status, void* stream) {
-  ensure_lds_attr();
-  if (max_mode >= 2)
+  if (max_mode >= 2) {
+    bs_internal::ensure_lds_limit((const void*)bsck_decode_kernel<true>, kLds, g_lds_compact);
     hipLaunchKernelGGL(bsck_decode_kernel<true>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
                        tasks, n_tasks, single, status);
-  else
+  } else {
+    bs_internal::ensure_lds_limit((const void*)bsck_decode_kernel<false>, kLds, g_lds_plain);
     hipLaunchKernelGGL(bsck_decode_kernel<false>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
                        tasks, n_tasks, single, status);
+  }
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 

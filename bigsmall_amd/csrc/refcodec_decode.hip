@@ -28,6 +28,7 @@
 #include <stdint.h>
 
 #include "../../include/bigsmall_hip.h"
+#include "lds_limit.h"
 
 namespace {
 
@@ -397,11 +398,8 @@ int bs_refcodec_decode(const bs_se_stream* d_streams, uint32_t n_streams, const 
   if (n_out == 0 || n_streams == 0) return BS_OK;
   hipStream_t s = (hipStream_t)stream;
   constexpr uint32_t kSeLds = 4096 * 8 + 256 * kSeLanes * 4;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)se_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSeLds);
-    attr = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  bs_internal::ensure_lds_limit((const void*)se_kernel, kSeLds, lds_set);
   hipLaunchKernelGGL(se_kernel, dim3((n_streams + kSeLanes - 1) / kSeLanes), dim3(kSeLanes), kSeLds, s, d_streams,
                      n_streams, d_se_table, d_bstart, n_out, d_out, d_perm, d_status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
@@ -435,11 +433,8 @@ int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams,
   const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
   const uint32_t tps = (uint32_t)((max_len + kTile - 1) / kTile);
   constexpr uint32_t kSerLds = kRingB + 4096 * 8;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)serial_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kSerLds);
-    attr = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, lds_set);
   hipLaunchKernelGGL(serial_kernel, dim3(n_streams + n_buckets), dim3(kWave), kSerLds, s, d_streams, n_streams,
                      tps * kTile, d_se_table, d_buckets, d_mant_tables, n_tables, d_out, n_out, mant, d_status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;

@@ -91,8 +91,10 @@ int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uin
                     uint32_t n_chunks, uint32_t plane_mode, int32_t *d_status, void *stream);
 
 /* Decode many BSCK blobs (a transformer layer, a batch of KV blocks) in one
- * launch; `max_plane_mode` is the largest plane_mode among the tasks (mode 2
- * launches reserve extra LDS for the compact-plane rings). Replaces the per-tensor `_decode_blob` loop of decoder.decompress
+ * launch; `max_plane_mode` is the largest plane_mode among the tasks (a launch
+ * without mode-2 tasks uses a kernel built without the compact-plane path;
+ * both use the same LDS and occupancy). Replaces the per-tensor `_decode_blob`
+ * loop of decoder.decompress
  * (bigsmall/decoder.py:128-136) and StreamingLoader.load_layer
  * (bigsmall/streaming.py:218-227). */
 int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32_t total_groups,

@@ -149,6 +149,38 @@ def test_batched_launch_mixing_every_plane_mode(torch_gpu):
             assert o.cpu().numpy().tobytes() == w.tobytes(), f"rep {rep} mode {m} lanes {ln} n {w.size}"
 
 
+def test_concurrent_host_threads_on_their_own_streams(torch_gpu):
+    """The C-ABI keeps no per-call global state: four host threads decode
+    different blobs (BSCK dense, BSCK compact, a partial-chunk BSCK blob and the
+    reference's bf16_parallel_v1) at once, each on its own stream, three rounds
+    each, every result bit-exact."""
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    rng = np.random.default_rng(16)
+    dense = _bf16(rng.standard_normal(600_001) * 0.02)
+    half = dense.copy()
+    half[rng.permutation(half.size)[: half.size // 2]] = 0
+    cases = [("bsck", bc.encode_array(dense, mode=1), dense),
+             ("bsck", bc.encode_array(half, mode=2), half),
+             ("bsck", bc.encode_array(dense[:77_777]), dense[:77_777]),
+             ("par1", oracle.par1_encode(dense[:300_000]), dense[:300_000])]
+    _say("[bsck] 4 host threads, one stream each")
+
+    def work(i):
+        kind, blob, w = cases[i]
+        with torch.cuda.stream(torch.cuda.Stream()):
+            for _ in range(3):
+                got = (bc.decode(blob, {}, w.size) if kind == "bsck"
+                       else _refstreams.decode_host("bf16_parallel_v1", blob, w.size))
+                assert got == w.tobytes(), (i, kind)
+        return i
+
+    with ThreadPoolExecutor(4) as ex:
+        assert sorted(ex.map(work, range(4))) == [0, 1, 2, 3]
+
+
 def test_corrupt_stream_is_reported(torch_gpu):
     import torch
     from bigsmall_amd.codecs import bf16_chunked as bc
