@@ -131,11 +131,14 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
             raise RuntimeError(f"GPU encoder returned a blob length {ln} that is not a multiple of 16")
         offs.append(pos)
         pos += ln
-    parts = [arena[slots[i][0]:slots[i][0] + ln] for i, ln in enumerate(lens) if ln]
+    # slots start at multiples of 256 and lengths are multiples of 16: copy as
+    # 8-byte words, in one batched kernel rather than one copy per blob
+    words = arena.view(torch.int64)
+    parts = [words[slots[i][0] // 8:(slots[i][0] + ln) // 8] for i, ln in enumerate(lens) if ln]
     if not parts:
         return torch.empty(256, dtype=torch.uint8, device=dev), list(zip(offs, lens))
     with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
-        tight = torch.cat(parts)          # one batched copy kernel, not one copy per blob
+        tight = torch.cat(parts).view(torch.uint8)
     return tight, list(zip(offs, lens))
 
 

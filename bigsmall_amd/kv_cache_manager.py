@@ -28,6 +28,17 @@ from .codecs import bf16_chunked
 from .codecs import kv_cache as _kv_codec
 
 
+def _block_major(blocked, td: int):
+    """blocked.movedim(td, 0).contiguous(): the block index first, every block
+    contiguous. Copied as 8-byte words when the innermost dimension allows it
+    (the same bytes in a quarter of the elements)."""
+    import torch
+    if (blocked.is_contiguous() and blocked.element_size() == 2 and blocked.shape[-1] % 4 == 0
+            and blocked.storage_offset() % 4 == 0 and blocked.data_ptr() % 8 == 0):
+        return blocked.view(torch.int64).movedim(td, 0).contiguous().view(blocked.dtype)
+    return blocked.movedim(td, 0).contiguous()
+
+
 @dataclass
 class _LayerBlocks:
     """Compressed blocks of one layer: one device arena, per-block offsets."""
@@ -114,7 +125,7 @@ class CompressedKVCache:
             for t in (keys, values):
                 shape = list(t.shape)
                 blocked = t.detach().reshape(shape[:td] + [nb, block_tokens] + shape[td + 1:])
-                blocked = blocked.movedim(td, 0).contiguous()
+                blocked = _block_major(blocked, td)
                 parts += [blocked[i] for i in range(nb)]
             arena, spans = bf16_chunked.encode_device(parts, steps=_kv_codec.KV_STEPS)
             per = bf16_chunked.GPU_ENCODE_LANES * _kv_codec.KV_STEPS

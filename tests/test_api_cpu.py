@@ -139,6 +139,19 @@ def test_kv_entry_framing():
             kv_cache.parse_kv_entry(bytes([ver]) + data[1:])
 
 
+@pytest.mark.parametrize("shape,td,bt", [((8, 1024, 128), 1, 256), ((2, 8, 512, 64), 2, 128),
+                                         ((8, 128, 1024), 2, 256), ((3, 1024, 6), 1, 256)])
+def test_block_major_copy_matches_movedim(shape, td, bt):
+    """The KV block split (copied as 8-byte words where the innermost
+    dimension allows) gives exactly movedim(token-block dim, 0).contiguous()."""
+    from bigsmall_amd.kv_cache_manager import _block_major
+    t = torch.randn(shape, generator=torch.Generator().manual_seed(len(shape))).bfloat16()
+    b = t.reshape(list(shape[:td]) + [shape[td] // bt, bt] + list(shape[td + 1:]))
+    got, want = _block_major(b, td), b.movedim(td, 0).contiguous()
+    assert got.dtype == want.dtype and got.shape == want.shape
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def test_streaming_index_without_gpu(container_file, tmp_path):
     p, src = container_file
     with StreamingLoader(p) as L:
