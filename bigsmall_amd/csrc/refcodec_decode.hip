@@ -143,8 +143,11 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
 // lane computes the same state; the compiler keeps it in scalar registers),
 // the decode table sits in LDS, and the lanes cooperate on everything around
 // it: they load the word stream 1 KB at a time into an LDS byte ring one
-// segment ahead of use, and they stage 64 consecutive outputs (lane j keeps
-// step j) for one coalesced store. The SE chain writes sign<<15 | exp<<7 of
+// segment ahead of use, hold a 128-word window of it in two registers (lane
+// l: words base + l and base + 64 + l, moved on at most once per 64 steps) so
+// that a renormalisation takes its word with a readlane and no branch, and
+// they stage 64 consecutive outputs (lane j keeps step j) for one coalesced
+// store. The SE chain writes sign<<15 | exp<<7 of
 // every element; the mantissa chains, which do not depend on it, run at the
 // same time in other workgroups and write their bucket's mantissas in bucket
 // order. Three parallel passes then give every element its position in its
@@ -183,22 +186,28 @@ __device__ __forceinline__ void seg_land(LDS uint8_t* ring, uint64_t q, uint32_t
   *(LDS u32x4*)(ring + ((q * kSegB + lane * 16u) & (kRingB - 1u))) = v;
 }
 
-// Decode one chain of n symbols. SE: M = 4096, LDS table of u64
-// {f | (slot-cf) << 13, output word sign<<15 | exp<<7}, output u16. Otherwise
-// (mantissa): M = 1024, LDS table of u32 {f | (slot-cf) << 11 | symbol << 21},
-// output one byte per symbol.
+// Decode one chain of n symbols. The LDS table has one 16-byte entry per slot,
+// {f, slot - cf, output, 0} (SE: M = 4096, output the word sign<<15 | exp<<7,
+// stored as u16; mantissa: M = 1024, output one byte per symbol), so a step is
+// one table read and one v_mad_u32_u24 on the state, which every lane holds.
+// One wavefront issues about one instruction per four cycles, so the step is
+// kept to a dozen instructions: the renormalisation is a scalar branch on the
+// state, its word comes from a register window by readlane, and the output is
+// staged with a lane select.
 //
 // Renormalisation: the reference loops `while x < L and words remain`. From a
 // state x >= L one decode step leaves x >= 2^4 (SE) or 2^6 (mantissa), so one
 // shifted-in word restores x >= L: a valid stream never takes the loop twice,
 // and an initial state below L, which no encoder writes, is reported as a
-// corrupt stream. A corrupt stream that runs out of words keeps reading (from
-// the ring, in bounds) and fails the end-of-stream check.
+// corrupt stream. A corrupt stream that runs out of words shifts in its tail
+// word (zero when it has none) and fails the end-of-stream check.
 template <bool SE>
 __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
-                                             uint32_t n, const LDS uint8_t* __restrict__ tbl,
+                                             uint32_t n, const LDS u32x4* __restrict__ tbl,
                                              LDS uint8_t* __restrict__ ring, GLB uint8_t* __restrict__ out,
                                              uint32_t stride, int32_t* status) {
+  constexpr uint32_t kSlotMask = SE ? 4095u : 1023u;
+  constexpr uint32_t kShift = SE ? 12u : 10u;
   const uint32_t lane = __lane_id();
   const uint64_t wa = (uint64_t)words;
   const GLB uint8_t* A = (const GLB uint8_t*)(wa & ~15ull);
@@ -210,20 +219,47 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   bool inflight = false;      // segment `landed / kSegB` is being loaded into `seg`
   u32x4 seg = {0u, 0u, 0u, 0u};
   uint32_t x = x0, pos = 0;
+  // Word window: lane l of w_lo / w_hi holds word base + l / base + 64 + l.
+  // At a batch start pos - base < 64, so the batch's at most 64 words are in it.
+  uint32_t base = 0, w_lo = 0, w_hi = 0;
   uint32_t keep = 0;
   if (x0 < kL) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
     return;
   }
+  auto ring_word = [&](uint32_t idx) {
+    const uint32_t b = s_off + 2u * idx;
+    return (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
+  };
+  // The state stays in a vector register (the empty asm hides its uniformity,
+  // which would otherwise move the update to scalar instructions plus two
+  // readfirstlanes); only the renormalisation test reads it back.
+  asm volatile("" : "+v"(x));
+  auto step = [&](uint32_t j) {
+    const u32x4 e = tbl[x & kSlotMask];
+    uint32_t xn = __umul24(e.x, x >> kShift) + e.y;         // v_mad_u32_u24 (f <= 4096)
+    if (__builtin_amdgcn_readfirstlane(xn) < kL) {         // uniform: a scalar branch
+      const uint32_t d = pos - base;                       // < 128
+      const uint32_t w_a = __builtin_amdgcn_readlane(w_lo, d & 63u);
+      const uint32_t w_b = __builtin_amdgcn_readlane(w_hi, d & 63u);
+      uint32_t w = d < (uint32_t)kWave ? w_a : w_b;
+      w = pos < n_words ? w : tail_word;
+      xn = (xn << 16) | w;
+      ++pos;
+    }
+    x = xn;
+    asm volatile("" : "+v"(x));
+    keep = lane == j ? e.z : keep;
+  };
   for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
-    // ring upkeep: the next 64 steps read at most 64 words (128 bytes)
+    // ring upkeep: the window reaches at most 128 words (256 bytes) past pos
     const uint64_t consumed = s_off + 2ull * pos;
     if (inflight) {
       seg_land(ring, landed / kSegB, lane, seg);
       landed += kSegB;
       inflight = false;
     }
-    while (landed < e_off && landed < consumed + 2u * kWave + 2u) {
+    while (landed < e_off && landed < consumed + 4u * kWave + 2u) {
       seg_land(ring, landed / kSegB, lane, seg_block(A, landed / kSegB, lane, s_off, e_off));
       landed += kSegB;
     }
@@ -232,37 +268,27 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
       inflight = true;
     }
     wave_sync();
+    if (i0 == 0) {
+      w_lo = ring_word(lane);
+      w_hi = ring_word(kWave + lane);
+    } else if (pos - base >= (uint32_t)kWave) {           // one move keeps pos - base < 64
+      base += kWave;
+      w_lo = w_hi;
+      w_hi = ring_word(base + kWave + lane);
+    }
     const uint32_t cnt = min((uint32_t)kWave, n - i0);
-    for (uint32_t j = 0; j < cnt; ++j) {
-      uint32_t v;
-      if (SE) {
-        const uint64_t ent = ((const LDS uint64_t*)tbl)[x & 4095u];
-        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)ent);
-        v = __builtin_amdgcn_readfirstlane((uint32_t)(ent >> 32));
-        x = (lo & 0x1FFFu) * (x >> 12) + (lo >> 13);
-      } else {
-        const uint32_t ent = __builtin_amdgcn_readfirstlane(((const LDS uint32_t*)tbl)[x & 1023u]);
-        x = (ent & 0x7FFu) * (x >> 10) + ((ent >> 11) & 0x3FFu);
-        v = (ent >> 21) & 0x7Fu;
-      }
-      if (x < kL) {
-        uint32_t w = tail_word;
-        if (pos < n_words) {
-          const uint32_t b = s_off + 2u * pos;
-          w = (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
-          w = __builtin_amdgcn_readfirstlane(w);
-        }
-        x = (x << 16) | w;
-        ++pos;
-      }
-      keep = lane == j ? v : keep;
+    if (cnt == (uint32_t)kWave) {
+#pragma unroll
+      for (uint32_t j = 0; j < (uint32_t)kWave; ++j) step(j);
+    } else {
+      for (uint32_t j = 0; j < cnt; ++j) step(j);
     }
     if (lane < cnt) {
       if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)keep;
       else out[i0 + lane] = (uint8_t)keep;
     }
   }
-  if (x != kL || pos != n_eff) {
+  if (__builtin_amdgcn_readfirstlane(x) != kL || pos != n_eff) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
   }
 }
@@ -278,7 +304,7 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
                                                        uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   LDS uint8_t* ring = (LDS uint8_t*)smem;
-  LDS uint8_t* tbl = (LDS uint8_t*)(smem + kRingB);
+  LDS u32x4* tbl = (LDS u32x4*)(smem + kRingB);      // {f, slot - cf, output, 0} per slot
   const uint32_t lane = threadIdx.x;
   if (blockIdx.x < n_streams) {
     const bs_se_stream S = se[blockIdx.x];
@@ -287,9 +313,9 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
       return;
     }
     for (uint32_t i = lane; i < 4096; i += kWave) {
-      const uint32_t sym = se_table[2 * i + 1];
+      const uint32_t lo = se_table[2 * i], sym = se_table[2 * i + 1];
       const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
-      ((LDS uint64_t*)tbl)[i] = (uint64_t)se_table[2 * i] | ((uint64_t)word << 32);
+      tbl[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
     }
     wave_sync();
     serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring,
@@ -301,7 +327,10 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
       return;
     }
     const GLB uint32_t* t = (const GLB uint32_t*)mant_tables + (uint64_t)B.table * 1024u;
-    for (uint32_t i = lane; i < 1024; i += kWave) ((LDS uint32_t*)tbl)[i] = t[i];
+    for (uint32_t i = lane; i < 1024; i += kWave) {
+      const uint32_t e = t[i];
+      tbl[i] = u32x4{e & 0x7FFu, (e >> 11) & 0x3FFu, (e >> 21) & 0x7Fu, 0u};
+    }
     wave_sync();
     serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring,
                         (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
@@ -432,7 +461,7 @@ int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams,
   uint32_t* hist = (uint32_t*)(mant + ((n_out + 255) & ~255ull));
   const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
   const uint32_t tps = (uint32_t)((max_len + kTile - 1) / kTile);
-  constexpr uint32_t kSerLds = kRingB + 4096 * 8;
+  constexpr uint32_t kSerLds = kRingB + 4096 * 16;
   static std::atomic<uint64_t> lds_set{0};
   bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, lds_set);
   hipLaunchKernelGGL(serial_kernel, dim3(n_streams + n_buckets), dim3(kWave), kSerLds, s, d_streams, n_streams,
