@@ -80,6 +80,24 @@ def zero_layer(words: dict, fraction: float, seed: int = 1) -> dict:
     return out
 
 
+def host_cpu_info() -> dict:
+    """The host CPU model and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "host_cpus": usable}
+
+
 def cpu_baseline(words: dict, budget_s: float = 12.0):
     """Oracle port of bf16_se_single_kernel decode (bigsmall/codecs/single_kernel.py:431-580)
     on the layer's seven matrices: all of them at once, one host thread per tensor
@@ -119,6 +137,8 @@ def cpu_baseline(words: dict, budget_s: float = 12.0):
         "single_thread": {"value": decoded / t_total / 1e9, "cores": 1,
                           "sample": f"{len(names)} tensors ({', '.join(names)}): "
                                     f"{decoded / 1e6:.0f} MB algorithmic in {t_total:.2f} s"},
+        "host": host_cpu_info(),
+        "note": "one serial sign+exponent chain per tensor, so at most one thread per tensor",
     }
 
 
@@ -418,7 +438,7 @@ def run_refcodecs(args) -> dict:
             "value": res["bf16_parallel_v1"]["GBps"], "unit": "GB/s", "n_gpus": 1,
             "ms_per_step": res["bf16_parallel_v1"]["ms"], "higher_is_better": True, "dtype": "u32",
             "data": "synthetic: torch seed 0, randn(4096*4096)*0.02 -> bf16; blobs byte-identical to the reference's",
-            "config": {"workload": "refcodecs_c0_4096sq", "elements": int(words.size)},
+            "host": host_cpu_info(), "config": {"workload": "refcodecs_c0_4096sq", "elements": int(words.size)},
             "codecs": res,
             "roofline": {"bound": "latency (serial rANS chains: 128 streams for bf16_parallel_v1, one for the others)",
                          "achieved": res["bf16_parallel_v1"]["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -513,7 +533,7 @@ def run_c3(args) -> dict:
                       "on the reference's bf16_se_tans)",
             "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "ms_per_step": head["ms"], "higher_is_better": True,
             "dtype": "u32", "data": "synthetic: Student-t df=3, half zeros, fp8 e4m3 + bf16 residual (seeded)",
-            "config": {"workload": "c3_stress_8192sq", "elements_per_tensor": 8192 * 8192}, "tensors": res,
+            "host": host_cpu_info(), "config": {"workload": "c3_stress_8192sq", "elements_per_tensor": 8192 * 8192}, "tensors": res,
             "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": head["frac"]}}
 
