@@ -85,10 +85,17 @@ class ChunkJob:
 
 
 def inspect_chunk_header(blob_head: bytes):
+    """Parse a BSCK header. A malformed or truncated header is a data error:
+    ValueError, as the reference raises for bad magic or counts
+    (bigsmall/codecs/bf16_parallel.py:153-163)."""
     info = _native.BsChunkInfo()
+    if len(blob_head) < 32:
+        raise ValueError(f"bf16_chunked: blob too short for its header ({len(blob_head)} bytes)")
     buf = (ctypes.c_uint8 * len(blob_head)).from_buffer_copy(blob_head)
-    _native.check(_native.lib().bs_chunk_inspect(ctypes.addressof(buf), len(blob_head), ctypes.byref(info)),
-                  "bs_chunk_inspect")
+    rc = _native.lib().bs_chunk_inspect(ctypes.addressof(buf), len(blob_head), ctypes.byref(info))
+    if rc == _native.BS_ERR_FORMAT:
+        raise ValueError("bf16_chunked: malformed blob header")
+    _native.check(rc, "bs_chunk_inspect")
     return info
 
 

@@ -181,6 +181,41 @@ def test_concurrent_host_threads_on_their_own_streams(torch_gpu):
         assert sorted(ex.map(work, range(4))) == [0, 1, 2, 3]
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+def test_single_byte_corruptions_decode_or_raise(torch_gpu, mode):
+    """Every single-byte corruption of a blob (header, symbol table, chunk
+    table, states, words, plane) either decodes or raises ValueError /
+    DecodeError: the kernel's header, table and bounds checks keep every
+    access inside the blob and the output, and most flips are reported."""
+    import torch
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.exceptions import DecodeError
+    rng = np.random.default_rng(17 + mode)
+    w = _bf16(rng.standard_normal(40_000) * 0.02)
+    if mode == 2:
+        w[rng.permutation(w.size)[: w.size // 2]] = 0
+    blob = bc.encode_array(w, steps=64, mode=mode)
+    ctab = (32 + 4 * int.from_bytes(blob[22:24], "little") + 15) & ~15
+    head = list(range(0, ctab + 16 * bc.info(blob).n_chunks))       # header, symbols, chunk table
+    positions = list(rng.choice(head, 80, replace=False)) + list(rng.integers(0, len(blob), 40))
+    _say(f"[bsck] {len(positions) * 2} single-byte corruptions, mode {mode}")
+    outcomes = {"ok": 0, "raised": 0}
+    for pos in positions:
+        for flip in (0xFF, 1 << int(rng.integers(0, 8))):
+            bad = bytearray(blob)
+            bad[pos] ^= flip
+            try:
+                bc.decode(bytes(bad), {}, w.size)
+                outcomes["ok"] += 1
+            except (ValueError, DecodeError):
+                outcomes["raised"] += 1
+    torch.cuda.synchronize()
+    # the clean blob still decodes after all of them
+    assert bc.decode(blob, {}, w.size) == w.tobytes()
+    _say(f"[bsck] outcomes {outcomes}")
+    assert outcomes["raised"] >= len(positions) // 2, outcomes
+
+
 def test_corrupt_stream_is_reported(torch_gpu):
     import torch
     from bigsmall_amd.codecs import bf16_chunked as bc
