@@ -186,6 +186,14 @@ __device__ __forceinline__ void seg_land(LDS uint8_t* ring, uint64_t q, uint32_t
   *(LDS u32x4*)(ring + ((q * kSegB + lane * 16u) & (kRingB - 1u))) = v;
 }
 
+// A stream descriptor every pass of the serial path may use: at most max_len
+// symbols (what the placement tiles cover) and every element index inside the
+// output. The three passes check it alike, so a bad descriptor is reported and
+// skipped, never followed.
+__device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint32_t max_len, uint64_t n_out) {
+  return S.n <= max_len && S.stride != 0 && (S.n == 0 || S.first + (uint64_t)(S.n - 1) * S.stride < n_out);
+}
+
 // Decode one chain of n symbols. The LDS table has one 16-byte entry per slot,
 // {f, slot - cf, output, 0} (SE: M = 4096, output the word sign<<15 | exp<<7,
 // stored as u16; mantissa: M = 1024, output one byte per symbol), so a step is
@@ -308,7 +316,7 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
   const uint32_t lane = threadIdx.x;
   if (blockIdx.x < n_streams) {
     const bs_se_stream S = se[blockIdx.x];
-    if (S.n > max_len || S.stride == 0 || (S.n && S.first + (uint64_t)(S.n - 1) * S.stride >= n_out)) {
+    if (!stream_ok(S, max_len, n_out)) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
@@ -339,7 +347,7 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
 
 // Exponent histogram of each tile: block k * tps + t covers symbols
 // [t*kTile, (t+1)*kTile) of stream k.
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out,
+__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out, uint64_t n_out,
                                                    const bs_se_stream* __restrict__ se, uint32_t tps,
                                                    uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[256];
@@ -347,7 +355,7 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ 
   const bs_se_stream S = se[k];
   h[tid] = 0;
   __syncthreads();
-  const uint32_t lo = t * kTile, hi = min(S.n, lo + kTile);
+  const uint32_t lo = t * kTile, hi = stream_ok(S, tps * kTile, n_out) ? min(S.n, lo + kTile) : lo;
   for (uint32_t i = lo + tid; i < hi; i += 256) atomicAdd(&h[(out[S.first + (uint64_t)i * S.stride] >> 7) & 0xFFu], 1u);
   __syncthreads();
   hist[(uint64_t)blockIdx.x * 256 + tid] = h[tid];
@@ -381,6 +389,7 @@ __global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out
   __shared__ uint32_t cnt[256];
   const uint32_t lane = threadIdx.x, k = blockIdx.x / tps, t = blockIdx.x % tps;
   const bs_se_stream S = se[k];
+  if (!stream_ok(S, tps * kTile, n)) return;     // reported by serial_kernel
   for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)blockIdx.x * 256 + e];
   wave_sync();
   const uint32_t lo = t * kTile, hi = min(S.n, lo + kTile);
@@ -467,7 +476,7 @@ int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams,
   hipLaunchKernelGGL(serial_kernel, dim3(n_streams + n_buckets), dim3(kWave), kSerLds, s, d_streams, n_streams,
                      tps * kTile, d_se_table, d_buckets, d_mant_tables, n_tables, d_out, n_out, mant, d_status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(hist_kernel, dim3(n_streams * tps), dim3(256), 0, s, d_out, d_streams, tps, hist);
+  hipLaunchKernelGGL(hist_kernel, dim3(n_streams * tps), dim3(256), 0, s, d_out, n_out, d_streams, tps, hist);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
   hipLaunchKernelGGL(scan_kernel, dim3(n_streams), dim3(256), 0, s, hist, tps, d_bstart, d_status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;

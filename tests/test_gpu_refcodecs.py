@@ -106,3 +106,30 @@ def test_corrupt_stream_is_reported(gpu):
     _say("[ref] corrupt tans stream -> DecodeError")
     with pytest.raises((DecodeError, ValueError)):
         _decode("bf16_se_tans", bytes(blob2), w.size)
+
+
+@pytest.mark.parametrize("codec", list(CODECS))
+@pytest.mark.parametrize("n", [30_000, 80_000])
+def test_single_byte_corruptions_decode_or_raise(gpu, codec, n):
+    """Single-byte corruptions of a reference-format blob (half in its first
+    4 KB of framing and tables, half anywhere) either decode or raise
+    ValueError / DecodeError, on the one-lane path (below 65,536 elements) and
+    on the wave-serial path; the clean blob still decodes afterwards."""
+    from bigsmall_amd.exceptions import DecodeError
+    rng = np.random.default_rng(n + len(codec))
+    w = _bf16(rng.standard_normal(n) * 0.02)
+    blob = CODECS[codec][0](w)
+    _say(f"[ref] {codec} n={n}: 60 single-byte corruptions")
+    outcomes = {"ok": 0, "raised": 0}
+    for t in range(60):
+        bad = bytearray(blob)
+        pos = int(rng.integers(0, min(len(blob), 4096))) if t % 2 else int(rng.integers(0, len(blob)))
+        bad[pos] ^= int(rng.integers(1, 256))
+        try:
+            _decode(codec, bytes(bad), n)
+            outcomes["ok"] += 1
+        except (ValueError, DecodeError):
+            outcomes["raised"] += 1
+    _say(f"[ref] outcomes {outcomes}")
+    assert _decode(codec, blob, n) == w.tobytes()
+    assert outcomes["raised"] > 0, outcomes
