@@ -28,7 +28,7 @@ def _declared_functions() -> list[str]:
     names = []
     for hdr in (ROOT / "include").glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
-        names += re.findall(r"^\s*int\s+(bs_\w+)\s*\(", text, flags=re.M)
+        names += re.findall(r"^\s*(?:int|uint64_t)\s+(bs_\w+)\s*\(", text, flags=re.M)
     return names
 
 
@@ -107,3 +107,28 @@ def test_planted_corruption_is_caught():
     bad[32 + 2] ^= 0x01                         # a frequency: sum != 4096
     with pytest.raises(oracle.OracleError):
         oracle.chunk_decode(bytes(bad), w.size)
+
+
+@pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 3), ("elem_bytes", 3), ("plane_mode", 3),
+                                         ("prec", 11), ("lanes", 96), ("steps", 24), ("n_syms", 0),
+                                         ("n_chunks", 7), ("truncated", None)])
+def test_malformed_header_raises_value_error(field, value):
+    """bs_chunk_inspect (host code) rejects every malformed header field, and
+    the codec turns that into ValueError, as the reference does for bad magic
+    or counts (bigsmall/codecs/bf16_parallel.py:153-163)."""
+    import struct
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    w = _bf16(np.random.default_rng(4).standard_normal(50_000) * 0.02)
+    head = bytearray(bc.encode_array(w)[:32])
+    assert bc.info(bytes(head)).n == w.size
+    offs = {"version": (4, "<B"), "elem_bytes": (5, "<B"), "plane_mode": (6, "<B"), "prec": (7, "<B"),
+            "lanes": (20, "<H"), "steps": (16, "<I"), "n_syms": (22, "<H"), "n_chunks": (24, "<I")}
+    if field == "magic":
+        head[0:4] = value
+    elif field == "truncated":
+        head = head[:31]
+    else:
+        o, fmt = offs[field]
+        struct.pack_into(fmt, head, o, value)
+    with pytest.raises(ValueError):
+        bc.info(bytes(head))
