@@ -7,8 +7,9 @@ container entries decoded together, normally one transformer layer
 one launch per codec family):
 
   1. the group's compressed bytes (one contiguous span of the data section)
-     are copied host -> device on a copy stream, from pinned buffers that
-     rotate so the disk read / memcpy of group g+1 overlaps the copy of g;
+     are read into a pinned buffer in parallel 16 MB pieces and copied
+     host -> device on a copy stream piece by piece as the reads complete;
+     the pinned buffers rotate, so the read of group g+1 overlaps the copy of g;
   2. the decode stream waits for that copy only, then launches
        - one batched BSCK launch (bs_chunk_decode_batch) for every
          bf16_chunked_v1 / fp8_chunked_v1 entry of the group,
@@ -26,7 +27,9 @@ Codecs whose bitstream is defined by libraries this engine does not carry
 from __future__ import annotations
 
 import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
+from typing import Optional
 
 import numpy as np
 
@@ -76,6 +79,10 @@ class GroupResult:
     keep: list = field(default_factory=list)
 
     def wait(self, what: str = "decode") -> dict:
+        """Synchronise with the decode, check its status word, and hand the
+        tensors to the caller's current stream: record_stream keeps the
+        allocator from reusing their memory for later decodes (on the decode
+        stream) while work the caller queues on its own stream still reads them."""
         import torch
         if self.done is not None:
             self.done.synchronize()
@@ -83,13 +90,18 @@ class GroupResult:
             torch.cuda.synchronize()
         self.status.check(what)
         self.keep.clear()
+        for t in self.tensors.values():
+            if t.is_cuda and t.numel():
+                t.record_stream(torch.cuda.current_stream(t.device))
         return self.tensors
 
 
 class GroupDecoder:
     """Decodes groups of container entries into device tensors.
 
-    stream: the decode stream (default: torch's current stream).
+    stream: the decode stream (default: torch's current stream; "private" for a
+        new stream of its own, whose outputs the caller then orders with
+        `GroupResult.wait`, which also records them on the caller's stream).
     copy_stream: where host->device copies run (default: a new stream).
     Pinned staging buffers are allocated lazily and reused (n_pinned of them).
     """
@@ -97,6 +109,10 @@ class GroupDecoder:
     def __init__(self, device=None, stream=None, copy_stream=None, n_pinned: int = 2):
         import torch
         self.device = require_gpu(device)
+        if isinstance(stream, str):
+            if stream != "private":
+                raise ValueError(f"GroupDecoder: stream must be a torch stream, None or 'private', got {stream!r}")
+            stream = torch.cuda.Stream(self.device)
         self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
         self.copy_stream = copy_stream if copy_stream is not None else torch.cuda.Stream(self.device)
         self._pinned: list = [None] * max(1, n_pinned)
@@ -117,21 +133,34 @@ class GroupDecoder:
             self._pinned[i] = buf
         return i, buf
 
-    def upload(self, fill, nbytes: int):
-        """Copy `nbytes` produced by `fill(np_view)` to a new device buffer on the
-        copy stream; returns (device tensor, event recorded after the copy)."""
+    def upload(self, read_span, offset: int, nbytes: int):
+        """Copy data-section bytes [offset, offset + nbytes) to a new device
+        buffer through a pinned staging buffer; returns (device tensor, the
+        pinned bytes as numpy, event recorded after the copy). The copy of
+        each piece the reader reports (`read_span(..., on_piece=...)`, in
+        order) is queued on the copy stream as soon as that piece is read, so
+        the disk/page-cache read and the PCIe transfer of one span overlap."""
         import torch
         i, buf = self._pinned_buffer(nbytes)
         view = buf[:nbytes]
-        fill(view.numpy())
         dev = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        dev.record_stream(self.copy_stream)     # freed early (a read error), it outlives queued copies
+
+        def on_piece(p0: int, p1: int) -> None:
+            with torch.cuda.stream(self.copy_stream):
+                dev[p0:p1].copy_(view[p0:p1], non_blocking=True)
+
+        if nbytes:
+            if getattr(read_span, "pieces", False):
+                read_span(offset, view.numpy(), on_piece=on_piece)
+            else:
+                read_span(offset, view.numpy())
+                on_piece(0, nbytes)
         with torch.cuda.stream(self.copy_stream):
-            if nbytes:
-                dev[:nbytes].copy_(view, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record(self.copy_stream)
         self._pinned_busy[i] = ev
-        return dev, ev
+        return dev, view.numpy(), ev
 
     # -- decoding --------------------------------------------------------------
     def decode_group(self, entries: list[dict], read_span, span_start: int, span_len: int,
@@ -144,15 +173,7 @@ class GroupDecoder:
         import torch
         for t in entries:
             check_supported(t)
-        host_view = {}
-
-        def fill(dst):
-            if span_len:
-                read_span(span_start, dst)
-            host_view["bytes"] = dst
-
-        d_span, copied = self.upload(fill, span_len)
-        host = host_view["bytes"]
+        d_span, host, copied = self.upload(read_span, span_start, span_len)
         with torch.cuda.stream(self.stream):       # allocations and launches on the decode stream
             status, out, keep = self._launch_group(entries, host, d_span, copied, span_start, span_len,
                                                    resolve_tied, dtype)
@@ -242,14 +263,21 @@ class GroupDecoder:
         return status, out, keep
 
 
-def file_span_reader(path):
-    """read_span(offset, np_out) over the data section of a container file."""
+READ_PIECE = 16 << 20          # bytes per parallel read of a span
+
+
+def file_span_reader(path, threads: Optional[int] = None):
+    """read_span(offset, np_out) over the data section of a container file.
+    Spans above READ_PIECE are read in pieces by `threads` threads at once
+    (pread releases the GIL), so filling a pinned staging buffer from the page
+    cache runs at memory speed rather than one thread's copy rate."""
     from .container import read_header
     _, data_offset = read_header(path)
     fd = os.open(str(path), os.O_RDONLY)
+    n_threads = threads if threads is not None else max(1, min(8, os.cpu_count() or 1))
+    pool = ThreadPoolExecutor(n_threads, thread_name_prefix="bs-read") if n_threads > 1 else None
 
-    def read_span(offset: int, dst: np.ndarray) -> None:
-        mv = memoryview(dst)
+    def read_range(mv: memoryview, offset: int) -> None:
         got = 0
         while got < len(mv):
             k = os.preadv(fd, [mv[got:]], data_offset + offset + got)
@@ -257,7 +285,37 @@ def file_span_reader(path):
                 raise ValueError(f"{path}: data section truncated at {offset + got}")
             got += k
 
-    read_span.close = lambda: os.close(fd)
+    def read_span(offset: int, dst: np.ndarray, on_piece=None) -> None:
+        """Fill dst; on_piece(p0, p1), if given, is called in order from this
+        thread as each piece [p0, p1) of dst is complete."""
+        mv = memoryview(dst).cast("B")
+        n = len(mv)
+        if pool is None or n <= READ_PIECE:
+            read_range(mv, offset)
+            if on_piece is not None and n:
+                on_piece(0, n)
+            return
+        starts = range(0, n, READ_PIECE)
+        futs = [pool.submit(read_range, mv[p:p + READ_PIECE], offset + p) for p in starts]
+        try:
+            for p, f in zip(starts, futs):
+                f.result()
+                if on_piece is not None:
+                    on_piece(p, min(n, p + READ_PIECE))
+        finally:
+            for f in futs:          # no read may still write into dst after an error
+                f.cancel()
+            for f in futs:
+                if not f.cancelled():
+                    f.exception()
+
+    def close() -> None:
+        if pool is not None:
+            pool.shutdown(wait=True)
+        os.close(fd)
+
+    read_span.close = close
+    read_span.pieces = True
     return read_span
 
 

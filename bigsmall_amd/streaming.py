@@ -9,15 +9,20 @@ or plain *.bs shards.
 
 Where the reference decodes each tensor on the CPU and copies it to the device
 (streaming.py:163-191), a layer here is one GroupDecoder group: its compressed
-span is copied host->device on a copy stream and decoded by one batched kernel
-launch straight into device tensors. `iter_layers` keeps `prefetch` layers in
-flight, so the host->device copy and the decode of layer i+1 overlap the
-consumer's work on layer i, with no host thread.
+span is read into pinned memory (in parallel pieces), copied host->device on a
+copy stream and decoded by one batched kernel launch, on the loader's own
+decode stream, straight into device tensors. With prefetch > 0 every
+submission runs on one worker thread, so `iter_layers` (and
+BigSmallStreamingModel) keep `prefetch` layers in flight: the file read, the
+host->device copy and the decode of layer i+1 overlap the consumer's work on
+layer i, which the caller queues on its own stream meanwhile. `collect` hands
+the tensors to the caller's stream (GroupResult.wait).
 """
 from __future__ import annotations
 
 import json
 import re
+from concurrent.futures import Future, ThreadPoolExecutor
 from pathlib import Path
 from typing import Iterator, Optional
 
@@ -58,13 +63,16 @@ class StreamingLoader:
         self._readers: dict[Path, object] = {}
         self._build_index()
         self._engine_obj = None
+        self._worker: Optional[ThreadPoolExecutor] = None
 
     @property
     def _engine(self):
-        # created on the first decode, so the index API works without a GPU
+        # created on the first decode, so the index API works without a GPU;
+        # its own decode stream lets a prefetched layer decode while the
+        # caller's stream runs the current one
         if self._engine_obj is None:
             from . import engine
-            self._engine_obj = engine.GroupDecoder(self.device, n_pinned=max(2, self.prefetch + 1))
+            self._engine_obj = engine.GroupDecoder(self.device, stream="private", n_pinned=max(2, self.prefetch + 1))
         return self._engine_obj
 
     def __enter__(self) -> "StreamingLoader":
@@ -74,6 +82,9 @@ class StreamingLoader:
         self.close()
 
     def close(self) -> None:
+        if self._worker is not None:
+            self._worker.shutdown(wait=True)
+            self._worker = None
         for r in self._readers.values():
             r.close()
         self._readers.clear()
@@ -139,8 +150,24 @@ class StreamingLoader:
             entry = nxt
         return entry
 
+    def _submit_async(self, names: list[str]):
+        """_submit on the worker thread (a Future), or inline without prefetch.
+        Every submission takes this path, so the engine's pinned buffers and the
+        file readers are only ever used by one thread at a time."""
+        if self.prefetch == 0:
+            return self._submit(names)
+        if self._worker is None:
+            self._worker = ThreadPoolExecutor(1, thread_name_prefix="bs-stream")
+        return self._worker.submit(self._submit, names)
+
     def _submit(self, names: list[str]):
         """Start decoding `names` (asynchronously); returns [(GroupResult, {out name: master name})]."""
+        import torch
+        eng = self._engine
+        with torch.cuda.device(eng.device):
+            return self._submit_on(eng, names)
+
+    def _submit_on(self, eng, names: list[str]):
         from . import engine
         by_shard: dict[Path, list] = {}
         alias: dict[str, str] = {}
@@ -154,7 +181,7 @@ class StreamingLoader:
         for shard, ents in by_shard.items():
             metas = [e.meta for e in ents]
             lo, hi = engine.group_span(metas)
-            res = self._engine.decode_group(metas, self._reader(shard), lo, hi - lo, dtype=self.dtype)
+            res = eng.decode_group(metas, self._reader(shard), lo, hi - lo, dtype=self.dtype)
             jobs.append(res)
         return jobs, alias
 
@@ -184,28 +211,31 @@ class StreamingLoader:
     def load_tensor(self, name: str):
         if name not in self._index:
             raise KeyError(f"Tensor {name!r} not in this BigSmall model")
-        return self._collect(*self._submit([name]))[name]
+        return self.collect(self._submit_async([name]))[name]
 
     def load_layer(self, layer_idx: int) -> dict:
         names = self._layers.get(layer_idx)
         if names is None:
             raise IndexError(f"Layer {layer_idx} not in this model (have {self.layer_count()} layers)")
-        return self._collect(*self._submit(names))
+        return self.collect(self._submit_async(names))
 
     def submit_layer(self, layer_idx: int):
         """Start decoding a layer; `collect(handle)` returns its tensors."""
         names = self._layers.get(layer_idx)
         if names is None:
             raise IndexError(f"Layer {layer_idx} not in this model (have {self.layer_count()} layers)")
-        return self._submit(names)
+        return self._submit_async(names)
 
     def collect(self, handle) -> dict:
+        """The tensors of a submitted group, ready for use on the caller's current stream."""
+        if isinstance(handle, Future):
+            handle = handle.result()
         return self._collect(*handle)
 
     def load_non_layer_tensors(self) -> dict:
         if not self._non_layer:
             return {}
-        return self._collect(*self._submit(self._non_layer))
+        return self.collect(self._submit_async(self._non_layer))
 
     def iter_layers(self, progress: bool = True) -> Iterator[tuple[int, dict]]:
         """Yield (layer_idx, tensors) in order; `prefetch` layers ahead are

@@ -9,10 +9,11 @@ decoded into HBM right before it runs and released right after.
 Prefetch: the reference runs a host thread that decodes layers on the CPU
 ahead of the forward pass, for exactly one pass over the layers
 (streaming_inference.py:287-308; a second pass then waits on an empty queue).
-Here prefetch is the loader's stream pipeline: when layer i's forward starts,
-the decode of layer (i + 1) mod n_layers is submitted (its compressed bytes
-are copied on a side stream and decoded by one batched launch), so it
-overlaps layer i's compute on every pass, with no host thread.
+Here, when layer i's forward starts, layer (i + 1) mod n_layers is submitted
+to the loader's worker thread (its compressed bytes are read into pinned
+memory, copied on a side stream and decoded by one batched launch on the
+loader's decode stream), so it overlaps layer i's forward, which runs on the
+caller's stream, on every pass.
 """
 from __future__ import annotations
 
