@@ -538,6 +538,93 @@ def run_c3(args) -> dict:
                          "frac": head["frac"]}}
 
 
+def measure_h2d(dev, mib: int = 1024, reps: int = 5) -> float:
+    """Host (pinned) -> device copy rate in the same run, bytes per second."""
+    import torch
+    n = mib << 20
+    h = torch.empty(n, dtype=torch.uint8, pin_memory=True).fill_(1)
+    d = torch.empty(n, dtype=torch.uint8, device=dev)
+    d.copy_(h, non_blocking=True)
+    ms = _timed(lambda: d.copy_(h, non_blocking=True), reps, torch.cuda.current_stream(dev))
+    del h, d
+    return n / (ms * 1e-3)
+
+
+def run_streaming(args) -> dict:
+    """BigSmallStreamingModel on a Llama-3-8B-shaped model cut to `--layers`
+    layers (bf16, seeded N(0, 0.02) weights, 1 + N(0, 0.01) norms, untied
+    embedding and lm_head 128256x4096): the container is written to a
+    temporary file, and every forward pass (batch 1, 128 tokens) reads,
+    copies and decodes each layer from it while the previous one runs. The
+    floor is the PCIe transfer of a layer's compressed bytes at the
+    host->device rate measured in the same run."""
+    import shutil
+    import tempfile
+    import torch
+    from transformers import LlamaConfig
+    from bigsmall_amd import container
+    from bigsmall_amd.encoder import compress
+    from bigsmall_amd.streaming_inference import BigSmallStreamingModel
+    n_layers = args.layers
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=n_layers,
+                      num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=2048,
+                      tie_word_embeddings=False, attn_implementation="sdpa", torch_dtype="bfloat16")
+    g = torch.Generator().manual_seed(0)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g) * 0.02).bfloat16()
+
+    def norm():
+        return (1 + torch.randn(4096, generator=g) * 0.01).bfloat16()
+
+    t0 = time.time()
+    sd = {"model.embed_tokens.weight": rnd(128256, 4096), "lm_head.weight": rnd(128256, 4096), "model.norm.weight": norm()}
+    for i in range(n_layers):
+        for name, shape in LAYER:
+            short = name.split("layers.0.")[1]
+            sd[f"model.layers.{i}.{short}"] = norm() if "norm" in short else rnd(*shape)
+    work = tempfile.mkdtemp(prefix="bs_stream_")
+    try:
+        path = os.path.join(work, "model.bs")
+        compress(sd, path)
+        cfg.save_pretrained(work)
+        del sd
+        log(f"[stream] {n_layers}-layer model written in {time.time() - t0:.1f}s ({os.path.getsize(path) / 1e9:.2f} GB)")
+        hdr, _ = container.read_header(path)
+        per_layer = sum(int(t["compressed_bytes"]) for t in hdr["tensors"] if t["name"].startswith("model.layers.0."))
+        dev = torch.device("cuda", 0)
+        h2d = measure_h2d(dev)
+        ids = torch.randint(0, 128256, (1, 128), generator=torch.Generator().manual_seed(1)).cuda()
+        res = {}
+        for prefetch in (0, 1):
+            m = BigSmallStreamingModel.from_pretrained(path, device="cuda", prefetch=prefetch)
+            m.forward(ids)
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(args.steps):
+                t1 = time.perf_counter()
+                m.forward(ids)
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t1)
+            m.close()
+            res[prefetch] = sorted(ts)[len(ts) // 2]
+            log(f"[stream] prefetch={prefetch}: {res[prefetch] * 1e3:.1f} ms per pass, "
+                f"{res[prefetch] * 1e3 / n_layers:.2f} ms per layer")
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    ms_layer = res[1] * 1e3 / n_layers
+    floor_ms = per_layer / h2d * 1e3
+    return {"metric": "ms per layer, BigSmallStreamingModel forward streaming an 8B-shaped model from a .bs file",
+            "value": round(ms_layer, 3), "unit": "ms/layer", "n_gpus": 1, "steps": args.steps,
+            "ms_per_step": round(res[1] * 1e3, 2), "higher_is_better": False, "dtype": "bf16",
+            "data": "synthetic: seeded N(0,0.02) weights, 1+N(0,0.01) norms; batch 1, 128 tokens",
+            "config": {"workload": "streaming_llama3_8b_shape", "layers": n_layers,
+                       "compressed_bytes_per_layer": per_layer, "prefetch": 1},
+            "prefetch0_ms_per_layer": round(res[0] * 1e3 / n_layers, 3),
+            "pcie_floor": {"h2d_GBps": round(h2d / 1e9, 2), "ms_per_layer": round(floor_ms, 3),
+                           "frac": round(floor_ms / ms_layer, 4)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -549,10 +636,11 @@ def main():
     ap.add_argument("--zero-fraction", type=float, default=0.0,
                     help="layer workload only: set this seeded share of every matrix's elements to +0.0 "
                          "(a pruned layer; such tensors take the compact plane mode)")
-    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3"], default="layer",
+    ap.add_argument("--layers", type=int, default=8, help="streaming workload: decoder layers of the model")
+    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3", "streaming"], default="layer",
                     help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache "
                          "blocks), refcodecs (the reference's own formats on the C0 tensor), c3 (stress "
-                         "tensors)")
+                         "tensors), streaming (BigSmallStreamingModel forward from a .bs file)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -566,7 +654,8 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     if args.workload != "layer":
-        run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs, "c3": run_c3}[args.workload]
+        run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs, "c3": run_c3,
+               "streaming": run_streaming}[args.workload]
         print(json.dumps(run(args)), flush=True)
         return
     from bigsmall_amd.codecs import bf16_chunked as bc
