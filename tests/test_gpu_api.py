@@ -161,6 +161,36 @@ def test_streaming_loader(model_file, prefetch):
                            src["model.layers.0.self_attn.q_proj.weight"].float())
 
 
+@pytest.mark.parametrize("prefetch", [0, 1])
+def test_streaming_loader_reports_a_corrupt_layer(model_file, tmp_path, prefetch):
+    """A renorm word flipped inside layer 1's q_proj blob: loading layer 1
+    raises DecodeError on the caller's thread (also when the decode ran on the
+    loader's worker thread), and the same loader still decodes the other
+    layers bit-exactly afterwards."""
+    from bigsmall_amd.exceptions import DecodeError
+    from bigsmall_amd.streaming import StreamingLoader
+    p, src = model_file
+    header, data_offset = container.read_header(p)
+    t = next(x for x in header["tensors"] if x["name"] == "model.layers.1.self_attn.q_proj.weight")
+    assert t["codec"] == "bf16_chunked_v1"
+    raw = bytearray(p.read_bytes())
+    blob0 = data_offset + int(t["offset"])
+    nsym = int.from_bytes(raw[blob0 + 22:blob0 + 24], "little")
+    ctab = (32 + 4 * nsym + 15) & ~15
+    c0 = int.from_bytes(raw[blob0 + ctab:blob0 + ctab + 8], "little")
+    lanes = int.from_bytes(raw[blob0 + 20:blob0 + 22], "little")
+    raw[blob0 + c0 + 4 * lanes + 6] ^= 0x5A             # a renorm word of chunk 0
+    bad = tmp_path / "bad.bs"
+    bad.write_bytes(bytes(raw))
+    _say(f"[api] corrupt layer 1, prefetch={prefetch}")
+    with StreamingLoader(bad, device="cuda", prefetch=prefetch) as L:
+        with pytest.raises(DecodeError):
+            L.load_layer(1)
+        for li in (0, 2):
+            lay = L.load_layer(li)
+            assert all(_bytes(v) == _bytes(src[k]) for k, v in lay.items()), li
+
+
 def test_kv_cache_entries_and_blocks():
     from bigsmall_amd.kv_cache_manager import CompressedKVCache
     g = torch.Generator().manual_seed(9)
