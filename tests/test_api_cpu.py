@@ -178,3 +178,18 @@ def test_no_cpu_fallback(container_file):
         kernels.decode_bf16_parallel(b"PAR1xxxx", {}, 10)
     with pytest.raises(RuntimeError):
         decoder.load(p)
+
+
+def test_kv_compression_ratio_below_75pct():
+    """Mirror of the reference's KV ratio gate (tests/test_kv_cache.py:34-49):
+    Gaussian KV-shaped tensors compress below 75 % of raw (host encoder)."""
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache
+    torch.manual_seed(0)
+    B, H, T, D = 1, 32, 512, 96
+    k = (torch.randn(B, H, T, D) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(B, H, T, D) * 0.5).to(torch.bfloat16)
+    raw = k.element_size() * k.numel() + v.element_size() * v.numel()
+    ratio = len(kv_cache.compress_kv_entry(k, v)) / raw
+    assert ratio < 0.75, f"KV compression ratio {ratio * 100:.2f}% exceeds the 75% gate"
+    cache = CompressedKVCache(device="cuda")       # the empty-cache API needs no GPU
+    assert len(cache) == 0 and cache.memory_usage() == 0 and cache.compression_ratio() is None

@@ -217,6 +217,68 @@ def test_kv_cache_entries_and_blocks():
     assert _bytes(v2[0]) == _bytes(K[:, 0:256])
 
 
+def _md5_tensor(t) -> str:
+    return hashlib.md5(t.contiguous().view(torch.uint8).cpu().numpy().tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("device", ["cuda", "cpu"])
+def test_reference_kv_cache_tests(device):
+    """Mirrors of the reference's KV-cache tests (tests/test_kv_cache.py:15-120):
+    entry round trip, CompressedKVCache set/get/has/len/memory_usage/
+    compression_ratio, several layers, clear(). Decoding runs on the GPU; with
+    device="cpu" the tensors come back to host memory."""
+    from bigsmall_amd.codecs.kv_cache import compress_kv_entry, decompress_kv_entry
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache
+    _say(f"[api] reference KV tests, device={device}")
+    torch.manual_seed(0)
+    k = torch.randn(1, 32, 64, 96, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn(1, 32, 64, 96, dtype=torch.float32).to(torch.bfloat16)
+    k2, v2 = decompress_kv_entry(compress_kv_entry(k, v), device=device)
+    assert k2.device.type == device and v2.device.type == device
+    assert _md5_tensor(k) == _md5_tensor(k2) and _md5_tensor(v) == _md5_tensor(v2)
+
+    torch.manual_seed(1)
+    cache = CompressedKVCache(device=device)
+    assert len(cache) == 0 and cache.memory_usage() == 0 and cache.compression_ratio() is None
+    k = torch.randn(1, 32, 64, 96).to(torch.bfloat16)
+    v = torch.randn(1, 32, 64, 96).to(torch.bfloat16)
+    cache.set(0, k, v)
+    assert cache.has(0) and len(cache) == 1
+    k2, v2 = cache.get(0)
+    assert _md5_tensor(k) == _md5_tensor(k2) and _md5_tensor(v) == _md5_tensor(v2)
+    cr = cache.compression_ratio()
+    assert cr is not None and 0.0 < cr < 1.0 and cache.memory_usage() > 0
+
+    cache = CompressedKVCache(device=device)
+    layers = {}
+    torch.manual_seed(2)
+    for li in range(4):
+        layers[li] = (torch.randn(1, 32, 32, 96).to(torch.bfloat16), torch.randn(1, 32, 32, 96).to(torch.bfloat16))
+        cache.set(li, *layers[li])
+    for li in range(4):
+        k2, v2 = cache.get(li)
+        assert _md5_tensor(layers[li][0]) == _md5_tensor(k2) and _md5_tensor(layers[li][1]) == _md5_tensor(v2), li
+
+    cache.clear()
+    assert len(cache) == 0 and cache.memory_usage() == 0 and cache.compression_ratio() is None
+
+
+def test_reference_bf16_parallel_lossless_gaussian():
+    """Mirror of the reference's tests/test_bf16_parallel.py:27-36: n = 2^20
+    N(0, 0.02) bf16 words, N in {1, 32, 128, 256} streams, decoded through the
+    plugin decode(blob, extras, n) on the GPU (blobs from the oracle's encoder,
+    byte-identical to the reference's on the golden vectors)."""
+    from bigsmall_amd.codecs import bf16_parallel
+    torch.manual_seed(0)
+    n = 1 << 20
+    raw = (torch.randn(n) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy().tobytes()
+    words = np.frombuffer(raw, np.uint16)
+    for ns in [1, 32, 128, 256]:
+        _say(f"[api] bf16_parallel_v1 n=2^20 N={ns}")
+        out = bf16_parallel.decode(oracle.par1_encode(words, ns), {}, n)
+        assert hashlib.md5(raw).hexdigest() == hashlib.md5(out).hexdigest(), f"mismatch at N={ns}"
+
+
 def test_streaming_model_matches_full_model(tmp_path):
     """A tiny Llama decoded layer by layer gives the same logits as the same
     weights loaded whole (float32 compute)."""
