@@ -49,13 +49,17 @@ class StreamingLoader:
     """Decode a .bs model one transformer layer at a time.
 
     path: a .bs file, or a directory with bigsmall.index.json + shards (or *.bs).
-    device: ROCm device for the returned tensors ("cuda", "cuda:0", ...).
+    device: where the returned tensors live: a ROCm device ("cuda", "cuda:0",
+        ...), or "cpu" (decoded on the GPU, then copied to host memory, as
+        decoder.load does; the reference decodes on the CPU for it).
     dtype: optional torch dtype to cast floating tensors to.
     prefetch: layers decoded ahead by `iter_layers` (0 = decode on demand).
     """
 
     def __init__(self, path: str | Path, device: str = "cuda", dtype=None, prefetch: int = 1):
         self.device, self.dtype, self.path = device, dtype, Path(path)
+        self._to_host = str(device).split(":")[0] == "cpu"
+        self._decode_device = "cuda" if self._to_host else device
         self.prefetch = max(0, int(prefetch))
         self._index: dict[str, _TensorEntry] = {}
         self._layers: dict[int, list[str]] = {}
@@ -72,7 +76,8 @@ class StreamingLoader:
         # caller's stream runs the current one
         if self._engine_obj is None:
             from . import engine
-            self._engine_obj = engine.GroupDecoder(self.device, stream="private", n_pinned=max(2, self.prefetch + 1))
+            self._engine_obj = engine.GroupDecoder(self._decode_device, stream="private",
+                                                   n_pinned=max(2, self.prefetch + 1))
         return self._engine_obj
 
     def __enter__(self) -> "StreamingLoader":
@@ -185,11 +190,12 @@ class StreamingLoader:
             jobs.append(res)
         return jobs, alias
 
-    @staticmethod
-    def _collect(jobs, alias: dict) -> dict:
+    def _collect(self, jobs, alias: dict) -> dict:
         decoded = {}
         for res in jobs:
             decoded.update(res.wait("streaming decode"))
+        if self._to_host:
+            decoded = {k: v.cpu() for k, v in decoded.items()}
         out = {}
         for n, m in alias.items():
             out[n] = decoded[m] if n == m else decoded[m].clone()

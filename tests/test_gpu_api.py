@@ -279,6 +279,63 @@ def test_reference_bf16_parallel_lossless_gaussian():
         assert hashlib.md5(raw).hexdigest() == hashlib.md5(out).hexdigest(), f"mismatch at N={ns}"
 
 
+def test_reference_bf16_parallel_edge_cases():
+    """Mirror of tests/test_bf16_parallel.py:39-62: NaN, +/-Inf, +/-0, the
+    smallest denormal and normal, 1.0, then 4096 normals, N in {1, 32, 128}."""
+    import struct
+    from bigsmall_amd.codecs import bf16_parallel
+    special = [0x7FC0, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x0080, 0x3F80]
+    torch.manual_seed(1)
+    normals = (torch.randn(4096) * 0.02).to(torch.bfloat16).view(torch.uint8).numpy()
+    raw = b"".join(struct.pack("<H", w) for w in special) + normals.tobytes()
+    n = len(raw) // 2
+    for ns in [1, 32, 128]:
+        out = bf16_parallel.decode(oracle.par1_encode(np.frombuffer(raw, np.uint16), ns), {}, n)
+        assert raw == out, f"byte mismatch at N={ns}"
+
+
+def test_reference_streaming_md5_roundtrip_all_layers(tmp_path):
+    """Mirror of tests/test_streaming.py:38-127: a synthetic 4-layer model
+    (embed, ln_f, q/k/up/down projections and a norm per layer, N(0, 1) bf16)
+    through compress_for_hub, then StreamingLoader on the output directory:
+    layer count, the non-layer names, and every tensor md5-equal to its source,
+    from load_non_layer_tensors and iter_layers (device="cpu": decoded on the
+    GPU, returned in host memory)."""
+    from safetensors.torch import save_file
+    import bigsmall_amd
+    from bigsmall_amd.streaming import StreamingLoader, layer_index
+    n_layers, hidden = 4, 256
+    torch.manual_seed(0)
+    src = {"embed.weight": torch.randn(1024, hidden, dtype=torch.bfloat16),
+           "ln_f.weight": torch.randn(hidden, dtype=torch.bfloat16),
+           "ln_f.bias": torch.zeros(hidden, dtype=torch.bfloat16)}
+    for i in range(n_layers):
+        p = f"model.layers.{i}"
+        src[f"{p}.self_attn.q_proj.weight"] = torch.randn(hidden, hidden, dtype=torch.bfloat16)
+        src[f"{p}.self_attn.k_proj.weight"] = torch.randn(hidden, hidden, dtype=torch.bfloat16)
+        src[f"{p}.mlp.up_proj.weight"] = torch.randn(hidden * 2, hidden, dtype=torch.bfloat16)
+        src[f"{p}.mlp.down_proj.weight"] = torch.randn(hidden, hidden * 2, dtype=torch.bfloat16)
+        src[f"{p}.input_layernorm.weight"] = torch.randn(hidden, dtype=torch.bfloat16)
+    (tmp_path / "src").mkdir()
+    save_file(src, str(tmp_path / "src" / "model.safetensors"))
+    out = tmp_path / "out"
+    bigsmall_amd.compress_for_hub(str(tmp_path / "src"), output_dir=out, overwrite=True)
+    want = {k: _md5_tensor(v) for k, v in src.items()}
+    seen = set()
+    with StreamingLoader(str(out), device="cpu") as L:
+        assert L.layer_count() == n_layers
+        assert sorted(L.non_layer_tensor_names()) == ["embed.weight", "ln_f.bias", "ln_f.weight"]
+        for name, t in L.load_non_layer_tensors().items():
+            seen.add(name)
+            assert _md5_tensor(t) == want[name], name
+        for li, layer in L.iter_layers():
+            for name, t in layer.items():
+                seen.add(name)
+                assert layer_index(name) == li and t.device.type == "cpu"
+                assert _md5_tensor(t) == want[name], name
+    assert seen == set(want)
+
+
 def test_streaming_model_matches_full_model(tmp_path):
     """A tiny Llama decoded layer by layer gives the same logits as the same
     weights loaded whole (float32 compute)."""
