@@ -7,6 +7,7 @@ kernels on the GPU:
     load(src, device="cuda")                -> dict[str, torch.Tensor] in HBM
     info(src), verify(src)
     StreamingLoader, BigSmallStreamingModel -> layer-at-a-time decode with prefetch
+    decompress_layers(src, [i, ...])        -> only the named layers
     CompressedKVCache                       -> KV entries and blocks decoded on the GPU
     codec_registry.register_codec / get_codec / auto_select_codec
     compress_for_hub(model_dir, out_dir), from_pretrained(path) -> multi-shard .bs models + index
@@ -19,7 +20,7 @@ from .encoder import compress
 from .exceptions import BigSmallVersionError, DecodeError
 from .hub import compress_for_hub, from_pretrained
 from .kv_cache_manager import CompressedKVCache
-from .streaming import StreamingLoader
+from .streaming import StreamingLoader, decompress_layers
 from .verify import verify
 
 
@@ -32,5 +33,6 @@ def __getattr__(name):
 
 
 __all__ = ["compress", "decompress", "load", "info", "verify", "StreamingLoader", "BigSmallStreamingModel",
+           "decompress_layers",
            "CompressedKVCache", "BigSmallVersionError", "DecodeError", "compress_for_hub", "from_pretrained",
            "__version__"]

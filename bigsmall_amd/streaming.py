@@ -259,3 +259,22 @@ class StreamingLoader:
                 yield li, layer
             finally:
                 layer.clear()
+
+
+def decompress_layers(bs_path: str | Path, layer_indices: list[int], *, device: str = "cpu", dtype=None,
+                      include_non_layer: bool = False) -> dict:
+    """Only the named transformer layers of a .bs file or shard directory
+    (bigsmall/hub_streaming.py:121-160): {name: tensor} on `device`, plus the
+    non-layer tensors when include_non_layer. A missing layer raises
+    ValueError. Each layer is one batched decode on the GPU."""
+    out: dict = {}
+    with StreamingLoader(bs_path, device=device, dtype=dtype, prefetch=0) as loader:
+        if include_non_layer:
+            out.update(loader.load_non_layer_tensors())
+        for li in layer_indices:
+            try:
+                out.update(loader.load_layer(li))
+            except IndexError:
+                raise ValueError(f"decompress_layers: layer {li} not present in this model "
+                                 f"(have {loader.layer_count()} layers)") from None
+    return out

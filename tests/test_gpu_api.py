@@ -336,6 +336,30 @@ def test_reference_streaming_md5_roundtrip_all_layers(tmp_path):
     assert seen == set(want)
 
 
+def test_reference_decompress_layers_returns_only_requested(tmp_path):
+    """Mirror of tests/test_opt_step6.py:93-135: decompress_layers returns the
+    requested layers only (equal to the source), non-layer tensors only on
+    request, and a missing layer raises ValueError."""
+    import bigsmall_amd
+    torch.manual_seed(2)
+    sd = {"model.embed_tokens.weight": (torch.randn(1024, 64) * 0.02).to(torch.bfloat16)}
+    for i in range(6):
+        sd[f"model.layers.{i}.q.weight"] = (torch.randn(64, 64) * 0.02).to(torch.bfloat16)
+        sd[f"model.layers.{i}.k.weight"] = (torch.randn(64, 64) * 0.02).to(torch.bfloat16)
+    sd["model.norm.weight"] = (torch.randn(64) * 0.02).to(torch.bfloat16)
+    bs = tmp_path / "model.bs"
+    compress(sd, bs)
+    partial = bigsmall_amd.decompress_layers(bs, layer_indices=[1, 3], device="cpu")
+    assert set(partial) == {f"model.layers.{li}.{w}.weight" for li in (1, 3) for w in ("q", "k")}
+    for k, v in partial.items():
+        assert v.device.type == "cpu" and _bytes(v) == _bytes(sd[k]), k
+    with_extras = bigsmall_amd.decompress_layers(bs, layer_indices=[0], device="cuda", include_non_layer=True)
+    assert {"model.embed_tokens.weight", "model.norm.weight", "model.layers.0.q.weight"} <= set(with_extras)
+    assert _bytes(with_extras["model.embed_tokens.weight"]) == _bytes(sd["model.embed_tokens.weight"])
+    with pytest.raises(ValueError):
+        bigsmall_amd.decompress_layers(bs, layer_indices=[7])
+
+
 def test_streaming_model_matches_full_model(tmp_path):
     """A tiny Llama decoded layer by layer gives the same logits as the same
     weights loaded whole (float32 compute)."""
