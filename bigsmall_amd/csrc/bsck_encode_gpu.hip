@@ -45,6 +45,8 @@ struct Plan {
   uint32_t sym_of_exp[256];   // exponent -> symbol index
   uint32_t freq[256];         // per symbol
   uint32_t cum[256];          // per symbol
+  uint32_t rcp[256];          // per symbol: multiplier for x / freq (see div_by_freq)
+  uint32_t shf[256];          // per symbol: its two shifts (s1 | s2 << 8)
   uint32_t nsym, ok, pad0, pad1;
 };
 constexpr uint64_t kPlanBytes = (sizeof(Plan) + 255) & ~uint64_t(255);
@@ -55,6 +57,21 @@ struct ChunkRec {
 };
 
 __host__ __device__ inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+
+// x / f for a fixed divisor 1 <= f <= 4096 and any 32-bit x, without a divide
+// instruction: Granlund and Montgomery, "Division by Invariant Integers using
+// Multiplication" (PLDI 1994), Figure 4.1. With l = ceil(log2 f),
+//   m = floor(2^32 * (2^l - f) / f) + 1,  s1 = min(l, 1),  s2 = max(l - 1, 0),
+//   t = mulhi(m, x),  x / f = (t + ((x - t) >> s1)) >> s2.
+__device__ __forceinline__ void div_constants(uint32_t f, uint32_t& m, uint32_t& shf) {
+  const uint32_t l = f > 1 ? 32u - (uint32_t)__clz(f - 1) : 0u;
+  m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - f)) / f + 1);
+  shf = (l ? 1u : 0u) | ((l ? l - 1 : 0u) << 8);
+}
+__device__ __forceinline__ uint32_t div_by_freq(uint32_t x, uint32_t m, uint32_t shf) {
+  const uint32_t t = __umulhi(m, x);
+  return (t + ((x - t) >> (shf & 0xFFu))) >> (shf >> 8);
+}
 __host__ __device__ inline uint64_t scratch_bytes(uint32_t steps) { return 4ull * kLanes + 2ull * kLanes * steps; }
 
 __device__ __forceinline__ void flag(int32_t* status, int32_t bits) { atomicOr(status, bits); }
@@ -204,6 +221,10 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
     if (c[r]) {
       P->freq[sidx[r]] = (uint32_t)f[r];
       P->cum[sidx[r]] = (uint32_t)cum;
+      uint32_t dm, ds;
+      div_constants((uint32_t)max(f[r], (int64_t)1), dm, ds);
+      P->rcp[sidx[r]] = dm;
+      P->shf[sidx[r]] = ds;
       if (fits)
         *(GLB uint32_t*)(T.dst + 32 + 4ull * sidx[r]) = (e << 7) | ((uint32_t)f[r] << 16) | 0x80000000u;
       cum += f[r];
@@ -237,14 +258,16 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
 __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
                                                           uint32_t steps, const uint8_t* __restrict__ plans,
                                                           ChunkRec* __restrict__ recs, uint8_t* __restrict__ scratch) {
-  __shared__ uint32_t s_sym[256], s_f[256], s_c[256];
+  __shared__ uint32_t s_sym[256], s_f[256], s_c[256], s_m[256], s_s[256];
   const uint32_t lane = threadIdx.x, cg = blockIdx.x;
   const uint32_t ti = task_of(tasks, n_tasks, cg);
   const bs_encode_task T = tasks[ti];
   const uint64_t per = (uint64_t)kLanes * steps;
   const Plan* P = (const Plan*)(plans + ti * kPlanBytes);
   if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
-  for (uint32_t i = lane; i < 256; i += kWave) { s_sym[i] = P->sym_of_exp[i]; s_f[i] = P->freq[i]; s_c[i] = P->cum[i]; }
+  for (uint32_t i = lane; i < 256; i += kWave) {
+    s_sym[i] = P->sym_of_exp[i]; s_f[i] = P->freq[i]; s_c[i] = P->cum[i]; s_m[i] = P->rcp[i]; s_s[i] = P->shf[i];
+  }
   __syncthreads();
   const uint64_t base = (uint64_t)(cg - T.chunk_begin) * per;
   const uint32_t nc = (uint32_t)min(per, T.n - base);
@@ -256,36 +279,52 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   uint32_t x[2] = {kL, kL};
   uint32_t wpos = (uint32_t)per;
   const uint64_t above = ~((2ull << lane) - 1ull);               // lanes with a higher index
-  for (uint32_t t = nsteps; t-- > 0;) {
+  // this lane's two words of step t, packed (first | second << 16); 0 past the end
+  auto load_step = [&](uint32_t t) -> uint32_t {
     const uint32_t j0 = t * kLanes + 2 * lane;
-    uint32_t wv[2];
-    if (j0 + 1 < nc) {
-      const uint32_t p = src2[j0 / 2];
-      wv[0] = p & 0xFFFFu;
-      wv[1] = p >> 16;
-    } else {
-      wv[0] = j0 < nc ? src1[j0] : 0u;
-      wv[1] = 0u;
+    if (j0 + 1 < nc) return src2[j0 / 2];
+    return j0 < nc ? (uint32_t)src1[j0] : 0u;
+  };
+  // Steps are encoded last to first in blocks of kPre; the next block's words
+  // are loaded while the current block is encoded, so the loads' latency is
+  // not on the encode chain.
+  constexpr uint32_t kPre = 8;
+  const uint32_t nblk = (nsteps + kPre - 1) / kPre;
+  uint32_t cur[kPre];
+#pragma unroll
+  for (uint32_t k = 0; k < kPre; ++k) cur[k] = load_step((nblk - 1) * kPre + k);
+  for (uint32_t b = nblk; b-- > 0;) {
+    uint32_t nxt[kPre];
+#pragma unroll
+    for (uint32_t k = 0; k < kPre; ++k) nxt[k] = b > 0 ? load_step((b - 1) * kPre + k) : 0u;
+#pragma unroll
+    for (int k = (int)kPre - 1; k >= 0; --k) {
+      const uint32_t t = b * kPre + (uint32_t)k;
+      if (t >= nsteps) continue;                                   // uniform: the last block may be short
+      const uint32_t j0 = t * kLanes + 2 * lane;
+      const uint32_t wv[2] = {cur[k] & 0xFFFFu, cur[k] >> 16};
+#pragma unroll
+      for (int g = 1; g >= 0; --g) {
+        const bool active = j0 + g < nc;
+        const uint32_t sym = s_sym[(wv[g] >> 7) & 0xFFu];
+        const uint32_t f = s_f[sym], cm = s_c[sym];
+        uint32_t xv = x[g];
+        const bool emit = active && (uint64_t)xv >= ((uint64_t)f << 20);
+        const uint64_t m = __ballot(emit);
+        if (emit) {
+          words[wpos - 1 - (uint32_t)__popcll(m & above)] = (uint16_t)(xv & 0xFFFFu);
+          xv >>= 16;
+        }
+        wpos -= (uint32_t)__popcll(m);
+        if (active) {
+          const uint32_t q = div_by_freq(xv, s_m[sym], s_s[sym]);   // xv / f
+          xv = (q << 12) + (xv - q * f) + cm;
+        }
+        x[g] = xv;
+      }
     }
 #pragma unroll
-    for (int g = 1; g >= 0; --g) {
-      const bool active = j0 + g < nc;
-      const uint32_t sym = s_sym[(wv[g] >> 7) & 0xFFu];
-      const uint32_t f = s_f[sym], cm = s_c[sym];
-      uint32_t xv = x[g];
-      const bool emit = active && (uint64_t)xv >= ((uint64_t)f << 20);
-      const uint64_t m = __ballot(emit);
-      if (emit) {
-        words[wpos - 1 - (uint32_t)__popcll(m & above)] = (uint16_t)(xv & 0xFFFFu);
-        xv >>= 16;
-      }
-      wpos -= (uint32_t)__popcll(m);
-      if (active) {
-        const uint32_t q = xv / f;
-        xv = (q << 12) + (xv - q * f) + cm;
-      }
-      x[g] = xv;
-    }
+    for (uint32_t k = 0; k < kPre; ++k) cur[k] = nxt[k];
   }
   GLB uint32_t* st = (GLB uint32_t*)chunk;
   st[lane] = x[0];

@@ -132,3 +132,27 @@ def test_malformed_header_raises_value_error(field, value):
         struct.pack_into(fmt, head, o, value)
     with pytest.raises(ValueError):
         bc.info(bytes(head))
+
+
+def test_invariant_divisor_multiply_shift_is_exact():
+    """The GPU encoder divides a 32-bit state by a symbol frequency f (1..4096)
+    with Granlund and Montgomery's multiply-shift (PLDI 1994, Figure 4.1;
+    div_constants / div_by_freq in csrc/bsck_encode_gpu.hip, restated here):
+    it must equal x // f for every divisor, on random dividends and on every
+    quotient boundary near the ends of the 32-bit range."""
+    rng = np.random.default_rng(9)
+    f = np.arange(1, 4097, dtype=np.uint64)
+    l = np.array([0 if v == 1 else int(v - 1).bit_length() for v in f], dtype=np.uint64)
+    m = ((np.uint64(1) << np.uint64(32)) * ((np.uint64(1) << l) - f)) // f + np.uint64(1)
+    assert int(m.max()) < (1 << 32)
+    s1 = np.minimum(l, 1)
+    s2 = np.where(l > 0, l - 1, 0).astype(np.uint64)
+    rand = rng.integers(0, 1 << 32, size=(4096, 64), dtype=np.uint64)
+    q_top = (np.uint64((1 << 32) - 1) // f)[:, None]
+    edges = np.concatenate([f[:, None] * q_top - np.uint64(1), f[:, None] * q_top, np.full((4096, 1), (1 << 32) - 1, np.uint64),
+                            np.zeros((4096, 1), np.uint64), f[:, None] - np.uint64(1), f[:, None], (f[:, None] << np.uint64(20)) - np.uint64(1)],
+                           axis=1) & np.uint64(0xFFFFFFFF)
+    x = np.concatenate([rand, edges], axis=1)
+    t = (m[:, None] * x) >> np.uint64(32)
+    q = (t + ((x - t) >> s1[:, None])) >> s2[:, None]
+    assert np.array_equal(q, x // f[:, None])
