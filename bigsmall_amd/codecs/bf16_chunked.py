@@ -67,6 +67,62 @@ assert ENCODE_TASK_DTYPE.itemsize == 40
 GPU_ENCODE_LANES = 128
 
 
+SPAN_DTYPE = np.dtype([("src", "<u8"), ("dst", "<u8"), ("len", "<u8")])     # bs_span
+
+
+def _encode_bound(n: int, steps: int, cache: dict) -> int:
+    if n not in cache:
+        bound = ctypes.c_uint64()
+        _native.check(_native.lib().bs_chunk_encode_bound(max(n, 1), 2, GPU_ENCODE_LANES, steps, ctypes.byref(bound)),
+                      "bs_chunk_encode_bound")
+        cache[n] = int(bound.value)
+    return cache[n]
+
+
+def _run_encode(dev, tasks: np.ndarray, total_chunks: int, steps: int, stream):
+    """bs_chunk_encode_gpu over `tasks` (ENCODE_TASK_DTYPE, sorted by
+    chunk_begin); waits for it and returns (blob lengths as int64 numpy, the
+    checked status word)."""
+    import torch
+    L = _native.lib()
+    d_tasks = upload_bytes(tasks.view(np.uint8), dev)
+    wb = int(L.bs_chunk_encode_gpu_work_bytes(len(tasks), total_chunks, steps))
+    work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
+    out_len = torch.zeros(len(tasks), dtype=torch.int64, device=dev)
+    st = StatusWord(dev)
+    _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), len(tasks), total_chunks, steps, work.data_ptr(), wb,
+                                        out_len.data_ptr(), st.ptr, stream_ptr(stream, dev)), "bs_chunk_encode_gpu")
+    torch.cuda.synchronize(dev)
+    st.check("bf16_chunked GPU encode")
+    return out_len.cpu().numpy(), st
+
+
+def _pack(arena, src_offs: np.ndarray, lens: np.ndarray, dev, st: StatusWord, stream):
+    """Copy the blobs arena[src_offs[i]:+lens[i]] back to back into a new
+    tensor with one bs_copy_spans launch; returns (tight, offsets)."""
+    import torch
+    if np.any(lens % 16):
+        raise RuntimeError("GPU encoder returned a blob length that is not a multiple of 16")
+    offs = np.zeros(len(lens), np.int64)
+    np.cumsum(lens[:-1], out=offs[1:])
+    total = int(lens.sum())
+    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+        tight = torch.empty(max(total, 256), dtype=torch.uint8, device=dev)     # owned by the copy's stream
+    live = lens > 0
+    if live.any():
+        spans = np.zeros(int(live.sum()), SPAN_DTYPE)
+        spans["src"] = arena.data_ptr() + src_offs[live].astype(np.uint64)
+        spans["dst"] = tight.data_ptr() + offs[live].astype(np.uint64)
+        spans["len"] = lens[live]
+        d_spans = upload_bytes(spans.view(np.uint8), dev)
+        _native.check(_native.lib().bs_copy_spans(d_spans.data_ptr(), len(spans), int(lens.max()), st.ptr,
+                                                  stream_ptr(stream, dev)), "bs_copy_spans")
+        if stream is not None:        # the launch's inputs stay allocated until it has run
+            for t in (d_spans, arena, st.t):
+                t.record_stream(stream)
+    return tight, offs
+
+
 def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: bool = True):
     """Encode device-resident bf16 tensors on the GPU (dense plane mode, 128
     states per chunk); the blobs equal encode_array(words, steps, MODE_DENSE).
@@ -80,7 +136,6 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
     if not tensors:
         return None, []
     dev = require_gpu(tensors[0].device)
-    L = _native.lib()
     per = GPU_ENCODE_LANES * steps
     srcs, slots, cap_total = [], [], 0
     bounds: dict[int, int] = {}
@@ -90,15 +145,10 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
         t = t.contiguous()
         if t.data_ptr() % 4:
             t = t.clone()
-        n = t.numel()
-        if n not in bounds:
-            bound = ctypes.c_uint64()
-            _native.check(L.bs_chunk_encode_bound(max(n, 1), 2, GPU_ENCODE_LANES, steps, ctypes.byref(bound)),
-                          "bs_chunk_encode_bound")
-            bounds[n] = int(bound.value)
+        bound = _encode_bound(t.numel(), steps, bounds)
         srcs.append(t)
-        slots.append((cap_total, bounds[n]))
-        cap_total += (bounds[n] + 255) & ~255
+        slots.append((cap_total, bound))
+        cap_total += (bound + 255) & ~255
     arena = torch.empty(max(cap_total, 256), dtype=torch.uint8, device=dev)
     live = [i for i, t in enumerate(srcs) if t.numel() > 0]
     tasks = np.zeros(len(live), ENCODE_TASK_DTYPE)
@@ -108,38 +158,74 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
         nch = (n + per - 1) // per
         tasks[k] = (srcs[i].data_ptr(), n, arena.data_ptr() + slots[i][0], slots[i][1], chunk, nch)
         chunk += nch
-    lens = [0] * len(srcs)
+    lens = np.zeros(len(srcs), np.int64)
+    st = None
     if live:
-        d_tasks = upload_bytes(tasks.view(np.uint8), dev)
-        wb = int(L.bs_chunk_encode_gpu_work_bytes(len(live), chunk, steps))
-        work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
-        out_len = torch.zeros(len(live), dtype=torch.int64, device=dev)
-        st = StatusWord(dev)
-        _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), len(live), chunk, steps, work.data_ptr(), wb,
-                                            out_len.data_ptr(), st.ptr, stream_ptr(stream, dev)),
-                      "bs_chunk_encode_gpu")
-        torch.cuda.synchronize(dev)
-        st.check("bf16_chunked GPU encode")
-        host_lens = out_len.cpu().tolist()
-        for k, i in enumerate(live):
-            lens[i] = int(host_lens[k])
+        got, st = _run_encode(dev, tasks, chunk, steps, stream)
+        lens[live] = got
     if not compact:
-        return arena, [(slots[i][0], lens[i]) for i in range(len(srcs))]
-    offs, pos = [], 0
-    for ln in lens:
-        if ln % 16:
-            raise RuntimeError(f"GPU encoder returned a blob length {ln} that is not a multiple of 16")
-        offs.append(pos)
-        pos += ln
-    # slots start at multiples of 256 and lengths are multiples of 16: copy as
-    # 8-byte words, in one batched kernel rather than one copy per blob
-    words = arena.view(torch.int64)
-    parts = [words[slots[i][0] // 8:(slots[i][0] + ln) // 8] for i, ln in enumerate(lens) if ln]
+        return arena, [(slots[i][0], int(lens[i])) for i in range(len(srcs))]
+    if st is None:
+        return torch.empty(256, dtype=torch.uint8, device=dev), [(0, 0)] * len(srcs)
+    tight, offs = _pack(arena, np.array([s[0] for s in slots], np.int64), lens, dev, st, stream)
+    return tight, list(zip(offs.tolist(), lens.tolist()))
+
+
+def encode_device_rows(groups, steps: int = DEFAULT_STEPS, stream=None):
+    """encode_device for many equal-size pieces: every row of each contiguous
+    2-D bf16 device tensor in `groups` becomes one blob (e.g. the 256-token
+    blocks of a KV layer), with the task table built without a per-row Python
+    loop. Returns (arena, offsets, lengths): blobs packed back to back in one
+    device uint8 tensor, offsets and lengths as int64 numpy arrays in row order
+    over all groups."""
+    import torch
+    if not groups:
+        return None, np.zeros(0, np.int64), np.zeros(0, np.int64)
+    dev = require_gpu(groups[0].device)
+    per = GPU_ENCODE_LANES * steps
+    bounds: dict[int, int] = {}
+    shapes, cap_total = [], 0
+    for g in groups:
+        if g.dtype != torch.bfloat16 or g.device != dev or g.dim() != 2 or not g.is_contiguous():
+            raise ValueError("encode_device_rows expects contiguous 2-D bf16 tensors on one GPU")
+        rows, n = g.shape
+        if rows and n and (g.data_ptr() % 4 or (rows > 1 and n % 2)):
+            raise ValueError("encode_device_rows needs 4-byte aligned rows (an even row length)")
+        slot = (_encode_bound(n, steps, bounds) + 255) & ~255 if rows and n else 0
+        shapes.append((rows, n, slot, cap_total))
+        cap_total += rows * slot
+    arena = torch.empty(max(cap_total, 256), dtype=torch.uint8, device=dev)
+    n_rows = sum(r for r, *_ in shapes)
+    lens = np.zeros(n_rows, np.int64)
+    src_offs = np.zeros(n_rows, np.int64)
+    parts, chunk, r0 = [], 0, 0
+    for g, (rows, n, slot, base) in zip(groups, shapes):
+        idx = np.arange(rows, dtype=np.uint64)
+        src_offs[r0:r0 + rows] = base + idx.astype(np.int64) * slot
+        if rows and n:
+            nch = (n + per - 1) // per
+            t = np.zeros(rows, ENCODE_TASK_DTYPE)
+            t["src"] = g.data_ptr() + idx * np.uint64(2 * n)
+            t["n"] = n
+            t["dst"] = arena.data_ptr() + np.uint64(base) + idx * np.uint64(slot)
+            t["cap"] = _encode_bound(n, steps, bounds)
+            t["chunk_begin"] = chunk + idx.astype(np.uint32) * np.uint32(nch)
+            t["n_chunks"] = nch
+            parts.append((r0, t))
+            chunk += rows * nch
+        r0 += rows
     if not parts:
-        return torch.empty(256, dtype=torch.uint8, device=dev), list(zip(offs, lens))
-    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
-        tight = torch.cat(parts).view(torch.uint8)
-    return tight, list(zip(offs, lens))
+        return torch.empty(256, dtype=torch.uint8, device=dev), np.zeros(n_rows, np.int64), lens
+    tasks = np.concatenate([t for _, t in parts])
+    if chunk >= 2 ** 32:
+        raise ValueError("encode_device_rows: more than 2^32 chunks in one batch")
+    got, st = _run_encode(dev, tasks, chunk, steps, stream)
+    k = 0
+    for r, t in parts:
+        lens[r:r + len(t)] = got[k:k + len(t)]
+        k += len(t)
+    tight, offs = _pack(arena, src_offs, lens, dev, st, stream)
+    return tight, offs, lens
 
 
 def encode(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:

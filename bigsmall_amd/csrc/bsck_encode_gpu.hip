@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "../../include/bigsmall_hip.h"
 
 namespace {
@@ -435,6 +437,19 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
   }
 }
 
+// Span j of the batch: blockIdx.y strides over its 16-byte vectors.
+__global__ __launch_bounds__(256) void copy_spans_kernel(const bs_span* __restrict__ spans, int32_t* __restrict__ status) {
+  const bs_span S = spans[blockIdx.x];
+  if (((uintptr_t)S.src | (uintptr_t)S.dst | S.len) & 15u) {
+    if (blockIdx.y == 0 && threadIdx.x == 0) flag(status, BS_DEV_ERR_HEADER);
+    return;
+  }
+  const uint64_t nv = S.len / 16;
+  const GLB u32x4* src = (const GLB u32x4*)S.src;
+  GLB u32x4* dst = (GLB u32x4*)S.dst;
+  for (uint64_t i = (uint64_t)blockIdx.y * 256u + threadIdx.x; i < nv; i += 256ull * gridDim.y) dst[i] = src[i];
+}
+
 }  // namespace
 
 extern "C" {
@@ -467,6 +482,16 @@ int bs_chunk_encode_gpu(const bs_encode_task* d_tasks, uint32_t n_tasks, uint32_
   if (total_chunks)
     hipLaunchKernelGGL(enc_assemble_kernel, dim3(total_chunks), dim3(kWave), 0, s, d_tasks, n_tasks, steps, plans,
                        recs, scratch);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
+
+int bs_copy_spans(const bs_span* d_spans, uint32_t n_spans, uint64_t max_len, int32_t* d_status, void* stream) {
+  if (!d_status || (n_spans && !d_spans) || n_spans > 0x7FFFFFFFu) return BS_ERR_ARG;
+  if (n_spans == 0 || max_len == 0) return BS_OK;
+  // about four 16-byte vectors per thread of the longest span, at most 1024 workgroups per span
+  const uint64_t per_block = 256ull * 16ull * 4ull;
+  const uint32_t gy = (uint32_t)std::min<uint64_t>((max_len + per_block - 1) / per_block, 1024ull);
+  hipLaunchKernelGGL(copy_spans_kernel, dim3(n_spans, gy), dim3(256), 0, (hipStream_t)stream, d_spans, d_status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 

@@ -110,8 +110,8 @@ class ChunkBatch:
         tasks = np.zeros(len(jobs), TASK_DTYPE)
         wg = 0
         for i, j in enumerate(jobs):
-            if j.blob_ptr % 16:
-                raise ValueError("BSCK blobs must be 16-byte aligned on the device")
+            if j.blob_ptr % 16 or j.out_ptr % 16:
+                raise ValueError("BSCK blobs and their outputs must be 16-byte aligned on the device")
             tasks[i] = (j.blob_ptr, j.blob_bytes, j.out_ptr, j.n, wg, j.n_chunks)
             wg += (j.n_chunks + per - 1) // per
         self.n_tasks = len(jobs)

@@ -49,6 +49,23 @@ class _LayerBlocks:
     v_blocks: list = field(default_factory=list)
 
 
+def _block_outputs(n_blocks: int, L, dev):
+    """K and V outputs [n_blocks] + block_shape. The decoder writes each block
+    at a 16-byte aligned address, so when a block is not a multiple of 8
+    elements the blocks sit in a buffer with a padded stride (a strided view)."""
+    import torch
+    stride = (L.block_elems + 7) // 8 * 8
+    if stride == L.block_elems:
+        k = torch.empty([n_blocks] + L.block_shape, dtype=torch.bfloat16, device=dev)
+        return k, torch.empty_like(k)
+    inner = [int(np.prod(L.block_shape[d + 1:])) for d in range(len(L.block_shape))]
+    outs = []
+    for _ in range(2):
+        buf = torch.empty(max(n_blocks, 1) * stride, dtype=torch.bfloat16, device=dev)
+        outs.append(buf.as_strided([n_blocks] + L.block_shape, [stride] + inner))
+    return outs[0], outs[1]
+
+
 class CompressedKVCache:
     """Compressed KV storage. device: where get()/get_blocks() materialise tensors."""
 
@@ -121,16 +138,20 @@ class CompressedKVCache:
         block_elems = int(np.prod(block_shape))
         if keys.is_cuda and values.is_cuda:
             # encode on the GPU: the blocks never leave HBM
-            parts = []
+            groups = []
             for t in (keys, values):
                 shape = list(t.shape)
                 blocked = t.detach().reshape(shape[:td] + [nb, block_tokens] + shape[td + 1:])
-                blocked = _block_major(blocked, td)
-                parts += [blocked[i] for i in range(nb)]
-            arena, spans = bf16_chunked.encode_device(parts, steps=_kv_codec.KV_STEPS)
+                groups.append(_block_major(blocked, td).reshape(nb, block_elems))
+            if block_elems % 2 == 0:
+                arena, offs, lens = bf16_chunked.encode_device_rows(groups, steps=_kv_codec.KV_STEPS)
+            else:       # odd blocks are not 4-byte aligned rows: one task per block view
+                arena, spans = bf16_chunked.encode_device([g[i] for g in groups for i in range(nb)],
+                                                          steps=_kv_codec.KV_STEPS)
+                offs, lens = np.array([o for o, _ in spans], np.int64), np.array([n for _, n in spans], np.int64)
             per = bf16_chunked.GPU_ENCODE_LANES * _kv_codec.KV_STEPS
             nch = (block_elems + per - 1) // per
-            ent = [(off, ln, nch, bf16_chunked.MODE_DENSE) for off, ln in spans]
+            ent = [(off, ln, nch, bf16_chunked.MODE_DENSE) for off, ln in zip(offs.tolist(), lens.tolist())]
             self._blocks[layer_idx] = _LayerBlocks(block_shape, block_elems, arena, ent[:nb], ent[nb:])
             self._block_raw += 2 * keys.numel() * 2
             return nb
@@ -172,8 +193,7 @@ class CompressedKVCache:
         for layer_idx, block_ids in requests:
             L = self._blocks[layer_idx]
             ids = [int(i) for i in block_ids]
-            k = torch.empty([len(ids)] + L.block_shape, dtype=torch.bfloat16, device=dev)
-            v = torch.empty_like(k)
+            k, v = _block_outputs(len(ids), L, dev)
             base = L.arena.data_ptr()
             for j, bi in enumerate(ids):
                 for blocks, out in ((L.k_blocks, k), (L.v_blocks, v)):
@@ -185,11 +205,12 @@ class CompressedKVCache:
             ChunkBatch(jobs, dev).launch(st, stream)
         torch.cuda.synchronize(dev)
         st.check("KV blocks")
-        return results
+        return [(k.contiguous(), v.contiguous()) for k, v in results]
 
     def prepare_blocks_multi(self, requests):
         """Allocate outputs and build the batched launch for `requests` once;
-        returns (launch, outputs) where launch(status, stream) decodes again."""
+        returns (launch, outputs) where launch(status, stream) decodes again.
+        Outputs are strided views when a block is not a multiple of 8 elements."""
         import torch
         from .device import ChunkBatch, ChunkJob, require_gpu
         dev = require_gpu(self.device)
@@ -197,8 +218,7 @@ class CompressedKVCache:
         for layer_idx, block_ids in requests:
             L = self._blocks[layer_idx]
             ids = [int(i) for i in block_ids]
-            k = torch.empty([len(ids)] + L.block_shape, dtype=torch.bfloat16, device=dev)
-            v = torch.empty_like(k)
+            k, v = _block_outputs(len(ids), L, dev)
             for j, bi in enumerate(ids):
                 for blocks, out in ((L.k_blocks, k), (L.v_blocks, v)):
                     off, nb, nch, mode = blocks[bi]

@@ -134,6 +134,20 @@ uint64_t bs_chunk_encode_gpu_work_bytes(uint32_t n_tasks, uint64_t total_chunks,
 int bs_chunk_encode_gpu(const bs_encode_task *d_tasks, uint32_t n_tasks, uint32_t total_chunks, uint32_t steps,
                         void *d_work, uint64_t work_bytes, uint64_t *d_out_len, int32_t *d_status, void *stream);
 
+/* Copy n_spans device byte ranges on `stream`, e.g. to pack the encoder's
+ * blobs (written at their worst-case slots) back to back. Every src, dst and
+ * len must be a multiple of 16 (a span that is not sets BS_DEV_ERR_HEADER in
+ * *d_status and is skipped); spans must not overlap one another's dst.
+ * max_len (>= every len) sizes the launch. Replaces the host byte
+ * concatenation that frames KV entries (bigsmall/codecs/kv_cache.py:74-83)
+ * for blobs that stay in HBM. */
+typedef struct {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint64_t len;
+} bs_span;
+int bs_copy_spans(const bs_span *d_spans, uint32_t n_spans, uint64_t max_len, int32_t *d_status, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* The reference's rANS-family bf16 formats, decoded on the GPU:
  *   bf16_parallel_v1      (bigsmall/codecs/bf16_parallel.py:262-352; the entry

@@ -118,3 +118,79 @@ def test_kv_cache_device_tensors_encode_on_gpu():
     assert torch.equal(k2.cpu().view(torch.int16), k.unsqueeze(0).view(torch.int16))
     assert torch.equal(v2.cpu().view(torch.int16), v.unsqueeze(0).view(torch.int16))
     assert 0.6 < c.compression_ratio() < 0.85
+
+
+def test_encode_device_rows_matches_per_row_encoding():
+    """encode_device_rows (the task table built per group, blobs packed by
+    bs_copy_spans) gives every row the host encoder's dense-mode blob, packed
+    back to back in row order; also on a side stream."""
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(31)
+    shapes = [(12, 262_144), (0, 64), (5, 2), (3, 3 * 128 * 256 + 10)]
+    words = [np.stack([_words(rng, "kv", n) for _ in range(r)]) if r else np.zeros((0, n), np.uint16)
+             for r, n in shapes]
+    groups = [torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).to(dev) for w in words]
+    side = torch.cuda.Stream()
+    for stream in (None, side):
+        _say(f"[enc] rows, stream={'side' if stream else 'current'}")
+        arena, offs, lens = bc.encode_device_rows(groups, steps=256, stream=stream)
+        torch.cuda.synchronize()
+        host = arena.cpu().numpy()
+        rows = [w[i] for w in words for i in range(w.shape[0])]
+        assert len(offs) == len(lens) == len(rows)
+        pos = 0
+        for w, off, ln in zip(rows, offs.tolist(), lens.tolist()):
+            want = bc.encode_array(w, steps=256, mode=bc.MODE_DENSE, lanes=128)
+            assert off == pos and ln == len(want)
+            assert host[off:off + ln].tobytes() == want
+            pos += ln
+
+
+def test_copy_spans_packs_and_rejects_misaligned():
+    """bs_copy_spans copies every 16-byte aligned span exactly, leaves bytes
+    outside the spans alone, and flags (and skips) a misaligned span."""
+    from bigsmall_amd import _native
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(5)
+    src_h = rng.integers(0, 256, 4 << 20, dtype=np.uint8)
+    src = torch.from_numpy(src_h).to(dev)
+    dst = torch.full((4 << 20,), 0xAB, dtype=torch.uint8, device=dev)
+    lens = [16, 32, 4096, 1 << 20, 48, 3 * 65536 + 16, 0]
+    spans = np.zeros(len(lens) + 1, bc.SPAN_DTYPE)
+    want = np.full(4 << 20, 0xAB, np.uint8)
+    s_off, d_off = 0, 4 << 20           # sources ascending, destinations descending: no overlap
+    for i, ln in enumerate(lens):
+        d_off -= ln + 512
+        d_off -= d_off % 16
+        spans[i] = (src.data_ptr() + s_off, dst.data_ptr() + d_off, ln)
+        want[d_off:d_off + ln] = src_h[s_off:s_off + ln]
+        s_off += ln + 256
+    assert s_off <= (4 << 20) and d_off >= 64
+    spans[len(lens)] = (src.data_ptr() + 8, dst.data_ptr(), 32)          # misaligned src
+    d_spans = upload_bytes(spans.view(np.uint8), dev)
+    st = StatusWord(dev)
+    _say("[enc] bs_copy_spans")
+    _native.check(_native.lib().bs_copy_spans(d_spans.data_ptr(), len(spans), max(lens), st.ptr,
+                                              torch.cuda.current_stream().cuda_stream), "bs_copy_spans")
+    torch.cuda.synchronize()
+    assert int(st.t.item()) == _native.BS_DEV_ERR_HEADER
+    assert np.array_equal(dst.cpu().numpy(), want)
+
+
+def test_kv_set_blocks_odd_block_size():
+    """Blocks whose element count is odd (not 4-byte aligned rows) take the
+    per-block-view encode path and still round-trip."""
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache
+    g = torch.Generator().manual_seed(4)
+    k = torch.randn(1, 514, 3, generator=g).bfloat16()
+    v = torch.randn(1, 514, 3, generator=g).bfloat16()
+    c = CompressedKVCache(device="cuda")
+    _say("[enc] kv set_blocks with 771-element blocks")
+    assert c.set_blocks(0, k.cuda(), v.cuda(), block_tokens=257) == 2
+    kb, vb = c.get_blocks(0, [1, 0])
+    for j, b in enumerate([1, 0]):
+        assert torch.equal(kb[j].cpu().view(torch.int16), k[:, b * 257:(b + 1) * 257].view(torch.int16))
+        assert torch.equal(vb[j].cpu().view(torch.int16), v[:, b * 257:(b + 1) * 257].view(torch.int16))
