@@ -1,0 +1,107 @@
+// Zstandard decoding on the GPU, for the reference's zstd-coded container
+// entries:
+//   codec "zstd"            the whole tensor is one zstd frame
+//                           (bigsmall/codecs/generic.py:15-18, bigsmall/decoder.py:80-81);
+//   codec "special/lowcard" a table of <= 255 distinct element values and a
+//                           zstd frame of one uint8 index per element
+//                           (bigsmall/codecs/special.py:23-85);
+//   codec "zstd_xor_delta"  a zstd frame of XOR differences to a base tensor
+//                           (bigsmall/decoder.py:88-90, 190-198).
+//
+// One 64-lane workgroup per task decodes all frames of its input with the
+// team-parallel decoder of zstd_core.h: tables in LDS (about 15 KB), literals
+// of the current block in a 128 KiB slice of the work buffer, matches copied
+// by all lanes. Zstandard is a sequential format (each match may copy bytes
+// of the one before), so a frame is not split across workgroups; the
+// reference's zstd entries are small (norm-weight indices, integer buffers)
+// and many of them go in one launch.
+//
+// lut_expand_kernel turns lowcard indices into element bytes.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "../../include/bigsmall_hip.h"
+#include "zstd_core.h"
+
+namespace {
+
+struct DevTeam {
+  static constexpr uint32_t size = 64;
+  __device__ uint32_t lane() const { return threadIdx.x; }
+  __device__ void sync() const { __syncthreads(); }
+};
+
+__device__ int32_t status_bits(int32_t e) {
+  switch (e) {
+    case bs_zstd::kOk: return 0;
+    case bs_zstd::kErrTruncated: return BS_DEV_ERR_BOUNDS;
+    case bs_zstd::kErrFormat: return BS_DEV_ERR_HEADER;
+    case bs_zstd::kErrOutput: return BS_DEV_ERR_COUNT;
+    default: return BS_DEV_ERR_STREAM;
+  }
+}
+
+__global__ __launch_bounds__(64) void zstd_kernel(const bs_zstd_task* __restrict__ tasks, uint8_t* __restrict__ work,
+                                                  uint64_t* __restrict__ out_len, int32_t* __restrict__ status) {
+  __shared__ bs_zstd::ZState z;
+  const bs_zstd_task T = tasks[blockIdx.x];
+  uint8_t* lit = work + (uint64_t)blockIdx.x * bs_zstd::kBlockMax;
+  uint64_t got = 0;
+  int32_t e = bs_zstd::kErrFormat;
+  if (T.src && (T.dst || T.dst_len == 0)) {
+    e = bs_zstd::zstd_frames(DevTeam{}, z, T.src, T.src_len, T.dst, T.dst_len, lit, got);
+    if (e == bs_zstd::kOk && got != T.dst_len) e = bs_zstd::kErrOutput;
+  }
+  if (threadIdx.x == 0) {
+    out_len[blockIdx.x] = e ? 0 : got;
+    if (e) atomicOr(status, status_bits(e));
+  }
+}
+
+__global__ __launch_bounds__(256) void lut_expand_kernel(const uint8_t* __restrict__ idx, uint64_t n,
+                                                         const uint8_t* __restrict__ lut, uint32_t n_lut,
+                                                         uint32_t item_bytes, uint8_t* __restrict__ out,
+                                                         int32_t* __restrict__ status) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  bool bad = false;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t v = idx[i];
+    if (v >= n_lut) {
+      bad = true;
+      continue;
+    }
+    for (uint32_t b = 0; b < item_bytes; ++b) out[i * item_bytes + b] = lut[v * item_bytes + b];
+  }
+  if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(status, BS_DEV_ERR_COUNT);
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t bs_zstd_work_bytes(uint32_t n_tasks) { return (uint64_t)n_tasks * bs_zstd::kBlockMax; }
+
+int bs_zstd_decode(const bs_zstd_task* d_tasks, uint32_t n_tasks, void* d_work, uint64_t work_bytes,
+                   uint64_t* d_out_len, int32_t* d_status, void* stream) {
+  if (!d_status || (n_tasks && (!d_tasks || !d_work || !d_out_len)) || n_tasks > 0x7FFFFFFFu) return BS_ERR_ARG;
+  if (n_tasks == 0) return BS_OK;
+  if (work_bytes < bs_zstd_work_bytes(n_tasks)) return BS_ERR_ARG;
+  hipLaunchKernelGGL(zstd_kernel, dim3(n_tasks), dim3(64), 0, (hipStream_t)stream, d_tasks, (uint8_t*)d_work,
+                     d_out_len, d_status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
+
+int bs_lut_expand(const uint8_t* d_idx, uint64_t n, const uint8_t* d_lut, uint32_t n_lut, uint32_t item_bytes,
+                  uint8_t* d_out, int32_t* d_status, void* stream) {
+  if (!d_status || item_bytes == 0 || item_bytes > 8 || n_lut > 256 || (n && (!d_idx || !d_lut || !d_out)))
+    return BS_ERR_ARG;
+  if (n == 0) return BS_OK;
+  const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(lut_expand_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, d_idx, n, d_lut,
+                     n_lut, item_bytes, d_out, d_status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
+
+}  // extern "C"

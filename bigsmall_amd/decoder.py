@@ -23,7 +23,8 @@ from typing import Optional
 import numpy as np
 
 from . import container, engine
-from .codecs import _refstreams, bf16_chunked
+from .codecs import _refstreams, bf16_chunked, zstd_gpu
+from .formats import DTYPE_BYTES
 from .streaming import layer_index
 
 _DTYPE_TO_NUMPY = {
@@ -53,6 +54,11 @@ def _decode_blob(t: dict, blob: bytes):
     if codec == "bf16_parallel_v1":
         from . import kernels
         return kernels.decode_bf16_parallel(blob, extras, n)
+    if codec in engine.ZSTD_CODECS:                  # zstd_xor_delta: the XOR delta itself (decoder.py:88-90)
+        ib = DTYPE_BYTES.get(t["dtype"])
+        return zstd_gpu.decode_zstd(blob, extras, n * ib if ib else None)
+    if codec == "special":
+        return zstd_gpu.decode_special(blob, extras, n * int(extras.get("item_bytes", 1)))
     return _refstreams.decode_host(codec, blob, n)
 
 

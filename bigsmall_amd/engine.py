@@ -15,14 +15,17 @@ one launch per codec family):
          bf16_chunked_v1 / fp8_chunked_v1 entry of the group,
        - bs_refcodec_decode per reference-format entry (bf16_parallel_v1,
          bf16_se_tans, bf16_se_single_kernel),
+       - one bs_zstd_decode launch for the group's zstd frames (`zstd`,
+         `zstd_xor_delta` and the index streams of `special` lowcard
+         entries), then bs_lut_expand per lowcard entry,
        - device-to-device copies for `raw` entries,
      writing straight into freshly allocated output tensors;
   3. tied entries become copies of their master after it is decoded.
 So decoding group g overlaps the host->device copy of group g+1.
 
 Codecs whose bitstream is defined by libraries this engine does not carry
-(constriction's bf16_se_rans / bf16_se_ac / fp8_cat_ac / ..., zstd-based
-`special`/`zstd`) raise BigSmallVersionError naming the codec.
+(constriction's bf16_se_rans / bf16_se_ac / fp8_cat_ac / ..., blosc2's
+`special` wpe_delta) raise BigSmallVersionError naming the codec.
 """
 from __future__ import annotations
 
@@ -35,6 +38,7 @@ import numpy as np
 
 from .codecs import _refstreams
 from .codecs import bf16_chunked
+from .codecs import zstd_gpu
 from .container import tensor_numel
 from .device import ChunkBatch, ChunkJob, StatusWord, require_gpu
 from .exceptions import BigSmallVersionError
@@ -48,8 +52,9 @@ UNSUPPORTED = {
     "fp8_cat_ac": "constriction range coder", "fp4_cat_ac": "constriction range coder",
     "fp16_se_ac": "constriction range coder", "fp32_se_ac": "constriction range coder",
     "bf16_sparsity_v1": "constriction-coded populations", "fp2_residual_v1": "constriction-coded residual",
-    "special": "zstd/blosc2", "zstd": "zstd", "zstd_xor_delta": "zstd",
+    "special": "blosc2 (wpe_delta)",
 }
+ZSTD_CODECS = {"zstd", "zstd_xor_delta"}
 
 
 def entry_numel(t: dict) -> int:
@@ -57,15 +62,22 @@ def entry_numel(t: dict) -> int:
     return tensor_numel(t) if t["shape"] else 1
 
 
+def is_lowcard(t: dict) -> bool:
+    return t["codec"] == "special" and (t.get("extra") or {}).get("special_kind") == "lowcard"
+
+
 def check_supported(t: dict) -> None:
     codec = t["codec"]
-    if codec in ("raw", "tied_ref") or codec in BSCK_CODECS or codec in REF_CODECS:
+    if codec in ("raw", "tied_ref") or codec in BSCK_CODECS or codec in REF_CODECS or codec in ZSTD_CODECS:
+        return
+    if is_lowcard(t):
         return
     from . import __version__
     detail = f"file references codec {codec!r}"
     if codec in UNSUPPORTED:
         detail += f", whose bitstream is defined by {UNSUPPORTED[codec]}; the MI355X engine decodes " \
-                  f"bf16_chunked_v1, fp8_chunked_v1, bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel and raw"
+                  f"bf16_chunked_v1, fp8_chunked_v1, bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel, " \
+                  f"zstd, zstd_xor_delta, special (lowcard) and raw"
     raise BigSmallVersionError(required="newer-than-installed", installed=__version__, detail=detail)
 
 
@@ -189,6 +201,7 @@ class GroupDecoder:
         jobs = []
         refs = []
         raws = []
+        zst = zstd_gpu.ZstdLaunch(self.device)
         base = d_span.data_ptr()
         for t in entries:
             if t["codec"] == "tied_ref":
@@ -231,6 +244,12 @@ class GroupDecoder:
                     continue
                 plan = _refstreams.PARSERS[codec](bytes(host[off:off + nb]), n)
                 refs.append((_refstreams.RefLaunch(plan, base + off, self.device), o))
+            elif codec in ZSTD_CODECS:
+                if nb == 0:
+                    raise ValueError(f"{t['name']}: empty {codec} blob")
+                zst.add_frame(base + off, nb, o.data_ptr(), o.numel() * o.element_size())
+            else:                                        # special/lowcard (check_supported)
+                zst.add_lowcard(base + off, host[off:off + nb], o.data_ptr(), o.numel(), o.element_size())
         self.stream.wait_event(copied)
         d_span.record_stream(self.stream)
         for o, off, nb in raws:
@@ -246,6 +265,9 @@ class GroupDecoder:
         for launch, o in refs:
             keep.append(launch)
             launch.launch(o.data_ptr(), status.ptr, int(self.stream.cuda_stream))
+        if zst.tasks or zst.expands:
+            zst.launch(status, self.stream)
+            keep.append(zst.keep)
         for t in entries:
             if t["codec"] != "tied_ref":
                 continue

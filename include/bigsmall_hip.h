@@ -218,6 +218,40 @@ int bs_refcodec_decode_serial(const bs_se_stream *d_streams, uint32_t n_streams,
                               const uint32_t *d_mant_tables, uint32_t n_tables, uint16_t *d_out, uint64_t n_out,
                               void *d_work, uint64_t work_bytes, int32_t *d_status, void *stream);
 
+/* ------------------------------------------------------------------------ */
+/* Zstandard (RFC 8878) frames on the GPU, for the reference's zstd-coded
+ * entries: codec "zstd" (bigsmall/codecs/generic.py:15-18, called from
+ * bigsmall/decoder.py:80-81), the index stream of "special" lowcard entries
+ * (bigsmall/codecs/special.py:67-85) and "zstd_xor_delta" deltas
+ * (bigsmall/decoder.py:88-90, 190-198). The reference decodes these with the
+ * zstandard package on the host. */
+typedef struct {
+    const uint8_t *src;   /* one or more zstd (or skippable) frames, back to back (device) */
+    uint64_t src_len;
+    uint8_t *dst;         /* decoded bytes (device); may be NULL when dst_len is 0 */
+    uint64_t dst_len;     /* the exact decoded size */
+} bs_zstd_task;
+
+/* Device scratch bytes bs_zstd_decode needs (128 KiB per task). */
+uint64_t bs_zstd_work_bytes(uint32_t n_tasks);
+
+/* Decode every task on `stream`, one workgroup per task. d_out_len[i]
+ * receives task i's decoded byte count (0 if it failed). Failures OR-ed into
+ * *d_status: BS_DEV_ERR_HEADER (bad magic, reserved bits, a dictionary
+ * frame), BS_DEV_ERR_BOUNDS (truncated input), BS_DEV_ERR_STREAM (invalid
+ * table or bitstream, a match before the frame start), BS_DEV_ERR_COUNT (the
+ * output is not dst_len bytes, or a frame's is not its recorded content size). Content
+ * checksums are skipped, not checked. Dictionaries are not supported. */
+int bs_zstd_decode(const bs_zstd_task *d_tasks, uint32_t n_tasks, void *d_work, uint64_t work_bytes,
+                   uint64_t *d_out_len, int32_t *d_status, void *stream);
+
+/* out[i * item_bytes + b] = lut[idx[i] * item_bytes + b] for i < n: the
+ * lowcard expansion unique_bytes[idx] of bigsmall/codecs/special.py:79-82.
+ * An index >= n_lut sets BS_DEV_ERR_COUNT and leaves its element unwritten.
+ * 1 <= item_bytes <= 8, n_lut <= 256. */
+int bs_lut_expand(const uint8_t *d_idx, uint64_t n, const uint8_t *d_lut, uint32_t n_lut, uint32_t item_bytes,
+                  uint8_t *d_out, int32_t *d_status, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,11 +97,15 @@ def test_info_and_verify_fast(container_file):
 
 
 def test_unsupported_codec_raises_version_error():
-    for codec in ["bf16_se_rans", "bf16_se_ac", "fp8_cat_ac", "zstd", "something_new"]:
+    for codec in ["bf16_se_rans", "bf16_se_ac", "fp8_cat_ac", "special", "something_new"]:
         with pytest.raises(BigSmallVersionError):
             engine.check_supported({"codec": codec, "name": "x"})
-    for codec in ["raw", "tied_ref", "bf16_chunked_v1", "bf16_parallel_v1", "bf16_se_tans", "bf16_se_single_kernel"]:
+    with pytest.raises(BigSmallVersionError, match="blosc2"):
+        engine.check_supported({"codec": "special", "name": "x", "extra": {"special_kind": "wpe_delta"}})
+    for codec in ["raw", "tied_ref", "bf16_chunked_v1", "bf16_parallel_v1", "bf16_se_tans", "bf16_se_single_kernel",
+                  "zstd", "zstd_xor_delta"]:
         engine.check_supported({"codec": codec, "name": "x"})
+    engine.check_supported({"codec": "special", "name": "x", "extra": {"special_kind": "lowcard"}})
 
 
 def test_registry_plugin_api_and_smallest_wins(monkeypatch):
