@@ -652,6 +652,89 @@ def run_streaming(args) -> dict:
                            "frac": round(floor_ms / ms_layer, 4)}}
 
 
+def run_zstd(args) -> dict:
+    """The reference's zstd-coded entries, decoded on the GPU from HBM:
+    (a) the 65 RMSNorm weights of a Llama-3-8B-shaped model (4096 bf16 each,
+    1 + N(0, 0.01)) as the reference's encoder writes them, special/lowcard
+    with a level-19 zstd index frame (bigsmall/codecs/special.py:23-64), all in
+    one bs_zstd_decode + bs_lut_expand launch pair; (b) one zstd_xor_delta frame
+    of a 4096x4096 bf16 fine-tune that differs from its base in 1% of the
+    elements (the reference's delta test shape, tests/test_delta.py:22-30),
+    compressed at level 19. Beside each, libzstd (the format's reference
+    implementation) on one host thread."""
+    import torch
+    from oracle import zstd_lib
+    from bigsmall_amd.codecs.zstd_gpu import ZstdLaunch
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    rng = np.random.default_rng(6)
+
+    def bf16(n, mean=0.0, std=0.02):
+        x = (mean + rng.standard_normal(n) * std).astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
+
+    norms = [bf16(4096, 1.0, 0.01).tobytes() for _ in range(65)]
+    blobs = [zstd_lib.encode_lowcard(r, 2)[0] for r in norms]
+    t0 = time.perf_counter()
+    for b, r in zip(blobs, norms):
+        assert zstd_lib.decode_lowcard(b, len(r)) == r
+    cpu_norms_ms = (time.perf_counter() - t0) * 1e3
+    offs = np.cumsum([0] + [len(b) for b in blobs])
+    d_blobs = upload_bytes(b"".join(blobs), dev)
+    out = torch.empty(65 * 4096, dtype=torch.bfloat16, device=dev)
+    z = ZstdLaunch(dev)
+    for i, b in enumerate(blobs):
+        z.add_lowcard(d_blobs.data_ptr() + int(offs[i]), b, out[i * 4096:].data_ptr(), 4096, 2)
+    st = StatusWord(dev)
+    z.launch(st, stream)
+    torch.cuda.synchronize()
+    st.check("norms")
+    norms_ms = _timed(lambda: z.launch(st, stream), max(args.steps, 20), stream)
+    st.check("norms timed")
+    assert out.view(torch.int16).cpu().numpy().view(np.uint16).tobytes() == b"".join(norms)
+    log(f"[zstd] 65 lowcard norms: {norms_ms * 1e3:.1f} us per launch pair on GPU; "
+        f"libzstd + numpy on one host thread {cpu_norms_ms * 1e3:.0f} us")
+
+    base = bf16(4096 * 4096)
+    ft = base.copy()
+    m = rng.random(base.size) < 0.01
+    ft[m] ^= rng.integers(1, 8, int(m.sum())).astype(np.uint16)
+    delta = (ft ^ base).tobytes()
+    frame = zstd_lib.compress(delta, 19)
+    t0 = time.perf_counter()
+    assert zstd_lib.decompress(frame, len(delta)) == delta
+    cpu_delta_ms = (time.perf_counter() - t0) * 1e3
+    d_frame = upload_bytes(frame, dev)
+    dst = torch.empty(len(delta), dtype=torch.uint8, device=dev)
+    zd = ZstdLaunch(dev)
+    zd.add_frame(d_frame.data_ptr(), len(frame), dst.data_ptr(), len(delta))
+    zd.launch(st, stream)
+    torch.cuda.synchronize()
+    st.check("delta")
+    delta_ms = _timed(lambda: zd.launch(st, stream), 2, stream)
+    st.check("delta timed")
+    assert dst.cpu().numpy().tobytes() == delta
+    log(f"[zstd] 4096x4096 1% delta frame: {delta_ms:.1f} ms on GPU ({len(delta) / delta_ms / 1e6:.3f} GB/s); "
+        f"libzstd one thread {cpu_delta_ms:.1f} ms")
+    return {"metric": "microseconds to decode the 65 lowcard (zstd) RMSNorm entries of a Llama-3-8B-shaped model "
+                      "on 1 MI355X",
+            "value": round(norms_ms * 1e3, 2), "unit": "us", "n_gpus": 1, "ms_per_step": round(norms_ms, 4),
+            "higher_is_better": False, "dtype": "u8",
+            "data": "synthetic: seeded 1 + N(0, 0.01) bf16 norms; 1% XOR delta of N(0, 0.02) bf16; frames by libzstd",
+            "host": host_cpu_info(),
+            "config": {"workload": "zstd_lowcard_norms_65x4096", "frames": len(blobs),
+                       "compressed_bytes": int(offs[-1]), "decoded_bytes": 65 * 4096 * 2},
+            "roofline": {"bound": "latency (one workgroup per frame; zstd is sequential within a frame)",
+                         "achieved": None, "peak": None, "unit": None, "frac": None},
+            "delta_frame": {"decoded_bytes": len(delta), "frame_bytes": len(frame), "ms": round(delta_ms, 2),
+                            "GBps": round(len(delta) / delta_ms / 1e6, 4),
+                            "cpu_libzstd_ms_1_thread": round(cpu_delta_ms, 2)},
+            "cpu_baseline": {"value": round(cpu_norms_ms * 1e3, 1), "unit": "us", "cores": 1, "kind": "reference",
+                             "sample": "the same 65 lowcard blobs decoded by libzstd + numpy indexing "
+                                       f"(libzstd {zstd_lib.version()})"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -664,10 +747,12 @@ def main():
                     help="layer workload only: set this seeded share of every matrix's elements to +0.0 "
                          "(a pruned layer; such tensors take the compact plane mode)")
     ap.add_argument("--layers", type=int, default=8, help="streaming workload: decoder layers of the model")
-    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3", "streaming"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "model", "kv", "refcodecs", "c3", "streaming", "zstd"],
+                    default="layer",
                     help="layer (default: the headline line), model (full 8B-shaped model), kv (KV-cache "
                          "blocks), refcodecs (the reference's own formats on the C0 tensor), c3 (stress "
-                         "tensors), streaming (BigSmallStreamingModel forward from a .bs file)")
+                         "tensors), streaming (BigSmallStreamingModel forward from a .bs file), zstd (the "
+                         "reference's zstd-coded entries: lowcard norms and a delta frame)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -682,7 +767,7 @@ def main():
         return
     if args.workload != "layer":
         run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs, "c3": run_c3,
-               "streaming": run_streaming}[args.workload]
+               "streaming": run_streaming, "zstd": run_zstd}[args.workload]
         print(json.dumps(run(args)), flush=True)
         return
     from bigsmall_amd.codecs import bf16_chunked as bc

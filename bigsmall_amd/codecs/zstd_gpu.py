@@ -22,6 +22,8 @@ from .. import _native
 from ..device import StatusWord, require_gpu, stream_ptr, upload_bytes
 
 ZSTD_TASK_DTYPE = np.dtype([("src", "<u8"), ("src_len", "<u8"), ("dst", "<u8"), ("dst_len", "<u8")])
+LUT_TASK_DTYPE = np.dtype([("idx", "<u8"), ("lut", "<u8"), ("out", "<u8"), ("n", "<u8"), ("n_lut", "<u4"),
+                           ("item_bytes", "<u4")])
 ZSTD_MAGIC = 0xFD2FB528
 
 
@@ -74,7 +76,7 @@ def frame_content_size(blob) -> int | None:
 
 class ZstdLaunch:
     """A set of zstd frames (and lowcard expansions) decoded by one
-    bs_zstd_decode launch and one bs_lut_expand launch per lowcard entry.
+    bs_zstd_decode launch, then one bs_lut_expand launch for every lowcard entry.
     Every pointer is a device address; the caller keeps the memory alive until
     the launch has run (`keep` holds what this object allocates)."""
 
@@ -83,7 +85,8 @@ class ZstdLaunch:
         self.tasks: list[tuple[int, int, int, int]] = []
         self.expands: list[tuple[int, int, int, int, int, int]] = []
         self.keep: list = []
-        self.out_len = None               # per-task decoded bytes (device int64), set by launch()
+        self.out_len = None               # per-task decoded bytes (device int64), set by prepare()
+        self._prepared = None
 
     def __len__(self) -> int:
         return len(self.tasks)
@@ -109,22 +112,44 @@ class ZstdLaunch:
         self.add_frame(blob_ptr + lc.idx_off, lc.idx_len, idx.data_ptr(), n_elem)
         self.expands.append((idx.data_ptr(), n_elem, blob_ptr + lc.lut_off, lc.n_unique, item_bytes, out_ptr))
 
-    def launch(self, status: StatusWord, stream=None) -> None:
+    def prepare(self) -> None:
+        """Build the device task arrays (once; later launches reuse them)."""
         import torch
+        if getattr(self, "_prepared", None) is not None:
+            return
         L = _native.lib()
-        s = stream_ptr(stream, self.device)
+        zst = None
         if self.tasks:
             t = np.array(self.tasks, dtype=np.uint64).view(ZSTD_TASK_DTYPE).reshape(-1)
             d_tasks = upload_bytes(t.view(np.uint8), self.device)
             wb = int(L.bs_zstd_work_bytes(len(self.tasks)))
             work = torch.empty(wb, dtype=torch.uint8, device=self.device)
-            out_len = torch.empty(len(self.tasks), dtype=torch.int64, device=self.device)
-            self.keep += [d_tasks, work, out_len]
-            self.out_len = out_len
+            self.out_len = torch.empty(len(self.tasks), dtype=torch.int64, device=self.device)
+            self.keep += [d_tasks, work, self.out_len]
+            zst = (d_tasks, work, wb)
+        luts = []
+        if self.expands:
+            t = np.zeros(len(self.expands), LUT_TASK_DTYPE)
+            for i, (idx_ptr, n, lut_ptr, n_lut, ib, out_ptr) in enumerate(self.expands):
+                t[i] = (idx_ptr, lut_ptr, out_ptr, n, n_lut, ib)
+            for c in range(0, len(t), 65535):           # grid.y limit of one launch
+                part = t[c:c + 65535]
+                d_lut = upload_bytes(part.view(np.uint8), self.device)
+                self.keep.append(d_lut)
+                luts.append((d_lut, len(part), int(part["n"].max())))
+        self._prepared = (zst, luts)
+
+    def launch(self, status: StatusWord, stream=None) -> None:
+        self.prepare()
+        L = _native.lib()
+        s = stream_ptr(stream, self.device)
+        zst, luts = self._prepared
+        if zst is not None:
+            d_tasks, work, wb = zst
             _native.check(L.bs_zstd_decode(d_tasks.data_ptr(), len(self.tasks), work.data_ptr(), wb,
-                                           out_len.data_ptr(), status.ptr, s), "bs_zstd_decode")
-        for idx_ptr, n, lut_ptr, n_lut, ib, out_ptr in self.expands:
-            _native.check(L.bs_lut_expand(idx_ptr, n, lut_ptr, n_lut, ib, out_ptr, status.ptr, s), "bs_lut_expand")
+                                           self.out_len.data_ptr(), status.ptr, s), "bs_zstd_decode")
+        for d_lut, n_tasks, max_n in luts:
+            _native.check(L.bs_lut_expand(d_lut.data_ptr(), n_tasks, max_n, status.ptr, s), "bs_lut_expand")
 
 
 def _decode_host_bytes(blob: bytes, n_bytes: int, lowcard_item_bytes: int = 0) -> bytes:

@@ -88,28 +88,53 @@ struct FwdBits {
 // the stream is read from its last byte towards its first; the highest set
 // bit of the last byte marks the end and is skipped. Reading n bits yields the
 // next n unread bits from the top as one number; past the start of the stream
-// the missing bits read as zeros and `bits` goes negative (overflow).
+// the missing bits read as zeros and `bits` goes negative (overflow). The next
+// unread bits sit left-aligned in a 64-bit register, refilled a byte at a time.
 struct BackBits {
   const uint8_t* p;
-  uint64_t len;
-  int64_t bits;      // bits [0, bits) are unread; bit b is bit (b & 7) of p[b >> 3]
+  int64_t bits;      // bits [0, bits) of the stream are unread; bit b is bit (b & 7) of p[b >> 3]
+  uint64_t acc;      // the top `have` unread bits, most significant first; zeros below
+  uint32_t have;
+  uint64_t lo;       // bytes [0, lo) are not yet in acc
   __host__ __device__ bool init(const uint8_t* q, uint64_t n) {
     p = q;
-    len = n;
     bits = 0;
+    acc = 0;
+    have = 0;
+    lo = 0;
     if (n == 0 || q[n - 1] == 0) return false;
-    bits = (int64_t)(n - 1) * 8 + (int64_t)highbit(q[n - 1]);
+    const uint32_t hb = highbit(q[n - 1]);
+    bits = (int64_t)(n - 1) * 8 + hb;
+    acc = hb ? (uint64_t)(q[n - 1] & ((1u << hb) - 1u)) << (64 - hb) : 0ull;
+    have = hb;
+    lo = n - 1;
+    refill();
     return true;
   }
-  __host__ __device__ uint32_t peek(uint32_t n) const {      // n <= 32
-    if (n == 0 || bits <= 0) return 0;
-    const int64_t start = bits - (int64_t)n;
-    if (start >= 0) return (uint32_t)((load_le(p, len, (uint64_t)start >> 3) >> (start & 7)) & mask64(n));
-    return (uint32_t)((load_le(p, len, 0) & mask64((uint32_t)bits)) << (uint32_t)(-start));
+  __host__ __device__ void refill() {         // as many whole bytes as fit, loaded together
+    if (have > 56 || lo == 0) return;
+    const uint64_t want = (64 - have) >> 3;
+    const uint32_t k = (uint32_t)(lo < want ? lo : want);
+    uint64_t v = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i)
+      if (i < k) v |= (uint64_t)p[lo - 1 - i] << (56 - 8 * i);
+    acc |= v >> have;
+    have += 8 * k;
+    lo -= k;
+  }
+  __host__ __device__ uint32_t peek(uint32_t n) {             // n <= 32
+    if (have < n) refill();
+    return n ? (uint32_t)(acc >> (64 - n)) : 0u;
+  }
+  __host__ __device__ void skip(uint32_t n) {                 // after a peek of >= n bits
+    acc = n < 64 ? acc << n : 0ull;
+    have = have > n ? have - n : 0u;
+    bits -= (int64_t)n;
   }
   __host__ __device__ uint32_t read(uint32_t n) {
     const uint32_t v = peek(n);
-    bits -= (int64_t)n;
+    skip(n);
     return v;
   }
 };
@@ -308,7 +333,7 @@ __host__ __device__ inline bool huf_stream(const ZState& z, const uint8_t* s, ui
   for (uint32_t k = 0; k < count; ++k) {
     const uint16_t e = z.huf[br.peek(log)];
     out[k] = (uint8_t)e;
-    br.bits -= e >> 8;
+    br.skip(e >> 8);
   }
   return br.bits == 0;
 }
@@ -496,6 +521,7 @@ __host__ __device__ int32_t zstd_block(const Team& tm, ZState& z, const uint8_t*
     BackBits br;
     if (pos >= n || !br.init(b + pos, n - pos)) return kErrStream;
     uint32_t sll = br.read(z.ll_log), sof = br.read(z.of_log), sml = br.read(z.ml_log);
+    uint64_t visible = o.op;            // every lane's output below this is visible to all
     for (uint32_t i = 0; i < nseq; ++i) {
       const FseCell cl = z.ll[sll], co = z.of[sof], cm = z.ml[sml];
       if (co.sym > kOFMax) return kErrStream;
@@ -528,16 +554,22 @@ __host__ __device__ int32_t zstd_block(const Team& tm, ZState& z, const uint8_t*
       if (lp + ll > lsize) return kErrStream;
       if (o.op + ll + ml > o.cap) return kErrOutput;
       if (off == 0 || off > o.op + ll - o.frame0) return kErrOffset;
+      // match byte i is d[ll - off + i % off]: earlier output, or this
+      // sequence's literals (then read from the literal buffer). Output below
+      // `visible` has been written before the last barrier; a match that reads
+      // above it waits for one first.
+      const uint64_t from = o.op + ll - off;
+      const uint64_t reach = from + (off < ml ? off : ml);
+      if ((reach < o.op ? reach : o.op) > visible) {
+        tm.sync();
+        visible = o.op;
+      }
       uint8_t* d = o.dst + o.op;
       team_copy(tm, d, lit + lp, ll);
-      // match byte i is d[ll - off + i % off]: earlier output, or this
-      // sequence's literals (then read from the literal buffer)
-      const uint64_t from = o.op + ll - off;
       for (uint64_t j = tm.lane(); j < ml; j += Team::size) {
         const uint64_t src = from + (off >= ml ? j : j % off);
         o.dst[o.op + ll + j] = src >= o.op ? lit[lp + (src - o.op)] : o.dst[src];
       }
-      tm.sync();
       o.op += ll + ml;
       lp += ll;
     }

@@ -60,19 +60,23 @@ __global__ __launch_bounds__(64) void zstd_kernel(const bs_zstd_task* __restrict
   }
 }
 
-__global__ __launch_bounds__(256) void lut_expand_kernel(const uint8_t* __restrict__ idx, uint64_t n,
-                                                         const uint8_t* __restrict__ lut, uint32_t n_lut,
-                                                         uint32_t item_bytes, uint8_t* __restrict__ out,
+// Task blockIdx.y; blockIdx.x strides over its elements.
+__global__ __launch_bounds__(256) void lut_expand_kernel(const bs_lut_task* __restrict__ tasks,
                                                          int32_t* __restrict__ status) {
+  const bs_lut_task T = tasks[blockIdx.y];
+  if (T.item_bytes == 0 || T.item_bytes > 8 || T.n_lut > 256) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
+    return;
+  }
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   bool bad = false;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint32_t v = idx[i];
-    if (v >= n_lut) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < T.n; i += stride) {
+    const uint32_t v = T.idx[i];
+    if (v >= T.n_lut) {
       bad = true;
       continue;
     }
-    for (uint32_t b = 0; b < item_bytes; ++b) out[i * item_bytes + b] = lut[v * item_bytes + b];
+    for (uint32_t b = 0; b < T.item_bytes; ++b) T.out[i * T.item_bytes + b] = T.lut[v * T.item_bytes + b];
   }
   if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(status, BS_DEV_ERR_COUNT);
 }
@@ -93,14 +97,12 @@ int bs_zstd_decode(const bs_zstd_task* d_tasks, uint32_t n_tasks, void* d_work, 
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 
-int bs_lut_expand(const uint8_t* d_idx, uint64_t n, const uint8_t* d_lut, uint32_t n_lut, uint32_t item_bytes,
-                  uint8_t* d_out, int32_t* d_status, void* stream) {
-  if (!d_status || item_bytes == 0 || item_bytes > 8 || n_lut > 256 || (n && (!d_idx || !d_lut || !d_out)))
-    return BS_ERR_ARG;
-  if (n == 0) return BS_OK;
-  const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 4096);
-  hipLaunchKernelGGL(lut_expand_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, d_idx, n, d_lut,
-                     n_lut, item_bytes, d_out, d_status);
+int bs_lut_expand(const bs_lut_task* d_tasks, uint32_t n_tasks, uint64_t max_n, int32_t* d_status, void* stream) {
+  if (!d_status || (n_tasks && !d_tasks) || n_tasks > 65535u) return BS_ERR_ARG;
+  if (n_tasks == 0 || max_n == 0) return BS_OK;
+  const uint64_t blocks = std::min<uint64_t>((max_n + 255) / 256, 1024);
+  hipLaunchKernelGGL(lut_expand_kernel, dim3((uint32_t)blocks, n_tasks), dim3(256), 0, (hipStream_t)stream, d_tasks,
+                     d_status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 

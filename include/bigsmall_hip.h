@@ -245,12 +245,20 @@ uint64_t bs_zstd_work_bytes(uint32_t n_tasks);
 int bs_zstd_decode(const bs_zstd_task *d_tasks, uint32_t n_tasks, void *d_work, uint64_t work_bytes,
                    uint64_t *d_out_len, int32_t *d_status, void *stream);
 
-/* out[i * item_bytes + b] = lut[idx[i] * item_bytes + b] for i < n: the
- * lowcard expansion unique_bytes[idx] of bigsmall/codecs/special.py:79-82.
- * An index >= n_lut sets BS_DEV_ERR_COUNT and leaves its element unwritten.
- * 1 <= item_bytes <= 8, n_lut <= 256. */
-int bs_lut_expand(const uint8_t *d_idx, uint64_t n, const uint8_t *d_lut, uint32_t n_lut, uint32_t item_bytes,
-                  uint8_t *d_out, int32_t *d_status, void *stream);
+/* Lowcard expansion, the unique_bytes[idx] of bigsmall/codecs/special.py:79-82:
+ * out[i * item_bytes + b] = lut[idx[i] * item_bytes + b] for i < n, one task
+ * per entry (all pointers device). An index >= n_lut sets BS_DEV_ERR_COUNT and
+ * leaves its element unwritten; item_bytes outside 1..8 or n_lut > 256 sets
+ * BS_DEV_ERR_HEADER. max_n (>= every n) sizes the launch; n_tasks <= 65535. */
+typedef struct {
+    const uint8_t *idx;
+    const uint8_t *lut;
+    uint8_t *out;
+    uint64_t n;
+    uint32_t n_lut;
+    uint32_t item_bytes;
+} bs_lut_task;
+int bs_lut_expand(const bs_lut_task *d_tasks, uint32_t n_tasks, uint64_t max_n, int32_t *d_status, void *stream);
 
 #ifdef __cplusplus
 }
