@@ -8,6 +8,7 @@ kernels on the GPU:
     info(src), verify(src)
     StreamingLoader, BigSmallStreamingModel -> layer-at-a-time decode with prefetch
     decompress_layers(src, [i, ...])        -> only the named layers
+    decompress_delta(delta, base), load_delta(delta, base) -> a fine-tune from its XOR delta
     CompressedKVCache                       -> KV entries and blocks decoded on the GPU
     codec_registry.register_codec / get_codec / auto_select_codec
     compress_for_hub(model_dir, out_dir), from_pretrained(path) -> multi-shard .bs models + index
@@ -15,7 +16,7 @@ kernels on the GPU:
 __version__ = "3.12.0+mi355x"
 
 from .container import info
-from .decoder import decompress, load
+from .decoder import decompress, decompress_delta, load, load_delta
 from .encoder import compress
 from .exceptions import BigSmallVersionError, DecodeError
 from .hub import compress_for_hub, from_pretrained
@@ -33,6 +34,6 @@ def __getattr__(name):
 
 
 __all__ = ["compress", "decompress", "load", "info", "verify", "StreamingLoader", "BigSmallStreamingModel",
-           "decompress_layers",
+           "decompress_layers", "decompress_delta", "load_delta",
            "CompressedKVCache", "BigSmallVersionError", "DecodeError", "compress_for_hub", "from_pretrained",
            "__version__"]

@@ -21,7 +21,8 @@ import numpy as np
 from .. import _native
 from ..device import StatusWord, require_gpu, stream_ptr, upload_bytes
 
-ZSTD_TASK_DTYPE = np.dtype([("src", "<u8"), ("src_len", "<u8"), ("dst", "<u8"), ("dst_len", "<u8")])
+ZSTD_TASK_DTYPE = np.dtype([("src", "<u8"), ("src_len", "<u8"), ("dst", "<u8"), ("dst_len", "<u8"),
+                            ("xor_src", "<u8")])
 LUT_TASK_DTYPE = np.dtype([("idx", "<u8"), ("lut", "<u8"), ("out", "<u8"), ("n", "<u8"), ("n_lut", "<u4"),
                            ("item_bytes", "<u4")])
 ZSTD_MAGIC = 0xFD2FB528
@@ -82,7 +83,7 @@ class ZstdLaunch:
 
     def __init__(self, device):
         self.device = require_gpu(device)
-        self.tasks: list[tuple[int, int, int, int]] = []
+        self.tasks: list[tuple[int, int, int, int, int]] = []
         self.expands: list[tuple[int, int, int, int, int, int]] = []
         self.keep: list = []
         self.out_len = None               # per-task decoded bytes (device int64), set by prepare()
@@ -91,9 +92,10 @@ class ZstdLaunch:
     def __len__(self) -> int:
         return len(self.tasks)
 
-    def add_frame(self, src_ptr: int, src_len: int, dst_ptr: int, dst_len: int) -> None:
-        """Frames at src decode to exactly dst_len bytes at dst."""
-        self.tasks.append((src_ptr, src_len, dst_ptr, dst_len))
+    def add_frame(self, src_ptr: int, src_len: int, dst_ptr: int, dst_len: int, xor_ptr: int = 0) -> None:
+        """Frames at src decode to exactly dst_len bytes at dst; with xor_ptr,
+        those bytes are XOR-ed with dst_len bytes there (a delta's base)."""
+        self.tasks.append((src_ptr, src_len, dst_ptr, dst_len, xor_ptr))
 
     def add_lowcard(self, blob_ptr: int, host_blob, out_ptr: int, n_elem: int, item_bytes: int) -> None:
         """A lowcard blob (device copy at blob_ptr, host bytes host_blob) into

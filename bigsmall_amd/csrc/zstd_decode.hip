@@ -6,7 +6,8 @@
 //                           zstd frame of one uint8 index per element
 //                           (bigsmall/codecs/special.py:23-85);
 //   codec "zstd_xor_delta"  a zstd frame of XOR differences to a base tensor
-//                           (bigsmall/decoder.py:88-90, 190-198).
+//                           (bigsmall/decoder.py:88-90, 190-198); with a base
+//                           given, the kernel XORs it into the output.
 //
 // One 64-lane workgroup per task decodes all frames of its input with the
 // team-parallel decoder of zstd_core.h: tables in LDS (about 15 KB), literals
@@ -53,6 +54,9 @@ __global__ __launch_bounds__(64) void zstd_kernel(const bs_zstd_task* __restrict
   if (T.src && (T.dst || T.dst_len == 0)) {
     e = bs_zstd::zstd_frames(DevTeam{}, z, T.src, T.src_len, T.dst, T.dst_len, lit, got);
     if (e == bs_zstd::kOk && got != T.dst_len) e = bs_zstd::kErrOutput;
+  }
+  if (e == bs_zstd::kOk && T.xor_src) {        // a delta: dst ^= base (the frames are all written)
+    for (uint64_t i = threadIdx.x; i < T.dst_len; i += 64) T.dst[i] ^= T.xor_src[i];
   }
   if (threadIdx.x == 0) {
     out_len[blockIdx.x] = e ? 0 : got;

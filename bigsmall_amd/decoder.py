@@ -81,8 +81,11 @@ def layer_groups(tensors: list[dict]) -> list[list[dict]]:
     return sorted(groups, key=key)
 
 
-def load_to_device(src, device="cuda", dtype=None, decoder: engine.GroupDecoder | None = None) -> dict:
-    """Decode every tensor of a container into device tensors (header order)."""
+def load_to_device(src, device="cuda", dtype=None, decoder: engine.GroupDecoder | None = None,
+                   xor_base: Optional[dict] = None) -> dict:
+    """Decode every tensor of a container into device tensors (header order).
+    xor_base: base tensors (same device) for the zstd_xor_delta entries of a
+    delta container, which then decode to base XOR delta."""
     src = Path(src)
     header, _ = container.read_header(src)
     tensors = header["tensors"]
@@ -99,14 +102,14 @@ def load_to_device(src, device="cuda", dtype=None, decoder: engine.GroupDecoder 
                 deferred.append(g)
                 continue
             lo, hi = engine.group_span(g)
-            res = dec.decode_group(g, reader, lo, hi - lo, dtype=dtype)
+            res = dec.decode_group(g, reader, lo, hi - lo, dtype=dtype, xor_base=xor_base)
             pending.append(res)
             decoded.update(res.tensors)
         for res in pending:
             res.wait("decode")
         for g in deferred:        # groups holding ties to tensors of other groups
             lo, hi = engine.group_span(g)
-            res = dec.decode_group(g, reader, lo, hi - lo, resolve_tied=decoded.get, dtype=dtype)
+            res = dec.decode_group(g, reader, lo, hi - lo, resolve_tied=decoded.get, dtype=dtype, xor_base=xor_base)
             decoded.update(res.wait("decode"))
     finally:
         reader.close()
@@ -146,6 +149,52 @@ def decompress(src: str | Path, dst: Optional[str | Path] = None, progress: bool
     return out
 
 
+def _load_base_device(base_src, device) -> dict:
+    """Base tensors of a delta on `device`, from a .bs container (decoded by
+    this engine) or a safetensors file (bigsmall/decoder.py:212-246)."""
+    base_src = Path(base_src)
+    if base_src.suffix == ".bs":
+        return load_to_device(base_src, device)
+    from safetensors import safe_open
+    out = {}
+    with safe_open(str(base_src), framework="pt") as f:
+        for k in f.keys():
+            out[k] = f.get_tensor(k).contiguous().to(device)
+    return out
+
+
+def load_delta(delta_src: str | Path, base_src: str | Path, device: str = "cuda") -> dict:
+    """A fine-tune stored as a delta container, reconstructed on the GPU: the
+    zstd_xor_delta entries decode and XOR with their base tensor in one
+    kernel; other entries decode as in `load`. Returns device tensors."""
+    import torch
+    dev = torch.device(device)
+    header, _ = container.read_header(Path(delta_src))
+    base = _load_base_device(base_src, dev)
+    xor = {}
+    for t in header["tensors"]:
+        if t["codec"] == "zstd_xor_delta":
+            if t["name"] not in base:
+                raise KeyError(t["name"])
+            b = base[t["name"]]
+            xor[t["name"]] = b.view(-1).view(torch.uint8) if b.numel() else b
+    return load_to_device(delta_src, dev, xor_base=xor)
+
+
+def decompress_delta(delta_src: str | Path, base_src: str | Path, dst: Optional[str | Path] = None,
+                     progress: bool = True) -> dict:
+    """Decompress a delta .bs file against its base (safetensors or .bs);
+    returns {name: numpy array} like bigsmall/decoder.py:160-210. The base
+    tensors go to the GPU, and every zstd_xor_delta entry is decoded and XOR-ed
+    with its base there."""
+    header, _ = container.read_header(Path(delta_src))
+    dev = load_delta(delta_src, base_src, "cuda")
+    out = {t["name"]: _to_numpy(dev[t["name"]], t["dtype"], t["shape"]) for t in header["tensors"]}
+    if dst is not None:
+        _write_safetensors(dst, out, header)
+    return out
+
+
 def _raw_to_numpy(raw: bytes, dtype_str: str, shape: list[int]) -> np.ndarray:
     """bigsmall/decoder.py:249-263."""
     np_dtype = _DTYPE_TO_NUMPY.get(dtype_str)
@@ -174,5 +223,5 @@ def _write_safetensors(dst, tensors: dict, header: dict) -> None:
     save_file({t["name"]: _numpy_to_torch(tensors[t["name"]], t["dtype"]) for t in header["tensors"]}, str(dst))
 
 
-__all__ = ["decompress", "load", "load_to_device", "layer_groups", "_decode_blob", "_raw_to_numpy",
-           "_numpy_to_torch"]
+__all__ = ["decompress", "decompress_delta", "load", "load_delta", "load_to_device", "layer_groups", "_decode_blob",
+           "_raw_to_numpy", "_numpy_to_torch"]

@@ -176,24 +176,27 @@ class GroupDecoder:
 
     # -- decoding --------------------------------------------------------------
     def decode_group(self, entries: list[dict], read_span, span_start: int, span_len: int,
-                     resolve_tied=None, dtype=None) -> GroupResult:
+                     resolve_tied=None, dtype=None, xor_base: Optional[dict] = None) -> GroupResult:
         """Decode `entries` (container tensor dicts). Their blobs lie in the data
         section range [span_start, span_start + span_len); `read_span(offset,
         np_out)` fills np_out with that many bytes of the data section starting
         at offset. `resolve_tied(name)` returns the decoded master tensor for a
-        tied entry whose master is outside the group."""
+        tied entry whose master is outside the group. `xor_base` maps names of
+        zstd_xor_delta entries to their base tensors on this device; such an
+        entry decodes to base XOR delta (without a base: to the delta bytes,
+        as bigsmall/decoder.py:88-90 returns them)."""
         import torch
         for t in entries:
             check_supported(t)
         d_span, host, copied = self.upload(read_span, span_start, span_len)
         with torch.cuda.stream(self.stream):       # allocations and launches on the decode stream
             status, out, keep = self._launch_group(entries, host, d_span, copied, span_start, span_len,
-                                                   resolve_tied, dtype)
+                                                   resolve_tied, dtype, xor_base or {})
             done = torch.cuda.Event()
             done.record(self.stream)
         return GroupResult(out, status, done, keep)
 
-    def _launch_group(self, entries, host, d_span, copied, span_start, span_len, resolve_tied, dtype):
+    def _launch_group(self, entries, host, d_span, copied, span_start, span_len, resolve_tied, dtype, xor_base):
         import torch
         status = StatusWord(self.device)
         out: dict = {}
@@ -247,7 +250,13 @@ class GroupDecoder:
             elif codec in ZSTD_CODECS:
                 if nb == 0:
                     raise ValueError(f"{t['name']}: empty {codec} blob")
-                zst.add_frame(base + off, nb, o.data_ptr(), o.numel() * o.element_size())
+                nbytes = o.numel() * o.element_size()
+                xb = xor_base.get(t["name"]) if codec == "zstd_xor_delta" else None
+                if xb is not None:
+                    if not xb.is_contiguous() or xb.numel() * xb.element_size() != nbytes or xb.device != o.device:
+                        raise ValueError(f"Delta size mismatch for {t['name']}")
+                    keep.append(xb)
+                zst.add_frame(base + off, nb, o.data_ptr(), nbytes, xb.data_ptr() if xb is not None else 0)
             else:                                        # special/lowcard (check_supported)
                 zst.add_lowcard(base + off, host[off:off + nb], o.data_ptr(), o.numel(), o.element_size())
         self.stream.wait_event(copied)

@@ -230,6 +230,7 @@ typedef struct {
     uint64_t src_len;
     uint8_t *dst;         /* decoded bytes (device); may be NULL when dst_len is 0 */
     uint64_t dst_len;     /* the exact decoded size */
+    const uint8_t *xor_src; /* NULL, or dst_len bytes XOR-ed into the decoded bytes (a delta's base) */
 } bs_zstd_task;
 
 /* Device scratch bytes bs_zstd_decode needs (128 KiB per task). */

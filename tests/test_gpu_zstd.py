@@ -274,3 +274,69 @@ def test_plugin_api_decoders():
     assert decode_special(lb, dict(le, special_kind="lowcard"), len(norm)) == norm
     with pytest.raises(ValueError):
         decode_special(lb, {"special_kind": "wpe_delta"}, len(norm))
+
+
+def _write_delta_container(path, base: dict, ft: dict, extra_ft: dict):
+    """A delta container as bigsmall/encoder.py:705-824 writes it: tensors that
+    match the base in shape, dtype and size as zstd_xor_delta (level 19, extras
+    is_xor_delta), a tensor with no base entry standalone (here raw bytes as
+    zstd, the reference's route for fmt "raw")."""
+    from bigsmall_amd import container
+    data, tensors = bytearray(), []
+    for name, arr in list(ft.items()) + list(extra_ft.items()):
+        raw = arr.tobytes()
+        if name in base:
+            blob, extra = zstd_lib.encode_zstd(np.frombuffer(raw, np.uint8) ^ np.frombuffer(base[name].tobytes(),
+                                                                                          np.uint8), 19)
+            codec, extra, special = "zstd_xor_delta", dict(extra, is_xor_delta=True), "delta"
+        else:
+            (blob, extra), codec, special = zstd_lib.encode_zstd(raw), "zstd", None
+        tensors.append({"name": name, "shape": list(arr.shape), "dtype": "bfloat16" if arr.dtype == np.uint16
+                        else "int64", "codec": codec, "special": special, "compressed_bytes": len(blob),
+                        "offset": len(data), "md5": hashlib.md5(raw).hexdigest(), "extra": extra})
+        data += blob
+    header = {"format": "bf16", "mode": "balanced", "model_type": "delta", "base_model": "base",
+              "tensor_count": len(tensors), "tensors": tensors}
+    container.write_container(path, header, bytes(data))
+
+
+def test_delta_roundtrip_against_safetensors_and_bs_base(tmp_path):
+    """Mirror of the reference's tests/test_delta.py:13-53: a fine-tune that
+    differs from its base in ~1% of the elements, stored as a delta, comes
+    back md5-identical from decompress_delta with the base given as
+    safetensors or as a .bs container."""
+    from safetensors.torch import save_file
+
+    import bigsmall_amd as bs
+    from bigsmall_amd import container
+    rng = np.random.default_rng(8)
+    shapes = {"embed.weight": (2000, 256), "layer.0.weight": (256, 512), "layer.1.weight": (512, 256)}
+    base = {k: _bf16_words(rng, int(np.prod(s)), 0.0, 1.0).reshape(s) for k, s in shapes.items()}
+    ft = {}
+    for k, v in base.items():                    # v + 0.01 where a 1% mask is set, rounded to bf16
+        f = (v.astype(np.uint32) << 16).view(np.float32)
+        m = rng.random(v.shape) < 0.01
+        x = (f + np.float32(0.01) * m).astype(np.float32).view(np.uint32).astype(np.uint64)
+        ft[k] = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
+    extra = {"position_ids": np.arange(512, dtype=np.int64).reshape(1, 512)}
+    delta = tmp_path / "delta.bs"
+    _write_delta_container(delta, base, ft, extra)
+    base_st = tmp_path / "base.safetensors"
+    save_file({k: torch.from_numpy(v.view(np.int16)).view(torch.bfloat16) for k, v in base.items()}, str(base_st))
+    base_bs = tmp_path / "base.bs"
+    bs.compress(base_st, base_bs)
+    header, _ = container.read_header(delta)
+    for base_src in (base_st, base_bs):
+        _say(f"[zstd] decompress_delta against {base_src.suffix}")
+        out = bs.decompress_delta(delta, base_src)
+        for t in header["tensors"]:
+            assert hashlib.md5(out[t["name"]].tobytes()).hexdigest() == t["md5"], t["name"]
+        dev = bs.load_delta(delta, base_src)
+        assert all(dev[k].is_cuda for k in dev)
+        assert _host_bytes(dev["layer.0.weight"]) == ft["layer.0.weight"].tobytes()
+    _say("[zstd] delta bytes without a base")
+    from bigsmall_amd import decoder
+    plain = decoder.load(delta)                  # no base: the XOR delta itself, as _decode_blob returns it
+    want = (np.frombuffer(ft["layer.1.weight"].tobytes(), np.uint8) ^
+            np.frombuffer(base["layer.1.weight"].tobytes(), np.uint8)).tobytes()
+    assert _host_bytes(plain["layer.1.weight"]) == want
