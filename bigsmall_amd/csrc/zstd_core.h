@@ -23,6 +23,7 @@ constexpr uint32_t kBlockMax = 128u << 10;     // RFC 8878 3.1.1.2.4: Block_Maxi
 constexpr uint32_t kHufLogMax = 12;
 constexpr uint32_t kLLLog = 9, kMLLog = 9, kOFLog = 8, kWeightLog = 6;
 constexpr uint32_t kLLMax = 35, kMLMax = 52, kOFMax = 31;
+constexpr uint32_t kStageBytes = 24u << 10;    // compressed blocks up to this size are read from shared memory
 
 enum : int32_t {
   kOk = 0,
@@ -55,6 +56,7 @@ struct ZState {
   uint32_t have_ll, have_ml, have_of; // a table exists for the Repeat mode
   uint32_t seq_pos;                   // broadcast: where the sequence bitstream starts
   int32_t err;                        // broadcast: error of single-lane work
+  uint8_t stage[kStageBytes];         // the current compressed block, when it fits
 };
 
 __host__ __device__ __forceinline__ uint32_t highbit(uint32_t v) { return 31u - (uint32_t)__builtin_clz(v); }
@@ -398,8 +400,8 @@ __host__ __device__ inline void team_copy(const Team& tm, uint8_t* d, const uint
 
 // One compressed block b[0, n) (RFC 8878 3.1.1.3). rep: repeat offsets.
 template <class Team>
-__host__ __device__ int32_t zstd_block(const Team& tm, ZState& z, const uint8_t* b, uint64_t n, Out& o, Rep& rep,
-                                       uint8_t* lit_buf) {
+__host__ __device__ __forceinline__ int32_t zstd_block(const Team& tm, ZState& z, const uint8_t* b, uint64_t n,
+                                                       Out& o, Rep& rep, uint8_t* lit_buf) {
   if (n < 1) return kErrTruncated;
   const uint32_t ltype = b[0] & 3u, sf = (b[0] >> 2) & 3u;
   uint32_t lh, lsize, lcsize = 0;
@@ -643,7 +645,14 @@ __host__ __device__ int32_t zstd_frames(const Team& tm, ZState& z, const uint8_t
       } else if (type == 2) {
         if (bsize > len - ip) return kErrTruncated;
         if (bsize > kBlockMax) return kErrFormat;
-        const int32_t e = zstd_block(tm, z, src + ip, bsize, o, rep, lit_buf);
+        int32_t e;
+        if (bsize <= kStageBytes) {     // bit reads then come from shared memory, not global memory
+          team_copy(tm, z.stage, src + ip, bsize);
+          tm.sync();
+          e = zstd_block(tm, z, z.stage, bsize, o, rep, lit_buf);
+        } else {
+          e = zstd_block(tm, z, src + ip, bsize, o, rep, lit_buf);
+        }
         if (e) return e;
         ip += bsize;
       } else {

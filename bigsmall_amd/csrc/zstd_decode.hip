@@ -10,7 +10,8 @@
 //                           given, the kernel XORs it into the output.
 //
 // One 64-lane workgroup per task decodes all frames of its input with the
-// team-parallel decoder of zstd_core.h: tables in LDS (about 15 KB), literals
+// team-parallel decoder of zstd_core.h: tables and the current compressed
+// block (when it is at most 24 KB) in LDS, about 39 KB in all; literals
 // of the current block in a 128 KiB slice of the work buffer, matches copied
 // by all lanes. Zstandard is a sequential format (each match may copy bytes
 // of the one before), so a frame is not split across workgroups; the
