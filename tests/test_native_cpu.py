@@ -8,6 +8,7 @@
 """
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -156,3 +157,60 @@ def test_invariant_divisor_multiply_shift_is_exact():
     t = (m[:, None] * x) >> np.uint64(32)
     q = (t + ((x - t) >> s1[:, None])) >> s2[:, None]
     assert np.array_equal(q, x // f[:, None])
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every struct the C-ABI takes has a host-side mirror (numpy dtype or
+    ctypes Structure) that the library reads as raw bytes; each field's offset
+    and size must equal the C compiler's layout of include/bigsmall_hip.h."""
+    import shutil
+    import subprocess
+
+    import numpy as np
+    from bigsmall_amd import _native
+    from bigsmall_amd.codecs import _refstreams, bf16_chunked, zstd_gpu
+    from bigsmall_amd.device import TASK_DTYPE
+    if shutil.which("gcc") is None:
+        pytest.skip("needs gcc")
+    structs = {
+        "bs_chunk_info": (["n", "n_chunks", "steps", "lanes", "n_syms", "elem_bytes", "plane_mode"],
+                          [(f[0], getattr(_native.BsChunkInfo, f[0]).offset, ctypes.sizeof(f[1]))
+                           for f in _native.BsChunkInfo._fields_]),
+        "bs_chunk_task": (["blob", "blob_bytes", "out", "n", "wg_begin", "n_chunks"], TASK_DTYPE),
+        "bs_encode_task": (["src", "n", "dst", "cap", "chunk_begin", "n_chunks"], bf16_chunked.ENCODE_TASK_DTYPE),
+        "bs_span": (["src", "dst", "len"], bf16_chunked.SPAN_DTYPE),
+        "bs_se_stream": (["words", "x0", "n_words", "tail", "n", "first", "stride", "reserved"],
+                         _refstreams.SE_STREAM_DTYPE),
+        "bs_mant_bucket": (["words", "x0", "n_words", "tail", "n", "perm_begin", "table", "reserved"],
+                           _refstreams.MANT_BUCKET_DTYPE),
+        "bs_zstd_task": (["src", "src_len", "dst", "dst_len", "xor_src"], zstd_gpu.ZSTD_TASK_DTYPE),
+        "bs_lut_task": (["idx", "lut", "out", "n", "n_lut", "item_bytes"], zstd_gpu.LUT_TASK_DTYPE),
+    }
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "bigsmall_hip.h"', "int main(void) {"]
+    for st, (fields, _) in structs.items():
+        lines.append(f'  printf("{st} sizeof %zu\\n", sizeof({st}));')
+        for f in fields:
+            lines.append(f'  printf("{st} {f} %zu %zu\\n", offsetof({st}, {f}), sizeof((({st}*)0)->{f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    inc = Path(__file__).resolve().parents[1] / "include"
+    subprocess.run(["gcc", "-I", str(inc), str(src), "-o", str(exe)], check=True, capture_output=True)
+    got: dict = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        parts = line.split()
+        if parts[1] == "sizeof":
+            got[(parts[0], "sizeof")] = int(parts[2])
+        else:
+            got[(parts[0], parts[1])] = (int(parts[2]), int(parts[3]))
+    for st, (fields, mirror) in structs.items():
+        if isinstance(mirror, np.dtype):
+            assert mirror.itemsize == got[(st, "sizeof")], st
+            py = [(name, mirror.fields[name][1], mirror.fields[name][0].itemsize) for name in mirror.names]
+        else:
+            assert ctypes.sizeof(_native.BsChunkInfo) == got[(st, "sizeof")], st
+            py = mirror
+        assert len(py) == len(fields), st
+        for (name, off, size), f in zip(py, fields):
+            assert (off, size) == got[(st, f)], (st, f, name)
