@@ -1,7 +1,7 @@
 """Mirrors of the reference's own tests of the container, version-error and
-tiny-tensor behaviour that the drop-in keeps (no GPU needed):
+tiny-tensor behaviour that the drop-in keeps, and of the streaming model's helpers (no GPU needed):
   tests/test_version_errors.py:12-73, tests/test_format_v2.py:55-103,
-  tests/test_raw_tiny.py:30-110.
+  tests/test_raw_tiny.py:30-110, tests/test_streaming_inference.py:14-55.
 The decode half of the tiny-tensor round trip runs on the GPU in the reference's
 API tests; here the raw blobs are compared byte for byte."""
 from __future__ import annotations
@@ -122,3 +122,33 @@ def test_threshold_boundary(tmp_path):
     codec = {t["name"]: t["codec"] for t in header["tensors"]}
     assert codec["below_threshold.weight"] == "raw"
     assert codec["at_threshold.weight"] != "raw"
+
+
+# tests/test_streaming_inference.py:14-55: the streaming model's helpers
+def test_streaming_inference_imports():
+    import bigsmall_amd.streaming_inference  # noqa: F401
+
+
+def test_set_param_data_swaps_parameter():
+    from torch import nn
+
+    from bigsmall_amd.streaming_inference import _set_param_data
+    m = nn.Linear(4, 4)
+    _set_param_data(m, "weight", torch.zeros(4, 4))
+    assert torch.equal(m.weight, torch.zeros(4, 4)) and isinstance(m.weight, nn.Parameter)
+
+
+def test_set_param_data_nested_index():
+    from torch import nn
+
+    from bigsmall_amd.streaming_inference import _set_param_data
+    m = nn.ModuleList([nn.Linear(2, 2), nn.Linear(2, 2)])
+    _set_param_data(m, "1.weight", torch.eye(2))
+    assert torch.equal(m[1].weight, torch.eye(2))
+
+
+def test_layer_prefix_format():
+    from bigsmall_amd.streaming_inference import _layer_prefix
+    assert _layer_prefix(0) == "model.layers.0."
+    assert _layer_prefix(31) == "model.layers.31."
+    assert _layer_prefix(5, "h.{}") == "h.5."
