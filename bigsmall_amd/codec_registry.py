@@ -17,7 +17,7 @@ from __future__ import annotations
 
 from typing import Callable, Optional
 
-from .codecs import bf16_chunked, bf16_parallel, bf16_tans, single_kernel
+from .codecs import bf16_chunked, bf16_parallel, bf16_tans, single_kernel, zstd_gpu
 
 _REGISTRY: dict[str, tuple[Callable, Callable]] = {}
 
@@ -57,6 +57,19 @@ register_codec(bf16_parallel.CODEC, bf16_parallel.encode, bf16_parallel.decode)
 register_codec(bf16_tans.CODEC, bf16_tans.encode, bf16_tans.decode)
 register_codec(single_kernel.CODEC, single_kernel.encode, single_kernel.decode)
 register_codec("raw", _enc_raw, _dec_raw)
+
+
+def _enc_zstd_unavailable(raw, **_):
+    raise NotImplementedError("this engine decodes zstd-coded entries; it does not write them")
+
+
+def _dec_zstd(blob, extras, n_weights):
+    """The reference registers zstd with generic.decode_zstd (codec_registry.py:171), which
+    returns the frame's content whatever n_weights is; the size comes from the frame."""
+    return zstd_gpu.decode_zstd(blob, extras)
+
+
+register_codec("zstd", _enc_zstd_unavailable, _dec_zstd)
 
 # Per-format ordered candidates. fp32/fp16 have no GPU codec here: they are
 # stored raw (the reference's constriction codecs for them are not available).

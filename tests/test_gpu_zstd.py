@@ -268,6 +268,8 @@ def test_plugin_api_decoders():
     blob, extras = zstd_lib.encode_zstd(raw)
     _say("[zstd] plugin decoders")
     assert decode_zstd(blob, extras) == raw                 # size from the frame header
+    from bigsmall_amd import codec_registry
+    assert codec_registry.get_codec("zstd")[1](blob, extras, 5000) == raw
     assert decode_zstd(blob, extras, len(raw)) == raw
     norm = _bf16_words(np.random.default_rng(5), 4096, 1.0, 0.01).tobytes()
     lb, le = zstd_lib.encode_lowcard(norm, 2)
