@@ -94,45 +94,43 @@ struct FwdBits {
 // unread bits sit left-aligned in a 64-bit register, refilled a byte at a time.
 struct BackBits {
   const uint8_t* p;
-  int64_t bits;      // bits [0, bits) of the stream are unread; bit b is bit (b & 7) of p[b >> 3]
   uint64_t acc;      // the top `have` unread bits, most significant first; zeros below
-  uint32_t have;
-  uint64_t lo;       // bytes [0, lo) are not yet in acc
+  int32_t have;      // negative once reads have gone past the start of the stream
+  uint32_t lo;       // bytes [0, lo) are not yet in acc
   __host__ __device__ bool init(const uint8_t* q, uint64_t n) {
     p = q;
-    bits = 0;
     acc = 0;
     have = 0;
     lo = 0;
-    if (n == 0 || q[n - 1] == 0) return false;
+    if (n == 0 || n > 0xFFFFFFFFull || q[n - 1] == 0) return false;
     const uint32_t hb = highbit(q[n - 1]);
-    bits = (int64_t)(n - 1) * 8 + hb;
     acc = hb ? (uint64_t)(q[n - 1] & ((1u << hb) - 1u)) << (64 - hb) : 0ull;
-    have = hb;
-    lo = n - 1;
+    have = (int32_t)hb;
+    lo = (uint32_t)(n - 1);
     refill();
     return true;
   }
+  // Unread bits; negative after an overflow.
+  __host__ __device__ int64_t bits() const { return (int64_t)lo * 8 + have; }
   __host__ __device__ void refill() {         // as many whole bytes as fit, loaded together
     if (have > 56 || lo == 0) return;
-    const uint64_t want = (64 - have) >> 3;
-    const uint32_t k = (uint32_t)(lo < want ? lo : want);
+    const uint32_t want = (uint32_t)(64 - have) >> 3;
+    const uint32_t k = lo < want ? lo : want;
     uint64_t v = 0;
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i)
       if (i < k) v |= (uint64_t)p[lo - 1 - i] << (56 - 8 * i);
     acc |= v >> have;
-    have += 8 * k;
+    have += (int32_t)(8 * k);
     lo -= k;
   }
   __host__ __device__ uint32_t peek(uint32_t n) {             // n <= 32
-    if (have < n) refill();
+    if (have < (int32_t)n) refill();
     return n ? (uint32_t)(acc >> (64 - n)) : 0u;
   }
   __host__ __device__ void skip(uint32_t n) {                 // after a peek of >= n bits
     acc = n < 64 ? acc << n : 0ull;
-    have = have > n ? have - n : 0u;
-    bits -= (int64_t)n;
+    have -= (int32_t)n;
   }
   __host__ __device__ uint32_t read(uint32_t n) {
     const uint32_t v = peek(n);
@@ -287,14 +285,14 @@ __host__ __device__ inline int32_t build_huffman(ZState& z, const uint8_t* q, ui
       if (nw >= 255) return kErrTable;
       z.weight[nw++] = z.wt[s1].sym;
       s1 = z.wt[s1].base + br.read(z.wt[s1].nb);
-      if (br.bits < 0) {
+      if (br.bits() < 0) {
         z.weight[nw++] = z.wt[s2].sym;
         break;
       }
       if (nw >= 255) return kErrTable;
       z.weight[nw++] = z.wt[s2].sym;
       s2 = z.wt[s2].base + br.read(z.wt[s2].nb);
-      if (br.bits < 0) {
+      if (br.bits() < 0) {
         z.weight[nw++] = z.wt[s1].sym;
         break;
       }
@@ -332,12 +330,24 @@ __host__ __device__ inline bool huf_stream(const ZState& z, const uint8_t* s, ui
   BackBits br;
   if (!br.init(s, n)) return false;
   const uint32_t log = z.huf_log;
-  for (uint32_t k = 0; k < count; ++k) {
+  uint32_t k = 0;
+  // four symbols per refill while at least 4 * log bits are loaded (log <= 12)
+  for (; k + 4 <= count; k += 4) {
+    br.refill();
+    if (br.have < (int32_t)(4 * log)) break;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint16_t e = z.huf[br.acc >> (64 - log)];
+      out[k + j] = (uint8_t)e;
+      br.skip(e >> 8);
+    }
+  }
+  for (; k < count; ++k) {
     const uint16_t e = z.huf[br.peek(log)];
     out[k] = (uint8_t)e;
     br.skip(e >> 8);
   }
-  return br.bits == 0;
+  return br.bits() == 0;
 }
 
 // Sets up one sequence table (literal lengths 0, offsets 1, match lengths 2)
@@ -552,7 +562,7 @@ __host__ __device__ __forceinline__ int32_t zstd_block(const Team& tm, ZState& z
         sml = cm.base + br.read(cm.nb);
         sof = co.base + br.read(co.nb);
       }
-      if (br.bits < 0) return kErrStream;
+      if (br.bits() < 0) return kErrStream;
       if (lp + ll > lsize) return kErrStream;
       if (o.op + ll + ml > o.cap) return kErrOutput;
       if (off == 0 || off > o.op + ll - o.frame0) return kErrOffset;
@@ -575,7 +585,7 @@ __host__ __device__ __forceinline__ int32_t zstd_block(const Team& tm, ZState& z
       o.op += ll + ml;
       lp += ll;
     }
-    if (br.bits != 0) return kErrStream;
+    if (br.bits() != 0) return kErrStream;
   }
   if (o.op + (lsize - lp) > o.cap) return kErrOutput;
   team_copy(tm, o.dst + o.op, lit + lp, lsize - lp);
