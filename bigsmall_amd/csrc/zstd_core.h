@@ -578,9 +578,23 @@ __host__ __device__ __forceinline__ int32_t zstd_block(const Team& tm, ZState& z
       }
       uint8_t* d = o.dst + o.op;
       team_copy(tm, d, lit + lp, ll);
-      for (uint64_t j = tm.lane(); j < ml; j += Team::size) {
-        const uint64_t src = from + (off >= ml ? j : j % off);
-        o.dst[o.op + ll + j] = src >= o.op ? lit[lp + (src - o.op)] : o.dst[src];
+      if (off >= ml) {
+        for (uint64_t j = tm.lane(); j < ml; j += Team::size) {
+          const uint64_t src = from + j;
+          o.dst[o.op + ll + j] = src >= o.op ? lit[lp + (src - o.op)] : o.dst[src];
+        }
+      } else {
+        // j mod off kept incrementally: j grows by the team size each round
+        // (off < ml < 2^32, so this is 32-bit arithmetic and two divisions per
+        // sequence instead of one 64-bit modulo per byte)
+        const uint32_t off32 = off, step = Team::size % off32;
+        uint32_t r = tm.lane() % off32;
+        for (uint64_t j = tm.lane(); j < ml; j += Team::size) {
+          const uint64_t src = from + r;
+          o.dst[o.op + ll + j] = src >= o.op ? lit[lp + (src - o.op)] : o.dst[src];
+          r += step;
+          if (r >= off32) r -= off32;
+        }
       }
       o.op += ll + ml;
       lp += ll;
