@@ -102,18 +102,21 @@ def load_to_device(src, device="cuda", dtype=None, decoder: engine.GroupDecoder 
                 deferred.append(g)
                 continue
             lo, hi = engine.group_span(g)
-            res = dec.decode_group(g, reader, lo, hi - lo, dtype=dtype, xor_base=xor_base)
+            res = dec.decode_group(g, reader, lo, hi - lo, xor_base=xor_base)
             pending.append(res)
             decoded.update(res.tensors)
         for res in pending:
             res.wait("decode")
         for g in deferred:        # groups holding ties to tensors of other groups
             lo, hi = engine.group_span(g)
-            res = dec.decode_group(g, reader, lo, hi - lo, resolve_tied=decoded.get, dtype=dtype, xor_base=xor_base)
+            res = dec.decode_group(g, reader, lo, hi - lo, resolve_tied=decoded.get, xor_base=xor_base)
             decoded.update(res.wait("decode"))
     finally:
         reader.close()
-    return {t["name"]: decoded[t["name"]] for t in tensors}
+    # dtype conversion after every tie is resolved: a follower takes its
+    # master's stored bytes, never converted ones
+    conv = lambda v: v.to(dtype) if dtype is not None and v.is_floating_point() and v.dtype != dtype else v
+    return {t["name"]: conv(decoded[t["name"]]) for t in tensors}
 
 
 def load(src: str | Path, device: str = "cuda", progress: bool = True) -> dict:

@@ -13,8 +13,10 @@ one launch per codec family):
   2. the decode stream waits for that copy only, then launches
        - one batched BSCK launch (bs_chunk_decode_batch) for every
          bf16_chunked_v1 / fp8_chunked_v1 entry of the group,
-       - bs_refcodec_decode per reference-format entry (bf16_parallel_v1,
-         bf16_se_tans, bf16_se_single_kernel),
+       - one bs_refcodec_decode_serial_batch launch for the group's
+         reference-format entries (bf16_parallel_v1, bf16_se_tans,
+         bf16_se_single_kernel) of 65,536 elements or more, so all their
+         chains run side by side, and bs_refcodec_decode per smaller one,
        - one bs_zstd_decode launch for the group's zstd frames (`zstd`,
          `zstd_xor_delta` and the index streams of `special` lowcard
          entries), then bs_lut_expand per lowcard entry,
@@ -64,6 +66,27 @@ def entry_numel(t: dict) -> int:
 
 def is_lowcard(t: dict) -> bool:
     return t["codec"] == "special" and (t.get("extra") or {}).get("special_kind") == "lowcard"
+
+
+def tied_copy(src, t: dict):
+    """A tied_ref follower: its master's bytes under the follower's own dtype
+    and shape. The reference hands the master's raw bytes to the follower's
+    _raw_to_numpy (bigsmall/decoder.py:138-155, bigsmall/streaming.py:163-190),
+    and its encoder ties entries by (item size, shape, md5) whatever their
+    dtypes (bigsmall/tensor_analysis.py:97-110), so F32 and I32 zeros, or BF16
+    and F16 words, can share one blob."""
+    import torch
+    dt = torch_dtype(t["dtype"])
+    shape = [int(s) for s in t["shape"]]
+    if src.dtype == dt and list(src.shape) == shape:
+        return src.clone()
+    raw = src.contiguous().view(-1)
+    raw = raw.view(torch.uint8) if raw.numel() else raw.to(torch.uint8)
+    need = tensor_numel(t) * torch.empty((), dtype=dt).element_size()
+    if raw.numel() != need:
+        raise ValueError(f"tied_ref {t['name']!r}: master holds {raw.numel()} bytes, "
+                         f"{t['dtype']} {shape} needs {need}")
+    return raw.clone().view(dt).reshape(shape)
 
 
 def check_supported(t: dict) -> None:
@@ -203,6 +226,7 @@ class GroupDecoder:
         keep = [d_span]
         jobs = []
         refs = []
+        serial_refs = []
         raws = []
         zst = zstd_gpu.ZstdLaunch(self.device)
         base = d_span.data_ptr()
@@ -246,7 +270,10 @@ class GroupDecoder:
                 if n == 0 or nb == 0:
                     continue
                 plan = _refstreams.PARSERS[codec](bytes(host[off:off + nb]), n)
-                refs.append((_refstreams.RefLaunch(plan, base + off, self.device), o))
+                if _refstreams.serial_ok(plan):
+                    serial_refs.append((plan, base + off, o.data_ptr()))
+                else:
+                    refs.append((_refstreams.RefLaunch(plan, base + off, self.device), o))
             elif codec in ZSTD_CODECS:
                 if nb == 0:
                     raise ValueError(f"{t['name']}: empty {codec} blob")
@@ -271,6 +298,12 @@ class GroupDecoder:
             batch = ChunkBatch([j for j, _ in jobs], self.device)
             keep.append(batch)
             batch.launch(status, self.stream)
+        if serial_refs:
+            # every large reference-format tensor of the group in one batched
+            # wave-serial launch: their chains run side by side
+            rb = _refstreams.RefBatch(serial_refs, self.device)
+            keep.append(rb)
+            rb.launch(status.ptr, int(self.stream.cuda_stream))
         for launch, o in refs:
             keep.append(launch)
             launch.launch(o.data_ptr(), status.ptr, int(self.stream.cuda_stream))
@@ -286,7 +319,7 @@ class GroupDecoder:
                 src = resolve_tied(master)
             if src is None:
                 raise KeyError(f"tied_ref master {master!r} of {t['name']!r} not found")
-            out[t["name"]] = src.clone()
+            out[t["name"]] = tied_copy(src, t)
         if dtype is not None:
             for k, v in out.items():
                 if v.is_floating_point() and v.dtype != dtype:

@@ -110,7 +110,8 @@ class CompressedKVCache:
         self._raw_size_bytes = self._block_raw = 0
 
     def __len__(self) -> int:
-        return len(self._compressed) + len(self._blocks)
+        # a layer stored through both set() and set_blocks() counts once
+        return len(set(self._compressed) | set(self._blocks))
 
     def __repr__(self) -> str:
         cr = self.compression_ratio()
@@ -181,6 +182,16 @@ class CompressedKVCache:
     def block_count(self, layer_idx) -> int:
         return len(self._blocks[layer_idx].k_blocks)
 
+    def _block_ids(self, L: _LayerBlocks, layer_idx, block_ids) -> list[int]:
+        """Block ids as ints, each in [0, block count): a negative id is an
+        error, not a block counted from the end."""
+        ids = [int(i) for i in block_ids]
+        n = len(L.k_blocks)
+        for bi in ids:
+            if not 0 <= bi < n:
+                raise IndexError(f"layer {layer_idx!r}: block {bi} out of range (layer has {n} blocks)")
+        return ids
+
     def get_blocks(self, layer_idx, block_ids):
         return self.get_blocks_multi([(layer_idx, block_ids)])[0]
 
@@ -192,7 +203,7 @@ class CompressedKVCache:
         jobs, results = [], []
         for layer_idx, block_ids in requests:
             L = self._blocks[layer_idx]
-            ids = [int(i) for i in block_ids]
+            ids = self._block_ids(L, layer_idx, block_ids)
             k, v = _block_outputs(len(ids), L, dev)
             base = L.arena.data_ptr()
             for j, bi in enumerate(ids):
@@ -217,7 +228,7 @@ class CompressedKVCache:
         jobs, results = [], []
         for layer_idx, block_ids in requests:
             L = self._blocks[layer_idx]
-            ids = [int(i) for i in block_ids]
+            ids = self._block_ids(L, layer_idx, block_ids)
             k, v = _block_outputs(len(ids), L, dev)
             for j, bi in enumerate(ids):
                 for blocks, out in ((L.k_blocks, k), (L.v_blocks, v)):

@@ -176,15 +176,25 @@ class StreamingLoader:
         from . import engine
         by_shard: dict[Path, list] = {}
         alias: dict[str, str] = {}
+        followers: dict[Path, list] = {}
         for n in names:
-            e = self._master(self._index[n])
-            alias[n] = e.name
+            own = self._index[n]
+            e = self._master(own)
             lst = by_shard.setdefault(e.shard_path, [])
             if all(x.name != e.name for x in lst):
                 lst.append(e)
+            if n != e.name and (own.meta["dtype"] != e.meta["dtype"] or
+                                [int(s) for s in own.meta["shape"]] != [int(s) for s in e.meta["shape"]]):
+                # a follower of another dtype or shape: the engine reinterprets the
+                # master's bytes for it before any dtype conversion
+                followers.setdefault(e.shard_path, []).append(
+                    {**own.meta, "name": n, "codec": "tied_ref", "extra": {"tied_to": e.name}})
+                alias[n] = n
+            else:
+                alias[n] = e.name
         jobs = []
         for shard, ents in by_shard.items():
-            metas = [e.meta for e in ents]
+            metas = [e.meta for e in ents] + followers.get(shard, [])
             lo, hi = engine.group_span(metas)
             res = eng.decode_group(metas, self._reader(shard), lo, hi - lo, dtype=self.dtype)
             jobs.append(res)

@@ -197,3 +197,45 @@ def test_kv_compression_ratio_below_75pct():
     assert ratio < 0.75, f"KV compression ratio {ratio * 100:.2f}% exceeds the 75% gate"
     cache = CompressedKVCache(device="cuda")       # the empty-cache API needs no GPU
     assert len(cache) == 0 and cache.memory_usage() == 0 and cache.compression_ratio() is None
+
+
+def test_kv_len_counts_a_layer_once_and_block_ids_are_checked():
+    """A layer stored through set() and set_blocks() counts once; a negative
+    or too-large block id raises IndexError instead of wrapping."""
+    from bigsmall_amd.kv_cache_manager import CompressedKVCache, _LayerBlocks
+    torch.manual_seed(1)
+    k = (torch.randn(1, 2, 64, 8) * 0.5).to(torch.bfloat16)
+    cache = CompressedKVCache(device="cuda")
+    cache.set(0, k, k)
+    cache._blocks[0] = _LayerBlocks([1, 2, 16, 8], 256, None, [(0, 16, 1, 1)] * 4, [(0, 16, 1, 1)] * 4)
+    cache._blocks[1] = cache._blocks[0]
+    assert len(cache) == 2
+    L = cache._blocks[0]
+    assert cache._block_ids(L, 0, [0, 3, 2]) == [0, 3, 2]
+    for bad in ([-1], [4], [0, 7]):
+        with pytest.raises(IndexError):
+            cache._block_ids(L, 0, bad)
+
+
+@pytest.mark.parametrize("master_dtype,follower_dtype,shape", [
+    (torch.float32, torch.int32, [4, 300]),          # all-zero buffers of two dtypes share one blob
+    (torch.bfloat16, torch.float16, [600]),          # same 16-bit words, other dtype
+    (torch.bfloat16, torch.bfloat16, [20, 30]),      # same dtype and shape: a plain copy
+    (torch.bfloat16, torch.bfloat16, [600]),         # same bytes, other shape
+])
+def test_tied_follower_takes_its_own_dtype_and_shape(master_dtype, follower_dtype, shape):
+    """The engine's tied copy reinterprets the master's bytes with the
+    follower's dtype and shape, as the reference's _raw_to_numpy does with the
+    master's raw bytes (bigsmall/decoder.py:138-155)."""
+    g = torch.Generator().manual_seed(3)
+    words = torch.randint(0, 1 << 15, (600,), generator=g, dtype=torch.int16)
+    master = words.view(master_dtype) if master_dtype != torch.float32 else torch.zeros(1200, dtype=torch.float32)
+    master = master.reshape(20, 30) if master.numel() == 600 else master.reshape(4, 300)
+    t = {"name": "f", "dtype": {torch.int32: "I32", torch.float16: "F16", torch.bfloat16: "BF16"}[follower_dtype],
+         "shape": shape}
+    out = engine.tied_copy(master, t)
+    assert out.dtype == follower_dtype and list(out.shape) == shape
+    assert out.contiguous().view(-1).view(torch.uint8).tolist() == master.contiguous().view(-1).view(torch.uint8).tolist()
+    assert out.data_ptr() != master.data_ptr()
+    with pytest.raises(ValueError):
+        engine.tied_copy(master, {**t, "shape": [7]})

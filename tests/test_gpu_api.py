@@ -422,3 +422,39 @@ def test_from_pretrained_multi_shard(tmp_path):
     for k, v in (a | b).items():
         assert _bytes(sd[k]) == _bytes(v), k
     assert sd["lm_head.weight"].data_ptr() == sd["model.embed_tokens.weight"].data_ptr()
+
+
+def test_tie_across_dtypes_round_trip(tmp_path):
+    """An all-zero F32 buffer and an all-zero I32 buffer of one shape, and BF16
+    and F16 tensors holding the same 16-bit words, are tied by the encoder
+    (item size, shape and md5 match, as in bigsmall/tensor_analysis.py:97-110);
+    load(), decompress() and the streaming loader give each its own dtype."""
+    from bigsmall_amd import decoder
+    from bigsmall_amd.streaming import StreamingLoader
+    g = torch.Generator().manual_seed(11)
+    words = (torch.randn(64, 128, generator=g) * 0.02).bfloat16()
+    src = {"model.layers.0.mlp.mask_f32": torch.zeros(8, 256, dtype=torch.float32),
+           "model.layers.0.mlp.mask_i32": torch.zeros(8, 256, dtype=torch.int32),
+           "model.layers.0.self_attn.w_bf16": words,
+           "model.layers.0.self_attn.w_f16": words.view(torch.float16).clone(),
+           "model.layers.1.self_attn.w_f16_2": words.view(torch.float16).clone()}
+    p = tmp_path / "tied.bs"
+    compress(src, p)
+    header, _ = container.read_header(p)
+    codecs = {t["name"]: t["codec"] for t in header["tensors"]}
+    assert codecs["model.layers.0.mlp.mask_i32"] == "tied_ref" and codecs["model.layers.0.self_attn.w_f16"] == "tied_ref"
+    _say("[api] tie across dtypes: load")
+    out = decoder.load(p)
+    for k, v in src.items():
+        assert out[k].dtype == v.dtype and tuple(out[k].shape) == tuple(v.shape), k
+        assert _bytes(out[k]) == _bytes(v), k
+    host = decoder.decompress(p)
+    for t in header["tensors"]:
+        assert hashlib.md5(np.ascontiguousarray(host[t["name"]]).tobytes()).hexdigest() == t["md5"], t["name"]
+    _say("[api] tie across dtypes: streaming")
+    with StreamingLoader(p, prefetch=1) as L:
+        got = {}
+        for li, layer in L.iter_layers():
+            got.update(layer)
+    for k, v in src.items():
+        assert got[k].dtype == v.dtype and _bytes(got[k]) == _bytes(v), k
