@@ -84,9 +84,14 @@ def compress(src, dst: str | Path, mode: str = "balanced", progress: bool = Fals
     stats = codec_registry.CodecStats()
     seen: dict[tuple, int] = {}
     header_tensors = []
+    # md5 of every tensor up front, on a few threads (hashlib releases the GIL
+    # on large buffers); the tie decisions below still run in tensor order
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max(1, min(8, len(tensors)))) as pool:
+        md5s = list(pool.map(lambda t: hashlib.md5(t["raw"]).hexdigest(), tensors))
     for i, t in enumerate(tensors):
         raw = t["raw"]
-        md5 = hashlib.md5(raw).hexdigest()
+        md5 = md5s[i]
         special = None
         key = (t["item_bytes"], tuple(t["shape"]), md5)
         if len(raw) >= TIE_MIN_BYTES and key in seen:
