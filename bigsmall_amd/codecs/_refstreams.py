@@ -37,7 +37,11 @@ SE_STREAM_DTYPE = np.dtype([("words", "<u8"), ("x0", "<u4"), ("n_words", "<u4"),
                             ("first", "<u8"), ("stride", "<u4"), ("reserved", "<u4")])
 MANT_BUCKET_DTYPE = np.dtype([("words", "<u8"), ("x0", "<u4"), ("n_words", "<u4"), ("tail", "<u4"), ("n", "<u4"),
                               ("perm_begin", "<u8"), ("table", "<u4"), ("reserved", "<u4")])
-assert SE_STREAM_DTYPE.itemsize == 40 and MANT_BUCKET_DTYPE.itemsize == 40
+REF_TASK_DTYPE = np.dtype([("streams", "<u8"), ("se_table", "<u8"), ("bstart", "<u8"), ("buckets", "<u8"),
+                           ("mant_tables", "<u8"), ("out", "<u8"), ("n_out", "<u8"), ("work_offset", "<u8"),
+                           ("n_streams", "<u4"), ("n_buckets", "<u4"), ("n_tables", "<u4"), ("chain_begin", "<u4"),
+                           ("tile_begin", "<u4"), ("stream_begin", "<u4")])
+assert SE_STREAM_DTYPE.itemsize == 40 and MANT_BUCKET_DTYPE.itemsize == 40 and REF_TASK_DTYPE.itemsize == 88
 
 
 class _Reader:
@@ -302,41 +306,115 @@ PARSERS = {"bf16_parallel_v1": parse_parallel, "bf16_se_tans": parse_tans,
            "bf16_se_single_kernel": parse_single_kernel}
 
 
+def _plan_arrays(plan: RefPlan, blob_ptr: int) -> list[np.ndarray]:
+    """The device arrays of one parsed blob, as host bytes: SE stream
+    descriptors, SE decode table, bucket starts, bucket descriptors, mantissa
+    decode tables."""
+    se = np.zeros(len(plan.se_streams), SE_STREAM_DTYPE)
+    for i, (s, first, stride, n) in enumerate(plan.se_streams):
+        se[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, first, stride, 0)
+    mb = np.zeros(len(plan.buckets), MANT_BUCKET_DTYPE)
+    for i, (s, pb, n, t) in enumerate(plan.buckets):
+        mb[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, pb, t, 0)
+    tables = (np.stack([decode_table_mant(f) for f in plan.mant_freqs]) if plan.mant_freqs
+              else np.zeros((1, M_MANT), np.uint32))
+    return [se.view(np.uint8), decode_table_se(plan.se_freqs).reshape(-1).view(np.uint8),
+            np.stack(plan.bstart).reshape(-1).view(np.uint8) if plan.bstart else np.zeros(0, np.uint8),
+            mb.view(np.uint8), tables.reshape(-1).view(np.uint8)]
+
+
+def _layout(arrays: list[np.ndarray]) -> tuple[int, list[int]]:
+    """Offsets of byte arrays placed one after another on 256-byte boundaries."""
+    offs, pos = [], 0
+    for h in arrays:
+        pos = (pos + 255) & ~255
+        offs.append(pos)
+        pos += h.nbytes
+    return max(pos, 1), offs
+
+
+def _pack(arrays: list[np.ndarray]) -> tuple[np.ndarray, list[int]]:
+    """Concatenate byte arrays at 256-byte offsets; returns (buffer, offsets)."""
+    size, offs = _layout(arrays)
+    buf = np.zeros(size, np.uint8)
+    for h, o in zip(arrays, offs):
+        buf[o:o + h.nbytes] = h
+    return buf, offs
+
+
+def serial_ok(plan: RefPlan) -> bool:
+    """The wave-serial path applies: a tensor of SERIAL_MIN_ELEMENTS or more
+    whose streams each hold at most ceil(n / streams) symbols (every blob the
+    reference's encoders write; a smaller tensor decodes as fast with one lane
+    per chain)."""
+    max_len = max((n for _, _, _, n in plan.se_streams), default=0)
+    return plan.n >= SERIAL_MIN_ELEMENTS and len(plan.se_streams) > 0 and max_len <= -(-plan.n // len(plan.se_streams))
+
+
+class RefBatch:
+    """The wave-serial decode of several parsed blobs (a layer's
+    reference-format tensors) as one bs_refcodec_decode_serial_batch launch:
+    all their chains run side by side. items: [(plan, blob_ptr, out_ptr)],
+    every plan accepted by serial_ok. Device buffers stay alive with this
+    object until the decode launched from it has completed."""
+
+    def __init__(self, items: list, device):
+        import torch
+        L = _native.lib()
+        arrays = []
+        tasks = np.zeros(len(items), REF_TASK_DTYPE)
+        chain = tile = stream = work = 0
+        for i, (plan, blob_ptr, out_ptr) in enumerate(items):
+            if not serial_ok(plan):
+                raise ValueError("RefBatch: a tensor the wave-serial path does not take")
+            arrays += _plan_arrays(plan, blob_ptr)
+            ns, nb = len(plan.se_streams), len(plan.buckets)
+            nt = max(1, len(plan.mant_freqs))
+            tiles = int(L.bs_refcodec_serial_tiles(plan.n, ns))
+            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, chain, tile, stream)
+            work += (int(L.bs_refcodec_serial_work_bytes(plan.n, ns)) + 255) & ~255
+            chain, tile, stream = chain + ns + nb, tile + ns * tiles, stream + ns
+        size, offs = _layout(arrays + [tasks.view(np.uint8)])
+        self.dev = torch.empty(size, dtype=torch.uint8, device=device)
+        base = self.dev.data_ptr()
+        for i in range(len(items)):        # descriptor pointers into the device buffer
+            o = offs[5 * i: 5 * i + 5]
+            for f, off in zip(("streams", "se_table", "bstart", "buckets", "mant_tables"), o):
+                tasks[f][i] = base + off
+        buf, _ = _pack(arrays + [tasks.view(np.uint8)])
+        self.dev.copy_(torch.from_numpy(buf))
+        self.p_tasks = base + offs[-1]
+        self.n_tasks = len(items)
+        self.totals = (chain, tile, stream)
+        self.work = torch.empty(max(work, 256), dtype=torch.uint8, device=device)
+
+    def launch(self, status_ptr: int, stream_ptr: int) -> None:
+        if not self.n_tasks:
+            return
+        rc = _native.lib().bs_refcodec_decode_serial_batch(self.p_tasks, self.n_tasks, *self.totals,
+                                                            self.work.data_ptr(), self.work.numel(), status_ptr,
+                                                            stream_ptr)
+        _native.check(rc, "bs_refcodec_decode_serial_batch")
+
+
 class RefLaunch:
     """Device-side tables and descriptors of one parsed blob (kept alive until
     the decode launched from them has completed)."""
 
     def __init__(self, plan: RefPlan, blob_ptr: int, device):
         import torch
-        se = np.zeros(len(plan.se_streams), SE_STREAM_DTYPE)
-        for i, (s, first, stride, n) in enumerate(plan.se_streams):
-            se[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, first, stride, 0)
-        mb = np.zeros(len(plan.buckets), MANT_BUCKET_DTYPE)
-        for i, (s, pb, n, t) in enumerate(plan.buckets):
-            mb[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, pb, t, 0)
-        tables = (np.stack([decode_table_mant(f) for f in plan.mant_freqs]) if plan.mant_freqs
-                  else np.zeros((1, M_MANT), np.uint32))
-        host = [se.view(np.uint8), decode_table_se(plan.se_freqs).reshape(-1).view(np.uint8),
-                np.stack(plan.bstart).reshape(-1).view(np.uint8) if plan.bstart else np.zeros(0, np.uint8),
-                mb.view(np.uint8), tables.reshape(-1).view(np.uint8)]
-        offs, pos = [], 0
-        for h in host:
-            pos = (pos + 255) & ~255
-            offs.append(pos)
-            pos += h.nbytes
-        buf = np.zeros(max(pos, 1), np.uint8)
-        for h, o in zip(host, offs):
-            buf[o:o + h.nbytes] = h
+        host = _plan_arrays(plan, blob_ptr)
+        buf, offs = _pack(host)
         self.dev = torch.from_numpy(buf).to(device)
         base = self.dev.data_ptr()
         self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets, self.p_tables = (base + o for o in offs)
-        self.n_streams, self.n_buckets, self.n_tables = len(se), len(mb), tables.shape[0]
+        self.n_streams, self.n_buckets = len(plan.se_streams), len(plan.buckets)
+        self.n_tables = max(1, len(plan.mant_freqs))
         self.n = plan.n
         # one wavefront per chain (bs_refcodec_decode_serial) unless the tensor
         # is small, where one lane per chain (bs_refcodec_decode) is as fast
-        max_len = max((n for _, _, _, n in plan.se_streams), default=0)
-        self.serial = (plan.n >= SERIAL_MIN_ELEMENTS and len(se) > 0 and
-                       max_len <= -(-plan.n // len(se)))
+        self.serial = serial_ok(plan)
+        se = plan.se_streams
         if self.serial:
             nbytes = int(_native.lib().bs_refcodec_serial_work_bytes(plan.n, len(se)))
             self.work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
@@ -376,5 +454,5 @@ def decode_host(codec: str, blob: bytes, n_weights: int) -> bytes:
     return out.cpu().numpy().tobytes()
 
 
-__all__ = ["PARSERS", "RefLaunch", "RefPlan", "decode_host", "parse_parallel", "parse_tans",
+__all__ = ["PARSERS", "RefBatch", "RefLaunch", "RefPlan", "serial_ok", "decode_host", "parse_parallel", "parse_tans",
            "parse_single_kernel", "decode_table_se", "decode_table_mant"]

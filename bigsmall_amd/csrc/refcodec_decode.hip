@@ -190,7 +190,7 @@ __device__ __forceinline__ void seg_land(LDS uint8_t* ring, uint64_t q, uint32_t
 // symbols (what the placement tiles cover) and every element index inside the
 // output. The three passes check it alike, so a bad descriptor is reported and
 // skipped, never followed.
-__device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint32_t max_len, uint64_t n_out) {
+__device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint64_t max_len, uint64_t n_out) {
   return S.n <= max_len && S.stride != 0 && (S.n == 0 || S.first + (uint64_t)(S.n - 1) * S.stride < n_out);
 }
 
@@ -301,40 +301,91 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   }
 }
 
-// Block k < n_streams: SE stream k (element first + i*stride for symbol i).
-// Block n_streams + b: mantissa bucket b, written to mant[perm_begin ...]
-// (bucket order). max_len: the longest stream the placement passes hold.
-__global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __restrict__ se, uint32_t n_streams,
-                                                       uint32_t max_len, const uint32_t* __restrict__ se_table,
-                                                       const bs_mant_bucket* __restrict__ buckets,
-                                                       const uint32_t* __restrict__ mant_tables, uint32_t n_tables,
-                                                       uint16_t* __restrict__ out, uint64_t n_out,
-                                                       uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
+// ---- tasks of a wave-serial launch. Every tensor of a batch is one task; its
+// chains, tiles and streams occupy consecutive workgroups of the four grids
+// (chain_begin, tile_begin, stream_begin), so one launch of each kernel covers
+// the whole batch and the chains of all its tensors run side by side. The
+// single-tensor entry point passes its one task by value (tasks == nullptr).
+
+__host__ __device__ inline uint64_t serial_max_len(uint64_t n_out, uint32_t n_streams) {
+  return (n_out + n_streams - 1) / n_streams;
+}
+__host__ __device__ inline uint32_t serial_tiles(uint64_t n_out, uint32_t n_streams) {
+  return (uint32_t)((serial_max_len(n_out, n_streams) + kTile - 1) / kTile);
+}
+__host__ __device__ inline uint64_t serial_work(uint64_t n_out, uint32_t n_streams) {
+  return ((n_out + 255) & ~255ull) + (uint64_t)n_streams * serial_tiles(n_out, n_streams) * 256 * 4;
+}
+
+// A task every kernel may follow: 1 <= n_out < 2^32, at least one stream, a
+// tile count that fits 32 bits, and its scratch inside the work buffer. Every
+// kernel checks it alike, so a bad task is reported once and skipped by all.
+__device__ __forceinline__ bool task_ok(const bs_ref_task& T, uint64_t work_bytes) {
+  if (T.n_out == 0 || T.n_out > 0xFFFFFFFFull || T.n_streams == 0 || (T.work_offset & 255u)) return false;
+  if ((uint64_t)T.n_streams * serial_tiles(T.n_out, T.n_streams) > 0xFFFFFFFFull) return false;
+  return T.work_offset <= work_bytes && serial_work(T.n_out, T.n_streams) <= work_bytes - T.work_offset;
+}
+
+enum { kChainGrid = 0, kTileGrid = 1, kStreamGrid = 2 };
+template <int G>
+__device__ __forceinline__ uint32_t grid_begin(const bs_ref_task& t) {
+  return G == kChainGrid ? t.chain_begin : G == kTileGrid ? t.tile_begin : t.stream_begin;
+}
+// The task whose range of grid G holds workgroup b (binary search over the
+// ascending begins; wave-uniform).
+template <int G>
+__device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
+                                                 const bs_ref_task& single, uint32_t b) {
+  if (tasks == nullptr) return single;
+  uint32_t lo = 0, hi = n_tasks;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (grid_begin<G>(tasks[mid]) <= b) lo = mid; else hi = mid;
+  }
+  return tasks[lo];
+}
+
+// Chain grid: workgroup chain_begin + k (k < n_streams) decodes SE stream k
+// (element first + i*stride for symbol i); chain_begin + n_streams + b decodes
+// mantissa bucket b into mant[perm_begin ...] (bucket order).
+__global__ __launch_bounds__(kWave) void serial_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
+                                                       bs_ref_task single, uint8_t* __restrict__ work,
+                                                       uint64_t work_bytes, int32_t* __restrict__ status) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   LDS uint8_t* ring = (LDS uint8_t*)smem;
   LDS u32x4* tbl = (LDS u32x4*)(smem + kRingB);      // {f, slot - cf, output, 0} per slot
   const uint32_t lane = threadIdx.x;
-  if (blockIdx.x < n_streams) {
-    const bs_se_stream S = se[blockIdx.x];
-    if (!stream_ok(S, max_len, n_out)) {
+  const bs_ref_task T = pick_task<kChainGrid>(tasks, n_tasks, single, blockIdx.x);
+  if (blockIdx.x < T.chain_begin) return;
+  const uint32_t c = blockIdx.x - T.chain_begin;
+  if ((uint64_t)c >= (uint64_t)T.n_streams + T.n_buckets) return;
+  if (!task_ok(T, work_bytes)) {
+    if (c == 0 && lane == 0) flag(status, BS_DEV_ERR_HEADER);
+    return;
+  }
+  const uint64_t max_len = (uint64_t)serial_tiles(T.n_out, T.n_streams) * kTile;
+  uint8_t* mant = work + T.work_offset;
+  if (c < T.n_streams) {
+    const bs_se_stream S = T.streams[c];
+    if (!stream_ok(S, max_len, T.n_out)) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
     for (uint32_t i = lane; i < 4096; i += kWave) {
-      const uint32_t lo = se_table[2 * i], sym = se_table[2 * i + 1];
+      const uint32_t lo = T.se_table[2 * i], sym = T.se_table[2 * i + 1];
       const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
       tbl[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
     }
     wave_sync();
     serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring,
-                       (GLB uint8_t*)(out + S.first), S.stride, status);
+                       (GLB uint8_t*)(T.out + S.first), S.stride, status);
   } else {
-    const bs_mant_bucket B = buckets[blockIdx.x - n_streams];
-    if (B.table >= n_tables || B.perm_begin + B.n > n_out) {
+    const bs_mant_bucket B = T.buckets[c - T.n_streams];
+    if (B.table >= T.n_tables || B.perm_begin + B.n > T.n_out) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
-    const GLB uint32_t* t = (const GLB uint32_t*)mant_tables + (uint64_t)B.table * 1024u;
+    const GLB uint32_t* t = (const GLB uint32_t*)T.mant_tables + (uint64_t)B.table * 1024u;
     for (uint32_t i = lane; i < 1024; i += kWave) {
       const uint32_t e = t[i];
       tbl[i] = u32x4{e & 0x7FFu, (e >> 11) & 0x3FFu, (e >> 21) & 0x7Fu, 0u};
@@ -345,30 +396,45 @@ __global__ __launch_bounds__(kWave) void serial_kernel(const bs_se_stream* __res
   }
 }
 
-// Exponent histogram of each tile: block k * tps + t covers symbols
-// [t*kTile, (t+1)*kTile) of stream k.
-__global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ out, uint64_t n_out,
-                                                   const bs_se_stream* __restrict__ se, uint32_t tps,
-                                                   uint32_t* __restrict__ hist) {
+// Tile grid, one workgroup per (stream k, tile t) of a task (t fastest):
+// exponent histogram of symbols [t*kTile, (t+1)*kTile) of stream k.
+__global__ __launch_bounds__(256) void hist_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
+                                                   bs_ref_task single, uint8_t* __restrict__ work,
+                                                   uint64_t work_bytes) {
   __shared__ uint32_t h[256];
-  const uint32_t tid = threadIdx.x, k = blockIdx.x / tps, t = blockIdx.x % tps;
-  const bs_se_stream S = se[k];
+  const uint32_t tid = threadIdx.x;
+  const bs_ref_task T = pick_task<kTileGrid>(tasks, n_tasks, single, blockIdx.x);
+  if (blockIdx.x < T.tile_begin || !task_ok(T, work_bytes)) return;
+  const uint32_t tps = serial_tiles(T.n_out, T.n_streams), local = blockIdx.x - T.tile_begin;
+  if (local >= T.n_streams * tps) return;
+  const uint32_t k = local / tps, t = local % tps;
+  uint32_t* hist = (uint32_t*)(work + T.work_offset + ((T.n_out + 255) & ~255ull));
+  const bs_se_stream S = T.streams[k];
   h[tid] = 0;
   __syncthreads();
-  const uint32_t lo = t * kTile, hi = stream_ok(S, tps * kTile, n_out) ? min(S.n, lo + kTile) : lo;
-  for (uint32_t i = lo + tid; i < hi; i += 256) atomicAdd(&h[(out[S.first + (uint64_t)i * S.stride] >> 7) & 0xFFu], 1u);
+  const uint32_t lo = t * kTile;
+  const uint32_t hi = stream_ok(S, (uint64_t)tps * kTile, T.n_out) ? (uint32_t)min((uint64_t)S.n, (uint64_t)lo + kTile) : lo;
+  for (uint32_t i = lo + tid; i < hi; i += 256)
+    atomicAdd(&h[(T.out[S.first + (uint64_t)i * S.stride] >> 7) & 0xFFu], 1u);
   __syncthreads();
-  hist[(uint64_t)blockIdx.x * 256 + tid] = h[tid];
+  hist[(uint64_t)local * 256 + tid] = h[tid];
 }
 
-// Block k, thread e: turn stream k's tile counts of exponent e into each
-// tile's first position in the bucket (bstart[k][e] + counts of the earlier
-// tiles), and check that the decoded exponents fill every bucket exactly.
-__global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, uint32_t tps,
-                                                   const uint32_t* __restrict__ bstart, int32_t* __restrict__ status) {
+// Stream grid, one workgroup per stream k of a task, thread e: turn stream
+// k's tile counts of exponent e into each tile's first position in the
+// bucket (bstart[k][e] + counts of the earlier tiles), and check that the
+// decoded exponents fill every bucket exactly.
+__global__ __launch_bounds__(256) void scan_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
+                                                   bs_ref_task single, uint8_t* __restrict__ work,
+                                                   uint64_t work_bytes, int32_t* __restrict__ status) {
   const uint32_t e = threadIdx.x;
-  const uint32_t* bs = bstart + (uint64_t)blockIdx.x * 257;
-  uint32_t* hk = hist + (uint64_t)blockIdx.x * tps * 256;
+  const bs_ref_task T = pick_task<kStreamGrid>(tasks, n_tasks, single, blockIdx.x);
+  if (blockIdx.x < T.stream_begin || !task_ok(T, work_bytes)) return;
+  const uint32_t k = blockIdx.x - T.stream_begin;
+  if (k >= T.n_streams) return;
+  const uint32_t tps = serial_tiles(T.n_out, T.n_streams);
+  const uint32_t* bs = T.bstart + (uint64_t)k * 257;
+  uint32_t* hk = (uint32_t*)(work + T.work_offset + ((T.n_out + 255) & ~255ull)) + (uint64_t)k * tps * 256;
   uint32_t run = bs[e];
   for (uint32_t t = 0; t < tps; ++t) {
     const uint32_t c = hk[(uint64_t)t * 256 + e];
@@ -378,21 +444,29 @@ __global__ __launch_bounds__(256) void scan_kernel(uint32_t* __restrict__ hist, 
   if (run != bs[e + 1]) flag(status, BS_DEV_ERR_COUNT);
 }
 
-// Per tile (one wavefront): the position of each element in its bucket, from
-// the tile's first positions plus its rank among the equal exponents before
-// it (64 elements at a time: lanes with the same exponent found with eight
-// ballots); then OR the element's mantissa into it.
-__global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out, uint64_t n,
-                                                      const bs_se_stream* __restrict__ se, uint32_t tps,
-                                                      const uint32_t* __restrict__ first,
-                                                      const uint8_t* __restrict__ mant, int32_t* __restrict__ status) {
+// Tile grid again, one wavefront per tile: the position of each element in
+// its bucket, from the tile's first positions plus its rank among the equal
+// exponents before it (64 elements at a time: lanes with the same exponent
+// found with eight ballots); then OR the element's mantissa into it.
+__global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
+                                                      bs_ref_task single, uint8_t* __restrict__ work,
+                                                      uint64_t work_bytes, int32_t* __restrict__ status) {
   __shared__ uint32_t cnt[256];
-  const uint32_t lane = threadIdx.x, k = blockIdx.x / tps, t = blockIdx.x % tps;
-  const bs_se_stream S = se[k];
-  if (!stream_ok(S, tps * kTile, n)) return;     // reported by serial_kernel
-  for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)blockIdx.x * 256 + e];
+  const uint32_t lane = threadIdx.x;
+  const bs_ref_task T = pick_task<kTileGrid>(tasks, n_tasks, single, blockIdx.x);
+  if (blockIdx.x < T.tile_begin || !task_ok(T, work_bytes)) return;
+  const uint32_t tps = serial_tiles(T.n_out, T.n_streams), local = blockIdx.x - T.tile_begin;
+  if (local >= T.n_streams * tps) return;
+  const uint32_t k = local / tps, t = local % tps;
+  const uint64_t n = T.n_out;
+  const uint8_t* mant = work + T.work_offset;
+  const uint32_t* first = (const uint32_t*)(mant + ((n + 255) & ~255ull));
+  uint16_t* out = T.out;
+  const bs_se_stream S = T.streams[k];
+  if (!stream_ok(S, (uint64_t)tps * kTile, n)) return;     // reported by serial_kernel
+  for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)local * 256 + e];
   wave_sync();
-  const uint32_t lo = t * kTile, hi = min(S.n, lo + kTile);
+  const uint32_t lo = t * kTile, hi = (uint32_t)min((uint64_t)S.n, (uint64_t)lo + kTile);
   const uint64_t lt = (1ull << lane) - 1ull;
   bool bad = false;
   for (uint32_t k0 = lo; k0 < hi; k0 += kWave) {
@@ -420,6 +494,24 @@ __global__ __launch_bounds__(kWave) void place_kernel(uint16_t* __restrict__ out
     wave_sync();
   }
   if (__ballot(bad) != 0 && lane == 0) flag(status, BS_DEV_ERR_COUNT);
+}
+
+std::atomic<uint64_t> g_serial_lds{0};
+
+int launch_serial(const bs_ref_task* tasks, uint32_t n_tasks, const bs_ref_task& single, uint32_t chains,
+                  uint32_t tiles, uint32_t streams, uint8_t* work, uint64_t work_bytes, int32_t* status,
+                  hipStream_t s) {
+  constexpr uint32_t kSerLds = kRingB + 4096 * 16;
+  bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, g_serial_lds);
+  hipLaunchKernelGGL(serial_kernel, dim3(chains), dim3(kWave), kSerLds, s, tasks, n_tasks, single, work, work_bytes,
+                     status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(scan_kernel, dim3(streams), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes, status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(place_kernel, dim3(tiles), dim3(kWave), 0, s, tasks, n_tasks, single, work, work_bytes, status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 
 }  // namespace
@@ -451,9 +543,12 @@ int bs_refcodec_decode(const bs_se_stream* d_streams, uint32_t n_streams, const 
 
 uint64_t bs_refcodec_serial_work_bytes(uint64_t n_out, uint32_t n_streams) {
   if (n_streams == 0) return 0;
-  const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
-  const uint64_t tps = (max_len + kTile - 1) / kTile;
-  return ((n_out + 255) & ~255ull) + (uint64_t)n_streams * tps * 256 * 4;
+  return serial_work(n_out, n_streams);
+}
+
+uint32_t bs_refcodec_serial_tiles(uint64_t n_out, uint32_t n_streams) {
+  if (n_streams == 0 || n_out == 0) return 0;
+  return serial_tiles(n_out, n_streams);
 }
 
 int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams, const uint32_t* d_se_table,
@@ -465,24 +560,33 @@ int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams,
     return BS_ERR_ARG;
   if (n_out == 0) return BS_OK;
   if (work_bytes < bs_refcodec_serial_work_bytes(n_out, n_streams) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
-  hipStream_t s = (hipStream_t)stream;
-  uint8_t* mant = (uint8_t*)d_work;
-  uint32_t* hist = (uint32_t*)(mant + ((n_out + 255) & ~255ull));
-  const uint64_t max_len = (n_out + n_streams - 1) / n_streams;
-  const uint32_t tps = (uint32_t)((max_len + kTile - 1) / kTile);
-  constexpr uint32_t kSerLds = kRingB + 4096 * 16;
-  static std::atomic<uint64_t> lds_set{0};
-  bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, lds_set);
-  hipLaunchKernelGGL(serial_kernel, dim3(n_streams + n_buckets), dim3(kWave), kSerLds, s, d_streams, n_streams,
-                     tps * kTile, d_se_table, d_buckets, d_mant_tables, n_tables, d_out, n_out, mant, d_status);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(hist_kernel, dim3(n_streams * tps), dim3(256), 0, s, d_out, n_out, d_streams, tps, hist);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(scan_kernel, dim3(n_streams), dim3(256), 0, s, hist, tps, d_bstart, d_status);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(place_kernel, dim3(n_streams * tps), dim3(kWave), 0, s, d_out, n_out, d_streams, tps, hist, mant,
-                     d_status);
-  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+  const uint64_t tiles = (uint64_t)n_streams * serial_tiles(n_out, n_streams);
+  if ((uint64_t)n_streams + n_buckets > 0xFFFFFFFFull || tiles > 0xFFFFFFFFull) return BS_ERR_ARG;
+  bs_ref_task t{};
+  t.streams = d_streams;
+  t.se_table = d_se_table;
+  t.bstart = d_bstart;
+  t.buckets = d_buckets;
+  t.mant_tables = d_mant_tables;
+  t.out = d_out;
+  t.n_out = n_out;
+  t.work_offset = 0;
+  t.n_streams = n_streams;
+  t.n_buckets = n_buckets;
+  t.n_tables = n_tables;
+  return launch_serial(nullptr, 0u, t, n_streams + n_buckets, (uint32_t)tiles, n_streams, (uint8_t*)d_work,
+                       work_bytes, d_status, (hipStream_t)stream);
+}
+
+int bs_refcodec_decode_serial_batch(const bs_ref_task* d_tasks, uint32_t n_tasks, uint32_t total_chains,
+                                    uint32_t total_tiles, uint32_t total_streams, void* d_work, uint64_t work_bytes,
+                                    int32_t* d_status, void* stream) {
+  if (!d_status || (n_tasks && (!d_tasks || !d_work)) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
+  if (n_tasks == 0) return BS_OK;
+  if (total_chains == 0 || total_tiles == 0 || total_streams == 0) return BS_ERR_ARG;
+  bs_ref_task dummy{};
+  return launch_serial(d_tasks, n_tasks, dummy, total_chains, total_tiles, total_streams, (uint8_t*)d_work,
+                       work_bytes, d_status, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -218,6 +218,44 @@ int bs_refcodec_decode_serial(const bs_se_stream *d_streams, uint32_t n_streams,
                               const uint32_t *d_mant_tables, uint32_t n_tables, uint16_t *d_out, uint64_t n_out,
                               void *d_work, uint64_t work_bytes, int32_t *d_status, void *stream);
 
+/* Tiles per SE stream of the placement passes of the wave-serial path (the
+ * tile grid of a task holds n_streams x this many workgroups). */
+uint32_t bs_refcodec_serial_tiles(uint64_t n_out, uint32_t n_streams);
+
+/* One tensor of a batched wave-serial launch: the descriptors, tables and
+ * output of bs_refcodec_decode_serial, plus where the task sits in the batch.
+ * A task's workgroups are consecutive in each of the three grids; across the
+ * task array (device memory) chain_begin, tile_begin and stream_begin all
+ * ascend, each task starting where the previous one ends. */
+typedef struct {
+    const bs_se_stream *streams;     /* n_streams SE stream descriptors */
+    const uint32_t *se_table;        /* 4096 x {f | (slot-cf) << 13, symbol} u32 pairs */
+    const uint32_t *bstart;          /* n_streams x 257 u32 */
+    const bs_mant_bucket *buckets;   /* n_buckets */
+    const uint32_t *mant_tables;     /* n_tables x 1024 u32 */
+    uint16_t *out;                   /* n_out bf16 words */
+    uint64_t n_out;                  /* 1 .. 2^32 - 1 */
+    uint64_t work_offset;            /* multiple of 256: the task's bs_refcodec_serial_work_bytes(n_out,
+                                        n_streams) bytes of scratch start at d_work + work_offset */
+    uint32_t n_streams, n_buckets, n_tables;
+    uint32_t chain_begin;            /* chain grid: n_streams + n_buckets workgroups per task */
+    uint32_t tile_begin;             /* tile grid: n_streams x bs_refcodec_serial_tiles(n_out, n_streams) */
+    uint32_t stream_begin;           /* stream grid: n_streams */
+} bs_ref_task;
+
+/* Decode every task of d_tasks (a transformer layer's reference-format
+ * tensors) with the wave-serial path, all tasks' chains in one launch: the
+ * layer takes as long as its longest chain instead of the sum of its tensors'
+ * chains. total_* are the grid sizes (the end of the last task's range in each
+ * grid). A task whose fields are inconsistent (n_out out of range, no stream,
+ * scratch outside d_work) sets BS_DEV_ERR_HEADER and is skipped. Replaces the
+ * per-tensor decode loop of decoder.decompress (bigsmall/decoder.py:128-136)
+ * and StreamingLoader.load_layer (bigsmall/streaming.py:218-227) for the
+ * formats of bs_refcodec_decode_serial. Asynchronous on `stream`. */
+int bs_refcodec_decode_serial_batch(const bs_ref_task *d_tasks, uint32_t n_tasks, uint32_t total_chains,
+                                    uint32_t total_tiles, uint32_t total_streams, void *d_work,
+                                    uint64_t work_bytes, int32_t *d_status, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Zstandard (RFC 8878) frames on the GPU, for the reference's zstd-coded
  * entries: codec "zstd" (bigsmall/codecs/generic.py:15-18, called from

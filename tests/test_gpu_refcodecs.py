@@ -133,3 +133,68 @@ def test_single_byte_corruptions_decode_or_raise(gpu, codec, n):
     _say(f"[ref] outcomes {outcomes}")
     assert _decode(codec, blob, n) == w.tobytes()
     assert outcomes["raised"] > 0, outcomes
+
+
+def test_serial_batch_mixed_formats(gpu):
+    """One bs_refcodec_decode_serial_batch launch decodes tensors of all three
+    formats side by side (different sizes, stream counts and exponent sets);
+    each output equals its source words, and equals the one-tensor entry
+    point's output for the same blob."""
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    torch = gpu
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(21)
+    srcs = [("bf16_parallel_v1", _bf16(rng.standard_normal(300_001) * 0.02)),
+            ("bf16_se_tans", _bf16(rng.standard_t(3, 200_003) * 0.02)),
+            ("bf16_se_single_kernel", _bf16(rng.standard_normal(131_072) * 0.5)),
+            ("bf16_parallel_v1", _bf16(rng.standard_normal(70_000) * 0.02)),
+            ("bf16_se_tans", rng.integers(0, 65536, 90_000).astype(np.uint16))]
+    blobs = [CODECS[c][0](w) for c, w in srcs]
+    d_blobs = [upload_bytes(b, dev) for b in blobs]
+    outs = [torch.empty(w.size, dtype=torch.int16, device=dev) for _, w in srcs]
+    items = [(_refstreams.PARSERS[c](b, w.size), d.data_ptr(), o.data_ptr())
+             for (c, w), b, d, o in zip(srcs, blobs, d_blobs, outs)]
+    assert all(_refstreams.serial_ok(p) for p, _, _ in items)
+    st = StatusWord(dev)
+    batch = _refstreams.RefBatch(items, dev)
+    _say(f"[ref] serial batch of {len(items)} tensors, totals {batch.totals}")
+    for rep in range(2):                 # the second launch reuses the scratch of the first
+        batch.launch(st.ptr, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+        st.check("serial batch")
+        for (c, w), o in zip(srcs, outs):
+            assert o.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), (rep, c, w.size)
+    for (c, w), b in zip(srcs, blobs):
+        assert _decode(c, b, w.size) == w.tobytes(), c
+
+
+def test_serial_batch_rejects_inconsistent_task(gpu):
+    """A task whose scratch lies outside the work buffer, or whose element
+    count is zero, is reported (BS_DEV_ERR_HEADER) and skipped by every kernel
+    of the batch; the other tasks still decode."""
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    from bigsmall_amd.exceptions import DecodeError
+    torch = gpu
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(22)
+    srcs = [_bf16(rng.standard_normal(100_000) * 0.02), _bf16(rng.standard_normal(80_000) * 0.02)]
+    blobs = [oracle.tans_encode(w) for w in srcs]
+    d_blobs = [upload_bytes(b, dev) for b in blobs]
+    for field, value in (("work_offset", 1 << 40), ("n_out", 0), ("work_offset", 128)):
+        outs = [torch.zeros(w.size, dtype=torch.int16, device=dev) for w in srcs]
+        items = [(_refstreams.PARSERS["bf16_se_tans"](b, w.size), d.data_ptr(), o.data_ptr())
+                 for w, b, d, o in zip(srcs, blobs, d_blobs, outs)]
+        batch = _refstreams.RefBatch(items, dev)
+        off = batch.p_tasks - batch.dev.data_ptr()
+        tasks = batch.dev[off:off + 2 * _refstreams.REF_TASK_DTYPE.itemsize].cpu().numpy().view(_refstreams.REF_TASK_DTYPE).copy()
+        tasks[field][1] = value
+        batch.dev[off:off + tasks.nbytes].copy_(torch.from_numpy(tasks.view(np.uint8)))
+        st = StatusWord(dev)
+        _say(f"[ref] serial batch with task 1 {field}={value}")
+        batch.launch(st.ptr, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+        with pytest.raises(DecodeError):
+            st.check("serial batch")
+        assert outs[0].cpu().numpy().view(np.uint16).tobytes() == srcs[0].tobytes()

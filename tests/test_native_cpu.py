@@ -29,7 +29,7 @@ def _declared_functions() -> list[str]:
     names = []
     for hdr in (ROOT / "include").glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
-        names += re.findall(r"^\s*(?:int|uint64_t)\s+(bs_\w+)\s*\(", text, flags=re.M)
+        names += re.findall(r"^\s*(?:int|uint32_t|uint64_t)\s+(bs_\w+)\s*\(", text, flags=re.M)
     return names
 
 
@@ -183,6 +183,9 @@ def test_struct_layouts_match_the_header(tmp_path):
                          _refstreams.SE_STREAM_DTYPE),
         "bs_mant_bucket": (["words", "x0", "n_words", "tail", "n", "perm_begin", "table", "reserved"],
                            _refstreams.MANT_BUCKET_DTYPE),
+        "bs_ref_task": (["streams", "se_table", "bstart", "buckets", "mant_tables", "out", "n_out", "work_offset",
+                         "n_streams", "n_buckets", "n_tables", "chain_begin", "tile_begin", "stream_begin"],
+                        _refstreams.REF_TASK_DTYPE),
         "bs_zstd_task": (["src", "src_len", "dst", "dst_len", "xor_src"], zstd_gpu.ZSTD_TASK_DTYPE),
         "bs_lut_task": (["idx", "lut", "out", "n", "n_lut", "item_bytes"], zstd_gpu.LUT_TASK_DTYPE),
     }
