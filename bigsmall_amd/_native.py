@@ -53,6 +53,7 @@ SIGNATURES = {
     "bs_copy_spans": (_INT, [_P, _U32, _U64, _P, _P]),
     "bs_zstd_work_bytes": (_U64, [_U32]),
     "bs_zstd_decode": (_INT, [_P, _U32, _P, _U64, _P, _P, _P]),
+    "bs_zstd_decode_static": (_INT, [_P, _U32, _P, _P, _P]),
     "bs_lut_expand": (_INT, [_P, _U32, _U64, _P, _P]),
     "bs_refcodec_decode_serial": (_INT, [_P, _U32, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _U64, _P, _P]),
     "bs_refcodec_serial_tiles": (_U32, [_U64, _U32]),

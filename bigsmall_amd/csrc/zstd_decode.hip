@@ -23,9 +23,20 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/bigsmall_hip.h"
 #include "zstd_core.h"
+
+// Work area of bs_zstd_decode_static: BS_ZSTD_STATIC_MAX_TASKS literal slices
+// of 128 KiB (8 MiB) in a file-scope device array, so that entry point
+// allocates nothing. Each GPU the library runs on holds its own copy until the
+// process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns on that device (the array's name is a host-side
+// stand-in, not a device address). Every call on one GPU shares it: the
+// kernel writes each literal before reading it, so nothing needs clearing, and
+// calls that overlap on one GPU race on it.
+static __device__ __align__(256) uint8_t scratch[(uint64_t)BS_ZSTD_STATIC_MAX_TASKS * bs_zstd::kBlockMax];
 
 namespace {
 
@@ -86,6 +97,25 @@ __global__ __launch_bounds__(256) void lut_expand_kernel(const bs_lut_task* __re
   if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(status, BS_DEV_ERR_COUNT);
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (with
+// that device current) and kept.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return BS_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return BS_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -98,6 +128,19 @@ int bs_zstd_decode(const bs_zstd_task* d_tasks, uint32_t n_tasks, void* d_work, 
   if (n_tasks == 0) return BS_OK;
   if (work_bytes < bs_zstd_work_bytes(n_tasks)) return BS_ERR_ARG;
   hipLaunchKernelGGL(zstd_kernel, dim3(n_tasks), dim3(64), 0, (hipStream_t)stream, d_tasks, (uint8_t*)d_work,
+                     d_out_len, d_status);
+  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+}
+
+int bs_zstd_decode_static(const bs_zstd_task* d_tasks, uint32_t n_tasks, uint64_t* d_out_len, int32_t* d_status,
+                          void* stream) {
+  if (!d_status || (n_tasks && (!d_tasks || !d_out_len))) return BS_ERR_ARG;
+  if (n_tasks > BS_ZSTD_STATIC_MAX_TASKS) return BS_ERR_CAP;
+  if (n_tasks == 0) return BS_OK;
+  void* work = nullptr;
+  const int rc = scratch_address(&work);
+  if (rc != BS_OK) return rc;
+  hipLaunchKernelGGL(zstd_kernel, dim3(n_tasks), dim3(64), 0, (hipStream_t)stream, d_tasks, (uint8_t*)work,
                      d_out_len, d_status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }

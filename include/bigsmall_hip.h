@@ -8,7 +8,8 @@
  * asynchronous on `stream`; integrity failures found on the device are OR-ed
  * into the caller-provided device word `d_status` (BS_DEV_* bits), which the
  * caller reads after synchronising. Host-side failures are returned as
- * negative BS_ERR_* codes. No entry point keeps global mutable state; calls on
+ * negative BS_ERR_* codes. No entry point keeps global mutable state, except
+ * bs_zstd_decode_static (a static device work area per GPU, below); calls on
  * different streams with disjoint buffers may run concurrently.
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
@@ -283,6 +284,19 @@ uint64_t bs_zstd_work_bytes(uint32_t n_tasks);
  * checksums are skipped, not checked. Dictionaries are not supported. */
 int bs_zstd_decode(const bs_zstd_task *d_tasks, uint32_t n_tasks, void *d_work, uint64_t work_bytes,
                    uint64_t *d_out_len, int32_t *d_status, void *stream);
+
+/* bs_zstd_decode without a work buffer, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. The literal slices
+ * live in a static device array of BS_ZSTD_STATIC_MAX_TASKS x 128 KiB (8 MiB)
+ * that every GPU the library runs on holds until the process ends; more
+ * tasks return BS_ERR_CAP. The call allocates nothing (the array's address is
+ * looked up once per device, on its first call there). All calls on one GPU
+ * share the array: calls that overlap on one GPU race, so serialise them
+ * (one stream, or events). Otherwise as bs_zstd_decode. */
+#define BS_ZSTD_STATIC_MAX_TASKS 64
+int bs_zstd_decode_static(const bs_zstd_task *d_tasks, uint32_t n_tasks, uint64_t *d_out_len, int32_t *d_status,
+                          void *stream);
 
 /* Lowcard expansion, the unique_bytes[idx] of bigsmall/codecs/special.py:79-82:
  * out[i * item_bytes + b] = lut[idx[i] * item_bytes + b] for i < n, one task
