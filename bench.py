@@ -967,7 +967,14 @@ def main():
     ms_per = ev0.elapsed_time(ev1) / args.steps
     gbps = algo_bytes / (ms_per * 1e-3) / 1e9
 
-    # verify bit-exactness (md5 per tensor, every layer copy) after timing
+    # verify bit-exactness (md5 per tensor, every layer copy) after timing; a
+    # copy this run never decoded (fewer launches than copies) is decoded once first
+    decoded = {i % R for i in range(args.warmup)} | {i % R for i in range(args.steps)}
+    for i in range(R):
+        if i not in decoded:
+            batches[i].launch(status, stream)
+    torch.cuda.synchronize(dev)
+    status.check("untimed decode of the remaining layers")
     for out, lw in zip(outs, layers):
         for name, _ in LAYER:
             got = out[name].view(torch.int16).cpu().numpy().view(np.uint16)
