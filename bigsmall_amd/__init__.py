@@ -7,6 +7,7 @@ kernels on the GPU:
     load(src, device="cuda")                -> dict[str, torch.Tensor] in HBM
     info(src), verify(src)
     StreamingLoader, BigSmallStreamingModel -> layer-at-a-time decode with prefetch
+    streaming_model.StreamingGPT2           -> GPT-2 run block by block from a StreamingLoader
     decompress_layers(src, [i, ...])        -> only the named layers
     decompress_delta(delta, base), load_delta(delta, base) -> a fine-tune from its XOR delta
     CompressedKVCache                       -> KV entries and blocks decoded on the GPU
@@ -30,6 +31,9 @@ def __getattr__(name):
     if name == "BigSmallStreamingModel":
         from .streaming_inference import BigSmallStreamingModel
         return BigSmallStreamingModel
+    if name == "StreamingGPT2":
+        from .streaming_model import StreamingGPT2
+        return StreamingGPT2
     raise AttributeError(name)
 
 

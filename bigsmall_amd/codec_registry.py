@@ -5,13 +5,27 @@ Plugin API, unchanged from the reference (codec_registry.py:39-55):
     encode_fn(raw: bytes, **ctx) -> (blob, extras)
     decode_fn(blob: bytes, extras: dict, n_weights: int) -> bytes
 
-Selection follows the reference's rules (codec_registry.py:210-398): try every
-candidate of the tensor's format, keep the smallest blob, ties go to the
-earliest candidate, a failing candidate is skipped, and the function never
-raises (the last resort is `raw`). The candidates are the codecs this engine
-can both encode and decode on the GPU. The reference's `prefer_speed` and
-`enable_gpu_parallel` knobs are accepted: every candidate here is already a
-GPU format, so they change nothing.
+auto_select_codec applies the reference's rules (codec_registry.py:210-398) to
+whatever candidates and codecs are registered:
+  * smallest blob over CODEC_CANDIDATES[fmt], ties to the earliest candidate,
+    a failing candidate skipped (:283-309);
+  * prefer_speed (bf16): bf16_se_single_kernel if within max(4 KB, 0.6 % of the
+    raw size) of the best, else bf16_se_tans if within
+    max(2 KB, prefer_speed_tolerance x raw) (:316-349);
+  * a bf16_se_ac winner yields to bf16_se_rans within max(1 KB, 0.01 % of raw)
+    (:356-370) (codecs a user may register; constriction is not bundled);
+  * enable_gpu_parallel (bf16): bf16_parallel_v1 with gpu_parallel_n_streams
+    streams if within gpu_parallel_tolerance of the best (:377-391);
+  * the function never raises.
+The bf16_sparsity_v1 / fp2_residual_v1 candidates of the reference's bf16 list
+are tried only when registered (their coders are constriction's), under the
+enable_a5 / enable_fp2_residual switches.
+
+Differences, by construction of this engine: the default candidates are the
+GPU-native formats (bf16_chunked_v1 / fp8_chunked_v1), and the last resort is
+`raw` instead of zstd (this engine decodes zstd entries but does not write them).
+The reference formats it writes (bf16_parallel_v1, bf16_se_tans,
+bf16_se_single_kernel) are byte-identical to the reference encoder's.
 """
 from __future__ import annotations
 
@@ -83,21 +97,54 @@ CODEC_CANDIDATES: dict[str, list[str]] = {
 }
 
 
+def _try(name: str, raw, **ctx):
+    """(blob, extras) of a registered codec, or None when it is missing or raises."""
+    pair = _REGISTRY.get(name)
+    if pair is None:
+        return None
+    try:
+        blob, extras = pair[0](raw, **ctx)
+    except Exception:
+        return None
+    return blob, extras or {}
+
+
 def auto_select_codec(raw: bytes, fmt: str, dtype: str, tensor_name: str = "", shape: tuple = (),
-                      item_bytes: int = 0, prefer_speed: bool = False, enable_gpu_parallel: bool = False,
-                      **_ignored) -> tuple[bytes, str, dict]:
-    """Smallest blob over CODEC_CANDIDATES[fmt]; never raises (falls back to raw)."""
+                      item_bytes: int = 0, enable_a5: bool = True, enable_fp2_residual: bool = True,
+                      enable_gpu_parallel: bool = False, gpu_parallel_n_streams: int = 128,
+                      gpu_parallel_tolerance: float = 0.01, prefer_speed: bool = False,
+                      prefer_speed_tolerance: float = 0.0015, **_ignored) -> tuple[bytes, str, dict]:
+    """(blob, codec name, extras) chosen by the reference's rules (codec_registry.py:210-398)."""
+    candidates = CODEC_CANDIDATES.get(fmt, ["raw"])
     best: Optional[tuple[bytes, str, dict]] = None
-    for name in CODEC_CANDIDATES.get(fmt, ["raw"]):
-        pair = _REGISTRY.get(name)
-        if pair is None:
+    for name in candidates:
+        if name == "bf16_sparsity_v1" and not enable_a5:
             continue
-        try:
-            blob, extras = pair[0](raw)
-        except Exception:
+        if name == "fp2_residual_v1" and not enable_fp2_residual:
             continue
-        if best is None or len(blob) < len(best[0]):
-            best = (blob, name, extras or {})
+        got = _try(name, raw)
+        if got is not None and (best is None or len(got[0]) < len(best[0])):
+            best = (got[0], name, got[1])
+
+    if prefer_speed and fmt == "bf16" and "bf16_se_tans" not in candidates and best is not None:
+        sk = _try("bf16_se_single_kernel", raw)
+        if sk is not None and len(sk[0]) <= len(best[0]) + max(4096, int(len(raw) * 0.006)):
+            best = (sk[0], "bf16_se_single_kernel", sk[1])
+        else:
+            tans = _try("bf16_se_tans", raw)
+            if tans is not None and len(tans[0]) <= len(best[0]) + max(2048, int(len(raw) * prefer_speed_tolerance)):
+                best = (tans[0], "bf16_se_tans", tans[1])
+
+    if fmt == "bf16" and best is not None and best[1] == "bf16_se_ac" and "bf16_se_rans" in candidates:
+        r = _try("bf16_se_rans", raw)
+        if r is not None and len(r[0]) - len(best[0]) <= max(1024, int(len(raw) * 0.0001)):
+            best = (r[0], "bf16_se_rans", r[1])
+
+    if enable_gpu_parallel and fmt == "bf16" and best is not None:
+        par = _try("bf16_parallel_v1", raw, n_streams=gpu_parallel_n_streams)
+        if par is not None and len(par[0]) <= int(len(best[0]) * (1.0 + gpu_parallel_tolerance)):
+            best = (par[0], "bf16_parallel_v1", par[1])
+
     if best is None:
         return bytes(raw), "raw", {"n_bytes": len(raw)}
     return best

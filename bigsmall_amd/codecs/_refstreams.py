@@ -436,6 +436,36 @@ class RefLaunch:
         _native.check(rc, "bs_refcodec_decode")
 
 
+ENCODER_IDS = {"bf16_parallel_v1": 0, "bf16_se_tans": 1, "bf16_se_single_kernel": 2}   # BS_REF_*
+
+
+def encode_host(codec: str, raw, n_streams: int = 128, threads: int | None = None) -> bytes:
+    """The reference encoder's blob for bf16 bytes `raw`, written by the host
+    encoder of this library (bs_refcodec_encode). Odd byte counts raise
+    ValueError, as the reference's encoders do."""
+    import ctypes
+    import os
+    mv = memoryview(raw).cast("B")
+    if len(mv) % 2:
+        raise ValueError(f"BF16 byte length must be even, got {len(mv)}")
+    words = np.frombuffer(mv, dtype=np.uint16)
+    n = int(words.size)
+    if n == 0:
+        return b""
+    L = _native.lib()
+    cid = ENCODER_IDS[codec]
+    cap = int(L.bs_refcodec_encode_bound(cid, n, n_streams))
+    out = np.empty(cap, np.uint8)
+    olen = ctypes.c_uint64(0)
+    src = np.ascontiguousarray(words)
+    rc = L.bs_refcodec_encode(cid, src.ctypes.data, n, n_streams, out.ctypes.data, cap, ctypes.byref(olen),
+                              threads or min(16, os.cpu_count() or 1))
+    if rc == _native.BS_ERR_FORMAT:
+        raise ValueError(f"{codec}: frequency quantisation failed")
+    _native.check(rc, "bs_refcodec_encode")
+    return out[:olen.value].tobytes()
+
+
 def decode_host(codec: str, blob: bytes, n_weights: int) -> bytes:
     """Reference-shaped decode: host bytes in, host bytes out; decoded on the GPU."""
     import torch
@@ -454,5 +484,5 @@ def decode_host(codec: str, blob: bytes, n_weights: int) -> bytes:
     return out.cpu().numpy().tobytes()
 
 
-__all__ = ["PARSERS", "RefBatch", "RefLaunch", "RefPlan", "serial_ok", "decode_host", "parse_parallel", "parse_tans",
+__all__ = ["PARSERS", "RefBatch", "RefLaunch", "RefPlan", "serial_ok", "decode_host", "encode_host", "parse_parallel", "parse_tans",
            "parse_single_kernel", "decode_table_se", "decode_table_mant"]

@@ -6,8 +6,9 @@ The blob's framing is parsed on the host (bigsmall_amd/codecs/_refstreams.py);
 every symbol is decoded by the HIP kernels behind bs_refcodec_decode. There is
 no CPU decode path: without a ROCm GPU this raises.
 
-This engine does not encode bf16_parallel_v1 (its own GPU format is bf16_chunked_v1);
-containers in this format come from the reference's encoder.
+encode(raw) writes the reference encoder's bytes (bigsmall/codecs/bf16_parallel.py:186-259) with this
+library's host encoder (bs_refcodec_encode); compress() uses it for the
+reference's gpu_optimised / prefer_speed choices.
 """
 from __future__ import annotations
 
@@ -26,6 +27,8 @@ def decode(blob: bytes, extras: dict, n_weights: int) -> bytes:
     return _refstreams.decode_host(CODEC, blob, n_weights)
 
 
-def encode(raw: bytes, **_) -> tuple[bytes, dict]:
-    raise NotImplementedError(f"{CODEC} blobs are produced by the reference encoder; "
-                              "this engine encodes bf16_chunked_v1")
+def encode(raw: bytes, n_streams: int = 128, **_) -> tuple[bytes, dict]:
+    """The reference's bf16_parallel.encode(raw, n_streams): N stride-interleaved
+    rANS streams with shared tables; extras {"n_streams": N} as the reference's."""
+    n = len(raw) // 2
+    return _refstreams.encode_host(CODEC, raw, n_streams), {"n_streams": max(1, min(n_streams, n)) if n else n_streams}

@@ -6,8 +6,9 @@ The blob's framing is parsed on the host (bigsmall_amd/codecs/_refstreams.py);
 every symbol is decoded by the HIP kernels behind bs_refcodec_decode. There is
 no CPU decode path: without a ROCm GPU this raises.
 
-This engine does not encode bf16_se_single_kernel (its own GPU format is bf16_chunked_v1);
-containers in this format come from the reference's encoder.
+encode(raw) writes the reference encoder's bytes (bigsmall/codecs/single_kernel.py:193-428, 586-600) with this
+library's host encoder (bs_refcodec_encode); compress() uses it for the
+reference's gpu_optimised / prefer_speed choices.
 """
 from __future__ import annotations
 
@@ -27,5 +28,5 @@ def decode(blob: bytes, extras: dict, n_weights: int) -> bytes:
 
 
 def encode(raw: bytes, **_) -> tuple[bytes, dict]:
-    raise NotImplementedError(f"{CODEC} blobs are produced by the reference encoder; "
-                              "this engine encodes bf16_chunked_v1")
+    """The reference's single_kernel.encode(raw): blob and empty extras."""
+    return _refstreams.encode_host(CODEC, raw), {}

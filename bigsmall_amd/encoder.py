@@ -68,9 +68,14 @@ def _detect_model_type(names: list[str]) -> str:
     return "diffusion" if any(m in blob for m in markers) else "llm"
 
 
-def compress(src, dst: str | Path, mode: str = "balanced", progress: bool = False,
-             exclude_names: Optional[set[str]] = None, steps: Optional[int] = None, **_ignored) -> str:
-    """Compress a safetensors file (or a {name: torch.Tensor} dict) into a .bs container."""
+def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int] = None, progress: bool = False,
+             exclude_names: Optional[set[str]] = None, enable_a5: bool = True, gpu_optimised: bool = False,
+             prefer_speed: bool = False, steps: Optional[int] = None, **_ignored) -> str:
+    """Compress a safetensors file (or a {name: torch.Tensor} dict) into a .bs container
+    (bigsmall/encoder.py:325-496). gpu_optimised and prefer_speed select the
+    reference's bf16_parallel_v1 / bf16_se_single_kernel / bf16_se_tans by its
+    rules (codec_registry.auto_select_codec); `workers` is accepted for the
+    reference's signature (the host encoders here thread internally)."""
     tensors, st_meta = _gather(src)
     if exclude_names:
         tensors = [t for t in tensors if t["name"] not in exclude_names]
@@ -106,8 +111,9 @@ def compress(src, dst: str | Path, mode: str = "balanced", progress: bool = Fals
                 blob, extras = bf16_chunked.encode(raw, steps=steps)
                 codec = bf16_chunked.CODEC_BF16
             else:
-                blob, codec, extras = codec_registry.auto_select_codec(raw, t["fmt"], t["dtype"], t["name"],
-                                                                       tuple(t["shape"]), t["item_bytes"])
+                blob, codec, extras = codec_registry.auto_select_codec(
+                    raw, t["fmt"], t["dtype"], t["name"], tuple(t["shape"]), t["item_bytes"], enable_a5=enable_a5,
+                    enable_gpu_parallel=gpu_optimised, prefer_speed=prefer_speed)
         off = data.add(blob)
         header_tensors.append({"name": t["name"], "shape": t["shape"], "dtype": t["dtype"], "codec": codec,
                                "special": special, "compressed_bytes": len(blob), "offset": off, "md5": md5,
@@ -116,8 +122,10 @@ def compress(src, dst: str | Path, mode: str = "balanced", progress: bool = Fals
     header = {"format": dominant, "mode": mode, "model_type": _detect_model_type([t["name"] for t in tensors]),
               "base_model": None, "tensor_count": len(tensors), "tensors": header_tensors,
               "safetensors_metadata": st_meta or None, "codec_stats": stats.as_dict()}
-    gpu_codecs = {"bf16_chunked_v1", "fp8_chunked_v1", "bf16_parallel_v1"}
-    version = formats.BS_FORMAT_VERSION_V2 if any(h["codec"] in gpu_codecs for h in header_tensors) \
+    # version 2 whenever a codec needs it: the reference's v2-only codecs
+    # (bigsmall/encoder.py:482-491) and this engine's GPU formats
+    v2_codecs = {"bf16_chunked_v1", "fp8_chunked_v1", "bf16_parallel_v1", "bf16_sparsity_v1", "fp2_residual_v1"}
+    version = formats.BS_FORMAT_VERSION_V2 if any(h["codec"] in v2_codecs for h in header_tensors) \
         else formats.BS_FORMAT_VERSION_V1
     container.write_container(dst, header, data.getvalue(), format_version=version)
     return str(dst)

@@ -257,6 +257,25 @@ int bs_refcodec_decode_serial_batch(const bs_ref_task *d_tasks, uint32_t n_tasks
                                     uint32_t total_tiles, uint32_t total_streams, void *d_work,
                                     uint64_t work_bytes, int32_t *d_status, void *stream);
 
+/* Host encoders of the same three formats, for compress() with the
+ * reference's gpu_optimised (bf16_parallel_v1) and prefer_speed
+ * (bf16_se_single_kernel, bf16_se_tans) choices
+ * (bigsmall/codec_registry.py:316-391). `codec`: BS_REF_*; h_src: n bf16
+ * words (n < 2^32); n_streams: bf16_parallel_v1's stream count (1..65535,
+ * clamped to n like the reference's encoder). The blob is byte-identical to the
+ * reference encoder's: bf16_parallel.encode (bigsmall/codecs/bf16_parallel.py:186-259),
+ * bf16_tans.encode (bigsmall/codecs/bf16_tans.py:68-118) and
+ * single_kernel.encode (bigsmall/codecs/single_kernel.py:193-428, 586-600).
+ * *out_len receives its length; a blob longer than cap returns BS_ERR_CAP
+ * (cap = bs_refcodec_encode_bound always suffices). An empty tensor is an
+ * empty blob. n_threads: host threads for independent streams and buckets. */
+#define BS_REF_PARALLEL 0
+#define BS_REF_TANS 1
+#define BS_REF_SINGLE_KERNEL 2
+uint64_t bs_refcodec_encode_bound(int32_t codec, uint64_t n, uint32_t n_streams);
+int bs_refcodec_encode(int32_t codec, const uint16_t *h_src, uint64_t n, uint32_t n_streams, uint8_t *h_dst,
+                       uint64_t cap, uint64_t *out_len, int n_threads);
+
 /* ------------------------------------------------------------------------ */
 /* Zstandard (RFC 8878) frames on the GPU, for the reference's zstd-coded
  * entries: codec "zstd" (bigsmall/codecs/generic.py:15-18, called from

@@ -155,7 +155,8 @@ def _cap(n: int) -> int:
 def par1_encode(words, n_streams: int = 128) -> bytes:
     """bf16_parallel.encode (bigsmall/codecs/bf16_parallel.py:186-259)."""
     w = _u16(words)
-    return _encode("orc_par1_encode", w, _cap(len(w)) + 64 * n_streams + 4096, n_streams)
+    # per stream: its lengths, up to 256 exponents and their bucket fields
+    return _encode("orc_par1_encode", w, _cap(len(w)) + 4096 * (n_streams + 1), n_streams)
 
 
 def par1_decode(blob: bytes, n: int) -> bytes:

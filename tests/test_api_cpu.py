@@ -239,3 +239,39 @@ def test_tied_follower_takes_its_own_dtype_and_shape(master_dtype, follower_dtyp
     assert out.data_ptr() != master.data_ptr()
     with pytest.raises(ValueError):
         engine.tied_copy(master, {**t, "shape": [7]})
+
+
+def test_streaming_gpt2_block_math_matches_transformers():
+    """StreamingGPT2's block (bigsmall/streaming_model.py:84-132), fed the
+    uncompressed weights on the CPU, gives transformers' GPT2LMHeadModel
+    logits to 1e-4 and the same greedy tokens."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    from bigsmall_amd.streaming_model import StreamingGPT2
+
+    class DictLoader:
+        def __init__(self, sd):
+            self.sd = sd
+
+        def load_non_layer_tensors(self):
+            return {k: v for k, v in self.sd.items() if not k.startswith("h.")}
+
+        def iter_layers(self, progress=True):
+            for i in range(3):
+                yield i, {k: v for k, v in self.sd.items() if k.startswith(f"h.{i}.")}
+
+    cfg = GPT2Config(n_layer=3, n_embd=64, n_head=4, vocab_size=300, n_positions=64, bos_token_id=0, eos_token_id=0)
+    torch.manual_seed(0)
+    model = GPT2LMHeadModel(cfg).eval()
+    with torch.no_grad():
+        for prm in model.parameters():        # weights large enough that logits have clear margins
+            prm.mul_(8.0)
+    sd = {k[len("transformer."):]: v.detach().clone() for k, v in model.state_dict().items()
+          if k.startswith("transformer.")}
+    sm = StreamingGPT2(DictLoader(sd), config=cfg, device="cpu")
+    ids = torch.randint(0, 300, (2, 11), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        hf = model(ids).logits
+    assert torch.allclose(sm.forward(ids), hf, atol=1e-4, rtol=1e-4)
+    with torch.no_grad():
+        hf_gen = model.generate(input_ids=ids[:1], max_new_tokens=4, do_sample=False, pad_token_id=0)
+    assert torch.equal(sm.generate_greedy(ids[:1], 4), hf_gen)

@@ -458,3 +458,76 @@ def test_tie_across_dtypes_round_trip(tmp_path):
             got.update(layer)
     for k, v in src.items():
         assert got[k].dtype == v.dtype and _bytes(got[k]) == _bytes(v), k
+
+
+class _DictLoader:
+    """The two StreamingLoader calls StreamingGPT2 makes, served from a dict of
+    uncompressed tensors: the same forward on the source weights."""
+
+    def __init__(self, sd: dict, device):
+        self.sd = {k: v.to(device) for k, v in sd.items()}
+
+    def load_non_layer_tensors(self):
+        return {k: v for k, v in self.sd.items() if not k.startswith("h.")}
+
+    def iter_layers(self, progress=True):
+        n = 1 + max(int(k.split(".")[1]) for k in self.sd if k.startswith("h."))
+        for i in range(n):
+            yield i, {k: v for k, v in self.sd.items() if k.startswith(f"h.{i}.")}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("prefetch", [0, 2])
+def test_streaming_gpt2(tmp_path, dtype, prefetch):
+    """StreamingGPT2 (bigsmall/streaming_model.py:29-176) over a random-init
+    GPT-2-shaped model stored with the GPT-2 safetensors names: logits and
+    greedy tokens equal the same forward on the uncompressed weights (the
+    decoded weights are bit-exact), and in fp32 the logits agree with
+    transformers' GPT2LMHeadModel to 1e-4."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    from bigsmall_amd.streaming import StreamingLoader
+    from bigsmall_amd.streaming_model import StreamingGPT2
+    cfg = GPT2Config(n_layer=3, n_embd=128, n_head=4, vocab_size=1000, n_positions=128, bos_token_id=0,
+                     eos_token_id=0)
+    torch.manual_seed(0)
+    model = GPT2LMHeadModel(cfg).eval()
+    sd = {k[len("transformer."):]: v.detach().clone().contiguous().to(dtype)
+          for k, v in model.state_dict().items() if k.startswith("transformer.")}
+    p = tmp_path / "gpt2.bs"
+    compress(sd, p)
+    ids = torch.randint(0, 1000, (2, 17), generator=torch.Generator().manual_seed(1))
+    dev = torch.device("cuda", 0)
+    _say(f"[api] StreamingGPT2 dtype={dtype} prefetch={prefetch}")
+    ref = StreamingGPT2(_DictLoader(sd, dev), config=cfg, device="cuda")
+    with StreamingLoader(p, device="cuda", prefetch=prefetch) as L:
+        sm = StreamingGPT2(L, config=cfg, device="cuda")
+        logits = sm.forward(ids)
+        gen = sm.generate_greedy(ids[:1], max_new_tokens=5)
+    want = ref.forward(ids)
+    assert logits.dtype == dtype and torch.equal(logits, want)
+    assert torch.equal(gen, ref.generate_greedy(ids[:1], max_new_tokens=5))
+    if dtype == torch.float32:
+        hf = model.to(dev)(ids.to(dev)).logits
+        assert torch.allclose(logits, hf, atol=1e-4, rtol=1e-4), (logits - hf).abs().max()
+
+
+@pytest.mark.parametrize("kw", [{"gpu_optimised": True}, {"prefer_speed": True}])
+def test_compress_reference_formats_round_trip(tmp_path, kw):
+    """Containers compress() writes with the reference's gpu_optimised /
+    prefer_speed choices (bf16_parallel_v1, bf16_se_single_kernel or
+    bf16_se_tans, by the reference's rules) load bit-exactly on the GPU, one
+    batched wave-serial launch per layer."""
+    from bigsmall_amd import decoder
+    g = torch.Generator().manual_seed(12)
+    src = {f"model.layers.{i}.mlp.{n}.weight": (torch.randn(1024, 1024 + 64 * i, generator=g) * 0.02).bfloat16()
+           for i in range(2) for n in ("up_proj", "down_proj")}
+    src["model.norm.weight"] = (1 + torch.randn(1024, generator=g) * 0.01).bfloat16()
+    p = tmp_path / "ref_formats.bs"
+    compress(src, p, **kw)
+    header, _ = container.read_header(p)
+    codecs = {t["codec"] for t in header["tensors"]}
+    _say(f"[api] compress({kw}) codecs {sorted(codecs)}")
+    assert codecs & {"bf16_parallel_v1", "bf16_se_single_kernel", "bf16_se_tans"}
+    out = decoder.load(p)
+    for k, v in src.items():
+        assert _bytes(out[k]) == _bytes(v), k
