@@ -519,7 +519,7 @@ def test_compress_reference_formats_round_trip(tmp_path, kw):
     batched wave-serial launch per layer."""
     from bigsmall_amd import decoder
     g = torch.Generator().manual_seed(12)
-    src = {f"model.layers.{i}.mlp.{n}.weight": (torch.randn(1024, 1024 + 64 * i, generator=g) * 0.02).bfloat16()
+    src = {f"model.layers.{i}.mlp.{n}.weight": (torch.randn(2048, 2048 + 64 * i, generator=g) * 0.02).bfloat16()
            for i in range(2) for n in ("up_proj", "down_proj")}
     src["model.norm.weight"] = (1 + torch.randn(1024, generator=g) * 0.01).bfloat16()
     p = tmp_path / "ref_formats.bs"
