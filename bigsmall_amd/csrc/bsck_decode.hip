@@ -41,16 +41,15 @@
 //   bytes (elem_bytes 1): {f | value << 24, slot - cf}, the same update, the
 //     output byte taken from bits 24..31 with v_perm;
 //   generic (bf16 plane modes 0/2): {f | (slot - cf) << 13, value | consume << 31}.
-#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "simt.h"
 
 #include "../../include/bigsmall_hip.h"
 #include "lds_limit.h"
 
 namespace {
 
-#define LDS __attribute__((address_space(3)))
-#define GLB __attribute__((address_space(1)))
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -61,6 +60,7 @@ constexpr int kWave = 64;                 // lanes of a wavefront
 #endif
 constexpr int kWaves = BSCK_WAVES;        // chunks (wavefronts) per workgroup
 constexpr int kThreads = kWaves * kWave;
+static_assert(kThreads >= 256, "the table build reads one symbol entry per thread (up to 256)");
 // Steps per block (dense-plane block, refill check): 8 for K <= 2 states per
 // lane, 4 for K = 4, so a block is at most 1024 elements (1024 renorm words of
 // worst-case demand) and a lane's plane bytes of a block are 16 bytes.
@@ -124,9 +124,9 @@ __device__ __forceinline__ void wave_sync() {
 // issued before it, and nothing can sink them under a later branch.
 template <int K>
 __device__ __forceinline__ void consume(const uint32_t (&v)[K]) {
-  if (K == 1) asm volatile("" ::"v"(v[0]));
-  if (K == 2) asm volatile("" ::"v"(v[0]), "v"(v[K - 1]));
-  if (K == 4) asm volatile("" ::"v"(v[0]), "v"(v[1 % K]), "v"(v[2 % K]), "v"(v[3 % K]));
+  if (K == 1) BS_KEEP1(v[0]);
+  if (K == 2) BS_KEEP2(v[0], v[K - 1]);
+  if (K == 4) BS_KEEP4(v[0], v[1 % K], v[2 % K], v[3 % K]);
 }
 
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
@@ -184,8 +184,8 @@ __device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, ui
 
 template <int K>
 __device__ __forceinline__ void consume_plane(const PlaneRegs<K>& p) {
-  if (PlaneRegs<K>::kWords == 1) asm volatile("" ::"v"(p.b[0]));
-  else asm volatile("" ::"v"(p.b[0]), "v"(p.b[PlaneRegs<K>::kWords - 1]));
+  if (PlaneRegs<K>::kWords == 1) BS_KEEP1(p.b[0]);
+  else BS_KEEP2(p.b[0], p.b[PlaneRegs<K>::kWords - 1]);
 }
 
 // Per-wavefront decode state of one chunk.
@@ -505,8 +505,8 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   request_segments<K, MODE>(S, F, C);
   consume<K>(S.x);
   if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
-  asm volatile("" ::"v"(F.w[0].x), "v"(F.w[1].x));
-  if (MODE == 2) asm volatile("" ::"v"(F.p[0].x), "v"(F.p[1].x));
+  BS_KEEP2(F.w[0].x, F.w[1].x);
+  if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
   for (uint32_t blk = 0;;) {
     // ---- pair start: land the previous pair's loads, issue the next pair's
@@ -537,8 +537,8 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
       // keep its own waits for these registers at this point.
       __builtin_amdgcn_s_waitcnt(kWaitVm4);
       if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
-      asm volatile("" ::"v"(F.w[0].x), "v"(F.w[1].x));
-      if (MODE == 2) asm volatile("" ::"v"(F.p[0].x), "v"(F.p[1].x));
+      BS_KEEP2(F.w[0].x, F.w[1].x);
+      if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
     }
   }
   // a partial chunk's last staged half: the second half of its last block, or
@@ -593,7 +593,7 @@ template <bool COMPACT>
 __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_task* __restrict__ tasks,
                                                                uint32_t n_tasks, bs_chunk_task single,
                                                                int32_t* __restrict__ status) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  BS_DYNAMIC_LDS(smem);
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
   LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
   LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWaves * kRingBytes);

@@ -2,7 +2,7 @@
 // device, safely from any number of host threads.
 #pragma once
 
-#include <hip/hip_runtime.h>
+#include "simt.h"
 #include <stdint.h>
 
 #include <atomic>

@@ -24,16 +24,15 @@
 //      order and ORs mantissa r into element perm[bucket_begin + r].
 // The SE decode tables sit in LDS; mantissa tables (1024 entries per
 // exponent, up to 256 of them) are read through the caches.
-#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "simt.h"
 
 #include "../../include/bigsmall_hip.h"
 #include "lds_limit.h"
 
 namespace {
 
-#define LDS __attribute__((address_space(3)))
-#define GLB __attribute__((address_space(1)))
 
 constexpr uint32_t kL = 1u << 16;
 constexpr int kWave = 64;
@@ -63,7 +62,7 @@ __global__ __launch_bounds__(kSeLanes) void se_kernel(const bs_se_stream* __rest
                                                       const uint32_t* __restrict__ bstart, uint64_t n_out,
                                                       uint16_t* __restrict__ out, uint32_t* __restrict__ perm,
                                                       int32_t* __restrict__ status) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  BS_DYNAMIC_LDS(smem);
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;                   // 4096 entries
   LDS uint32_t* s_cur = (LDS uint32_t*)(smem + 4096 * 8);      // cursor of exponent e for lane l at e*64 + l
   const uint32_t lane = threadIdx.x;
@@ -242,7 +241,7 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   // The state stays in a vector register (the empty asm hides its uniformity,
   // which would otherwise move the update to scalar instructions plus two
   // readfirstlanes); only the renormalisation test reads it back.
-  asm volatile("" : "+v"(x));
+  BS_OPAQUE(x);
   auto step = [&](uint32_t j) {
     const u32x4 e = tbl[x & kSlotMask];
     uint32_t xn = __umul24(e.x, x >> kShift) + e.y;         // v_mad_u32_u24 (f <= 4096)
@@ -256,7 +255,7 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
       ++pos;
     }
     x = xn;
-    asm volatile("" : "+v"(x));
+    BS_OPAQUE(x);
     keep = lane == j ? e.z : keep;
   };
   for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
@@ -351,7 +350,7 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 __global__ __launch_bounds__(kWave) void serial_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
                                                        bs_ref_task single, uint8_t* __restrict__ work,
                                                        uint64_t work_bytes, int32_t* __restrict__ status) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  BS_DYNAMIC_LDS(smem);
   LDS uint8_t* ring = (LDS uint8_t*)smem;
   LDS u32x4* tbl = (LDS u32x4*)(smem + kRingB);      // {f, slot - cf, output, 0} per slot
   const uint32_t lane = threadIdx.x;

@@ -1,0 +1,30 @@
+// What the decode kernels need from the compiler beyond plain C++: the HIP
+// runtime and kernel language, the LDS / global address spaces, and empty asm
+// statements that pin values in vector registers at chosen points. The
+// library is built for gfx950 by hipcc; the same kernel sources also build as
+// host C++ for sanitizer runs on the CPU (BS_SIMT_CPU, simt_cpu.h), where the
+// address spaces and register pins are empty and every lane is a thread.
+#pragma once
+
+#ifdef BS_SIMT_CPU
+#include "simt_cpu.h"
+#define LDS
+#define GLB
+#define BS_DYNAMIC_LDS(name) uint8_t* name = bs_simt::dynamic_lds()
+#define BS_KEEP1(a) ((void)(a))
+#define BS_KEEP2(a, b) ((void)(a), (void)(b))
+#define BS_KEEP4(a, b, c, d) ((void)(a), (void)(b), (void)(c), (void)(d))
+#define BS_OPAQUE(x) ((void)(x))
+#else
+#include <hip/hip_runtime.h>
+#define LDS __attribute__((address_space(3)))
+#define GLB __attribute__((address_space(1)))
+#define BS_DYNAMIC_LDS(name) extern __shared__ __attribute__((aligned(16))) uint8_t name[]
+// Makes the values available at this point: every load producing them is
+// issued before it, and nothing can sink them under a later branch.
+#define BS_KEEP1(a) asm volatile("" ::"v"(a))
+#define BS_KEEP2(a, b) asm volatile("" ::"v"(a), "v"(b))
+#define BS_KEEP4(a, b, c, d) asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(d))
+// Hides a value's provenance from the optimiser (it stays in a vector register).
+#define BS_OPAQUE(x) asm volatile("" : "+v"(x))
+#endif

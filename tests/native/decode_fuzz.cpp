@@ -1,0 +1,150 @@
+// CPU runs of the GPU decode kernels (bigsmall_amd/csrc/bsck_decode.hip,
+// refcodec_decode.hip), built as host C++ with the SIMT emulation of
+// bigsmall_amd/csrc/simt_cpu.h under AddressSanitizer and UBSan
+// (tests/test_decode_cores_cpu.py builds and drives it).
+//
+// Input: a case file written by the test. Each case is a BSCK blob, or a
+// reference-format blob with the stream descriptors and decode tables the
+// library's host parser (bigsmall_amd/codecs/_refstreams.py) made from it
+// (word arrays as blob offsets). Clean cases must decode to their expected
+// bytes with a zero status word; corrupted cases may decode to anything or
+// report a status, but every access must stay inside its buffers, which
+// are allocated at their exact sizes so that the sanitizer sees any overrun.
+// Prints one summary line; exit status 0 when every clean case decoded right.
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "bigsmall_hip.h"
+
+namespace {
+
+struct Reader {
+  const uint8_t* p;
+  const uint8_t* end;
+  template <class T>
+  T get() {
+    T v;
+    if (p + sizeof(T) > end) {
+      fprintf(stderr, "case file truncated\n");
+      exit(3);
+    }
+    memcpy(&v, p, sizeof(T));
+    p += sizeof(T);
+    return v;
+  }
+  const uint8_t* take(uint64_t n) {
+    if (n > (uint64_t)(end - p)) {
+      fprintf(stderr, "case file truncated\n");
+      exit(3);
+    }
+    const uint8_t* r = p;
+    p += n;
+    return r;
+  }
+};
+
+// A buffer of exactly n bytes at a 256-byte aligned address (aligned_alloc
+// sizes must be multiples of the alignment: the slack is poisoned by
+// allocating it separately is not possible, so n is what the sanitizer
+// guards when n is a multiple of 256; other sizes use malloc's 16-byte
+// alignment, which every kernel access here needs at most).
+struct Buf {
+  uint8_t* p = nullptr;
+  explicit Buf(uint64_t n, bool align256 = false) {
+    if (align256) p = (uint8_t*)aligned_alloc(256, ((n + 255) / 256) * 256 + 256);
+    else p = (uint8_t*)malloc(n ? n : 1);
+    if (!p) exit(4);
+  }
+  ~Buf() { free(p); }
+  Buf(const Buf&) = delete;
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) return 2;
+  FILE* f = fopen(argv[1], "rb");
+  if (!f) return 2;
+  std::vector<uint8_t> file;
+  uint8_t tmp[1 << 16];
+  size_t got;
+  while ((got = fread(tmp, 1, sizeof tmp, f)) > 0) file.insert(file.end(), tmp, tmp + got);
+  fclose(f);
+  Reader r{file.data(), file.data() + file.size()};
+  if (r.get<uint32_t>() != 0x5A465342u) return 2;   // "BSFZ"
+  const uint32_t n_cases = r.get<uint32_t>();
+  uint64_t clean_ok = 0, clean_bad = 0, refused_host = 0, flagged = 0, decoded = 0;
+  for (uint32_t c = 0; c < n_cases; ++c) {
+    const uint8_t kind = r.get<uint8_t>(), clean = r.get<uint8_t>();
+    r.get<uint16_t>();
+    const uint64_t n_out = r.get<uint64_t>();
+    const uint32_t eb = r.get<uint32_t>();
+    const uint64_t blob_len = r.get<uint64_t>();
+    const uint8_t* blob_src = r.take(blob_len);
+    Buf blob(blob_len);
+    memcpy(blob.p, blob_src, blob_len);
+    Buf out(n_out * eb);
+    memset(out.p, 0x5A, n_out * eb);
+    int32_t status = 0;
+    int rc = BS_OK;
+    if (kind == 0) {   // BSCK: the kernel reads the blob's own header
+      bs_chunk_info info;
+      rc = bs_chunk_inspect(blob.p, blob_len, &info);
+      if (rc == BS_OK) rc = bs_chunk_decode(blob.p, blob_len, out.p, n_out, info.n_chunks, info.plane_mode, &status, nullptr);
+    } else {           // reference formats: descriptors with blob-relative word arrays
+      const uint32_t ns = r.get<uint32_t>(), nb = r.get<uint32_t>(), nt = r.get<uint32_t>();
+      std::vector<bs_se_stream> se(ns);
+      memcpy(se.data(), r.take((uint64_t)ns * sizeof(bs_se_stream)), (uint64_t)ns * sizeof(bs_se_stream));
+      Buf se_table(4096 * 8);
+      memcpy(se_table.p, r.take(4096 * 8), 4096 * 8);
+      Buf bstart((uint64_t)ns * 257 * 4);
+      memcpy(bstart.p, r.take((uint64_t)ns * 257 * 4), (uint64_t)ns * 257 * 4);
+      std::vector<bs_mant_bucket> mb(nb);
+      memcpy(mb.data(), r.take((uint64_t)nb * sizeof(bs_mant_bucket)), (uint64_t)nb * sizeof(bs_mant_bucket));
+      Buf tables((uint64_t)nt * 4096);
+      memcpy(tables.p, r.take((uint64_t)nt * 4096), (uint64_t)nt * 4096);
+      for (auto& s : se) s.words = blob.p + (uintptr_t)s.words;
+      for (auto& b : mb) b.words = blob.p + (uintptr_t)b.words;
+      Buf d_se(ns * sizeof(bs_se_stream)), d_mb(nb * sizeof(bs_mant_bucket));
+      memcpy(d_se.p, se.data(), ns * sizeof(bs_se_stream));
+      memcpy(d_mb.p, mb.data(), nb * sizeof(bs_mant_bucket));
+      if (kind == 1) {
+        const uint64_t wb = bs_refcodec_serial_work_bytes(n_out, ns);
+        Buf work(wb, true);
+        rc = bs_refcodec_decode_serial((const bs_se_stream*)d_se.p, ns, (const uint32_t*)se_table.p,
+                                       (const uint32_t*)bstart.p, (const bs_mant_bucket*)d_mb.p, nb,
+                                       (const uint32_t*)tables.p, nt, (uint16_t*)out.p, n_out, work.p, wb, &status,
+                                       nullptr);
+      } else {
+        Buf perm(n_out * 4);
+        rc = bs_refcodec_decode((const bs_se_stream*)d_se.p, ns, (const uint32_t*)se_table.p, (const uint32_t*)bstart.p,
+                                (const bs_mant_bucket*)d_mb.p, nb, (const uint32_t*)tables.p, nt, (uint16_t*)out.p,
+                                n_out, (uint32_t*)perm.p, &status, nullptr);
+      }
+    }
+    const uint8_t* want = clean ? r.take(n_out * eb) : nullptr;
+    if (clean) {
+      if (rc == BS_OK && status == 0 && memcmp(out.p, want, n_out * eb) == 0) {
+        ++clean_ok;
+      } else {
+        ++clean_bad;
+        fprintf(stderr, "clean case %u (kind %u, n %llu): rc %d status 0x%x\n", c, kind, (unsigned long long)n_out,
+                rc, status);
+      }
+    } else if (rc != BS_OK) {
+      ++refused_host;
+    } else if (status != 0) {
+      ++flagged;
+    } else {
+      ++decoded;
+    }
+  }
+  printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu\n", n_cases,
+         (unsigned long long)clean_ok, (unsigned long long)clean_bad, (unsigned long long)refused_host,
+         (unsigned long long)flagged, (unsigned long long)decoded);
+  return clean_bad == 0 ? 0 : 1;
+}

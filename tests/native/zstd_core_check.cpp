@@ -1,17 +1,25 @@
 // CPU check of the GPU zstd decoder's core (bigsmall_amd/csrc/zstd_core.h),
-// run as a one-lane team, against libzstd (the format's reference
-// implementation). Built by tests/test_zstd_core_cpu.py with g++ under
-// AddressSanitizer and UBSan, so any read or write outside the input, output
-// or literal buffers fails the run.
+// run as a one-lane team and, when built with BS_ZSTD_TEAM64, also as the GPU's
+// 64-lane team (lanes as fibers, bigsmall_amd/csrc/simt_cpu.h), against
+// libzstd (the format's reference implementation). Built by
+// tests/test_zstd_core_cpu.py under AddressSanitizer and UBSan, so any read or
+// write outside the input, output or literal buffers fails the run. The
+// 64-lane team must give the one-lane team's error code and bytes on every
+// frame: its lanes run one after another between barriers, so a lane that
+// reads what another writes without a barrier between them is caught.
 //   1. round trips: several data kinds x compression levels, checksum and
 //      no-content-size frames, back-to-back frames with a skippable frame;
 //   2. corruptions: single-bit flips, byte overwrites and truncations of
 //      frames; every mutated frame must decode to what libzstd decodes it to,
 //      or return an error (never decode where libzstd refuses).
 // Prints one summary line; exit status 0 when every check holds.
+#ifdef BS_ZSTD_TEAM64
+#include "../../bigsmall_amd/csrc/simt_cpu.h"
+#else
 #define __host__
 #define __device__
 #define __forceinline__ inline
+#endif
 #include "../../bigsmall_amd/csrc/zstd_core.h"
 
 #include <cmath>
@@ -60,19 +68,56 @@ Bytes compress(const Bytes& in, int level, int checksum = 0, int content_size = 
 
 bs_zstd::ZState g_state;
 
+#ifdef BS_ZSTD_TEAM64
+// The GPU's team: 64 lanes, the workgroup barrier as sync().
+struct FiberTeam {
+  static constexpr uint32_t size = 64;
+  uint32_t lane() const { return __lane_id(); }
+  void sync() const { __syncthreads(); }
+};
+long g_team_mismatch = 0;
+#endif
+
 // Decodes `frame` (copied to an exact-size heap block) into an exact-size
 // block of `cap` bytes; returns the error code, output in *out.
-int decode(const Bytes& frame, size_t cap, Bytes* out) {
+template <class Run>
+int decode_with(const Bytes& frame, size_t cap, Bytes* out, Run run) {
   static Bytes lit(bs_zstd::kBlockMax);
   uint8_t* src = new uint8_t[frame.size() ? frame.size() : 1];
   if (!frame.empty()) std::memcpy(src, frame.data(), frame.size());
   uint8_t* dst = new uint8_t[cap ? cap : 1];
   uint64_t got = 0;
-  int e = bs_zstd::zstd_frames(OneLane{}, g_state, src, frame.size(), dst, cap, lit.data(), got);
+  int e = run(src, frame.size(), dst, cap, lit.data(), got);
   if (e == 0 && got != cap) e = bs_zstd::kErrOutput;
   out->assign(dst, dst + (e ? 0 : got));
   delete[] src;
   delete[] dst;
+  return e;
+}
+
+int decode(const Bytes& frame, size_t cap, Bytes* out) {
+  const int e = decode_with(frame, cap, out, [](const uint8_t* s, uint64_t n, uint8_t* d, uint64_t c, uint8_t* lit,
+                                                 uint64_t& got) {
+    return bs_zstd::zstd_frames(OneLane{}, g_state, s, n, d, c, lit, got);
+  });
+#ifdef BS_ZSTD_TEAM64
+  Bytes out64;
+  const int e64 = decode_with(frame, cap, &out64, [](const uint8_t* s, uint64_t n, uint8_t* d, uint64_t c,
+                                                     uint8_t* lit, uint64_t& got) {
+    int err = 0;
+    bs_simt::launch([&] {
+      __shared__ bs_zstd::ZState z;
+      uint64_t g = 0;
+      const int r = bs_zstd::zstd_frames(FiberTeam{}, z, s, n, d, c, lit, g);
+      if (__lane_id() == 0) {
+        err = r;
+        got = g;
+      }
+    }, dim3(1), dim3(64), 0, nullptr);
+    return err;
+  });
+  if (e64 != e || out64 != *out) ++g_team_mismatch;
+#endif
   return e;
 }
 
@@ -164,8 +209,13 @@ int main(int argc, char** argv) {
       }
     }
   }
+  long team = 0;
+#ifdef BS_ZSTD_TEAM64
+  team = g_team_mismatch;
+  std::printf("64-lane team differs from one lane on %ld frames\n", team);
+#endif
   std::printf("round trips %ld (failed %ld); corruptions: decoded like libzstd %ld, decoded differently %ld, "
               "decoded where libzstd refuses %ld, refused where libzstd decodes %ld, both refuse %ld\n",
               round_trips, failures, same, differ, only_ours, only_lib, both_reject);
-  return (failures || differ || only_ours) ? 1 : 0;
+  return (failures || differ || only_ours || team) ? 1 : 0;
 }

@@ -1,0 +1,152 @@
+"""The GPU decode kernels themselves (bigsmall_amd/csrc/bsck_decode.hip and
+refcodec_decode.hip) run on the CPU under AddressSanitizer and UBSan, built
+as host C++ with the SIMT emulation of bigsmall_amd/csrc/simt_cpu.h (one fiber
+per lane, wavefront operations and barriers as switch points), driven by
+tests/native/decode_fuzz.cpp.
+
+Cases: clean blobs of every BSCK plane mode, state width and element size,
+and of the reference's three formats on both decode paths (wave-serial and
+lane-per-chain), each of which must decode to its source; then thousands of
+corrupted copies (single and multiple byte changes, biased to the headers,
+tables and chunk tables, and truncations). A corrupted BSCK blob goes to the
+kernel whenever the host header check passes; a corrupted reference-format
+blob goes to the kernels with the descriptors the library's own host parser
+makes from it, whenever that parser accepts it. Every access stays inside its
+buffer, or the sanitizer fails the run. The same corruption sweeps run on the
+GPU in smaller numbers (tests/test_gpu_bsck.py, tests/test_gpu_refcodecs.py).
+"""
+from __future__ import annotations
+
+import shutil
+import struct
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from bigsmall_amd.codecs import _refstreams
+from bigsmall_amd.codecs import bf16_chunked as bc
+
+ROOT = Path(__file__).resolve().parents[1]
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _case(kind: int, clean: bool, n: int, eb: int, blob: bytes, extra: bytes = b"", want: bytes = b"") -> bytes:
+    return struct.pack("<BBHQIQ", kind, int(clean), 0, n, eb, len(blob)) + blob + extra + (want if clean else b"")
+
+
+def _ref_extra(plan) -> bytes:
+    se, tab, bst, mb, mt = _refstreams._plan_arrays(plan, 0)
+    ns, nb, nt = len(plan.se_streams), len(plan.buckets), max(1, len(plan.mant_freqs))
+    return struct.pack("<III", ns, nb, nt) + se.tobytes() + tab.tobytes() + bst.tobytes() + mb.tobytes() + mt.tobytes()
+
+
+def _corrupt(rng, blob: bytes) -> bytes:
+    b = bytearray(blob)
+    r = rng.random()
+    if r < 0.1 and len(b) > 1:                               # truncation
+        return bytes(b[: int(rng.integers(0, len(b)))])
+    for _ in range(1 if r < 0.7 else int(rng.integers(2, 6))):
+        hi = min(len(b), 512) if rng.random() < 0.5 else len(b)  # half in the header / tables / chunk table
+        p = int(rng.integers(0, hi))
+        b[p] ^= int(rng.integers(1, 256))
+    return bytes(b)
+
+
+def _bsck_inputs(rng):
+    g = _bf16(rng.standard_normal(3000) * 0.02)
+    hz = _bf16(rng.standard_normal(5000) * 0.02)
+    hz[rng.permutation(hz.size)[: hz.size // 2]] = 0
+    norms = _bf16(1 + rng.standard_normal(4096) * 0.01)
+    yield g, dict(lanes=128, steps=16)
+    yield g[:200], dict(lanes=64, steps=16)
+    yield _bf16(rng.standard_t(3, 9000) * 0.02), dict(lanes=256, steps=32)
+    yield hz, dict(lanes=128, steps=16, mode=2)
+    yield hz[:1500], dict(lanes=64, steps=32, mode=2)
+    yield norms, dict(lanes=128, steps=16)                   # exact-value mode
+    yield rng.integers(0, 65536, 2500).astype(np.uint16), dict(lanes=128, steps=16, mode=1)
+    yield rng.integers(0, 256, 4000).astype(np.uint8), dict(lanes=128, steps=16)     # byte elements
+    yield np.array([0x3F80], np.uint16), dict(lanes=64, steps=16)
+
+
+def _ref_inputs(rng):
+    yield "bf16_parallel_v1", _bf16(rng.standard_normal(1200) * 0.02), lambda w: oracle.par1_encode(w, 8)
+    yield "bf16_parallel_v1", _bf16(rng.standard_t(3, 700) * 0.02), lambda w: oracle.par1_encode(w, 3)
+    yield "bf16_se_tans", _bf16(rng.standard_normal(600) * 0.02), oracle.tans_encode
+    yield "bf16_se_single_kernel", _bf16(rng.standard_normal(600) * 0.5), oracle.sk_encode
+    hz = _bf16(rng.standard_normal(800) * 0.02)
+    hz[rng.permutation(hz.size)[:400]] = 0
+    yield "bf16_se_tans", hz, oracle.tans_encode
+
+
+def _write_cases(path: Path, n_bsck: int, n_ref: int) -> dict:
+    rng = np.random.default_rng(2024)
+    cases, counts = [], {"bsck_clean": 0, "bsck_corrupt": 0, "ref_clean": 0, "ref_corrupt": 0, "ref_parser_refused": 0}
+    bsck = list(_bsck_inputs(rng))
+    for w, kw in bsck:
+        blob = bc.encode_array(w, **kw)
+        eb = w.dtype.itemsize
+        cases.append(_case(0, True, w.size, eb, blob, want=w.tobytes()))
+        counts["bsck_clean"] += 1
+        for _ in range(n_bsck // len(bsck)):
+            cases.append(_case(0, False, w.size, eb, _corrupt(rng, blob)))
+            counts["bsck_corrupt"] += 1
+    refs = list(_ref_inputs(rng))
+    for codec, w, enc in refs:
+        blob = enc(w)
+        plan = _refstreams.PARSERS[codec](blob, w.size)
+        for kind in (1, 2):                                   # wave-serial, lane per chain
+            cases.append(_case(kind, True, w.size, 2, blob, _ref_extra(plan), w.tobytes()))
+            counts["ref_clean"] += 1
+        made = 0
+        while made < n_ref // len(refs):
+            bad = _corrupt(rng, blob)
+            try:                                              # the host parse and table build, as in RefLaunch
+                plan = _refstreams.PARSERS[codec](bad, w.size)
+                extra = _ref_extra(plan) if plan.se_streams else None
+            except ValueError:
+                counts["ref_parser_refused"] += 1
+                continue
+            if extra is None:
+                continue
+            kind = 1 if made % 2 == 0 else 2
+            cases.append(_case(kind, False, w.size, 2, bad, extra))
+            counts["ref_corrupt"] += 1
+            made += 1
+    path.write_bytes(struct.pack("<II", 0x5A465342, len(cases)) + b"".join(cases))
+    return counts
+
+
+def _build(tmp_path: Path) -> Path:
+    exe = tmp_path / "decode_fuzz"
+    csrc = ROOT / "bigsmall_amd" / "csrc"
+    cmd = [CLANG, "-std=c++17", "-O2", "-g", "-pthread", "-DBS_SIMT_CPU", "-DBSCK_WAVES=4",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-fsanitize-address-use-after-return=never",
+           "-I", str(ROOT / "include"), "-I", str(csrc),
+           "-x", "c++", str(csrc / "bsck_decode.hip"), str(csrc / "refcodec_decode.hip"),
+           str(ROOT / "tests" / "native" / "decode_fuzz.cpp"), "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return exe
+
+
+@pytest.mark.skipif(not Path(CLANG).exists() or shutil.which("make") is None, reason="needs ROCm's clang++")
+def test_decode_kernels_under_sanitizers(tmp_path):
+    oracle.build()
+    exe = _build(tmp_path)
+    cases = tmp_path / "cases.bin"
+    counts = _write_cases(cases, n_bsck=3000, n_ref=2400)
+    r = subprocess.run([str(exe), str(cases)], capture_output=True, text=True, timeout=1800,
+                       env={"ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1", "UBSAN_OPTIONS": "print_stacktrace=1"})
+    print(counts, r.stdout, r.stderr[-3000:])
+    assert r.returncode == 0, r.stdout + r.stderr[-3000:]
+    line = r.stdout.strip().splitlines()[-1]
+    assert "clean failed 0" in line, line
+    assert counts["bsck_corrupt"] + counts["ref_corrupt"] >= 5000
