@@ -2,15 +2,28 @@
 // engine, decoded on CDNA4 (gfx950).
 //
 // Format (little-endian; produced by bsck_encode.cpp):
-//   [0]  "BSCK"  [4] u8 version=2  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+//   [0]  "BSCK"  [4] u8 version=3  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
 //   [7]  u8 prec_log2 = 12  [8] u64 n  [16] u32 steps  [20] u16 lanes = 64*K
 //   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
 //   [32] n_syms x u32 symbol entries: bits 0..15 output value (bf16 word with
 //        zero sign/mantissa for exponent symbols, or the exact word/byte),
 //        bits 16..28 quantised frequency (sum 4096), bit 31 = reads one plane byte
 //   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
+//   pad to 16; plane_mode 1 only: the dense plane region, nf*per bytes
 //   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l) |
-//        n_words x u16 renorm words (pad 16) | n_plane plane bytes (pad 16)
+//        n_words x u16 renorm words (pad 16) | n_plane plane bytes (pad 16),
+//        the plane bytes omitted for a full chunk in plane_mode 1
+//
+// Chunks and elements: per = 64*K*steps elements per chunk, nf = n / per full
+// chunks, and a partial chunk (c = nf) when per does not divide n. A full
+// chunk's elements are 512-element units of the tensor interleaved across the
+// full chunks: chunk element j is tensor element ((j/512)*nf + c)*512 + j%512.
+// The partial chunk holds the tail: chunk element j is element nf*per + j.
+// The chunks that run side by side therefore read and write neighbouring
+// addresses, which the memory system serves faster than one separate stream
+// per chunk. The dense planes of the full chunks are interleaved the same way,
+// per plane block (B*64*K bytes, below): block b of full chunk c is block
+// b*nf + c of the plane region.
 //
 // A chunk is decoded by one wavefront. Lane l owns K interleaved rANS states
 // (g = 0..K-1); at step t state (g, l) decodes element t*64K + l*K + g of the
@@ -22,7 +35,9 @@
 // Plane bytes (sign<<7 | mantissa) complete bf16 exponent symbols:
 //   plane_mode 1 (dense): every element has one, stored per block of B steps
 //                         (B = 8 for K <= 2, 4 for K = 4) with lane l's B*K
-//                         bytes contiguous, step-major (byte q*K+g);
+//                         bytes contiguous, step-major (byte q*K+g); the
+//                         blocks of a full chunk in the plane region, of the
+//                         partial chunk inline;
 //   plane_mode 2 (compact): only elements whose symbol has bit 31 set have one,
 //                         in decode order (ballot + mbcnt again);
 //   plane_mode 0: no plane (every symbol is an exact value).
@@ -53,7 +68,8 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kVersion = 2;
+constexpr uint32_t kVersion = 3;
+constexpr uint32_t kUnit = 512;           // elements per interleave unit of the output
 constexpr int kWave = 64;                 // lanes of a wavefront
 #ifndef BSCK_WAVES
 #define BSCK_WAVES 8
@@ -168,10 +184,11 @@ struct PlaneRegs {   // dense plane bytes of one block: 8 (K = 1) or 16 (K = 2, 
   uint64_t b[kWords];
 };
 template <int K>
-__device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, uint32_t blk, uint32_t lane) {
+__device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, uint64_t stride, uint32_t blk,
+                                                   uint32_t lane) {
   PlaneRegs<K> r;
   constexpr uint32_t kLaneBytes = block_steps<K>() * K;   // 8 (K=1) or 16 (K=2, 4)
-  const GLB uint8_t* p = dplane + (uint64_t)blk * (kLaneBytes * kWave) + lane * kLaneBytes;
+  const GLB uint8_t* p = dplane + (uint64_t)blk * stride + lane * kLaneBytes;
   if (kLaneBytes == 16) {
     const u32x4 v = *(const GLB u32x4*)p;
     r.b[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
@@ -212,10 +229,11 @@ struct Inflight {
 struct ChunkParams {
   const GLB uint8_t* wsrc;      // renorm words
   const GLB uint8_t* psrc;      // compact plane
-  const GLB uint8_t* dplane;    // dense plane: B*K bytes per lane per block of B steps
+  const GLB uint8_t* dplane;    // dense plane block 0: B*K bytes per lane per block of B steps
+  uint64_t pstride;             // bytes from one dense plane block of the chunk to its next
   const GLB uint8_t* safe;      // the chunk's state words: an always-valid dummy address
   GLB uint8_t* out8;
-  uint64_t base;                // first element of the chunk
+  uint64_t ubase, ustride;      // chunk element j is element (j/512)*ustride + ubase + j%512
   uint32_t n_words, n_plane;
   uint32_t wvalid, pvalid;      // readable words / plane bytes, in segment-lane units
   uint32_t nc, nsteps, nblk, lane;
@@ -226,7 +244,8 @@ template <int K, int EB, bool PARTIAL, int HS>
 __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
   constexpr uint32_t kBlkElems = (uint32_t)HS * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
-  const uint64_t blk_byte0 = (C.base + (uint64_t)hb * kBlkElems) * EB;
+  const uint32_t e0 = hb * kBlkElems;                  // a half block lies inside one 512-element unit
+  const uint64_t blk_byte0 = ((uint64_t)(e0 / kUnit) * C.ustride + C.ubase + e0 % kUnit) * EB;
   // Streaming stores: the decoded tensor is far larger than the L2 (the hint
   // measured 3-4% faster than plain stores on an 8B layer). A full chunk's
   // half block is 256, 512 or 1024 bytes: every lane stores its 4, 8 or 16
@@ -470,7 +489,8 @@ template <int K, int MODE, int EB, bool PARTIAL>
 __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
                                              LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage,
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
-                                             uint32_t n_plane, GLB uint8_t* __restrict__ out8, uint64_t base,
+                                             uint32_t n_plane, const GLB uint8_t* dplane, uint64_t pstride,
+                                             GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
                                              uint32_t nc, uint32_t nsteps, int32_t* status) {
   typedef Geo<K, MODE> G;
   constexpr uint32_t kStates = kWave * K;
@@ -479,10 +499,12 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   const uint32_t wbytes = pad16(n_words * 2u);
   C.wsrc = cbase + 4u * kStates;
   C.psrc = cbase + 4u * kStates + wbytes;
-  C.dplane = C.psrc;
+  C.dplane = dplane ? dplane : C.psrc;
+  C.pstride = pstride;
   C.safe = cbase;
   C.out8 = out8;
-  C.base = base;
+  C.ubase = ubase;
+  C.ustride = ustride;
   C.n_words = n_words;
   C.n_plane = n_plane;
   C.wvalid = wbytes / G::kLaneSeg;
@@ -501,7 +523,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   Inflight<K, MODE> F;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
-    F.pl[i] = MODE == 1 ? load_plane<K>(C.dplane, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
+    F.pl[i] = MODE == 1 ? load_plane<K>(C.dplane, C.pstride, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
   request_segments<K, MODE>(S, F, C);
   consume<K>(S.x);
   if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
@@ -517,8 +539,8 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk - 1, C, stage);
     request_segments<K, MODE>(S, F, C);
     if (MODE == 1) {
-      F.pl[0] = load_plane<K>(C.dplane, min(blk + 2, C.nblk - 1), C.lane);
-      F.pl[1] = load_plane<K>(C.dplane, min(blk + 3, C.nblk - 1), C.lane);
+      F.pl[0] = load_plane<K>(C.dplane, C.pstride, min(blk + 2, C.nblk - 1), C.lane);
+      F.pl[1] = load_plane<K>(C.dplane, C.pstride, min(blk + 3, C.nblk - 1), C.lane);
     }
     wave_sync();
     decode_block<K, MODE, EB, PARTIAL>(blk, cur0, S, C, tbl, wring, pring, stage);
@@ -559,18 +581,19 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
 template <int K, int EB, bool PARTIAL, bool COMPACT>
 __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint64_t* tbl, LDS uint16_t* wring,
                                                   LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
-                                                  uint32_t nw, uint32_t np, GLB uint8_t* out, uint64_t base,
+                                                  uint32_t nw, uint32_t np, const GLB uint8_t* dplane,
+                                                  uint64_t pstride, GLB uint8_t* out, uint64_t ubase, uint64_t ustride,
                                                   uint32_t nc, uint32_t nsteps, int32_t* status) {
   if constexpr (EB == 1) {   // byte elements have no plane
-    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
   } else {
     if (mode == 0) {
-      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
     } else if (mode == 1) {
-      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
     } else {
       if constexpr (COMPACT)
-        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
     }
   }
 }
@@ -578,14 +601,16 @@ __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint6
 template <int K, bool COMPACT>
 __device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32_t mode, const LDS uint64_t* tbl,
                                                LDS uint16_t* wring, LDS uint8_t* pring, LDS uint8_t* stage,
-                                               const GLB uint8_t* cbase, uint32_t nw, uint32_t np, GLB uint8_t* out,
-                                               uint64_t base, uint32_t nc, uint32_t nsteps, int32_t* status) {
+                                               const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
+                                               const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
+                                               uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
+                                               int32_t* status) {
   if (eb == 2) {
-    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
-    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
   } else {
-    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
-    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, out, base, nc, nsteps, status);
+    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
   }
 }
 
@@ -638,7 +663,10 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     return;
   }
   const uint32_t ctab = pad16(32u + 4u * nsym);
-  if ((uint64_t)ctab + 16ull * nch > T.blob_bytes) {
+  const uint64_t nf = n / per;                                // full chunks
+  const uint64_t preg = ((uint64_t)ctab + 16ull * nch + 15u) & ~15ull;   // dense plane region (plane_mode 1)
+  if ((uint64_t)ctab + 16ull * nch > T.blob_bytes ||
+      (mode == 1 && (preg > T.blob_bytes || nf * per > T.blob_bytes - preg))) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_BOUNDS);
     return;
   }
@@ -696,12 +724,15 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const GLB uint8_t* ce = b + ctab + 16ull * chunk;
   const uint64_t off = (uint64_t)ld_u32(ce) | ((uint64_t)ld_u32(ce + 4) << 32);
   const uint32_t nw = ld_u32(ce + 8), np = ld_u32(ce + 12);
-  const uint64_t cbase_idx = (uint64_t)chunk * per;
-  const uint32_t nc = (uint32_t)((n - cbase_idx) < per ? (n - cbase_idx) : per);
+  const uint64_t cbase_idx = (uint64_t)chunk * per;     // the partial chunk's first element (nf * per)
+  const bool full = chunk < nf;
+  const uint32_t nc = full ? (uint32_t)per : (uint32_t)(n - cbase_idx);
   const uint32_t nsteps = (nc + lanes - 1) / lanes;
   const uint32_t bsteps = lanes == 256 ? 4u : 8u;     // block_steps<K>()
   const uint32_t dense_plane = ((nsteps + bsteps - 1) / bsteps) * bsteps * lanes;
-  bool ok = (off % 16) == 0 && off + 4ull * lanes + pad16(nw * 2u) + pad16(np) <= T.blob_bytes &&
+  const bool split = mode == 1 && full;               // dense plane in the plane region
+  const uint64_t pblk = (uint64_t)bsteps * lanes;      // plane bytes per block
+  bool ok = (off % 16) == 0 && off + 4ull * lanes + pad16(nw * 2u) + (split ? 0u : pad16(np)) <= T.blob_bytes &&
             nw <= nsteps * lanes && T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
   if (mode == 1) ok = ok && np == dense_plane;
   if (mode == 2) ok = ok && np <= nc;
@@ -715,13 +746,20 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   LDS uint8_t* pring = s_wring + wave * kRingBytes + Geo<1, 2>::kPRingOff;   // compact chunks only
   LDS uint8_t* stage = s_stage + wave * kStageMax;
   GLB uint8_t* out = (GLB uint8_t*)T.out;
-  const bool partial = nc != per;
+  const bool partial = !full;
+  const GLB uint8_t* dplane = split ? b + preg + chunk * pblk : nullptr;   // nullptr: inline after the words
+  const uint64_t pstride = split ? nf * pblk : pblk;
+  const uint64_t ubase = full ? (uint64_t)chunk * kUnit : cbase_idx;
+  const uint64_t ustride = full ? nf * kUnit : kUnit;
   if (lanes == 64)
-    decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
+    decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
+                               ustride, nc, nsteps, status);
   else if (lanes == 128)
-    decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
+    decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
+                               ustride, nc, nsteps, status);
   else
-    decode_chunk_k<4, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, out, cbase_idx, nc, nsteps, status);
+    decode_chunk_k<4, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
+                               ustride, nc, nsteps, status);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
@@ -746,7 +784,7 @@ int launch(const bs_chunk_task* tasks, uint32_t n_tasks, const bs_chunk_task& si
 
 extern "C" {
 
-int bs_version(void) { return 200; }
+int bs_version(void) { return 300; }
 
 int bs_chunk_chunks_per_group(void) { return kWaves; }
 

@@ -17,6 +17,13 @@
 // group g) codes element t*64K + l*K + g at step t. States are walked from the
 // last step back to the first, v descending within a step, so the decoder
 // consumes the renorm words step-ascending, v-ascending.
+//
+// Chunk c holds elements of the tensor in 512-element units: a full chunk
+// (c < nf = n / (lanes*steps)) holds units c, nf + c, 2nf + c, ..., so the
+// chunks that a launch decodes side by side write neighbouring addresses; the
+// last, partial chunk holds the tail [nf*lanes*steps, n) in order. The dense
+// planes of the full chunks are interleaved the same way, per plane block, in
+// one region before the chunks; the partial chunk keeps its plane inline.
 #include <stdint.h>
 #include <string.h>
 
@@ -30,13 +37,19 @@
 
 namespace {
 
-constexpr uint8_t kVersion = 2;       // BSCK layout version
+constexpr uint8_t kVersion = 3;       // BSCK layout version
 constexpr uint32_t kWave = 64;        // lanes of a wavefront
 constexpr uint32_t kL = 1u << 16;
 constexpr uint32_t kM = 4096;
 // steps per dense-plane block: 8 for 64 or 128 states per chunk, 4 for 256
 inline uint32_t block_steps(uint32_t lanes) { return lanes == 256 ? 4u : 8u; }
 constexpr uint32_t kStepAlign = 16;   // steps per chunk: a multiple of two blocks
+constexpr uint32_t kUnit = 512;       // elements per output interleave unit (divides lanes * kStepAlign)
+
+// Tensor element holding element j of chunk c (nf full chunks of `per` elements).
+inline uint64_t chunk_elem(uint64_t c, uint64_t j, uint64_t nf, uint64_t per) {
+  return c < nf ? ((j / kUnit) * nf + c) * kUnit + j % kUnit : nf * per + j;
+}
 
 inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
 
@@ -211,11 +224,13 @@ bool make_plan(const std::vector<uint64_t>& hist, uint32_t eb, int forced, Plan&
   return c == kM && P.nsym >= 1 && P.nsym <= 256;
 }
 
-// Encode one chunk into `out` (states | words | plane, each 16-padded).
-// `lanes` = 64*K interleaved states; virtual lane v = g*64 + l is state group g
-// of wavefront lane l. Step t covers elements t*lanes .. t*lanes+lanes-1.
-void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, uint32_t lanes,
-                  uint32_t& n_words, uint32_t& n_plane, std::vector<uint8_t>& out) {
+// Encode one chunk, whose nc elements are src[0..nc), into `out` (states |
+// words | plane, each 16-padded; the plane goes to *plane_out instead when
+// that is given). `lanes` = 64*K interleaved states; virtual lane v = g*64 + l
+// is state group g of wavefront lane l. Step t covers chunk elements
+// t*lanes .. t*lanes+lanes-1.
+void encode_chunk(const Plan& P, const void* src, uint32_t nc, uint32_t lanes, uint32_t& n_words, uint32_t& n_plane,
+                  std::vector<uint8_t>& out, std::vector<uint8_t>* plane_out) {
   const uint32_t nsteps = (nc + lanes - 1) / lanes;
   const uint32_t K = lanes / kWave;
   std::vector<uint16_t> words(nc + 1);
@@ -223,7 +238,7 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
   std::vector<uint32_t> x(lanes, kL);
   const uint16_t* w16 = (const uint16_t*)src;
   const uint8_t* w8 = (const uint8_t*)src;
-  auto sym_at = [&](uint64_t j) -> uint32_t { return P.sym_of[P.eb == 2 ? w16[base + j] : w8[base + j]]; };
+  auto sym_at = [&](uint64_t j) -> uint32_t { return P.sym_of[P.eb == 2 ? w16[j] : w8[j]]; };
   uint64_t xmax[256];
   for (uint32_t s = 0; s < P.nsym; ++s) xmax[s] = (uint64_t)P.freq[s] << 20;
   auto elem = [&](uint32_t t, uint32_t v) -> uint64_t { return (uint64_t)t * lanes + (v % kWave) * K + v / kWave; };
@@ -247,7 +262,7 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
     const uint32_t nblk = (nsteps + bs - 1) / bs;
     plane.assign((size_t)nblk * bs * lanes, 0);
     for (uint32_t j = 0; j < nc; ++j) {
-      const uint32_t w = w16[base + j], t = j / lanes, r = j % lanes, l = r / K, g = r % K;
+      const uint32_t w = w16[j], t = j / lanes, r = j % lanes, l = r / K, g = r % K;
       plane[(size_t)(t / bs) * bs * lanes + l * bs * K + (t % bs) * K + g] =
           (uint8_t)(((w >> 8) & 0x80) | (w & 0x7F));
     }
@@ -258,16 +273,17 @@ void encode_chunk(const Plan& P, const void* src, uint64_t base, uint32_t nc, ui
       for (uint32_t v = 0; v < lanes; ++v) {
         const uint64_t j = elem(t, v);
         if (j >= nc) continue;
-        const uint32_t w = w16[base + j];
+        const uint32_t w = w16[j];
         if (P.consume[P.sym_of[w]]) plane.push_back((uint8_t)(((w >> 8) & 0x80) | (w & 0x7F)));
       }
   }
   n_plane = (uint32_t)plane.size();
-  const uint64_t wb = pad16((uint64_t)n_words * 2), pb = pad16(n_plane);
+  const uint64_t wb = pad16((uint64_t)n_words * 2), pb = plane_out ? 0 : pad16(n_plane);
   out.assign(4 * lanes + wb + pb, 0);
   for (uint32_t l = 0; l < lanes; ++l) put32(out.data() + 4 * l, x[l]);
   for (uint32_t i = 0; i < n_words; ++i) put16(out.data() + 4 * lanes + 2 * i, words[pos + i]);
-  if (n_plane) memcpy(out.data() + 4 * lanes + wb, plane.data(), n_plane);
+  if (plane_out) plane_out->swap(plane);
+  else if (n_plane) memcpy(out.data() + 4 * lanes + wb, plane.data(), n_plane);
 }
 
 }  // namespace
@@ -300,21 +316,33 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
   const uint64_t nch64 = (n + per - 1) / per;
   if (nch64 > 0xFFFFFFFFull) return BS_ERR_ARG;
   const uint32_t nch = (uint32_t)nch64;
+  const uint64_t nf = n / per;                       // full chunks
+  const bool split_plane = P.mode == 1;              // full chunks' dense planes go to the plane region
+  const uint64_t ctab = pad16(32 + 4ull * P.nsym);
+  const uint64_t preg = pad16(ctab + 16ull * nch);   // plane region: nf*per bytes in mode 1
+  const uint64_t pblk = (uint64_t)block_steps(lanes) * lanes;   // plane bytes per block
   std::vector<std::vector<uint8_t>> chunks(nch);
   std::vector<uint32_t> nw(nch), np(nch);
+  std::vector<uint8_t> plane_region(split_plane ? nf * per : 0);
   parallel_for(nch, n_threads, [&](uint64_t c) {
-    const uint64_t base = c * per;
-    const uint32_t nc = (uint32_t)std::min<uint64_t>(per, n - base);
-    encode_chunk(P, src, base, nc, lanes, nw[c], np[c], chunks[c]);
+    const uint32_t nc = (uint32_t)std::min<uint64_t>(per, n - c * per);
+    std::vector<uint8_t> gathered((size_t)nc * elem_bytes);   // the chunk's elements in chunk order
+    for (uint32_t j = 0; j < nc; j += (c < nf ? kUnit : nc))
+      memcpy(gathered.data() + (size_t)j * elem_bytes, (const uint8_t*)src + chunk_elem(c, j, nf, per) * elem_bytes,
+             (size_t)std::min<uint32_t>(c < nf ? kUnit : nc, nc - j) * elem_bytes);
+    std::vector<uint8_t> plane;
+    const bool split = split_plane && c < nf;
+    encode_chunk(P, gathered.data(), nc, lanes, nw[c], np[c], chunks[c], split ? &plane : nullptr);
+    if (split)
+      for (uint64_t b = 0; b * pblk < plane.size(); ++b)
+        memcpy(plane_region.data() + (b * nf + c) * pblk, plane.data() + b * pblk, pblk);
   });
 
-  const uint64_t ctab = pad16(32 + 4ull * P.nsym);
-  uint64_t total = ctab + 16ull * nch;
-  total = pad16(total);
+  uint64_t total = preg + plane_region.size();
   std::vector<uint64_t> offs(nch);
   for (uint32_t c = 0; c < nch; ++c) { offs[c] = total; total += chunks[c].size(); }
   if (total > cap) return BS_ERR_CAP;
-  memset(dst, 0, ctab + 16ull * nch + 16);
+  memset(dst, 0, preg);
   memcpy(dst, "BSCK", 4);
   dst[4] = kVersion; dst[5] = (uint8_t)elem_bytes; dst[6] = (uint8_t)P.mode; dst[7] = 12;
   put64(dst + 8, n); put32(dst + 16, steps); put16(dst + 20, lanes); put16(dst + 22, P.nsym);
@@ -326,6 +354,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
     put32(dst + ctab + 16ull * c + 8, nw[c]);
     put32(dst + ctab + 16ull * c + 12, np[c]);
   }
+  if (!plane_region.empty()) memcpy(dst + preg, plane_region.data(), plane_region.size());
   parallel_for(nch, n_threads, [&](uint64_t c) { memcpy(dst + offs[c], chunks[c].data(), chunks[c].size()); });
   *out_len = total;
   return BS_OK;

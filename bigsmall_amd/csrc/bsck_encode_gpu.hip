@@ -19,8 +19,12 @@
 //             its end backwards, final states to its head;
 //   layout    per task: chunk offsets (prefix sum of chunk sizes), chunk table,
 //             blob length (or a capacity error);
-//   assemble  per chunk: states, renorm words and the dense sign|mantissa
-//             plane at the chunk's offset in the blob.
+//   assemble  per chunk: states and renorm words at the chunk's offset in
+//             the blob, the dense sign|mantissa plane in the plane region
+//             (full chunks, interleaved per block) or after the words (the
+//             partial chunk).
+// Chunk k's elements follow the layout's interleave: a full chunk (k < nf)
+// takes 512-element units k, nf + k, 2nf + k, ...; the partial chunk the tail.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,7 +43,8 @@ constexpr uint32_t kLanes = 128;       // states per chunk (two per wavefront la
 constexpr uint32_t kBlock = 8;         // steps per dense-plane block
 constexpr uint32_t kM = 4096;
 constexpr uint32_t kL = 1u << 16;
-constexpr uint8_t kVersion = 2;
+constexpr uint8_t kVersion = 3;
+constexpr uint32_t kUnit = 512;        // elements per output interleave unit
 
 // Per-task plan in the work area.
 struct Plan {
@@ -59,6 +64,11 @@ struct ChunkRec {
 };
 
 __host__ __device__ inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+
+// Tensor element holding element j of chunk k (nf full chunks of `per` elements).
+__device__ __forceinline__ uint64_t chunk_elem(uint64_t k, uint64_t j, uint64_t nf, uint64_t per) {
+  return k < nf ? ((j / kUnit) * nf + k) * kUnit + j % kUnit : nf * per + j;
+}
 
 // x / f for a fixed divisor 1 <= f <= 4096 and any 32-bit x, without a divide
 // instruction: Granlund and Montgomery, "Division by Invariant Integers using
@@ -110,7 +120,7 @@ __global__ __launch_bounds__(256) void enc_hist_kernel(const bs_encode_task* __r
   if (!task_ok(T, per) || c < T.chunk_begin || c - T.chunk_begin >= T.n_chunks) return;
   h[tid] = 0;
   __syncthreads();
-  const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;
+  const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;   // a contiguous slice: the slices cover the tensor once
   const uint32_t nc = (uint32_t)min(per, T.n - base);
   const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
   for (uint32_t j = tid; j < nc; j += 256) atomicAdd(&h[(src[j] >> 7) & 0xFFu], 1u);
@@ -271,11 +281,11 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
     s_sym[i] = P->sym_of_exp[i]; s_f[i] = P->freq[i]; s_c[i] = P->cum[i]; s_m[i] = P->rcp[i]; s_s[i] = P->shf[i];
   }
   __syncthreads();
-  const uint64_t base = (uint64_t)(cg - T.chunk_begin) * per;
-  const uint32_t nc = (uint32_t)min(per, T.n - base);
+  const uint64_t k = cg - T.chunk_begin, nf = T.n / per;
+  const uint32_t nc = (uint32_t)min(per, T.n - k * per);
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
-  const GLB uint32_t* src2 = (const GLB uint32_t*)((const GLB uint16_t*)T.src + base);   // two words per lane-step
-  const GLB uint16_t* src1 = (const GLB uint16_t*)T.src + base;
+  const GLB uint32_t* src2 = (const GLB uint32_t*)T.src;   // two words per lane-step (even elements)
+  const GLB uint16_t* src1 = (const GLB uint16_t*)T.src;
   uint8_t* chunk = scratch + (uint64_t)cg * scratch_bytes(steps);
   GLB uint16_t* words = (GLB uint16_t*)(chunk + 4u * kLanes);   // capacity per; filled from the end
   uint32_t x[2] = {kL, kL};
@@ -284,8 +294,9 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   // this lane's two words of step t, packed (first | second << 16); 0 past the end
   auto load_step = [&](uint32_t t) -> uint32_t {
     const uint32_t j0 = t * kLanes + 2 * lane;
-    if (j0 + 1 < nc) return src2[j0 / 2];
-    return j0 < nc ? (uint32_t)src1[j0] : 0u;
+    const uint64_t e = chunk_elem(k, j0, nf, per);     // j0 and j0 + 1 share a unit
+    if (j0 + 1 < nc) return src2[e / 2];
+    return j0 < nc ? (uint32_t)src1[e] : 0u;
   };
   // Steps are encoded last to first in blocks of kPre; the next block's words
   // are loaded while the current block is encoded, so the loads' latency is
@@ -334,10 +345,11 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   if (lane == 0) recs[cg].nw = (uint32_t)per - wpos;
 }
 
-__device__ __forceinline__ uint64_t chunk_bytes(uint32_t nc, uint32_t nw) {
+// Bytes of a chunk's region: states, words and, for the partial chunk, its plane.
+__device__ __forceinline__ uint64_t chunk_bytes(uint32_t nc, uint32_t nw, bool full) {
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
   const uint64_t np = (uint64_t)((nsteps + kBlock - 1) / kBlock) * kBlock * kLanes;
-  return 4ull * kLanes + pad16(2ull * nw) + np;
+  return 4ull * kLanes + pad16(2ull * nw) + (full ? 0ull : np);
 }
 
 // One wavefront per task: chunk offsets, chunk table, blob length.
@@ -352,7 +364,8 @@ __global__ __launch_bounds__(kWave) void enc_layout_kernel(const bs_encode_task*
   if (lane == 0) out_len[ti] = 0;
   if (!task_ok(T, per) || !P->ok) return;
   const uint64_t ctab = pad16(32 + 4ull * P->nsym);
-  uint64_t run = pad16(ctab + 16ull * T.n_chunks);
+  const uint64_t nf = T.n / per;
+  uint64_t run = pad16(ctab + 16ull * T.n_chunks) + nf * per;   // after the plane region
   for (uint32_t b0 = 0; b0 < T.n_chunks; b0 += kWave) {
     const uint32_t k = b0 + lane;
     const bool live = k < T.n_chunks;
@@ -361,7 +374,7 @@ __global__ __launch_bounds__(kWave) void enc_layout_kernel(const bs_encode_task*
     if (live) {
       nw = recs[T.chunk_begin + k].nw;
       nc = (uint32_t)min(per, T.n - (uint64_t)k * per);
-      sz = chunk_bytes(nc, nw);
+      sz = chunk_bytes(nc, nw, k < nf);
     }
     uint64_t inc = sz;
     for (uint32_t d = 1; d < kWave; d <<= 1) {
@@ -403,8 +416,8 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
   const Plan* P = (const Plan*)(plans + ti * kPlanBytes);
   if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
   const ChunkRec R = recs[cg];
-  const uint64_t base = (uint64_t)(cg - T.chunk_begin) * per;
-  const uint32_t nc = (uint32_t)min(per, T.n - base);
+  const uint64_t k = cg - T.chunk_begin, nf = T.n / per;
+  const uint32_t nc = (uint32_t)min(per, T.n - k * per);
   const uint8_t* chunk = scratch + (uint64_t)cg * scratch_bytes(steps);
   GLB uint8_t* out = (GLB uint8_t*)(T.dst + R.off);
   // states: 512 bytes
@@ -415,11 +428,16 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
   const uint32_t nw_pad = (uint32_t)(pad16(2ull * R.nw) / 2);
   for (uint32_t i = lane; i < nw_pad; i += kWave) wdst[i] = i < R.nw ? wsrc[i] : (uint16_t)0;
   // dense plane: per 8-step block, lane l's 16 bytes hold (q, g) at q*2 + g for
-  // element (blk*8 + q)*128 + 2l + g
-  GLB uint8_t* plane = out + 4u * kLanes + 2ull * nw_pad;
+  // chunk element (blk*8 + q)*128 + 2l + g; block blk of a full chunk is block
+  // blk*nf + k of the plane region
+  constexpr uint64_t kBlkBytes = (uint64_t)kBlock * kLanes;
+  const bool full = k < nf;
+  GLB uint8_t* plane = full ? (GLB uint8_t*)T.dst + pad16(pad16(32 + 4ull * P->nsym) + 16ull * T.n_chunks) + k * kBlkBytes
+                            : out + 4u * kLanes + 2ull * nw_pad;
+  const uint64_t pstride = full ? nf * kBlkBytes : kBlkBytes;
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
   const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
-  const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
+  const GLB uint16_t* src = (const GLB uint16_t*)T.src;
   for (uint32_t blk = 0; blk < nblk; ++blk) {
     uint32_t b[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -427,13 +445,13 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
 #pragma unroll
       for (uint32_t g = 0; g < 2; ++g) {
         const uint32_t j = (blk * kBlock + q) * kLanes + 2 * lane + g;
-        const uint32_t w = j < nc ? src[j] : 0u;
+        const uint32_t w = j < nc ? src[chunk_elem(k, j, nf, per)] : 0u;
         const uint32_t byte = ((w >> 8) & 0x80u) | (w & 0x7Fu);
         const uint32_t k = q * 2 + g;
         b[k >> 2] |= byte << (8 * (k & 3));
       }
     }
-    *(GLB u32x4*)(plane + (uint64_t)blk * kBlock * kLanes + 16u * lane) = u32x4{b[0], b[1], b[2], b[3]};
+    *(GLB u32x4*)(plane + (uint64_t)blk * pstride + 16u * lane) = u32x4{b[0], b[1], b[2], b[3]};
   }
 }
 

@@ -765,19 +765,26 @@ out:
 /* BSCK — the build's GPU-native chunked rANS container format (no reference
  * counterpart). CPU restatement of the device decoder's semantics, used as a
  * checker of the product encoder. Format:
- *   [0]  "BSCK"  [4] u8 version=2  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+ *   [0]  "BSCK"  [4] u8 version=3  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
  *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2)
  *   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
  *   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
- *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16)
- * Element j of chunk c sits at c*lanes*steps + j. With K = lanes/64, state
+ *   pad to 16; plane_mode 1: the full chunks' dense planes (nf*lanes*steps bytes)
+ *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16),
+ *          the plane omitted for a full chunk in plane_mode 1
+ * With per = lanes*steps and nf = n / per full chunks, element j of full
+ * chunk c sits at ((j / 512) * nf + c) * 512 + j % 512 (512-element units
+ * interleaved across the full chunks); element j of the partial chunk (c = nf)
+ * at nf*per + j. With K = lanes/64, state
  * v = g*64 + l (wavefront lane l, group g) decodes element t*lanes + l*K + g at
  * step t. Decode step order: steps ascending; renorm words consumed in ascending
  * v order among states that fell below L. plane_mode 1 (dense): every element
  * consumes one byte, stored in blocks of B steps (B = 8 for K <= 2, 4 for K = 4);
- * the byte of state (g, l) for step B*b+q sits at b*B*lanes + l*B*K + q*K + g.
+ * the byte of state (g, l) for step B*b+q sits at byte l*B*K + q*K + g of the
+ * chunk's plane block b (B*lanes bytes), which is block b*nf + c of the plane
+ * region for a full chunk, and at b*B*lanes of the inline plane otherwise.
  * plane_mode 2 (compact): consuming elements read bytes in decode order.
  * plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
  * ------------------------------------------------------------------------ */
@@ -786,7 +793,7 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
-    if (ver != 2 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128 && lanes != 256) ||
+    if (ver != 3 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128 && lanes != 256) ||
         steps == 0 || steps % 16)
         return ORC_ERR_FORMAT;
     if (n != n_weights) return ORC_ERR_COUNT;
@@ -796,6 +803,9 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     size_t tab = 32 + 4 * (size_t)nsym;
     size_t ctab = (tab + 15) & ~(size_t)15;
     if (ctab + 16 * (size_t)nch > len) return ORC_ERR_FORMAT;
+    uint64_t nf = n / per;                                   /* full chunks */
+    size_t preg = (ctab + 16 * (size_t)nch + 15) & ~(size_t)15;
+    if (mode == 1 && preg + nf * per > len) return ORC_ERR_FORMAT;
     uint32_t val[256], fr[256], cons[256], cum[256], c = 0;
     for (uint32_t s = 0; s < nsym; s++) {
         uint32_t e = get32(blob + 32 + 4 * s);
@@ -809,11 +819,11 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     for (uint32_t ci = 0; ci < nch; ci++) {
         const uint8_t *ce = blob + ctab + 16 * (size_t)ci;
         uint64_t off = get64(ce); uint32_t nw = get32(ce + 8), np = get32(ce + 12);
-        size_t wbytes = ((size_t)nw * 2 + 15) & ~(size_t)15, pbytes = ((size_t)np + 15) & ~(size_t)15;
+        int split = mode == 1 && ci < nf;                   /* plane in the plane region */
+        size_t wbytes = ((size_t)nw * 2 + 15) & ~(size_t)15, pbytes = split ? 0 : ((size_t)np + 15) & ~(size_t)15;
         if (off % 16 || off + 4 * lanes + wbytes + pbytes > len) return ORC_ERR_FORMAT;
         const uint8_t *st = blob + off, *wd = st + 4 * lanes, *pl = wd + wbytes;
-        uint64_t base = (uint64_t)ci * per;
-        uint64_t nc = n - base < per ? n - base : per;
+        uint64_t nc = ci < nf ? per : n - nf * per;
         uint64_t nsteps = (nc + lanes - 1) / lanes;
         uint32_t x[256];
         for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
@@ -836,17 +846,18 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
                     if (mode == 1) {
                         uint64_t bs = lanes == 256 ? 4 : 8;   /* steps per plane block */
                         uint64_t blk = t / bs, q = t % bs;
-                        uint64_t idx = blk * bs * lanes + (uint64_t)wl * bs * K + q * K + g;
-                        if (idx >= np) return ORC_ERR_FORMAT;
-                        b = pl[idx];
+                        uint64_t in_blk = (uint64_t)wl * bs * K + q * K + g;
+                        if (blk * bs * lanes + in_blk >= np) return ORC_ERR_FORMAT;
+                        b = split ? blob[preg + (blk * nf + ci) * bs * lanes + in_blk] : pl[blk * bs * lanes + in_blk];
                     } else if (mode == 2) {
                         if (pp >= np) return ORC_ERR_FORMAT;
                         b = pl[pp++];
                     } else return ORC_ERR_FORMAT;
                     v = v | (b & 0x7F) | ((b & 0x80) << 8);
                 }
-                if (eb == 2) ((uint16_t *)out_v)[base + j] = (uint16_t)v;
-                else ((uint8_t *)out_v)[base + j] = (uint8_t)v;
+                uint64_t e = ci < nf ? ((j / 512) * nf + ci) * 512 + j % 512 : nf * per + j;
+                if (eb == 2) ((uint16_t *)out_v)[e] = (uint16_t)v;
+                else ((uint8_t *)out_v)[e] = (uint8_t)v;
             }
         }
         for (uint32_t l = 0; l < lanes; l++) if (x[l] != RANS_L) return ORC_ERR_FORMAT;

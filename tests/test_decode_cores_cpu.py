@@ -74,6 +74,11 @@ def _bsck_inputs(rng):
     yield rng.integers(0, 65536, 2500).astype(np.uint16), dict(lanes=128, steps=16, mode=1)
     yield rng.integers(0, 256, 4000).astype(np.uint8), dict(lanes=128, steps=16)     # byte elements
     yield np.array([0x3F80], np.uint16), dict(lanes=64, steps=16)
+    # three or more full chunks (interleaved output units and plane blocks) and a tail, every state width
+    yield _bf16(rng.standard_normal(3 * 1024 + 700) * 0.02), dict(lanes=64, steps=16, mode=1)
+    yield _bf16(rng.standard_normal(4 * 2048 + 5) * 0.02), dict(lanes=128, steps=16, mode=1)
+    yield _bf16(rng.standard_normal(3 * 4096 + 300) * 0.02), dict(lanes=256, steps=16, mode=1)
+    yield rng.integers(0, 40, 5 * 2048 + 77).astype(np.uint8), dict(lanes=128, steps=16)
 
 
 def _ref_inputs(rng):

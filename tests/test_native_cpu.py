@@ -110,7 +110,7 @@ def test_planted_corruption_is_caught():
         oracle.chunk_decode(bytes(bad), w.size)
 
 
-@pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 3), ("elem_bytes", 3), ("plane_mode", 3),
+@pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 2), ("elem_bytes", 3), ("plane_mode", 3),
                                          ("prec", 11), ("lanes", 96), ("steps", 24), ("n_syms", 0),
                                          ("n_chunks", 7), ("truncated", None)])
 def test_malformed_header_raises_value_error(field, value):
