@@ -9,10 +9,11 @@
 //        zero sign/mantissa for exponent symbols, or the exact word/byte),
 //        bits 16..28 quantised frequency (sum 4096), bit 31 = reads one plane byte
 //   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
-//   pad to 16; plane_mode 1 only: the dense plane region, nf*per bytes
+//   pad to 256; plane_mode 1 only: the dense plane region, nf*per bytes
 //   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l) |
 //        n_words x u16 renorm words (pad 16) | n_plane plane bytes (pad 16),
 //        the plane bytes omitted for a full chunk in plane_mode 1
+//   pad to 256 (the blob length is a multiple of 256)
 //
 // Chunks and elements: per = 64*K*steps elements per chunk, nf = n / per full
 // chunks, and a partial chunk (c = nf) when per does not divide n. A full
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   }
   const uint32_t ctab = pad16(32u + 4u * nsym);
   const uint64_t nf = n / per;                                // full chunks
-  const uint64_t preg = ((uint64_t)ctab + 16ull * nch + 15u) & ~15ull;   // dense plane region (plane_mode 1)
+  const uint64_t preg = ((uint64_t)ctab + 16ull * nch + 255u) & ~255ull;   // dense plane region (plane_mode 1)
   if ((uint64_t)ctab + 16ull * nch > T.blob_bytes ||
       (mode == 1 && (preg > T.blob_bytes || nf * per > T.blob_bytes - preg))) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_BOUNDS);

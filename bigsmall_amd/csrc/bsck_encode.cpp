@@ -23,7 +23,10 @@
 // chunks that a launch decodes side by side write neighbouring addresses; the
 // last, partial chunk holds the tail [nf*lanes*steps, n) in order. The dense
 // planes of the full chunks are interleaved the same way, per plane block, in
-// one region before the chunks; the partial chunk keeps its plane inline.
+// one region before the chunks; the partial chunk keeps its plane inline. The
+// plane region starts on a 256-byte boundary of the blob and blob lengths are
+// multiples of 256, so blobs placed at 256-byte aligned addresses read whole
+// cache lines.
 #include <stdint.h>
 #include <string.h>
 
@@ -52,6 +55,7 @@ inline uint64_t chunk_elem(uint64_t c, uint64_t j, uint64_t nf, uint64_t per) {
 }
 
 inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+inline uint64_t pad256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 
 struct Plan {
   int mode = 1;
@@ -297,7 +301,7 @@ int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint3
     return BS_ERR_ARG;
   const uint64_t per = (uint64_t)lanes * steps;
   const uint64_t nch = (n + per - 1) / per;
-  *bound = pad16(32 + 4 * 256) + 16 * nch + nch * (4 * lanes + pad16(2 * per) + pad16(per) + 32);
+  *bound = pad16(32 + 4 * 256) + 16 * nch + nch * (4 * lanes + pad16(2 * per) + pad16(per) + 32) + 512;
   return BS_OK;
 }
 
@@ -319,7 +323,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
   const uint64_t nf = n / per;                       // full chunks
   const bool split_plane = P.mode == 1;              // full chunks' dense planes go to the plane region
   const uint64_t ctab = pad16(32 + 4ull * P.nsym);
-  const uint64_t preg = pad16(ctab + 16ull * nch);   // plane region: nf*per bytes in mode 1
+  const uint64_t preg = pad256(ctab + 16ull * nch);  // plane region: nf*per bytes in mode 1
   const uint64_t pblk = (uint64_t)block_steps(lanes) * lanes;   // plane bytes per block
   std::vector<std::vector<uint8_t>> chunks(nch);
   std::vector<uint32_t> nw(nch), np(nch);
@@ -341,6 +345,8 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
   uint64_t total = preg + plane_region.size();
   std::vector<uint64_t> offs(nch);
   for (uint32_t c = 0; c < nch; ++c) { offs[c] = total; total += chunks[c].size(); }
+  const uint64_t end = total;
+  total = pad256(total);                             // blob lengths are multiples of 256
   if (total > cap) return BS_ERR_CAP;
   memset(dst, 0, preg);
   memcpy(dst, "BSCK", 4);
@@ -354,6 +360,7 @@ int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t l
     put32(dst + ctab + 16ull * c + 8, nw[c]);
     put32(dst + ctab + 16ull * c + 12, np[c]);
   }
+  memset(dst + end, 0, total - end);
   if (!plane_region.empty()) memcpy(dst + preg, plane_region.data(), plane_region.size());
   parallel_for(nch, n_threads, [&](uint64_t c) { memcpy(dst + offs[c], chunks[c].data(), chunks[c].size()); });
   *out_len = total;

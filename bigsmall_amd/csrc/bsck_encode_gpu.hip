@@ -64,6 +64,7 @@ struct ChunkRec {
 };
 
 __host__ __device__ inline uint64_t pad16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
+__host__ __device__ inline uint64_t pad256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 
 // Tensor element holding element j of chunk k (nf full chunks of `per` elements).
 __device__ __forceinline__ uint64_t chunk_elem(uint64_t k, uint64_t j, uint64_t nf, uint64_t per) {
@@ -225,7 +226,8 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
   int64_t cum = finc - fl;
   const uint64_t nch = T.n_chunks;
   const uint64_t ctab = pad16(32 + 4ull * nsym);
-  const bool fits = ctab + 16 * nch + 16 <= T.cap && nsym >= 1;
+  const uint64_t preg = pad256(ctab + 16 * nch);   // plane region (or the first chunk)
+  const bool fits = preg <= T.cap && nsym >= 1;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const uint32_t e = lane * 4 + r;
@@ -246,10 +248,11 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
     if (lane == 0) flag(status, BS_DEV_ERR_BOUNDS);
     return;
   }
-  // header, and zeros from the symbol table's end to the chunk table plus 16
-  // (the chunk table itself is written by the layout pass)
+  // header, and zeros from the symbol table's end to the chunk table and from
+  // the chunk table's end to the plane region (the chunk table itself is
+  // written by the layout pass)
   for (uint64_t b = 32 + 4ull * nsym + lane; b < ctab; b += kWave) T.dst[b] = 0;
-  for (uint64_t b = ctab + 16 * nch + lane; b < ctab + 16 * nch + 16; b += kWave) T.dst[b] = 0;
+  for (uint64_t b = ctab + 16 * nch + lane; b < preg; b += kWave) T.dst[b] = 0;
   if (lane == 0) {
     P->nsym = nsym;
     uint8_t* d = T.dst;
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(kWave) void enc_layout_kernel(const bs_encode_task*
   if (!task_ok(T, per) || !P->ok) return;
   const uint64_t ctab = pad16(32 + 4ull * P->nsym);
   const uint64_t nf = T.n / per;
-  uint64_t run = pad16(ctab + 16ull * T.n_chunks) + nf * per;   // after the plane region
+  uint64_t run = pad256(ctab + 16ull * T.n_chunks) + nf * per;   // after the plane region
   for (uint32_t b0 = 0; b0 < T.n_chunks; b0 += kWave) {
     const uint32_t k = b0 + lane;
     const bool live = k < T.n_chunks;
@@ -394,14 +397,16 @@ __global__ __launch_bounds__(kWave) void enc_layout_kernel(const bs_encode_task*
     }
     run += shfl64(inc, kWave - 1);
   }
-  if (lane == 0) {
-    if (run > T.cap) {
+  const uint64_t total = pad256(run);                              // blob lengths are multiples of 256
+  if (total > T.cap) {
+    if (lane == 0) {
       flag(status, BS_DEV_ERR_BOUNDS);
       P->ok = 0;
-    } else {
-      out_len[ti] = run;
     }
+    return;
   }
+  for (uint64_t b = run + lane; b < total; b += kWave) T.dst[b] = 0;
+  if (lane == 0) out_len[ti] = total;
 }
 
 // One wavefront per chunk: states, words (zero-padded to 16), dense plane.
@@ -432,7 +437,7 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
   // blk*nf + k of the plane region
   constexpr uint64_t kBlkBytes = (uint64_t)kBlock * kLanes;
   const bool full = k < nf;
-  GLB uint8_t* plane = full ? (GLB uint8_t*)T.dst + pad16(pad16(32 + 4ull * P->nsym) + 16ull * T.n_chunks) + k * kBlkBytes
+  GLB uint8_t* plane = full ? (GLB uint8_t*)T.dst + pad256(pad16(32 + 4ull * P->nsym) + 16ull * T.n_chunks) + k * kBlkBytes
                             : out + 4u * kLanes + 2ull * nw_pad;
   const uint64_t pstride = full ? nf * kBlkBytes : kBlkBytes;
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;

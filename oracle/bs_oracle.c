@@ -771,9 +771,10 @@ out:
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
  *   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
- *   pad to 16; plane_mode 1: the full chunks' dense planes (nf*lanes*steps bytes)
+ *   pad to 256; plane_mode 1: the full chunks' dense planes (nf*lanes*steps bytes)
  *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16),
  *          the plane omitted for a full chunk in plane_mode 1
+ *   pad to 256 (blob lengths are multiples of 256)
  * With per = lanes*steps and nf = n / per full chunks, element j of full
  * chunk c sits at ((j / 512) * nf + c) * 512 + j % 512 (512-element units
  * interleaved across the full chunks); element j of the partial chunk (c = nf)
@@ -804,7 +805,7 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     size_t ctab = (tab + 15) & ~(size_t)15;
     if (ctab + 16 * (size_t)nch > len) return ORC_ERR_FORMAT;
     uint64_t nf = n / per;                                   /* full chunks */
-    size_t preg = (ctab + 16 * (size_t)nch + 15) & ~(size_t)15;
+    size_t preg = (ctab + 16 * (size_t)nch + 255) & ~(size_t)255;
     if (mode == 1 && preg + nf * per > len) return ORC_ERR_FORMAT;
     uint32_t val[256], fr[256], cons[256], cum[256], c = 0;
     for (uint32_t s = 0; s < nsym; s++) {
