@@ -56,7 +56,8 @@
 //     and the exponent byte is placed with v_perm;
 //   bytes (elem_bytes 1): {f | value << 24, slot - cf}, the same update, the
 //     output byte taken from bits 24..31 with v_perm;
-//   generic (bf16 plane modes 0/2): {f | (slot - cf) << 13, value | consume << 31}.
+//   generic (bf16 plane modes 0/2): {f, value | (slot - cf) << 16 | consume << 31};
+//     the update is one shift, one bit-field extract and one v_mad_u32_u24.
 #include <stdint.h>
 
 #include "simt.h"
@@ -85,7 +86,12 @@ template <int K>
 constexpr int block_steps() { return K == 4 ? 4 : 8; }
 constexpr int kBlockMax = 8;
 constexpr uint32_t kMirror = 64;          // word-ring entries [0, 64) are mirrored after the ring end
-constexpr uint32_t kRingBytes = (2048 + kMirror) * 2;   // per-wave ring area
+constexpr uint32_t kPMirror = 64;         // compact plane-ring bytes [0, 64) likewise
+// per-wave ring area: a 2048-word ring and its mirror, or (compact chunks) a
+// 1024-word ring and its mirror, a 2048-byte plane ring and its mirror, and a
+// 16-byte zero slot that non-consuming lanes read as their plane byte
+constexpr uint32_t kRingBytes = (1024 + kMirror) * 2 + 2048 + kPMirror + 16;
+static_assert(kRingBytes >= (2048 + kMirror) * 2, "ring area");
 constexpr uint32_t kL = 1u << 16;
 // s_waitcnt immediate for gfx9: vmcnt(4), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
@@ -93,7 +99,7 @@ constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
 // dynamic LDS layout (bytes): decode table | per-wave ring areas | per-wave output staging
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
-constexpr uint32_t kLds = kTblBytes + kWaves * (kRingBytes + kStageMax);   // 74752: two workgroups per CU
+constexpr uint32_t kLds = kTblBytes + kWaves * (kRingBytes + kStageMax);   // 75392: two workgroups per CU
 
 template <bool HALF> struct SegVec { typedef u32x4 T; };
 template <> struct SegVec<true> { typedef u32x2 T; };
@@ -117,8 +123,9 @@ struct Geo {
   static constexpr uint32_t kPRing = 2048;                               // plane ring bytes (mode 2)
   static constexpr uint32_t kPSeg = kLaneSeg * kWave;                    // plane bytes per segment
   static constexpr uint32_t kPRingOff = (kRing + kMirror) * 2;           // plane ring offset in the ring area
+  static constexpr uint32_t kPZero = kPRing + kPMirror;                  // zero slot, from the plane ring
   typedef typename SegVec<kHalf>::T Seg;
-  static_assert(!kHalf || kPRingOff + kPRing <= kRingBytes, "compact rings exceed the ring area");
+  static_assert(!kHalf || kPRingOff + kPZero + 16 <= kRingBytes, "compact rings exceed the ring area");
   static_assert(kHalf || (kRing + kMirror) * 2 <= kRingBytes, "word ring exceeds the ring area");
 };
 
@@ -174,9 +181,13 @@ __device__ __forceinline__ void store_wseg(LDS uint16_t* ring, uint32_t pos, typ
   *(LDS typename G::Seg*)(ring + r) = v;
   if (r < kMirror) *(LDS typename G::Seg*)(ring + G::kRing + r) = v;
 }
+// Plane ring (compact chunks): bytes [0, kPMirror) also live after the ring
+// end, so a read at (ring position mod kPRing) + rank, rank < 64, never wraps.
 template <class G>
 __device__ __forceinline__ void store_pseg(LDS uint8_t* ring, uint32_t pos, typename G::Seg v, uint32_t lane) {
-  *(LDS typename G::Seg*)(ring + ((pos + lane * G::kLaneSeg) & (G::kPRing - 1u))) = v;
+  const uint32_t r = (pos + lane * G::kLaneSeg) & (G::kPRing - 1u);
+  *(LDS typename G::Seg*)(ring + r) = v;
+  if (r < kPMirror) *(LDS typename G::Seg*)(ring + G::kPRing + r) = v;
 }
 
 template <int K>
@@ -242,7 +253,7 @@ struct ChunkParams {
 
 // Store the staged outputs of half-block `hb` (HS steps) to the output.
 template <int K, int EB, bool PARTIAL, int HS>
-__device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* __restrict__ stage) {
+__device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LDS uint8_t* stage) {
   constexpr uint32_t kBlkElems = (uint32_t)HS * kWave * K;
   constexpr uint32_t kBlkBytes = kBlkElems * EB;
   const uint32_t e0 = hb * kBlkElems;                  // a half block lies inside one 512-element unit
@@ -291,8 +302,8 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
 // merged into d.
 template <int K, int MODE, bool FAST, bool PARTIAL>
 __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C,
-                                          const LDS uint64_t* __restrict__ tbl, const LDS uint16_t* __restrict__ wring,
-                                          const LDS uint8_t* __restrict__ pring, uint32_t (&d)[K]) {
+                                          const LDS uint64_t* __restrict__ tbl, const LDS uint16_t* wring,
+                                          const LDS uint8_t* pring, uint32_t (&d)[K]) {
   typedef Geo<K, MODE> G;
   uint64_t e[K];
 #pragma unroll
@@ -307,8 +318,8 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
       xn[g] = __umul24(lo, S.x[g] >> 12) + hi;             // v_mad_u32_u24: f = bits 0..23 of lo
       d[g] = lo;                                           // exponent or byte value in byte 3
     } else {
-      xn[g] = __umul24(lo & 0x1FFFu, S.x[g] >> 12) + (lo >> 13);
-      d[g] = hi;                                           // value | consume << 31
+      xn[g] = __umul24(lo, S.x[g] >> 12) + ((hi >> 16) & 0xFFFu);
+      d[g] = hi;                                           // value | (slot - cf) << 16 | consume << 31
     }
     bool act = true;
     if (PARTIAL) {
@@ -320,10 +331,12 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
     w[g] = wring[(pos & (G::kRing - 1u)) + lane_rank(m)];   // < kRing + 64: the mirror covers it
     pos += (uint32_t)__popcll(m);
     if (MODE == 2) {
-      // plane bytes follow decode order: groups ascending, then lanes ascending
+      // plane bytes follow decode order: groups ascending, then lanes ascending;
+      // a non-consuming lane reads the zero slot, so the merge below needs no select
       cons[g] = act && (int32_t)hi < 0;
       const uint64_t cm = __ballot(cons[g]);
-      pb[g] = pring[(ppos + lane_rank(cm)) & (G::kPRing - 1u)];
+      const uint32_t at = (ppos & (G::kPRing - 1u)) + lane_rank(cm);   // < kPRing + 64: the mirror covers it
+      pb[g] = pring[cons[g] ? at : G::kPZero];
       ppos += (uint32_t)__popcll(cm);
     }
   }
@@ -334,7 +347,7 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 #pragma unroll
   for (int g = 0; g < K; ++g) {
     S.x[g] = need[g] ? ((xn[g] << 16) | w[g]) : xn[g];
-    if (MODE == 2 && cons[g]) d[g] = byte_merge(d[g], pb[g]);
+    if (MODE == 2) d[g] = byte_merge(d[g], pb[g]);       // pb = 0 for a non-consuming element
   }
 }
 
@@ -350,8 +363,8 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 
 // Land the in-flight ring segments, in request order.
 template <int K, int MODE>
-__device__ __forceinline__ void land_segments(ChunkState<K>& S, Inflight<K, MODE>& F, LDS uint16_t* __restrict__ wring,
-                                              LDS uint8_t* __restrict__ pring, uint32_t lane) {
+__device__ __forceinline__ void land_segments(ChunkState<K>& S, Inflight<K, MODE>& F, LDS uint16_t* wring,
+                                              LDS uint8_t* pring, uint32_t lane) {
   typedef Geo<K, MODE> G;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -390,7 +403,7 @@ __device__ __forceinline__ void request_segments(const ChunkState<K>& S, Infligh
 // in-flight segments early (waiting for them) and loads synchronously.
 template <int K, int MODE>
 __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C,
-                                       LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring) {
+                                       LDS uint16_t* wring, LDS uint8_t* pring) {
   typedef Geo<K, MODE> G;
   typedef typename G::Seg V;
   constexpr uint32_t kBlkElems = G::kBlkElems;
@@ -418,8 +431,8 @@ __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, c
 template <int K, int MODE, int EB, bool PARTIAL>
 __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, ChunkState<K>& S,
                                              const ChunkParams& C, const LDS uint64_t* __restrict__ tbl,
-                                             const LDS uint16_t* __restrict__ wring, LDS uint8_t* __restrict__ pring,
-                                             LDS uint8_t* __restrict__ stage) {
+                                             const LDS uint16_t* wring, LDS uint8_t* pring,
+                                             LDS uint8_t* stage) {
   constexpr uint32_t kStates = kWave * K;
   constexpr int kBlock = Geo<K, MODE>::kBlock;
   constexpr int kHalf = kBlock / 2;
@@ -487,8 +500,8 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
 // plane mode, EB = element bytes, PARTIAL = chunk may be shorter than
 // 64*K*steps (the tensor's last chunk).
 template <int K, int MODE, int EB, bool PARTIAL>
-__device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* __restrict__ wring,
-                                             LDS uint8_t* __restrict__ pring, LDS uint8_t* __restrict__ stage,
+__device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* wring,
+                                             LDS uint8_t* pring, LDS uint8_t* stage,
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
                                              uint32_t n_plane, const GLB uint8_t* dplane, uint64_t pstride,
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
@@ -519,8 +532,10 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   for (int g = 0; g < K; ++g) S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
   S.wptr = S.wld = S.pptr = S.pld = 0;
 
-  // First pair's loads; land all of them before the loop so that the loop
-  // header's wait-count state holds no load issued here.
+  if (MODE == 2 && C.lane == 0) *(LDS u32x4*)(pring + G::kPZero) = u32x4{0u, 0u, 0u, 0u};
+
+  // First loads; land all of them before the loop so that the loop header's
+  // wait-count state holds no load issued here.
   Inflight<K, MODE> F;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -713,7 +728,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
       const uint32_t c0 = s_cum[lo], f = s_cum[lo + 1] - c0, val = s_val[lo];
       s_tbl[slot] = fast    ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
                     : eb == 1 ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
-                              : ((uint64_t)(f | ((slot - c0) << 13)) | ((uint64_t)val << 32));
+                              : ((uint64_t)f | ((uint64_t)(val | ((slot - c0) << 16)) << 32));
     }
   }
   __syncthreads();

@@ -211,7 +211,7 @@ __device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint64_t max_le
 template <bool SE>
 __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
                                              uint32_t n, const LDS u32x4* __restrict__ tbl,
-                                             LDS uint8_t* __restrict__ ring, GLB uint8_t* __restrict__ out,
+                                             LDS uint8_t* ring, GLB uint8_t* __restrict__ out,
                                              uint32_t stride, int32_t* status) {
   constexpr uint32_t kSlotMask = SE ? 4095u : 1023u;
   constexpr uint32_t kShift = SE ? 12u : 10u;

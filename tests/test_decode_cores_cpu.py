@@ -2,7 +2,8 @@
 refcodec_decode.hip) run on the CPU under AddressSanitizer and UBSan, built
 as host C++ with the SIMT emulation of bigsmall_amd/csrc/simt_cpu.h (one fiber
 per lane, wavefront operations and barriers as switch points), driven by
-tests/native/decode_fuzz.cpp.
+tests/native/decode_fuzz.cpp; a second build at -O2 without instrumentation
+decodes the clean blobs and a share of the corrupted ones.
 
 Cases: clean blobs of every BSCK plane mode, state width and element size,
 and of the reference's three formats on both decode paths (wave-serial and
@@ -79,6 +80,13 @@ def _bsck_inputs(rng):
     yield _bf16(rng.standard_normal(4 * 2048 + 5) * 0.02), dict(lanes=128, steps=16, mode=1)
     yield _bf16(rng.standard_normal(3 * 4096 + 300) * 0.02), dict(lanes=256, steps=16, mode=1)
     yield rng.integers(0, 40, 5 * 2048 + 77).astype(np.uint8), dict(lanes=128, steps=16)
+    # long chunks: the ring pipelines run many blocks; uniform bytes need about one renorm word per
+    # two elements, which empties the word ring faster than loads refill it
+    yield rng.integers(0, 256, 3 * 8192 + 100).astype(np.uint8), dict(lanes=128, steps=64)
+    hz2 = _bf16(rng.standard_normal(3 * 8192 + 33) * 0.02)
+    hz2[rng.permutation(hz2.size)[: hz2.size // 2]] = 0
+    yield hz2, dict(lanes=128, steps=64, mode=2)
+    yield _bf16(rng.standard_normal(2 * 8192 + 9) * 0.02), dict(lanes=128, steps=64, mode=1)
 
 
 def _ref_inputs(rng):
@@ -129,11 +137,14 @@ def _write_cases(path: Path, n_bsck: int, n_ref: int) -> dict:
     return counts
 
 
-def _build(tmp_path: Path) -> Path:
-    exe = tmp_path / "decode_fuzz"
+SANITIZE = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer",
+            "-fsanitize-address-use-after-return=never"]
+
+
+def _build(tmp_path: Path, flags: list[str], name: str) -> Path:
+    exe = tmp_path / name
     csrc = ROOT / "bigsmall_amd" / "csrc"
-    cmd = [CLANG, "-std=c++17", "-O2", "-g", "-pthread", "-DBS_SIMT_CPU", "-DBSCK_WAVES=4",
-           "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-fsanitize-address-use-after-return=never",
+    cmd = [CLANG, "-std=c++17", "-O2", "-g", "-pthread", "-DBS_SIMT_CPU", "-DBSCK_WAVES=4", *flags,
            "-I", str(ROOT / "include"), "-I", str(csrc),
            "-x", "c++", str(csrc / "bsck_decode.hip"), str(csrc / "refcodec_decode.hip"),
            str(ROOT / "tests" / "native" / "decode_fuzz.cpp"), "-o", str(exe)]
@@ -145,7 +156,7 @@ def _build(tmp_path: Path) -> Path:
 @pytest.mark.skipif(not Path(CLANG).exists() or shutil.which("make") is None, reason="needs ROCm's clang++")
 def test_decode_kernels_under_sanitizers(tmp_path):
     oracle.build()
-    exe = _build(tmp_path)
+    exe = _build(tmp_path, SANITIZE, "decode_fuzz")
     cases = tmp_path / "cases.bin"
     counts = _write_cases(cases, n_bsck=3000, n_ref=2400)
     r = subprocess.run([str(exe), str(cases)], capture_output=True, text=True, timeout=1800,
@@ -155,3 +166,18 @@ def test_decode_kernels_under_sanitizers(tmp_path):
     line = r.stdout.strip().splitlines()[-1]
     assert "clean failed 0" in line, line
     assert counts["bsck_corrupt"] + counts["ref_corrupt"] >= 5000
+
+
+@pytest.mark.skipif(not Path(CLANG).exists() or shutil.which("make") is None, reason="needs ROCm's clang++")
+def test_decode_kernels_optimised_without_instrumentation(tmp_path):
+    """The same kernels at -O2 with no sanitizer: instrumentation changes what
+    the optimiser may assume, and code that is only right when unoptimised (an
+    LDS access moved across a wavefront barrier, say) shows here as a clean
+    blob decoding wrong."""
+    oracle.build()
+    exe = _build(tmp_path, [], "decode_plain")
+    cases = tmp_path / "cases.bin"
+    _write_cases(cases, n_bsck=600, n_ref=480)
+    r = subprocess.run([str(exe), str(cases)], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout + r.stderr[-3000:]
+    assert "clean failed 0" in r.stdout.strip().splitlines()[-1]
