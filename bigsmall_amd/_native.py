@@ -59,7 +59,8 @@ SIGNATURES = {
     "bs_refcodec_serial_tiles": (_U32, [_U64, _U32]),
     "bs_refcodec_encode_bound": (_U64, [_I32, _U64, _U32]),
     "bs_refcodec_encode": (_INT, [_I32, _P, _U64, _U32, _P, _U64, ctypes.POINTER(_U64), _INT]),
-    "bs_refcodec_decode_serial_batch": (_INT, [_P, _U32, _U32, _U32, _U32, _P, _U64, _P, _P]),
+    "bs_refcodec_decode_serial_batch": (_INT, [_P, _U32, _U32, _U32, _U32, _U32, _P, _U64, _P, _P]),
+    "bs_refcodec_serial_chains_per_group": (_U32, []),
 }
 
 _lib = None

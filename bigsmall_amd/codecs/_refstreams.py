@@ -39,9 +39,10 @@ MANT_BUCKET_DTYPE = np.dtype([("words", "<u8"), ("x0", "<u4"), ("n_words", "<u4"
                               ("perm_begin", "<u8"), ("table", "<u4"), ("reserved", "<u4")])
 REF_TASK_DTYPE = np.dtype([("streams", "<u8"), ("se_table", "<u8"), ("bstart", "<u8"), ("buckets", "<u8"),
                            ("mant_tables", "<u8"), ("out", "<u8"), ("n_out", "<u8"), ("work_offset", "<u8"),
-                           ("n_streams", "<u4"), ("n_buckets", "<u4"), ("n_tables", "<u4"), ("chain_begin", "<u4"),
-                           ("tile_begin", "<u4"), ("stream_begin", "<u4")])
-assert SE_STREAM_DTYPE.itemsize == 40 and MANT_BUCKET_DTYPE.itemsize == 40 and REF_TASK_DTYPE.itemsize == 88
+                           ("n_streams", "<u4"), ("n_buckets", "<u4"), ("n_tables", "<u4"), ("se_group_begin", "<u4"),
+                           ("tile_begin", "<u4"), ("stream_begin", "<u4"), ("mant_group_begin", "<u4"),
+                           ("reserved", "<u4")])
+assert SE_STREAM_DTYPE.itemsize == 40 and MANT_BUCKET_DTYPE.itemsize == 40 and REF_TASK_DTYPE.itemsize == 96
 
 
 class _Reader:
@@ -313,8 +314,13 @@ def _plan_arrays(plan: RefPlan, blob_ptr: int) -> list[np.ndarray]:
     se = np.zeros(len(plan.se_streams), SE_STREAM_DTYPE)
     for i, (s, first, stride, n) in enumerate(plan.se_streams):
         se[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, first, stride, 0)
+    # buckets longest first: the wave-serial kernel decodes them in groups of
+    # four wavefronts, and a group holds its slot until its longest bucket ends
+    # (every bucket carries its own output position, so the order is free)
     mb = np.zeros(len(plan.buckets), MANT_BUCKET_DTYPE)
-    for i, (s, pb, n, t) in enumerate(plan.buckets):
+    order = sorted(range(len(plan.buckets)), key=lambda i: -plan.buckets[i][2])
+    for i, j in enumerate(order):
+        s, pb, n, t = plan.buckets[j]
         mb[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, pb, t, 0)
     tables = (np.stack([decode_table_mant(f) for f in plan.mant_freqs]) if plan.mant_freqs
               else np.zeros((1, M_MANT), np.uint32))
@@ -354,7 +360,7 @@ def serial_ok(plan: RefPlan) -> bool:
 class RefBatch:
     """The wave-serial decode of several parsed blobs (a layer's
     reference-format tensors) as one bs_refcodec_decode_serial_batch launch:
-    all their chains run side by side. items: [(plan, blob_ptr, out_ptr)],
+    all their chains run side by side, the SE chains (the longest) first. items: [(plan, blob_ptr, out_ptr)],
     every plan accepted by serial_ok. Device buffers stay alive with this
     object until the decode launched from it has completed."""
 
@@ -363,7 +369,8 @@ class RefBatch:
         L = _native.lib()
         arrays = []
         tasks = np.zeros(len(items), REF_TASK_DTYPE)
-        chain = tile = stream = work = 0
+        per = int(L.bs_refcodec_serial_chains_per_group())
+        se_g = mant_g = tile = stream = work = 0
         for i, (plan, blob_ptr, out_ptr) in enumerate(items):
             if not serial_ok(plan):
                 raise ValueError("RefBatch: a tensor the wave-serial path does not take")
@@ -371,9 +378,10 @@ class RefBatch:
             ns, nb = len(plan.se_streams), len(plan.buckets)
             nt = max(1, len(plan.mant_freqs))
             tiles = int(L.bs_refcodec_serial_tiles(plan.n, ns))
-            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, chain, tile, stream)
+            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, se_g, tile, stream, mant_g, 0)
             work += (int(L.bs_refcodec_serial_work_bytes(plan.n, ns)) + 255) & ~255
-            chain, tile, stream = chain + ns + nb, tile + ns * tiles, stream + ns
+            se_g, mant_g = se_g + -(-ns // per), mant_g + -(-nb // per)
+            tile, stream = tile + ns * tiles, stream + ns
         size, offs = _layout(arrays + [tasks.view(np.uint8)])
         self.dev = torch.empty(size, dtype=torch.uint8, device=device)
         base = self.dev.data_ptr()
@@ -385,7 +393,7 @@ class RefBatch:
         self.dev.copy_(torch.from_numpy(buf))
         self.p_tasks = base + offs[-1]
         self.n_tasks = len(items)
-        self.totals = (chain, tile, stream)
+        self.totals = (se_g, mant_g, tile, stream)
         self.work = torch.empty(max(work, 256), dtype=torch.uint8, device=device)
 
     def launch(self, status_ptr: int, stream_ptr: int) -> None:

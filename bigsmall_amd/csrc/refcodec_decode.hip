@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
 // stream: per-tile histograms, a scan over the stream's tiles, per-tile ranks
 // by wavefront ballots) and OR in its mantissa.
 
-constexpr uint32_t kRingB = 4096;     // word-stream byte ring per chain
+constexpr uint32_t kRingB = 2048;     // word-stream byte ring per chain (two segments: one landed, one in flight)
 constexpr uint32_t kSegB = 1024;      // bytes per cooperative load (64 lanes x 16 B)
 constexpr uint32_t kTile = 16384;     // elements per tile of the placement passes
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -301,10 +301,11 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
 }
 
 // ---- tasks of a wave-serial launch. Every tensor of a batch is one task; its
-// chains, tiles and streams occupy consecutive workgroups of the four grids
-// (chain_begin, tile_begin, stream_begin), so one launch of each kernel covers
-// the whole batch and the chains of all its tensors run side by side. The
-// single-tensor entry point passes its one task by value (tasks == nullptr).
+// chain groups, tiles and streams occupy consecutive workgroups of the grids
+// (se_group_begin, mant_group_begin, tile_begin, stream_begin), so one launch
+// of each kernel covers the whole batch and the chains of all its tensors run
+// side by side. The single-tensor entry point passes its one task by value
+// (tasks == nullptr).
 
 __host__ __device__ inline uint64_t serial_max_len(uint64_t n_out, uint32_t n_streams) {
   return (n_out + n_streams - 1) / n_streams;
@@ -325,10 +326,11 @@ __device__ __forceinline__ bool task_ok(const bs_ref_task& T, uint64_t work_byte
   return T.work_offset <= work_bytes && serial_work(T.n_out, T.n_streams) <= work_bytes - T.work_offset;
 }
 
-enum { kChainGrid = 0, kTileGrid = 1, kStreamGrid = 2 };
+enum { kSeGrid = 0, kMantGrid = 1, kTileGrid = 2, kStreamGrid = 3 };
 template <int G>
 __device__ __forceinline__ uint32_t grid_begin(const bs_ref_task& t) {
-  return G == kChainGrid ? t.chain_begin : G == kTileGrid ? t.tile_begin : t.stream_begin;
+  return G == kSeGrid ? t.se_group_begin : G == kMantGrid ? t.mant_group_begin
+                                         : G == kTileGrid ? t.tile_begin : t.stream_begin;
 }
 // The task whose range of grid G holds workgroup b (binary search over the
 // ascending begins; wave-uniform).
@@ -344,46 +346,67 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
   return tasks[lo];
 }
 
-// Chain grid: workgroup chain_begin + k (k < n_streams) decodes SE stream k
-// (element first + i*stride for symbol i); chain_begin + n_streams + b decodes
-// mantissa bucket b into mant[perm_begin ...] (bucket order).
-__global__ __launch_bounds__(kWave) void serial_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
-                                                       bs_ref_task single, uint8_t* __restrict__ work,
-                                                       uint64_t work_bytes, int32_t* __restrict__ status) {
+// Chain grid: workgroups of kSerWaves wavefronts, one chain each. The first
+// se_groups workgroups are SE groups (task by se_group_begin): wave w of
+// group j decodes SE stream j*kSerWaves + w (element first + i*stride for
+// symbol i) with the task's SE table, built once per workgroup and shared.
+// The rest are mantissa groups (task by mant_group_begin): wave w decodes
+// bucket j*kSerWaves + w into mant[perm_begin ...] with its own bucket table.
+// Sharing the 64 KB SE table lets a CU hold eight chains instead of two. The
+// host lists buckets longest first, so the four buckets of a group end at
+// about the same time and the longest start first.
+constexpr uint32_t kSerWaves = 4;
+constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16;   // 73728: rings | SE table or kSerWaves mantissa tables
+static_assert(2 * kSerLds <= 160 * 1024 - 8192, "two chain groups per CU");
+static_assert(kSerWaves * 1024 * 16 <= 4096 * 16, "mantissa tables exceed the table area");
+
+__global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_task* __restrict__ tasks,
+                                                                   uint32_t n_tasks, bs_ref_task single,
+                                                                   uint32_t se_groups, uint8_t* __restrict__ work,
+                                                                   uint64_t work_bytes, int32_t* __restrict__ status) {
   BS_DYNAMIC_LDS(smem);
-  LDS uint8_t* ring = (LDS uint8_t*)smem;
-  LDS u32x4* tbl = (LDS u32x4*)(smem + kRingB);      // {f, slot - cf, output, 0} per slot
-  const uint32_t lane = threadIdx.x;
-  const bs_ref_task T = pick_task<kChainGrid>(tasks, n_tasks, single, blockIdx.x);
-  if (blockIdx.x < T.chain_begin) return;
-  const uint32_t c = blockIdx.x - T.chain_begin;
-  if ((uint64_t)c >= (uint64_t)T.n_streams + T.n_buckets) return;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  LDS uint8_t* ring = (LDS uint8_t*)smem + wave * kRingB;
+  LDS u32x4* tbl_area = (LDS u32x4*)(smem + kSerWaves * kRingB);
+  const bool se = blockIdx.x < se_groups;                 // uniform over the workgroup
+  const uint32_t g = se ? blockIdx.x : blockIdx.x - se_groups;
+  const bs_ref_task T = se ? pick_task<kSeGrid>(tasks, n_tasks, single, g)
+                           : pick_task<kMantGrid>(tasks, n_tasks, single, g);
+  const uint32_t begin = se ? T.se_group_begin : T.mant_group_begin;
+  if (g < begin) return;
+  const uint32_t local = g - begin, count = se ? T.n_streams : T.n_buckets;
+  if ((uint64_t)local * kSerWaves >= count) return;
   if (!task_ok(T, work_bytes)) {
-    if (c == 0 && lane == 0) flag(status, BS_DEV_ERR_HEADER);
+    if (local == 0 && tid == 0) flag(status, BS_DEV_ERR_HEADER);
     return;
   }
+  const uint32_t c = local * kSerWaves + wave;            // this wave's stream or bucket (none when >= count)
   const uint64_t max_len = (uint64_t)serial_tiles(T.n_out, T.n_streams) * kTile;
   uint8_t* mant = work + T.work_offset;
-  if (c < T.n_streams) {
+  if (se) {
+    for (uint32_t i = tid; i < 4096; i += kSerWaves * kWave) {
+      const uint32_t lo = T.se_table[2 * i], sym = T.se_table[2 * i + 1];
+      const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
+      tbl_area[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
+    }
+    __syncthreads();
+    if (c >= count) return;
     const bs_se_stream S = T.streams[c];
     if (!stream_ok(S, max_len, T.n_out)) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
-    for (uint32_t i = lane; i < 4096; i += kWave) {
-      const uint32_t lo = T.se_table[2 * i], sym = T.se_table[2 * i + 1];
-      const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
-      tbl[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
-    }
-    wave_sync();
-    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl, ring,
+    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl_area, ring,
                        (GLB uint8_t*)(T.out + S.first), S.stride, status);
   } else {
-    const bs_mant_bucket B = T.buckets[c - T.n_streams];
+    if (c >= count) return;
+    const bs_mant_bucket B = T.buckets[c];
     if (B.table >= T.n_tables || B.perm_begin + B.n > T.n_out) {
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
+    LDS u32x4* tbl = tbl_area + wave * 1024u;
     const GLB uint32_t* t = (const GLB uint32_t*)T.mant_tables + (uint64_t)B.table * 1024u;
     for (uint32_t i = lane; i < 1024; i += kWave) {
       const uint32_t e = t[i];
@@ -497,13 +520,13 @@ __global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restr
 
 std::atomic<uint64_t> g_serial_lds{0};
 
-int launch_serial(const bs_ref_task* tasks, uint32_t n_tasks, const bs_ref_task& single, uint32_t chains,
-                  uint32_t tiles, uint32_t streams, uint8_t* work, uint64_t work_bytes, int32_t* status,
-                  hipStream_t s) {
-  constexpr uint32_t kSerLds = kRingB + 4096 * 16;
+int launch_serial(const bs_ref_task* tasks, uint32_t n_tasks, const bs_ref_task& single, uint32_t se_groups,
+                  uint32_t mant_groups, uint32_t tiles, uint32_t streams, uint8_t* work, uint64_t work_bytes,
+                  int32_t* status, hipStream_t s) {
+  if ((uint64_t)se_groups + mant_groups > 0xFFFFFFFFull) return BS_ERR_ARG;
   bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, g_serial_lds);
-  hipLaunchKernelGGL(serial_kernel, dim3(chains), dim3(kWave), kSerLds, s, tasks, n_tasks, single, work, work_bytes,
-                     status);
+  hipLaunchKernelGGL(serial_kernel, dim3(se_groups + mant_groups), dim3(kSerWaves * kWave), kSerLds, s, tasks,
+                     n_tasks, single, se_groups, work, work_bytes, status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
   hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
@@ -573,19 +596,22 @@ int bs_refcodec_decode_serial(const bs_se_stream* d_streams, uint32_t n_streams,
   t.n_streams = n_streams;
   t.n_buckets = n_buckets;
   t.n_tables = n_tables;
-  return launch_serial(nullptr, 0u, t, n_streams + n_buckets, (uint32_t)tiles, n_streams, (uint8_t*)d_work,
-                       work_bytes, d_status, (hipStream_t)stream);
+  return launch_serial(nullptr, 0u, t, (n_streams + kSerWaves - 1) / kSerWaves,
+                       (uint32_t)(((uint64_t)n_buckets + kSerWaves - 1) / kSerWaves), (uint32_t)tiles, n_streams,
+                       (uint8_t*)d_work, work_bytes, d_status, (hipStream_t)stream);
 }
 
-int bs_refcodec_decode_serial_batch(const bs_ref_task* d_tasks, uint32_t n_tasks, uint32_t total_chains,
-                                    uint32_t total_tiles, uint32_t total_streams, void* d_work, uint64_t work_bytes,
-                                    int32_t* d_status, void* stream) {
+uint32_t bs_refcodec_serial_chains_per_group(void) { return kSerWaves; }
+
+int bs_refcodec_decode_serial_batch(const bs_ref_task* d_tasks, uint32_t n_tasks, uint32_t total_se_groups,
+                                    uint32_t total_mant_groups, uint32_t total_tiles, uint32_t total_streams,
+                                    void* d_work, uint64_t work_bytes, int32_t* d_status, void* stream) {
   if (!d_status || (n_tasks && (!d_tasks || !d_work)) || ((uintptr_t)d_work & 255u)) return BS_ERR_ARG;
   if (n_tasks == 0) return BS_OK;
-  if (total_chains == 0 || total_tiles == 0 || total_streams == 0) return BS_ERR_ARG;
+  if (total_se_groups == 0 || total_tiles == 0 || total_streams == 0) return BS_ERR_ARG;
   bs_ref_task dummy{};
-  return launch_serial(d_tasks, n_tasks, dummy, total_chains, total_tiles, total_streams, (uint8_t*)d_work,
-                       work_bytes, d_status, (hipStream_t)stream);
+  return launch_serial(d_tasks, n_tasks, dummy, total_se_groups, total_mant_groups, total_tiles, total_streams,
+                       (uint8_t*)d_work, work_bytes, d_status, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -225,9 +225,14 @@ uint32_t bs_refcodec_serial_tiles(uint64_t n_out, uint32_t n_streams);
 
 /* One tensor of a batched wave-serial launch: the descriptors, tables and
  * output of bs_refcodec_decode_serial, plus where the task sits in the batch.
- * A task's workgroups are consecutive in each of the three grids; across the
- * task array (device memory) chain_begin, tile_begin and stream_begin all
- * ascend, each task starting where the previous one ends. */
+ * The chains run in workgroups of bs_refcodec_serial_chains_per_group()
+ * wavefronts: first every task's SE groups (ceil(n_streams / per group) each,
+ * from se_group_begin), then every task's mantissa-bucket groups
+ * (ceil(n_buckets / per group) each, from mant_group_begin, counted from the
+ * end of the SE groups), so the longest chains start first. A task's
+ * workgroups are consecutive in each grid; across the task array (device
+ * memory) every *_begin ascends, each task starting where the previous one
+ * ends. */
 typedef struct {
     const bs_se_stream *streams;     /* n_streams SE stream descriptors */
     const uint32_t *se_table;        /* 4096 x {f | (slot-cf) << 13, symbol} u32 pairs */
@@ -239,10 +244,15 @@ typedef struct {
     uint64_t work_offset;            /* multiple of 256: the task's bs_refcodec_serial_work_bytes(n_out,
                                         n_streams) bytes of scratch start at d_work + work_offset */
     uint32_t n_streams, n_buckets, n_tables;
-    uint32_t chain_begin;            /* chain grid: n_streams + n_buckets workgroups per task */
+    uint32_t se_group_begin;         /* chain grid, SE part: ceil(n_streams / per group) workgroups */
     uint32_t tile_begin;             /* tile grid: n_streams x bs_refcodec_serial_tiles(n_out, n_streams) */
     uint32_t stream_begin;           /* stream grid: n_streams */
+    uint32_t mant_group_begin;       /* chain grid, mantissa part: ceil(n_buckets / per group) workgroups */
+    uint32_t reserved;
 } bs_ref_task;
+
+/* Wavefronts (chains) per workgroup of the wave-serial chain grid. */
+uint32_t bs_refcodec_serial_chains_per_group(void);
 
 /* Decode every task of d_tasks (a transformer layer's reference-format
  * tensors) with the wave-serial path, all tasks' chains in one launch: the
@@ -253,9 +263,9 @@ typedef struct {
  * per-tensor decode loop of decoder.decompress (bigsmall/decoder.py:128-136)
  * and StreamingLoader.load_layer (bigsmall/streaming.py:218-227) for the
  * formats of bs_refcodec_decode_serial. Asynchronous on `stream`. */
-int bs_refcodec_decode_serial_batch(const bs_ref_task *d_tasks, uint32_t n_tasks, uint32_t total_chains,
-                                    uint32_t total_tiles, uint32_t total_streams, void *d_work,
-                                    uint64_t work_bytes, int32_t *d_status, void *stream);
+int bs_refcodec_decode_serial_batch(const bs_ref_task *d_tasks, uint32_t n_tasks, uint32_t total_se_groups,
+                                    uint32_t total_mant_groups, uint32_t total_tiles, uint32_t total_streams,
+                                    void *d_work, uint64_t work_bytes, int32_t *d_status, void *stream);
 
 /* Host encoders of the same three formats, for compress() with the
  * reference's gpu_optimised (bf16_parallel_v1) and prefer_speed
