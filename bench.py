@@ -212,9 +212,10 @@ def measured_traffic(workload: str):
 
 def _variants(base: np.ndarray, i: int) -> np.ndarray:
     """Per-layer variant of a seeded draw: flip each sign bit with a seeded
-    coin. Same distribution (N(0, s) is symmetric), different data per layer."""
+    coin. Same distribution (N(0, s) is symmetric), different data per layer.
+    Exact zeros stay +0.0, as a pruned layer holds them."""
     flips = np.random.default_rng(1000 + i).integers(0, 2, base.size, dtype=np.uint16) << 15
-    return base ^ flips
+    return base ^ (flips * (base != 0)).astype(np.uint16)
 
 
 def _timed(fn, steps: int, stream):
