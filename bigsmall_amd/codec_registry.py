@@ -23,15 +23,23 @@ enable_a5 / enable_fp2_residual switches.
 
 Differences, by construction of this engine: the default candidates are the
 GPU-native formats (bf16_chunked_v1 / fp8_chunked_v1), and the last resort is
-`raw` instead of zstd (this engine decodes zstd entries but does not write them).
-The reference formats it writes (bf16_parallel_v1, bf16_se_tans,
-bf16_se_single_kernel) are byte-identical to the reference encoder's.
+`raw` instead of zstd. The reference formats it writes (bf16_parallel_v1,
+bf16_se_tans, bf16_se_single_kernel) are byte-identical to the reference
+encoder's.
+
+auto_select_reference_codec picks only codecs the reference itself decodes,
+for containers compress() writes with gpu_optimised or prefer_speed: the same
+speed and GPU rules, measured against bf16_se_tans's size where the reference
+measures against its constriction winner (bf16_se_rans / bf16_se_ac, order-0
+coders of the same sign/exponent and mantissa symbols, which this engine
+cannot write); when no rule picks a faster format it writes bf16_se_tans, and
+every other format as zstd (the last entry of each reference candidate list).
 """
 from __future__ import annotations
 
 from typing import Callable, Optional
 
-from .codecs import bf16_chunked, bf16_parallel, bf16_tans, single_kernel, zstd_gpu
+from .codecs import bf16_chunked, bf16_parallel, bf16_tans, single_kernel, zstd_gpu, zstd_host
 
 _REGISTRY: dict[str, tuple[Callable, Callable]] = {}
 
@@ -73,8 +81,9 @@ register_codec(single_kernel.CODEC, single_kernel.encode, single_kernel.decode)
 register_codec("raw", _enc_raw, _dec_raw)
 
 
-def _enc_zstd_unavailable(raw, **_):
-    raise NotImplementedError("this engine decodes zstd-coded entries; it does not write them")
+def _enc_zstd(raw, **_):
+    """generic.encode_zstd (bigsmall/codecs/generic.py:9-12) through the system libzstd."""
+    return zstd_host.encode_zstd(raw)
 
 
 def _dec_zstd(blob, extras, n_weights):
@@ -83,7 +92,7 @@ def _dec_zstd(blob, extras, n_weights):
     return zstd_gpu.decode_zstd(blob, extras)
 
 
-register_codec("zstd", _enc_zstd_unavailable, _dec_zstd)
+register_codec("zstd", _enc_zstd, _dec_zstd)
 
 # Per-format ordered candidates. fp32/fp16 have no GPU codec here: they are
 # stored raw (the reference's constriction codecs for them are not available).
@@ -148,6 +157,34 @@ def auto_select_codec(raw: bytes, fmt: str, dtype: str, tensor_name: str = "", s
     if best is None:
         return bytes(raw), "raw", {"n_bytes": len(raw)}
     return best
+
+
+def auto_select_reference_codec(raw: bytes, fmt: str, enable_gpu_parallel: bool = False,
+                                gpu_parallel_n_streams: int = 128, gpu_parallel_tolerance: float = 0.01,
+                                prefer_speed: bool = False, prefer_speed_tolerance: float = 0.0015,
+                                **_ignored) -> tuple[bytes, str, dict]:
+    """(blob, codec name, extras) among the codecs the reference decodes, by the
+    rules of codec_registry.py:316-349 (prefer_speed) and :377-391 (GPU
+    parallel), applied in that order to a running best. prefer_speed's second
+    rule (bf16_se_tans within a tolerance of the best) holds by construction:
+    bf16_se_tans is the starting best."""
+    if fmt == "bf16":
+        best = _try("bf16_se_tans", raw)   # the stand-in for the reference's smallest candidate
+        if best is not None:
+            best = (best[0], "bf16_se_tans", best[1])
+            if prefer_speed:
+                sk = _try("bf16_se_single_kernel", raw)
+                if sk is not None and len(sk[0]) <= len(best[0]) + max(4096, int(len(raw) * 0.006)):
+                    best = (sk[0], "bf16_se_single_kernel", sk[1])
+            if enable_gpu_parallel:
+                par = _try("bf16_parallel_v1", raw, n_streams=gpu_parallel_n_streams)
+                if par is not None and len(par[0]) <= int(len(best[0]) * (1.0 + gpu_parallel_tolerance)):
+                    best = (par[0], "bf16_parallel_v1", par[1])
+            return best
+    z = _try("zstd", raw)
+    if z is not None:
+        return z[0], "zstd", z[1]
+    return bytes(raw), "raw", {"n_bytes": len(raw)}
 
 
 class CodecStats:

@@ -9,10 +9,19 @@ before codec selection:
     item size, at least 1024 bytes, becomes `tied_ref` (tensor_analysis.py:97-110);
   * tiny: fewer than RAW_TINY_THRESHOLD bytes are stored `raw` (encoder.py:57, 386-388);
   * everything else goes through codec_registry.auto_select_codec.
-The codecs are bf16_chunked_v1 / fp8_chunked_v1 (GPU-decodable); the
-reference's `lowcard` (zstd) route for tensors with <= 16 distinct values is
-covered by bf16_chunked_v1's exact-value mode, which codes up to 256 distinct
-values per tensor and decodes on the GPU.
+By default the codecs are bf16_chunked_v1 / fp8_chunked_v1 (GPU-native); the
+reference's `lowcard` route for tensors with <= 16 distinct values is covered
+by bf16_chunked_v1's exact-value mode, which codes up to 256 distinct values
+per tensor and decodes in the same launch as its layer.
+With gpu_optimised or prefer_speed the container holds only codecs the
+reference decodes, routed as the reference routes them (encoder.py:140-189):
+lowcard tensors (tensor_analysis.py:111-119) become `special` entries
+(special.py:23-64, zstd through the system libzstd), bf16 tensors take
+bf16_parallel_v1 / bf16_se_single_kernel / bf16_se_tans by
+codec_registry.auto_select_reference_codec, anything else `zstd`. The
+reference's wpe_delta route (blosc2, not installed here) is not taken: such
+tensors go through the generic selection, as the reference's own encoder does
+when that codec fails.
 Blobs start on 256-byte boundaries of the data section (offsets are explicit
 in the header, so any reader finds them).
 """
@@ -25,6 +34,7 @@ from typing import Optional
 import numpy as np
 
 from . import codec_registry, container, formats
+from .codecs import zstd_host
 
 RAW_TINY_THRESHOLD = 512
 TIE_MIN_BYTES = 1024
@@ -74,8 +84,9 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
     """Compress a safetensors file (or a {name: torch.Tensor} dict) into a .bs container
     (bigsmall/encoder.py:325-496). gpu_optimised and prefer_speed select the
     reference's bf16_parallel_v1 / bf16_se_single_kernel / bf16_se_tans by its
-    rules (codec_registry.auto_select_codec); `workers` is accepted for the
-    reference's signature (the host encoders here thread internally)."""
+    rules and write a container the reference itself reads (every entry in one
+    of its codecs); `workers` is accepted for the reference's signature (the
+    host encoders here thread internally)."""
     tensors, st_meta = _gather(src)
     if exclude_names:
         tensors = [t for t in tensors if t["name"] not in exclude_names]
@@ -85,6 +96,7 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
             counts[t["fmt"]] = counts.get(t["fmt"], 0) + 1
     dominant = max(counts, key=counts.get) if counts else "bf16"
 
+    reference_readable = gpu_optimised or prefer_speed
     data = container.DataSectionBuilder()
     stats = codec_registry.CodecStats()
     seen: dict[tuple, int] = {}
@@ -106,7 +118,19 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
         else:
             if len(raw) >= TIE_MIN_BYTES:
                 seen[key] = i
-            if steps is not None and t["fmt"] == "bf16":
+            lowcard = reference_readable and zstd_host.is_lowcard(raw, t["item_bytes"])
+            if lowcard:
+                try:
+                    blob, extras = zstd_host.encode_lowcard(raw, t["item_bytes"])
+                    blob, codec, extras, special = blob, "special", {**extras, "special_kind": "lowcard"}, "lowcard"
+                except (ValueError, RuntimeError):
+                    lowcard = False                     # the generic selection, as the reference falls back
+            if lowcard:
+                pass
+            elif reference_readable:
+                blob, codec, extras = codec_registry.auto_select_reference_codec(
+                    raw, t["fmt"], enable_gpu_parallel=gpu_optimised, prefer_speed=prefer_speed)
+            elif steps is not None and t["fmt"] == "bf16":
                 from .codecs import bf16_chunked
                 blob, extras = bf16_chunked.encode(raw, steps=steps)
                 codec = bf16_chunked.CODEC_BF16
@@ -114,6 +138,8 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
                 blob, codec, extras = codec_registry.auto_select_codec(
                     raw, t["fmt"], t["dtype"], t["name"], tuple(t["shape"]), t["item_bytes"], enable_a5=enable_a5,
                     enable_gpu_parallel=gpu_optimised, prefer_speed=prefer_speed)
+            if codec == "bf16_parallel_v1":
+                special = "gpu_parallel"                # the reference's label (encoder.py:185-186)
         off = data.add(blob)
         header_tensors.append({"name": t["name"], "shape": t["shape"], "dtype": t["dtype"], "codec": codec,
                                "special": special, "compressed_bytes": len(blob), "offset": off, "md5": md5,

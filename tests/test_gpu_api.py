@@ -515,19 +515,28 @@ def test_streaming_gpt2(tmp_path, dtype, prefetch):
 def test_compress_reference_formats_round_trip(tmp_path, kw):
     """Containers compress() writes with the reference's gpu_optimised /
     prefer_speed choices (bf16_parallel_v1, bf16_se_single_kernel or
-    bf16_se_tans, by the reference's rules) load bit-exactly on the GPU, one
-    batched wave-serial launch per layer."""
+    bf16_se_tans, by the reference's rules; lowcard tensors as `special`,
+    other formats as `zstd`: only codecs the reference decodes) load
+    bit-exactly on the GPU, one batched wave-serial launch per layer plus the
+    GPU zstd decoder for the special and zstd entries."""
     from bigsmall_amd import decoder
     g = torch.Generator().manual_seed(12)
     src = {f"model.layers.{i}.mlp.{n}.weight": (torch.randn(2048, 2048 + 64 * i, generator=g) * 0.02).bfloat16()
            for i in range(2) for n in ("up_proj", "down_proj")}
     src["model.norm.weight"] = (1 + torch.randn(1024, generator=g) * 0.01).bfloat16()
+    src["model.layers.0.attn.bias"] = torch.tril(torch.ones(128, 128)).bfloat16()
+    src["model.layers.0.scale.f32"] = torch.randn(3000, generator=g)
+    src["model.layers.0.ids"] = torch.arange(500, dtype=torch.int64)
     p = tmp_path / "ref_formats.bs"
     compress(src, p, **kw)
     header, _ = container.read_header(p)
-    codecs = {t["codec"] for t in header["tensors"]}
+    by = {t["name"]: t["codec"] for t in header["tensors"]}
+    codecs = set(by.values())
     _say(f"[api] compress({kw}) codecs {sorted(codecs)}")
     assert codecs & {"bf16_parallel_v1", "bf16_se_single_kernel", "bf16_se_tans"}
+    assert codecs <= {"bf16_parallel_v1", "bf16_se_single_kernel", "bf16_se_tans", "special", "zstd", "raw",
+                      "tied_ref"}
+    assert by["model.norm.weight"] == "special" and by["model.layers.0.ids"] == "zstd"
     out = decoder.load(p)
     for k, v in src.items():
         assert _bytes(out[k]) == _bytes(v), k
