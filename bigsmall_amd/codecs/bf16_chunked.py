@@ -1,9 +1,13 @@
 """`bf16_chunked_v1` / `fp8_chunked_v1`: the engine's GPU-native codec.
 
-A tensor is cut into chunks of 64 x `steps` elements. Each chunk is 64
-interleaved rANS streams (one per wavefront lane) over the tensor's exponent
-(or exact-value) symbols, sharing one 16-bit renormalisation word stream, plus
-a plane of raw sign|mantissa bytes. The blob layout is documented in
+A tensor is cut into chunks of `lanes` x `steps` elements (128 x 448 by
+default). Each chunk is `lanes` interleaved rANS states (lanes / 64 per
+wavefront lane) over the tensor's exponent (or exact-value) symbols, sharing
+one 16-bit renormalisation word stream, plus raw sign|mantissa bytes. Full
+chunks own 512-element units of the tensor interleaved across all of them
+(chunk c: units c, nf + c, 2 nf + c, ...), so the chunks a launch decodes side
+by side write neighbouring addresses; their dense planes are interleaved the
+same way in one region of the blob. The blob layout is documented in
 bigsmall_amd/csrc/bsck_decode.hip.
 
 Plugin shape of the reference codec API (bigsmall/codec_registry.py:39-42):

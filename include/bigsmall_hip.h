@@ -60,7 +60,7 @@ typedef struct {
     uint64_t n;          /* elements */
     uint32_t n_chunks;
     uint32_t steps;      /* rANS steps per lane per full chunk */
-    uint32_t lanes;      /* interleaved rANS states per chunk (64 or 128) */
+    uint32_t lanes;      /* interleaved rANS states per chunk (64, 128 or 256) */
     uint32_t n_syms;
     uint32_t elem_bytes; /* 2 = bf16 words, 1 = bytes (fp8) */
     uint32_t plane_mode; /* 0 none, 1 dense, 2 compact */
