@@ -155,6 +155,14 @@ __device__ __forceinline__ void consume(const uint32_t (&v)[K]) {
 
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
 
+// The builtin returns int: each half goes through uint32_t so that the low
+// half is zero-extended (a plain cast would copy its bit 31 into the high half).
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l);
+  return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
 __device__ __forceinline__ void report(int32_t* status, int32_t bits) {
   if (__lane_id() == 0) atomicOr(status, bits);
 }
@@ -643,18 +651,39 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   LDS uint32_t* s_val = s_cum + 260;                    // 256 entries
   LDS uint32_t* s_flag = s_val + 256;                   // table-check flag
 
-  // ---- which tensor does this workgroup serve (wave-uniform binary search)
+  // ---- which tensor does this workgroup serve. The prologue is a chain of
+  // dependent global loads (task, header and symbols, chunk entry, states),
+  // each a full memory latency at launch, so it is kept short: up to 64 tasks
+  // are read one per lane in a single load and the task found by a ballot
+  // (wg_begin ascends, so the tasks starting at or before this workgroup are
+  // a prefix); more tasks take a binary search.
   bs_chunk_task T = single;
   if (tasks != nullptr) {
-    uint32_t lo = 0, hi = n_tasks;
-    while (hi - lo > 1) {
-      uint32_t mid = (lo + hi) >> 1;
-      if (tasks[mid].wg_begin <= blockIdx.x) lo = mid; else hi = mid;
+    if (n_tasks <= (uint32_t)kWave) {
+      const uint32_t l = __lane_id();
+      const bs_chunk_task mine = l < n_tasks ? tasks[l] : bs_chunk_task{};
+      const uint64_t before = __ballot(l < n_tasks && mine.wg_begin <= blockIdx.x);
+      const uint32_t lo = before ? (uint32_t)__popcll(before) - 1u : 0u;
+      T.blob = (const uint8_t*)readlane64((uint64_t)mine.blob, lo);
+      T.blob_bytes = readlane64(mine.blob_bytes, lo);
+      T.out = (void*)readlane64((uint64_t)mine.out, lo);
+      T.n = readlane64(mine.n, lo);
+      T.wg_begin = __builtin_amdgcn_readlane(mine.wg_begin, lo);
+      T.n_chunks = __builtin_amdgcn_readlane(mine.n_chunks, lo);
+    } else {
+      uint32_t lo = 0, hi = n_tasks;
+      while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (tasks[mid].wg_begin <= blockIdx.x) lo = mid; else hi = mid;
+      }
+      T = tasks[lo];
     }
-    T = tasks[lo];
   }
   const uint32_t group = blockIdx.x - T.wg_begin;
   const GLB uint8_t* __restrict__ b = (const GLB uint8_t*)T.blob;
+  const uint32_t tid = threadIdx.x;
+  // the symbol entries load beside the header (both need only the blob address)
+  const uint32_t ent = tid < 256 && 36ull + 4ull * tid <= T.blob_bytes ? ld_u32(b + 32 + 4 * tid) : 0u;
 
   // ---- header checks (uniform across the workgroup)
   if (T.blob_bytes < 32 || b[0] != 'B' || b[1] != 'S' || b[2] != 'C' || b[3] != 'K' || b[4] != kVersion ||
@@ -688,12 +717,23 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   }
   const bool fast = eb == 2 && mode == 1;
 
+  // this wave's chunk-table entry, requested before the table build so that
+  // its latency passes under it (the build's barriers wait for LDS only)
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform: keeps chunk state scalar
+  const uint32_t chunk = group * kWaves + wave;
+  uint64_t off = 0;
+  uint32_t nw = 0, np = 0;
+  if (chunk < nch) {                                   // wave-uniform; the entry lies inside the checked table
+    const GLB uint8_t* ce = b + ctab + 16ull * chunk;
+    off = (uint64_t)ld_u32(ce) | ((uint64_t)ld_u32(ce + 4) << 32);
+    nw = ld_u32(ce + 8);
+    np = ld_u32(ce + 12);
+  }
+
   // ---- decode table in LDS (layouts in the file comment)
-  const uint32_t tid = threadIdx.x;
   uint32_t f_own = 0;
   bool bad_sym = false;
   if (tid < nsym) {
-    const uint32_t ent = ld_u32(b + 32 + 4 * tid);
     f_own = (ent >> 16) & 0x1FFFu;
     s_val[tid] = (ent & 0xFFFFu) | (ent & 0x80000000u);
     // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each
@@ -734,12 +774,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   __syncthreads();
 
   // ---- one chunk per wavefront
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform: keeps chunk state scalar
-  const uint32_t chunk = group * kWaves + wave;
   if (chunk >= nch) return;
-  const GLB uint8_t* ce = b + ctab + 16ull * chunk;
-  const uint64_t off = (uint64_t)ld_u32(ce) | ((uint64_t)ld_u32(ce + 4) << 32);
-  const uint32_t nw = ld_u32(ce + 8), np = ld_u32(ce + 12);
   const uint64_t cbase_idx = (uint64_t)chunk * per;     // the partial chunk's first element (nf * per)
   const bool full = chunk < nf;
   const uint32_t nc = full ? (uint32_t)per : (uint32_t)(n - cbase_idx);

@@ -308,10 +308,11 @@ inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t m, uint32_t acc) {
   return acc + __builtin_popcount(m & (l <= 32 ? 0u : ((1u << (l - 32)) - 1u)));
 }
 // readfirstlane is only applied to wave-uniform values here, so every lane's
-// copy is the first lane's; readlane exchanges through the wave.
-inline uint32_t __builtin_amdgcn_readfirstlane(uint32_t x) { return x; }
-inline uint32_t __builtin_amdgcn_readlane(uint32_t x, uint32_t lane) {
-  return (uint32_t)bs_simt::exchange(x, [lane](bs_simt::Wave& w) { return w.slot[lane & 63]; });
+// copy is the first lane's; readlane exchanges through the wave. Both return
+// int, as the GPU builtins do, so that a widening cast sign-extends here too.
+inline int __builtin_amdgcn_readfirstlane(int x) { return x; }
+inline int __builtin_amdgcn_readlane(int x, int lane) {
+  return (int)(uint32_t)bs_simt::exchange((uint32_t)x, [lane](bs_simt::Wave& w) { return w.slot[lane & 63]; });
 }
 inline void __builtin_amdgcn_wave_barrier() { bs_simt::ctx().wave->bar.arrive_and_wait(); }
 inline void __builtin_amdgcn_fence(int, const char*) {}

@@ -10,11 +10,14 @@
 // bytes with a zero status word; corrupted cases may decode to anything or
 // report a status, but every access must stay inside its buffers, which
 // are allocated at their exact sizes so that the sanitizer sees any overrun.
-// Prints one summary line; exit status 0 when every clean case decoded right.
+// The clean BSCK blobs are then decoded again in batched launches.
+// Prints a batch line and a summary line; exit status 0 when every clean
+// case decoded right, alone and batched.
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/mman.h>
 
 #include <vector>
 
@@ -63,6 +66,35 @@ struct Buf {
   Buf(const Buf&) = delete;
 };
 
+// Buffers for the batched launches, carved from one mapping that straddles
+// an address whose low 32 bits cross 2^31: the first buffers have bit 31 of
+// the low half clear, the later ones set. A 4 GiB + n reservation always
+// holds such an address; only the n bytes around it are made accessible.
+struct Pool {
+  uint8_t* res = nullptr;
+  uint8_t* base = nullptr;
+  uint64_t res_size = 0, size = 0, used = 0;
+  explicit Pool(uint64_t n) : size(n) {
+    res_size = (4ull << 30) + 2 * n;
+    void* m = mmap(nullptr, res_size, PROT_NONE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+    if (m == MAP_FAILED) exit(4);
+    res = (uint8_t*)m;
+    const uintptr_t lo = (uintptr_t)res + n;                       // room below the crossing
+    const uintptr_t cross = (lo & ~0xFFFFFFFFull) | 0x80000000ull;
+    const uintptr_t at = (cross >= lo ? cross : cross + (1ull << 32)) - (256u << 10);   // 256 KiB below it
+    base = (uint8_t*)at;
+    if (mprotect(base, n, PROT_READ | PROT_WRITE) != 0) exit(4);
+  }
+  ~Pool() { munmap(res, res_size); }
+  uint8_t* take(uint64_t n) {
+    used = (used + 255) & ~255ull;
+    if (used + n > size) exit(4);
+    uint8_t* r = base + used;
+    used += n ? n : 1;
+    return r;
+  }
+};
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -78,6 +110,12 @@ int main(int argc, char** argv) {
   if (r.get<uint32_t>() != 0x5A465342u) return 2;   // "BSFZ"
   const uint32_t n_cases = r.get<uint32_t>();
   uint64_t clean_ok = 0, clean_bad = 0, refused_host = 0, flagged = 0, decoded = 0;
+  struct Clean {
+    std::vector<uint8_t> blob, want;
+    uint64_t n;
+    uint32_t eb;
+  };
+  std::vector<Clean> clean_bsck;   // decoded again together, through the batched entry point
   for (uint32_t c = 0; c < n_cases; ++c) {
     const uint8_t kind = r.get<uint8_t>(), clean = r.get<uint8_t>();
     r.get<uint16_t>();
@@ -127,6 +165,9 @@ int main(int argc, char** argv) {
       }
     }
     const uint8_t* want = clean ? r.take(n_out * eb) : nullptr;
+    if (clean && kind == 0)
+      clean_bsck.push_back({std::vector<uint8_t>(blob_src, blob_src + blob_len),
+                            std::vector<uint8_t>(want, want + n_out * eb), n_out, eb});
     if (clean) {
       if (rc == BS_OK && status == 0 && memcmp(out.p, want, n_out * eb) == 0) {
         ++clean_ok;
@@ -143,6 +184,52 @@ int main(int argc, char** argv) {
       ++decoded;
     }
   }
+  // Batched launches of the clean BSCK blobs: once as they are (up to 64
+  // tasks, which a workgroup finds by a wavefront vote) and once five times
+  // over (more than 64, found by binary search). Some buffers sit at
+  // addresses with bit 31 of the low half set, so a lookup that widened that
+  // half with sign extension would decode from a wrong address.
+  uint64_t batch_ok = 0, batch_bad = 0, high_bit = 0;
+  for (const int reps : {1, 5}) {
+    const size_t nt = clean_bsck.size() * reps;
+    if (nt == 0) break;
+    Pool pool(64ull << 20);
+    std::vector<uint8_t*> blobs, outs;
+    std::vector<bs_chunk_task> tasks(nt);
+    uint32_t groups = 0, max_mode = 0;
+    const uint32_t per_group = (uint32_t)bs_chunk_chunks_per_group();
+    for (size_t t = 0; t < nt; ++t) {
+      const Clean& c = clean_bsck[t % clean_bsck.size()];
+      blobs.push_back(pool.take(c.blob.size()));
+      memcpy(blobs.back(), c.blob.data(), c.blob.size());
+      outs.push_back(pool.take(c.n * c.eb));
+      memset(outs.back(), 0x5A, c.n * c.eb);
+      bs_chunk_info info;
+      if (bs_chunk_inspect(blobs.back(), c.blob.size(), &info) != BS_OK) return 5;
+      tasks[t] = bs_chunk_task{blobs.back(), c.blob.size(), outs.back(), c.n, groups, info.n_chunks};
+      groups += (info.n_chunks + per_group - 1) / per_group;
+      if (info.plane_mode > max_mode) max_mode = info.plane_mode;
+      high_bit += (((uintptr_t)blobs.back() >> 31) & 1u) + (((uintptr_t)outs.back() >> 31) & 1u);
+    }
+    Buf d_tasks(nt * sizeof(bs_chunk_task));
+    memcpy(d_tasks.p, tasks.data(), nt * sizeof(bs_chunk_task));
+    int32_t status = 0;
+    const int rc = bs_chunk_decode_batch((const bs_chunk_task*)d_tasks.p, (uint32_t)nt, groups, max_mode, &status,
+                                         nullptr);
+    for (size_t t = 0; t < nt; ++t) {
+      const Clean& c = clean_bsck[t % clean_bsck.size()];
+      if (rc == BS_OK && status == 0 && memcmp(outs[t], c.want.data(), c.n * c.eb) == 0) {
+        ++batch_ok;
+      } else {
+        ++batch_bad;
+        ++clean_bad;
+        fprintf(stderr, "batch of %zu, task %zu (n %llu): rc %d status 0x%x\n", nt, t, (unsigned long long)c.n, rc,
+                status);
+      }
+    }
+  }
+  printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu\n", (unsigned long long)batch_ok,
+         (unsigned long long)batch_bad, (unsigned long long)high_bit);
   printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu\n", n_cases,
          (unsigned long long)clean_ok, (unsigned long long)clean_bad, (unsigned long long)refused_host,
          (unsigned long long)flagged, (unsigned long long)decoded);

@@ -15,9 +15,12 @@ blob goes to the kernels with the descriptors the library's own host parser
 makes from it, whenever that parser accepts it. Every access stays inside its
 buffer, or the sanitizer fails the run. The same corruption sweeps run on the
 GPU in smaller numbers (tests/test_gpu_bsck.py, tests/test_gpu_refcodecs.py).
+The clean BSCK blobs are also decoded together in batched launches of up to
+64 tasks and of more, the two ways a workgroup finds its task.
 """
 from __future__ import annotations
 
+import re
 import shutil
 import struct
 import subprocess
@@ -163,9 +166,12 @@ def test_decode_kernels_under_sanitizers(tmp_path):
                        env={"ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1", "UBSAN_OPTIONS": "print_stacktrace=1"})
     print(counts, r.stdout, r.stderr[-3000:])
     assert r.returncode == 0, r.stdout + r.stderr[-3000:]
-    line = r.stdout.strip().splitlines()[-1]
+    batch, line = r.stdout.strip().splitlines()[-2:]
     assert "clean failed 0" in line, line
     assert counts["bsck_corrupt"] + counts["ref_corrupt"] >= 5000
+    # every clean BSCK blob decoded in both batched launches, some from addresses with bit 31 set
+    ok, failed, high = (int(v) for v in re.findall(r"\d+", batch.replace("bit 31", "")))
+    assert ok == 6 * counts["bsck_clean"] and failed == 0 and high > 0, batch
 
 
 @pytest.mark.skipif(not Path(CLANG).exists() or shutil.which("make") is None, reason="needs ROCm's clang++")
