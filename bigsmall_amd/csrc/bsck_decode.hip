@@ -93,9 +93,9 @@ constexpr uint32_t kPMirror = 64;         // compact plane-ring bytes [0, 64) li
 constexpr uint32_t kRingBytes = (1024 + kMirror) * 2 + 2048 + kPMirror + 16;
 static_assert(kRingBytes >= (2048 + kMirror) * 2, "ring area");
 constexpr uint32_t kL = 1u << 16;
-// s_waitcnt immediate for gfx9: vmcnt(4), expcnt and lgkmcnt not waited on
+// s_waitcnt immediate for gfx9: vmcnt(n), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
-constexpr int kWaitVm4 = 4 | (7 << 4) | (15 << 8);
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 // dynamic LDS layout (bytes): decode table | per-wave ring areas | per-wave output staging
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
@@ -300,6 +300,32 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
   }
 }
 
+// Full chunks of bf16 elements with K >= 2 store each step's outputs straight
+// from registers: a step's 64*K elements are contiguous in the output (a
+// quarter or half of a 512-element unit), so every lane writes its K adjacent
+// words (4 or 8 bytes) and the wavefront writes 256 or 512 contiguous bytes,
+// whole cache lines, with no LDS staging. Byte tensors, K = 1 and the partial
+// chunk stage their outputs in LDS and store whole half blocks.
+template <int K, int EB, bool PARTIAL>
+constexpr bool direct_stores() { return !PARTIAL && EB == 2 && K >= 2; }
+
+// Output stores a chunk issues per pair of blocks (the pipeline's wait counts).
+template <int K, int MODE, int EB, bool PARTIAL>
+constexpr int stores_per_pair() { return direct_stores<K, EB, PARTIAL>() ? 2 * Geo<K, MODE>::kBlock : 4; }
+
+// Store step q of block blk (KB steps per block): lane l's K words go to
+// chunk elements t*64K + l*K .. +K-1, t = blk*KB + q, which lie in 512-element
+// unit t*K/8 at offset (t*K % 8)*64.
+template <int K, int KB>
+__device__ __forceinline__ void store_step(const ChunkParams& C, uint32_t blk, int q, uint32_t v0, uint32_t v1) {
+  static_assert((KB * K) % 8 == 0, "a block is whole units");
+  const uint32_t unit = blk * (uint32_t)(KB * K / 8) + (uint32_t)(q * K / 8);   // wave-uniform
+  GLB uint8_t* p = C.out8 + ((uint64_t)unit * C.ustride + C.ubase) * 2u + (uint32_t)((q * K) % 8) * 128u +
+                   C.lane * (2u * K);
+  if (K == 2) __builtin_nontemporal_store(v0, (GLB uint32_t*)p);
+  else __builtin_nontemporal_store((uint64_t)v0 | ((uint64_t)v1 << 32), (GLB uint64_t*)p);
+}
+
 // One step of the K states of every lane. Phased so the K dependency chains of
 // a lane overlap: K table reads, then the K state updates with their ballots,
 // then the K ring reads (one wait for all), then the renormalisations.
@@ -446,12 +472,13 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
   constexpr int kHalf = kBlock / 2;
   constexpr bool DENSE = MODE == 1 && EB == 2;
   constexpr bool FAST = DENSE || EB == 1;               // mad24 table layouts
+  constexpr bool DIRECT = direct_stores<K, EB, PARTIAL>();
   const uint32_t lane = C.lane;
 #pragma unroll
   for (int q = 0; q < kBlock; ++q) {
     const uint32_t t = blk * kBlock + q;
     if (PARTIAL && t >= C.nsteps) break;                 // wave-uniform
-    if (q == kHalf) {                                    // first half of the block is staged: store it
+    if (!DIRECT && q == kHalf) {                         // first half of the block is staged: store it
       wave_sync();
       flush_half<K, EB, PARTIAL, kHalf>(2 * blk, C, stage);
     }
@@ -474,9 +501,13 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
           const uint32_t ex = __builtin_amdgcn_perm(d[(2 * h + 1) % K], d[(2 * h) % K], 0x070C030Cu) >> 1;
           v[h] = (dup & 0x807F807Fu) | ex;
         }
-        LDS uint8_t* dst = stage + qs * (kStates * 2) + lane * (2u * K);
-        if (K == 2) *(LDS uint32_t*)dst = v[0];
-        else *(LDS uint64_t*)dst = (uint64_t)v[0] | ((uint64_t)v[kPairs - 1] << 32);
+        if (DIRECT) {
+          store_step<K, kBlock>(C, blk, q, v[0], v[kPairs - 1]);
+        } else {
+          LDS uint8_t* dst = stage + qs * (kStates * 2) + lane * (2u * K);
+          if (K == 2) *(LDS uint32_t*)dst = v[0];
+          else *(LDS uint64_t*)dst = (uint64_t)v[0] | ((uint64_t)v[kPairs - 1] << 32);
+        }
       } else {
         const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
         const uint32_t v = (dup & 0x807Fu) | (d[0] >> 17);
@@ -485,7 +516,10 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     } else {
       // the lane's K outputs of this step are adjacent: one LDS store
       LDS uint8_t* dst = stage + (qs * kStates + lane * K) * EB;
-      if (EB == 2) {
+      if (DIRECT) {
+        store_step<K, kBlock>(C, blk, q, __builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u),
+                              __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u));
+      } else if (EB == 2) {
         if (K == 1) *(LDS uint16_t*)dst = (uint16_t)d[0];
         else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], 0x05040100u);
         else *(LDS uint64_t*)dst = (uint64_t)__builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u) |
@@ -498,7 +532,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
       }
     }
   }
-  if (!PARTIAL) {
+  if (!PARTIAL && !DIRECT) {
     wave_sync();
     flush_half<K, EB, PARTIAL, kHalf>(2 * blk + 1, C, stage);
   }
@@ -577,11 +611,11 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     blk += 2;
     if (blk >= C.nblk) break;
     if (!PARTIAL) {
-      // The pair's loads were followed by its four output stores: vmcnt(4)
+      // The pair's loads were followed by its output stores: vmcnt(stores)
       // lands the loads and leaves the stores in flight. Stating it gives the
       // compiler's wait-count tracking an exact state here; the uses below
       // keep its own waits for these registers at this point.
-      __builtin_amdgcn_s_waitcnt(kWaitVm4);
+      __builtin_amdgcn_s_waitcnt(wait_vm(stores_per_pair<K, MODE, EB, PARTIAL>()));
       if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
       BS_KEEP2(F.w[0].x, F.w[1].x);
       if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
