@@ -634,8 +634,8 @@ def run_c3(args) -> dict:
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
     res = {}
-    # the format's default chunk (448 steps: sized for layer batches) gives one
-    # 67M-element tensor 1,171 chunks, fewer than the 4,096 wavefront slots of
+    # the format's default chunk (432 steps: sized for layer batches) gives one
+    # 67M-element tensor 1,214 chunks, fewer than the 4,096 wavefront slots of
     # the GPU; 128 steps fill them (4,096 chunks) at a small ratio cost
     steps = args.chunk_steps or 128
     R = max(1, args.rotate)

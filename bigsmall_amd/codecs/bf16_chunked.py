@@ -30,12 +30,15 @@ from ..device import (ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, re
 
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
-# 448 steps x 128 states = 57,344 elements per chunk: a 14336x4096 matrix is
-# 1024 chunks (128 full 8-wave workgroups) and a Llama-3-8B-shaped layer fits
-# in one round of 480 workgroups on 256 CUs (two per CU). Measured on MI355X:
-# 0.175 ms/layer vs 0.184 at 512 steps; the ratio cost of the shorter chunks
-# is +0.05 pp (one 32-bit initial state per 448 elements).
-DEFAULT_STEPS = 448
+# 432 steps x 128 states = 55,296 elements per chunk: a Llama-3-8B-shaped
+# layer is 3,948 chunks in 497 eight-wave workgroups, one dispatch round of
+# the 512 workgroup slots of 256 CUs (two per CU), with 15 CUs holding one
+# workgroup (32 at 448 steps; 416 steps need 516 workgroups, four of them in
+# a second round). Measured
+# on MI355X with the decoder's progress priority: 151.1 us per layer against
+# 154.9 us at 448 steps; the ratio cost is +0.013 pp (one 32-bit initial
+# state per 432 elements).
+DEFAULT_STEPS = 432
 DEFAULT_LANES = 128
 MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT = -1, 0, 1, 2
 

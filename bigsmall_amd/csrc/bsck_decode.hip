@@ -538,6 +538,21 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
   }
 }
 
+// A wavefront's issue priority falls as its chunk progresses: 3 in the first
+// quarter of its blocks, then 2, 1 and 0. The SIMD arbiter otherwise favours
+// the oldest waves, so the first of a CU's two workgroups ran ahead and the
+// CU's last 20-30 us ran the second one alone, at lower throughput; with the
+// priority the waves that are behind issue first and the chunks of a CU end
+// closer together (Llama-3-8B-shaped layer: 157.4 -> 154.9 us per launch).
+// Partial chunks, which have fewer blocks, lower their priority sooner.
+__device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk) {
+  const uint32_t quarter = (blk * 4u) / nblk;            // wave-uniform
+  if (quarter == 0) __builtin_amdgcn_s_setprio(3);
+  else if (quarter == 1) __builtin_amdgcn_s_setprio(2);
+  else if (quarter == 2) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Decode one chunk with one wavefront: K interleaved states per lane, MODE =
 // plane mode, EB = element bytes, PARTIAL = chunk may be shorter than
 // 64*K*steps (the tensor's last chunk).
@@ -589,6 +604,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
   for (uint32_t blk = 0;;) {
+    progress_priority(blk, C.nblk);
     // ---- pair start: land the previous pair's loads, issue the next pair's
     const PlaneRegs<K> cur0 = F.pl[0], cur1 = F.pl[1];
     land_segments<K, MODE>(S, F, wring, pring, C.lane);

@@ -315,6 +315,7 @@ inline int __builtin_amdgcn_readlane(int x, int lane) {
   return (int)(uint32_t)bs_simt::exchange((uint32_t)x, [lane](bs_simt::Wave& w) { return w.slot[lane & 63]; });
 }
 inline void __builtin_amdgcn_wave_barrier() { bs_simt::ctx().wave->bar.arrive_and_wait(); }
+inline void __builtin_amdgcn_s_setprio(int) {}   // issue priority: no effect on results
 inline void __builtin_amdgcn_fence(int, const char*) {}
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 // v_perm_b32: byte i of the result is selected by byte i of sel from the
