@@ -697,8 +697,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
   LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWaves * kRingBytes);
   // table-build scratch overlaps the staging area (unused until decoding starts)
-  LDS uint32_t* s_cum = (LDS uint32_t*)s_stage;        // 257 entries
-  LDS uint32_t* s_val = s_cum + 260;                    // 256 entries
+  LDS uint32_t* s_cum = (LDS uint32_t*)s_stage + 3;    // 257 entries; s_cum + 1 is 16-byte aligned
+  LDS uint32_t* s_val = s_cum + 257;                    // 256 entries, 16-byte aligned
   LDS uint32_t* s_flag = s_val + 256;                   // table-check flag
 
   // ---- which tensor does this workgroup serve. The prologue is a chain of
@@ -732,8 +732,19 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t group = blockIdx.x - T.wg_begin;
   const GLB uint8_t* __restrict__ b = (const GLB uint8_t*)T.blob;
   const uint32_t tid = threadIdx.x;
-  // the symbol entries load beside the header (both need only the blob address)
-  const uint32_t ent = tid < 256 && 36ull + 4ull * tid <= T.blob_bytes ? ld_u32(b + 32 + 4 * tid) : 0u;
+  // the symbol entries load beside the header (both need only the blob
+  // address): wavefront 0, lane l entries 4l..4l+3 in one 16-byte load
+  u32x4 ent4 = {0u, 0u, 0u, 0u};
+  if (tid < (uint32_t)kWave) {
+    const uint64_t at = 32ull + 16ull * tid;
+    if (at + 16u <= T.blob_bytes) {
+      ent4 = *(const GLB u32x4*)(b + at);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (at + 4u * i + 4u <= T.blob_bytes) ent4[i] = ld_u32(b + at + 4u * i);
+    }
+  }
 
   // ---- header checks (uniform across the workgroup)
   if (T.blob_bytes < 32 || b[0] != 'B' || b[1] != 'S' || b[2] != 'C' || b[3] != 'K' || b[4] != kVersion ||
@@ -780,45 +791,78 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     np = ld_u32(ce + 12);
   }
 
-  // ---- decode table in LDS (layouts in the file comment)
-  uint32_t f_own = 0;
-  bool bad_sym = false;
-  if (tid < nsym) {
-    f_own = (ent >> 16) & 0x1FFFu;
-    s_val[tid] = (ent & 0xFFFFu) | (ent & 0x80000000u);
-    // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each
-    bad_sym = f_own == 0 || (fast && ((ent & 0x807Fu) != 0 || (ent >> 31) == 0));
+  // ---- decode table in LDS (layouts in the file comment). Wavefront 0
+  // checks the symbol entries and writes their values and the inclusive
+  // prefix of their frequencies (each lane sums its four, a shuffle scan over
+  // the lanes adds the sums before it); one barrier publishes them. Then every
+  // thread fills a run of consecutive slots: a binary search for the run's
+  // first symbol, a walk that reloads only where the symbol changes, and the
+  // entries written two at a time.
+  if (tid < (uint32_t)kWave) {
+    const uint32_t l = tid;
+    uint32_t f[4], c = 0;
+    bool bad = false;
+    u32x4 vals;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t e = ent4[i];
+      const bool live = 4u * l + i < nsym;
+      f[i] = live ? (e >> 16) & 0x1FFFu : 0u;
+      // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each
+      bad |= live && (f[i] == 0 || (fast && ((e & 0x807Fu) != 0 || (e >> 31) == 0)));
+      vals[i] = (e & 0xFFFFu) | (e & 0x80000000u);
+      c += f[i];
+    }
+    uint32_t incl = c;
+#pragma unroll
+    for (uint32_t d = 1; d < (uint32_t)kWave; d <<= 1) {
+      const uint32_t u = (uint32_t)__builtin_amdgcn_ds_bpermute((int)(((l - d) & 63u) << 2), (int)incl);
+      if (l >= d) incl += u;
+    }
+    const uint32_t c1 = incl - c + f[0], c2 = c1 + f[1], c3 = c2 + f[2];
+    *(LDS u32x4*)(s_cum + 1 + 4 * l) = u32x4{c1, c2, c3, incl};
+    *(LDS u32x4*)(s_val + 4 * l) = vals;
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+    const bool any_bad = __ballot(bad) != 0;
+    if (l == 0) {
+      s_cum[0] = 0;
+      *s_flag = any_bad || total != 4096u;
+    }
   }
-  if (tid < 256) s_cum[tid + 1] = f_own;
-  if (tid == 0) { s_cum[0] = 0; *s_flag = 0; }
   __syncthreads();
-  for (uint32_t d = 1; d < 256; d <<= 1) {        // inclusive scan of s_cum[1..256]
-    uint32_t add = (tid < 256 && tid >= d) ? s_cum[tid + 1 - d] : 0u;
-    __syncthreads();
-    if (tid < 256) s_cum[tid + 1] += add;
-    __syncthreads();
-  }
-  if ((tid == 0 && s_cum[256] != 4096u) || bad_sym) *s_flag = 1;
-  __syncthreads();
-  if (*s_flag) {
+  if (*s_flag) {                                  // the same value for every thread
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
-  // each thread fills a run of consecutive slots: one binary search, then a forward walk
-  constexpr uint32_t kRun = (4096u + kThreads - 1) / kThreads;
-  if (tid * kRun < 4096u) {
-    uint32_t slot = tid * kRun;
-    uint32_t lo = 0, hi = nsym;                      // cum[lo] <= slot < cum[hi]
+  constexpr uint32_t kRun = 4096u / kThreads;
+  static_assert(4096u % kThreads == 0 && kRun % 2 == 0, "slot runs");
+  {
+    const uint32_t slot0 = tid * kRun;
+    uint32_t lo = 0, hi = nsym;                      // cum[lo] <= slot0 < cum[hi]
     while (hi - lo > 1) {
-      uint32_t mid = (lo + hi) >> 1;
-      if (s_cum[mid] <= slot) lo = mid; else hi = mid;
+      const uint32_t mid = (lo + hi) >> 1;
+      if (s_cum[mid] <= slot0) lo = mid; else hi = mid;
     }
-    for (uint32_t k = 0; k < kRun && slot < 4096u; ++k, ++slot) {
-      while (s_cum[lo + 1] <= slot) ++lo;
-      const uint32_t c0 = s_cum[lo], f = s_cum[lo + 1] - c0, val = s_val[lo];
-      s_tbl[slot] = fast    ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
-                    : eb == 1 ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
-                              : ((uint64_t)f | ((uint64_t)(val | ((slot - c0) << 16)) << 32));
+    uint32_t c0 = s_cum[lo], c1 = s_cum[lo + 1], val = s_val[lo];
+#pragma unroll
+    for (uint32_t k = 0; k < kRun; k += 2) {
+      uint64_t e2[2];
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t slot = slot0 + k + h;
+        while (c1 <= slot) {                         // cum[nsym] = 4096 > slot ends it
+          ++lo;
+          c0 = c1;
+          c1 = s_cum[lo + 1];
+          val = s_val[lo];
+        }
+        const uint32_t f = c1 - c0;
+        e2[h] = fast    ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
+                : eb == 1 ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
+                          : ((uint64_t)f | ((uint64_t)(val | ((slot - c0) << 16)) << 32));
+      }
+      *(LDS u32x4*)(s_tbl + slot0 + k) =
+          u32x4{(uint32_t)e2[0], (uint32_t)(e2[0] >> 32), (uint32_t)e2[1], (uint32_t)(e2[1] >> 32)};
     }
   }
   __syncthreads();

@@ -315,6 +315,11 @@ inline int __builtin_amdgcn_readlane(int x, int lane) {
   return (int)(uint32_t)bs_simt::exchange((uint32_t)x, [lane](bs_simt::Wave& w) { return w.slot[lane & 63]; });
 }
 inline void __builtin_amdgcn_wave_barrier() { bs_simt::ctx().wave->bar.arrive_and_wait(); }
+// ds_bpermute: each lane reads the value of lane (index / 4) mod 64
+inline int __builtin_amdgcn_ds_bpermute(int index, int v) {
+  const uint32_t src = ((uint32_t)index >> 2) & 63u;
+  return (int)(uint32_t)bs_simt::exchange((uint32_t)v, [src](bs_simt::Wave& w) { return w.slot[src]; });
+}
 inline void __builtin_amdgcn_s_setprio(int) {}   // issue priority: no effect on results
 inline void __builtin_amdgcn_fence(int, const char*) {}
 inline void __builtin_amdgcn_s_waitcnt(int) {}
