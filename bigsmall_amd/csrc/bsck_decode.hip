@@ -138,6 +138,15 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Workgroup barrier that publishes LDS only: its fences cover the LDS address
+// space, so loads from global memory issued before it stay in flight across
+// it (__syncthreads() also waits for every outstanding vector-memory load).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -154,6 +163,10 @@ __device__ __forceinline__ void consume(const uint32_t (&v)[K]) {
 }
 
 __device__ __forceinline__ uint32_t pad16(uint32_t v) { return (v + 15u) & ~15u; }
+
+// readfirstlane of a 32-bit value, as unsigned (the builtin returns int, and
+// widening an int to 64 bits would copy its bit 31 into the high half)
+__device__ __forceinline__ uint32_t rfl(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 
 // The builtin returns int: each half goes through uint32_t so that the low
 // half is zero-extended (a plain cast would copy its bit 31 into the high half).
@@ -732,32 +745,42 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t group = blockIdx.x - T.wg_begin;
   const GLB uint8_t* __restrict__ b = (const GLB uint8_t*)T.blob;
   const uint32_t tid = threadIdx.x;
-  // the symbol entries load beside the header (both need only the blob
-  // address): wavefront 0, lane l entries 4l..4l+3 in one 16-byte load
-  u32x4 ent4 = {0u, 0u, 0u, 0u};
-  if (tid < (uint32_t)kWave) {
-    const uint64_t at = 32ull + 16ull * tid;
-    if (at + 16u <= T.blob_bytes) {
-      ent4 = *(const GLB u32x4*)(b + at);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (at + 4u * i + 4u <= T.blob_bytes) ent4[i] = ld_u32(b + at + 4u * i);
-    }
-  }
-
-  // ---- header checks (uniform across the workgroup)
-  if (T.blob_bytes < 32 || b[0] != 'B' || b[1] != 'S' || b[2] != 'C' || b[3] != 'K' || b[4] != kVersion ||
-      (b[5] != 1 && b[5] != 2) || b[6] > 2 || b[7] != 12 || (!COMPACT && b[6] == 2)) {
+  // The loads of the prologue are issued without branches around them, at
+  // clamped or known-valid addresses, so that the compiler's in-order count
+  // of outstanding loads stays exact and a use of one load waits for it alone,
+  // not for the loads issued after it. A valid blob has at least 64 bytes
+  // (header, one symbol entry padded to 16, one chunk-table entry).
+  if (T.blob_bytes < 64) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
-  const uint32_t eb = b[5], mode = b[6];
-  const uint64_t n = (uint64_t)ld_u32(b + 8) | ((uint64_t)ld_u32(b + 12) << 32);
-  const uint32_t steps = ld_u32(b + 16);
-  const uint32_t lanes = (uint32_t)b[20] | ((uint32_t)b[21] << 8);
-  const uint32_t nsym = (uint32_t)b[22] | ((uint32_t)b[23] << 8);
-  const uint32_t nch = ld_u32(b + 24);
+  const uint32_t lane = __lane_id();
+  // The 32-byte header (two 16-byte loads at one address for the whole
+  // wavefront) and the symbol entries are requested together: both need only
+  // the blob address, and the header fields are then taken from registers,
+  // not read one dependent byte load at a time.
+  const u32x4 h0 = ((const GLB u32x4*)b)[0], h1 = ((const GLB u32x4*)b)[1];
+  // symbol entries: lane l entries 4l..4l+3 in one 16-byte load (every wave
+  // loads them, wavefront 0 uses them); lanes past the blob's end read its
+  // last 16 bytes, which belong to no live symbol when the header is valid
+  const u32x4 ent4 =
+      *(const GLB u32x4*)(b + (32u + 16u * lane + 16u <= T.blob_bytes ? (uint64_t)(32u + 16u * lane)
+                                                                         : (T.blob_bytes - 16u) & ~(uint64_t)15));
+
+  // ---- header checks (uniform across the workgroup)
+  const uint32_t magic = rfl(h0.x), w1 = rfl(h0.y);
+  const uint32_t eb = (w1 >> 8) & 0xFFu, mode = (w1 >> 16) & 0xFFu;
+  if (magic != 0x4B435342u ||                                             // "BSCK"
+      (w1 & 0xFFu) != (uint32_t)kVersion || (eb != 1 && eb != 2) || mode > 2 || (w1 >> 24) != 12 ||
+      (!COMPACT && mode == 2)) {
+    if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
+    return;
+  }
+  const uint64_t n = (uint64_t)rfl(h0.z) | ((uint64_t)rfl(h0.w) << 32);
+  const uint32_t steps = rfl(h1.x);
+  const uint32_t w5 = rfl(h1.y);
+  const uint32_t lanes = w5 & 0xFFFFu, nsym = w5 >> 16;
+  const uint32_t nch = rfl(h1.z);
   const uint64_t per = (uint64_t)lanes * steps;
   if ((lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || (steps % (2 * kBlockMax)) != 0 || nsym == 0 ||
       nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per == 0 || nch != (n + per - 1) / per) {
@@ -782,14 +805,11 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   // its latency passes under it (the build's barriers wait for LDS only)
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform: keeps chunk state scalar
   const uint32_t chunk = group * kWaves + wave;
-  uint64_t off = 0;
-  uint32_t nw = 0, np = 0;
-  if (chunk < nch) {                                   // wave-uniform; the entry lies inside the checked table
-    const GLB uint8_t* ce = b + ctab + 16ull * chunk;
-    off = (uint64_t)ld_u32(ce) | ((uint64_t)ld_u32(ce + 4) << 32);
-    nw = ld_u32(ce + 8);
-    np = ld_u32(ce + 12);
-  }
+  // (nch >= 1 here; a wave past the last chunk reads the last entry and does not use it)
+  // a scalar load (the address is wave-uniform): its wait is on the scalar
+  // counter, apart from the vector loads issued around it
+  const u32x4 centry = *(const CST u32x4*)((const CST uint8_t*)b + ctab + 16ull * min(chunk, nch - 1u));
+
 
   // ---- decode table in LDS (layouts in the file comment). Wavefront 0
   // checks the symbol entries and writes their values and the inclusive
@@ -829,7 +849,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
       *s_flag = any_bad || total != 4096u;
     }
   }
-  __syncthreads();
+  lds_barrier();
+  const uint64_t off = (uint64_t)rfl(centry.x) | ((uint64_t)rfl(centry.y) << 32);
+  const uint32_t nw = rfl(centry.z), np = rfl(centry.w);
   if (*s_flag) {                                  // the same value for every thread
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
@@ -865,7 +887,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
           u32x4{(uint32_t)e2[0], (uint32_t)(e2[0] >> 32), (uint32_t)e2[1], (uint32_t)(e2[1] >> 32)};
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- one chunk per wavefront
   if (chunk >= nch) return;

@@ -1,5 +1,5 @@
 // What the decode kernels need from the compiler beyond plain C++: the HIP
-// runtime and kernel language, the LDS / global address spaces, and empty asm
+// runtime and kernel language, the LDS / global / constant address spaces, and empty asm
 // statements that pin values in vector registers at chosen points. The
 // library is built for gfx950 by hipcc; the same kernel sources also build as
 // host C++ for sanitizer runs on the CPU (BS_SIMT_CPU, simt_cpu.h), where the
@@ -10,6 +10,7 @@
 #include "simt_cpu.h"
 #define LDS
 #define GLB
+#define CST
 #define BS_DYNAMIC_LDS(name) uint8_t* name = bs_simt::dynamic_lds()
 #define BS_KEEP1(a) ((void)(a))
 #define BS_KEEP2(a, b) ((void)(a), (void)(b))
@@ -19,6 +20,9 @@
 #include <hip/hip_runtime.h>
 #define LDS __attribute__((address_space(3)))
 #define GLB __attribute__((address_space(1)))
+// Read-only global memory at wave-uniform addresses: loads through the scalar
+// cache into scalar registers (reads only; nothing stores through it).
+#define CST __attribute__((address_space(4)))
 #define BS_DYNAMIC_LDS(name) extern __shared__ __attribute__((aligned(16))) uint8_t name[]
 // Makes the values available at this point: every load producing them is
 // issued before it, and nothing can sink them under a later branch.

@@ -322,6 +322,8 @@ inline int __builtin_amdgcn_ds_bpermute(int index, int v) {
 }
 inline void __builtin_amdgcn_s_setprio(int) {}   // issue priority: no effect on results
 inline void __builtin_amdgcn_fence(int, const char*) {}
+inline void __builtin_amdgcn_fence(int, const char*, const char*) {}
+inline void __builtin_amdgcn_s_barrier() { bs_simt::ctx().blk->bar.arrive_and_wait(); }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 // v_perm_b32: byte i of the result is selected by byte i of sel from the
 // 8 bytes {a, b} (b the low dword): 0-7 that byte, 8-11 the sign of bytes
