@@ -551,18 +551,24 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
   }
 }
 
-// A wavefront's issue priority falls as its chunk progresses: 3 in the first
-// quarter of its blocks, then 2, 1 and 0. The SIMD arbiter otherwise favours
-// the oldest waves, so the first of a CU's two workgroups ran ahead and the
-// CU's last 20-30 us ran the second one alone, at lower throughput; with the
-// priority the waves that are behind issue first and the chunks of a CU end
-// closer together (Llama-3-8B-shaped layer: 157.4 -> 154.9 us per launch).
-// Partial chunks, which have fewer blocks, lower their priority sooner.
-__device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk) {
-  const uint32_t quarter = (blk * 4u) / nblk;            // wave-uniform
-  if (quarter == 0) __builtin_amdgcn_s_setprio(3);
-  else if (quarter == 1) __builtin_amdgcn_s_setprio(2);
-  else if (quarter == 2) __builtin_amdgcn_s_setprio(1);
+// A wavefront's issue priority falls as its chunk progresses, from 3 to 0 in
+// four bands. The SIMD arbiter otherwise favours the oldest waves, so the
+// first of a CU's two workgroups ran ahead and the CU's last 20-30 us ran the
+// second one alone, at lower throughput; with the priority the waves that
+// are behind issue first and the chunks of a CU end closer together. The
+// dispatcher places workgroups in index order, one per CU before any CU gets
+// a second, so workgroups from index `first_round` (the device's CU count) on
+// are the younger of their CU's two: their bands end at 40/60/80 % of the
+// chunk's blocks, the others' at 20/40/60 %. Partial chunks, which have fewer
+// blocks, lower their priority sooner. A wrong guess (another kernel sharing
+// the CUs) changes only the order of issue. Llama-3-8B-shaped layer: 157.4 us
+// per launch without the priority, 154.9 with quarter bands for every wave,
+// 148.5 with the shifted bands (and the later prologue changes).
+__device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, bool younger) {
+  const uint32_t fifth = (blk * 5u) / nblk + (younger ? 0u : 1u);   // wave-uniform, 0..5
+  if (fifth <= 1) __builtin_amdgcn_s_setprio(3);
+  else if (fifth == 2) __builtin_amdgcn_s_setprio(2);
+  else if (fifth == 3) __builtin_amdgcn_s_setprio(1);
   else __builtin_amdgcn_s_setprio(0);
 }
 
@@ -575,7 +581,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
                                              uint32_t n_plane, const GLB uint8_t* dplane, uint64_t pstride,
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
-                                             uint32_t nc, uint32_t nsteps, int32_t* status) {
+                                             uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
   typedef Geo<K, MODE> G;
   constexpr uint32_t kStates = kWave * K;
   ChunkParams C;
@@ -617,7 +623,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
   for (uint32_t blk = 0;;) {
-    progress_priority(blk, C.nblk);
+    progress_priority(blk, C.nblk, younger);
     // ---- pair start: land the previous pair's loads, issue the next pair's
     const PlaneRegs<K> cur0 = F.pl[0], cur1 = F.pl[1];
     land_segments<K, MODE>(S, F, wring, pring, C.lane);
@@ -670,17 +676,17 @@ __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint6
                                                   LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
                                                   uint32_t nw, uint32_t np, const GLB uint8_t* dplane,
                                                   uint64_t pstride, GLB uint8_t* out, uint64_t ubase, uint64_t ustride,
-                                                  uint32_t nc, uint32_t nsteps, int32_t* status) {
+                                                  uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
   if constexpr (EB == 1) {   // byte elements have no plane
-    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   } else {
     if (mode == 0) {
-      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     } else if (mode == 1) {
-      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     } else {
       if constexpr (COMPACT)
-        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     }
   }
 }
@@ -691,20 +697,20 @@ __device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32
                                                const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
                                                const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
                                                uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
-                                               int32_t* status) {
+                                               int32_t* status, bool younger) {
   if (eb == 2) {
-    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
-    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   } else {
-    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
-    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status);
+    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   }
 }
 
 template <bool COMPACT>
 __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_task* __restrict__ tasks,
                                                                uint32_t n_tasks, bs_chunk_task single,
-                                                               int32_t* __restrict__ status) {
+                                                               int32_t* __restrict__ status, uint32_t first_round) {
   BS_DYNAMIC_LDS(smem);
   LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
   LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
@@ -918,31 +924,50 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint64_t pstride = split ? nf * pblk : pblk;
   const uint64_t ubase = full ? (uint64_t)chunk * kUnit : cbase_idx;
   const uint64_t ustride = full ? nf * kUnit : kUnit;
+  const bool younger = blockIdx.x >= first_round;      // the later of its CU's two workgroups
   if (lanes == 64)
     decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status);
+                               ustride, nc, nsteps, status, younger);
   else if (lanes == 128)
     decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status);
+                               ustride, nc, nsteps, status, younger);
   else
     decode_chunk_k<4, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status);
+                               ustride, nc, nsteps, status, younger);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
 
 std::atomic<uint64_t> g_lds_plain{0}, g_lds_compact{0};   // devices configured, one bit each
 
+// Compute units of the current device, asked once per device (devices 0..63);
+// 2^32-1 when unknown, which marks no workgroup as the younger of its CU's two.
+std::atomic<uint32_t> g_cus[64];
+uint32_t device_cus() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0xFFFFFFFFu;
+  uint32_t v = g_cus[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 0xFFFFFFFFu;
+    v = (uint32_t)n;
+    g_cus[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 int launch(const bs_chunk_task* tasks, uint32_t n_tasks, const bs_chunk_task& single, uint32_t groups,
            uint32_t max_mode, int32_t* status, void* stream) {
+  const uint32_t first_round = device_cus();
   if (max_mode >= 2) {
     bs_internal::ensure_lds_limit((const void*)bsck_decode_kernel<true>, kLds, g_lds_compact);
     hipLaunchKernelGGL(bsck_decode_kernel<true>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
-                       tasks, n_tasks, single, status);
+                       tasks, n_tasks, single, status, first_round);
   } else {
     bs_internal::ensure_lds_limit((const void*)bsck_decode_kernel<false>, kLds, g_lds_plain);
     hipLaunchKernelGGL(bsck_decode_kernel<false>, dim3(groups), dim3(kThreads), kLds, (hipStream_t)stream,
-                       tasks, n_tasks, single, status);
+                       tasks, n_tasks, single, status, first_round);
   }
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }

@@ -52,6 +52,11 @@ inline hipError_t hipGetDevice(int* d) {
   return hipSuccess;
 }
 inline hipError_t hipFuncSetAttribute(const void*, hipFuncAttribute, int) { return hipSuccess; }
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 63 };
+inline hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t, int) {   // an MI355X's compute units
+  *v = 256;
+  return hipSuccess;
+}
 
 // Saves the callee-saved registers and the stack pointer of the running
 // context in *from_sp and resumes the context whose stack pointer is to_sp
