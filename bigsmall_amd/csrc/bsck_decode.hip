@@ -15,7 +15,7 @@
 //        the plane bytes omitted for a full chunk in plane_mode 1
 //   pad to 256 (the blob length is a multiple of 256)
 //
-// Chunks and elements: per = 64*K*steps elements per chunk, nf = n / per full
+// Chunks and elements: per = 64*K*steps elements per chunk (at most 2^24), nf = n / per full
 // chunks, and a partial chunk (c = nf) when per does not divide n. A full
 // chunk's elements are 512-element units of the tensor interleaved across the
 // full chunks: chunk element j is tensor element ((j/512)*nf + c)*512 + j%512.
@@ -93,6 +93,8 @@ constexpr uint32_t kPMirror = 64;         // compact plane-ring bytes [0, 64) li
 constexpr uint32_t kRingBytes = (1024 + kMirror) * 2 + 2048 + kPMirror + 16;
 static_assert(kRingBytes >= (2048 + kMirror) * 2, "ring area");
 constexpr uint32_t kL = 1u << 16;
+// elements per chunk at most (lanes * steps): byte offsets inside a chunk fit 32 bits
+constexpr uint64_t kMaxChunk = 1ull << 24;
 // s_waitcnt immediate for gfx9: vmcnt(n), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -187,12 +189,18 @@ __device__ __forceinline__ uint32_t byte_merge(uint32_t v, uint32_t b) { return 
 
 // Load this lane's part of the segment at `pos` (in units of V); out-of-range
 // lanes read `safe` (the chunk's state words, 256 bytes or more, always in
-// bounds), so every call issues exactly one load per lane.
+// bounds), so every call issues exactly one load per lane. The source lies
+// after `safe` inside the chunk, so the lane's address is one 32-bit offset
+// from the wave-uniform `safe` (a select of two offsets, not of two 64-bit
+// addresses).
 template <typename V>
 __device__ __forceinline__ V load_seg(const GLB uint8_t* src, uint32_t pos, uint32_t valid, uint32_t lane,
                                       const GLB uint8_t* safe) {
   const uint32_t slot = pos + lane;
-  return *(slot < valid ? (const GLB V*)src + slot : (const GLB V*)safe + (lane & (256u / sizeof(V) - 1u)));
+  const uint32_t src_off = (uint32_t)(src - safe) + pos * (uint32_t)sizeof(V);   // wave-uniform
+  const uint32_t off = slot < valid ? src_off + lane * (uint32_t)sizeof(V)
+                                    : (lane & (256u / sizeof(V) - 1u)) * (uint32_t)sizeof(V);
+  return *(const GLB V*)(safe + off);
 }
 // Word ring: words [0, kMirror) also live at [kRing, kRing + kMirror), so a
 // read at (ring position mod kRing) + rank, rank < 64, never wraps.
@@ -382,7 +390,10 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
       // a non-consuming lane reads the zero slot, so the merge below needs no select
       cons[g] = act && (int32_t)hi < 0;
       const uint64_t cm = __ballot(cons[g]);
-      const uint32_t at = (ppos & (G::kPRing - 1u)) + lane_rank(cm);   // < kPRing + 64: the mirror covers it
+      // ring position + rank (< kPRing + 64: the mirror covers it), the position
+      // added by mbcnt's accumulator
+      const uint32_t at = __builtin_amdgcn_mbcnt_hi((uint32_t)(cm >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)cm, ppos & (G::kPRing - 1u)));
       pb[g] = pring[cons[g] ? at : G::kPZero];
       ppos += (uint32_t)__popcll(cm);
     }
@@ -789,7 +800,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t nch = rfl(h1.z);
   const uint64_t per = (uint64_t)lanes * steps;
   if ((lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || (steps % (2 * kBlockMax)) != 0 || nsym == 0 ||
-      nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per == 0 || nch != (n + per - 1) / per) {
+      nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per > kMaxChunk || nch != (n + per - 1) / per) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
@@ -996,7 +1007,7 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
       info->n_syms > 256 || (info->elem_bytes != 1 && info->elem_bytes != 2) || info->plane_mode > 2)
     return BS_ERR_FORMAT;
   const uint64_t per = (uint64_t)info->lanes * info->steps;
-  if (info->n_chunks != (info->n + per - 1) / per) return BS_ERR_FORMAT;
+  if (per > kMaxChunk || info->n_chunks != (info->n + per - 1) / per) return BS_ERR_FORMAT;
   return BS_OK;
 }
 

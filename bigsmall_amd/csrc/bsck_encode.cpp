@@ -295,9 +295,13 @@ void encode_chunk(const Plan& P, const void* src, uint32_t nc, uint32_t lanes, u
 extern "C" {
 
 static bool lanes_ok(uint32_t lanes) { return lanes == 64 || lanes == 128 || lanes == 256; }
+// A chunk holds at most 2^24 elements (the decoder refuses larger), so every
+// byte offset inside a chunk fits 32 bits.
+static bool chunk_ok(uint32_t lanes, uint32_t steps) { return (uint64_t)lanes * steps <= (1ull << 24); }
 
 int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t* bound) {
-  if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes))
+  if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes) ||
+      !chunk_ok(lanes, steps))
     return BS_ERR_ARG;
   const uint64_t per = (uint64_t)lanes * steps;
   const uint64_t nch = (n + per - 1) / per;
@@ -307,7 +311,8 @@ int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint3
 
 int bs_chunk_encode(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t* dst, uint64_t cap, uint64_t* out_len, int n_threads) {
-  if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes))
+  if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes) ||
+      !chunk_ok(lanes, steps))
     return BS_ERR_ARG;
   if (n == 0) { *out_len = 0; return BS_OK; }
   if (!src || !dst) return BS_ERR_ARG;

@@ -485,7 +485,7 @@ uint64_t bs_chunk_encode_gpu_work_bytes(uint32_t n_tasks, uint64_t total_chunks,
 int bs_chunk_encode_gpu(const bs_encode_task* d_tasks, uint32_t n_tasks, uint32_t total_chunks, uint32_t steps,
                         void* d_work, uint64_t work_bytes, uint64_t* d_out_len, int32_t* d_status, void* stream) {
   if (!d_status || (n_tasks && (!d_tasks || !d_work || !d_out_len)) || steps == 0 || steps % 16 ||
-      ((uintptr_t)d_work & 255u))
+      128ull * steps > (1ull << 24) || ((uintptr_t)d_work & 255u))   // chunks of at most 2^24 elements
     return BS_ERR_ARG;
   if (n_tasks == 0) return BS_OK;
   if (work_bytes < bs_chunk_encode_gpu_work_bytes(n_tasks, total_chunks, steps)) return BS_ERR_ARG;

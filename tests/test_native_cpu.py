@@ -135,6 +135,29 @@ def test_malformed_header_raises_value_error(field, value):
         bc.info(bytes(head))
 
 
+def test_chunk_size_is_capped_at_2_pow_24_elements():
+    """A chunk holds at most 2^24 elements (lanes x steps), so byte offsets
+    inside a chunk fit 32 bits: the host header check and both encoders'
+    argument checks refuse one more step block, and accept the cap itself."""
+    import ctypes
+    import struct
+    from bigsmall_amd import _native
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    w = _bf16(np.random.default_rng(5).standard_normal(50_000) * 0.02)
+    head = bytearray(bc.encode_array(w)[:32])
+    assert struct.unpack_from("<I", head, 24)[0] == 1          # one chunk either way
+    struct.pack_into("<I", head, 16, (1 << 24) // 128)          # 128 x 131072 = 2^24: accepted
+    assert bc.info(bytes(head)).steps == 131072
+    struct.pack_into("<I", head, 16, (1 << 24) // 128 + 16)     # one step block more: refused
+    with pytest.raises(ValueError):
+        bc.info(bytes(head))
+    L = _native.lib()
+    bound = ctypes.c_uint64()
+    assert L.bs_chunk_encode_bound(1000, 2, 128, 131072, ctypes.byref(bound)) == 0
+    assert L.bs_chunk_encode_bound(1000, 2, 128, 131072 + 16, ctypes.byref(bound)) != 0
+    assert L.bs_chunk_encode_bound(1000, 2, 256, 65536 + 16, ctypes.byref(bound)) != 0
+
+
 def test_invariant_divisor_multiply_shift_is_exact():
     """The GPU encoder divides a 32-bit state by a symbol frequency f (1..4096)
     with Granlund and Montgomery's multiply-shift (PLDI 1994, Figure 4.1;
