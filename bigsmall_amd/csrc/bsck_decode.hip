@@ -321,14 +321,14 @@ __device__ __forceinline__ void flush_half(uint32_t hb, const ChunkParams& C, LD
   }
 }
 
-// Full chunks of bf16 elements with K >= 2 store each step's outputs straight
-// from registers: a step's 64*K elements are contiguous in the output (a
-// quarter or half of a 512-element unit), so every lane writes its K adjacent
-// words (4 or 8 bytes) and the wavefront writes 256 or 512 contiguous bytes,
-// whole cache lines, with no LDS staging. Byte tensors, K = 1 and the partial
-// chunk stage their outputs in LDS and store whole half blocks.
+// Full chunks with K >= 2 store each step's outputs straight from registers:
+// a step's 64*K elements are contiguous in the output (a quarter or half of a
+// 512-element unit), so every lane writes its K adjacent elements (4 or 8
+// bytes of bf16, 2 or 4 bytes of fp8) and the wavefront writes 128 to 512
+// contiguous bytes, whole cache lines, with no LDS staging. K = 1 and the
+// partial chunk stage their outputs in LDS and store whole half blocks.
 template <int K, int EB, bool PARTIAL>
-constexpr bool direct_stores() { return !PARTIAL && EB == 2 && K >= 2; }
+constexpr bool direct_stores() { return !PARTIAL && K >= 2; }
 
 // Output stores a chunk issues per pair of blocks (the pipeline's wait counts).
 template <int K, int MODE, int EB, bool PARTIAL>
@@ -337,13 +337,14 @@ constexpr int stores_per_pair() { return direct_stores<K, EB, PARTIAL>() ? 2 * G
 // Store step q of block blk (KB steps per block): lane l's K words go to
 // chunk elements t*64K + l*K .. +K-1, t = blk*KB + q, which lie in 512-element
 // unit t*K/8 at offset (t*K % 8)*64.
-template <int K, int KB>
+template <int K, int KB, int EB>
 __device__ __forceinline__ void store_step(const ChunkParams& C, uint32_t blk, int q, uint32_t v0, uint32_t v1) {
   static_assert((KB * K) % 8 == 0, "a block is whole units");
   const uint32_t unit = blk * (uint32_t)(KB * K / 8) + (uint32_t)(q * K / 8);   // wave-uniform
-  GLB uint8_t* p = C.out8 + ((uint64_t)unit * C.ustride + C.ubase) * 2u + (uint32_t)((q * K) % 8) * 128u +
-                   C.lane * (2u * K);
-  if (K == 2) __builtin_nontemporal_store(v0, (GLB uint32_t*)p);
+  GLB uint8_t* p = C.out8 + ((uint64_t)unit * C.ustride + C.ubase) * EB + (uint32_t)((q * K) % 8) * (64u * EB) +
+                   C.lane * (EB * K);
+  if (EB * K == 2) __builtin_nontemporal_store((uint16_t)v0, (GLB uint16_t*)p);
+  else if (EB * K == 4) __builtin_nontemporal_store(v0, (GLB uint32_t*)p);
   else __builtin_nontemporal_store((uint64_t)v0 | ((uint64_t)v1 << 32), (GLB uint64_t*)p);
 }
 
@@ -526,7 +527,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
           v[h] = (dup & 0x807F807Fu) | ex;
         }
         if (DIRECT) {
-          store_step<K, kBlock>(C, blk, q, v[0], v[kPairs - 1]);
+          store_step<K, kBlock, EB>(C, blk, q, v[0], v[kPairs - 1]);
         } else {
           LDS uint8_t* dst = stage + qs * (kStates * 2) + lane * (2u * K);
           if (K == 2) *(LDS uint32_t*)dst = v[0];
@@ -540,9 +541,14 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     } else {
       // the lane's K outputs of this step are adjacent: one LDS store
       LDS uint8_t* dst = stage + (qs * kStates + lane * K) * EB;
-      if (DIRECT) {
-        store_step<K, kBlock>(C, blk, q, __builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u),
-                              __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u));
+      if (DIRECT && EB == 2) {
+        store_step<K, kBlock, EB>(C, blk, q, __builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u),
+                                  __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u));
+      } else if (DIRECT) {                               // bytes: K = 2 in one half word, K = 4 in one word
+        store_step<K, kBlock, EB>(C, blk, q,
+                                  __builtin_amdgcn_perm(d[1 % K], d[0], 0x0C0C0703u) |
+                                      (K == 4 ? __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x0C0C0703u) << 16 : 0u),
+                                  0u);
       } else if (EB == 2) {
         if (K == 1) *(LDS uint16_t*)dst = (uint16_t)d[0];
         else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], 0x05040100u);
