@@ -640,7 +640,7 @@ def run_c3(args) -> dict:
     steps = args.chunk_steps or 128
     R = max(1, args.rotate)
     for name, w in tensors:
-        blob = bc.encode_array(w, steps=steps)
+        blob = bc.encode_array(w, steps=steps, lanes=args.lanes or bc.DEFAULT_LANES)
         inf = bc.info(blob)
         # R copies of the blob and of the output, decoded in turn: the working
         # set (R x up to 245 MB) is far beyond the 256 MB Infinity Cache
