@@ -113,6 +113,35 @@ def test_batched_launch_matches_single(torch_gpu):
             assert np.array_equal(o.cpu().numpy().view(np.uint16), w), f"rep {rep}"
 
 
+@pytest.mark.parametrize("n_tasks", [64, 65])
+def test_batched_launch_at_the_task_lookup_boundary(torch_gpu, n_tasks):
+    """A workgroup finds its task by a wavefront vote over up to 64 tasks and
+    by binary search beyond: 64 and 65 blobs of one to three chunks each, the
+    outputs in separate allocations so that their addresses differ in every
+    bit range, each decoded bit-exact."""
+    import torch
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
+    rng = np.random.default_rng(17 + n_tasks)
+    words = [_bf16(rng.standard_normal(int(s)) * 0.02) for s in rng.integers(1, 3 * 8192, n_tasks)]
+    blobs = [bc.encode_array(w, steps=64) for w in words]
+    _say(f"[bsck] batch of {n_tasks} blobs")
+    dev = torch.device("cuda")
+    d = [upload_bytes(b, dev) for b in blobs]
+    outs = [torch.empty(w.size, dtype=torch.int16, device=dev) for w in words]
+    jobs = [ChunkJob(db.data_ptr(), len(b), o.data_ptr(), w.size, bc.info(b).n_chunks, bc.info(b).plane_mode)
+            for db, b, o, w in zip(d, blobs, outs, words)]
+    st = StatusWord(dev)
+    batch = ChunkBatch(jobs, dev)
+    for o in outs:
+        o.fill_(0)
+    batch.launch(st)
+    torch.cuda.synchronize()
+    st.check()
+    for i, (o, w) in enumerate(zip(outs, words)):
+        assert np.array_equal(o.cpu().numpy().view(np.uint16), w), f"task {i} of {n_tasks}"
+
+
 def test_batched_launch_mixing_every_plane_mode(torch_gpu):
     """One launch holding compact (mode 2), dense (1) and exact (0) bf16 blobs
     and an fp8 blob, at every lane count, with partial last chunks: the
