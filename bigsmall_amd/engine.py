@@ -139,9 +139,15 @@ class GroupDecoder:
         `GroupResult.wait`, which also records them on the caller's stream).
     copy_stream: where host->device copies run (default: a new stream).
     Pinned staging buffers are allocated lazily and reused (n_pinned of them).
+    pipeline: consecutive groups alternate between the decode stream and a
+        second stream of the decoder's own, so that a group's decode starts
+        while the previous one's last workgroups finish (its prologue over the
+        other's tail: 137 against 144 us per 8B-shaped layer). A group's
+        inputs reach its stream through the copy's event; results are ordered
+        for the caller by `GroupResult.wait`, which every caller uses.
     """
 
-    def __init__(self, device=None, stream=None, copy_stream=None, n_pinned: int = 2):
+    def __init__(self, device=None, stream=None, copy_stream=None, n_pinned: int = 2, pipeline: bool = True):
         import torch
         self.device = require_gpu(device)
         if isinstance(stream, str):
@@ -150,6 +156,8 @@ class GroupDecoder:
             stream = torch.cuda.Stream(self.device)
         self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
         self.copy_stream = copy_stream if copy_stream is not None else torch.cuda.Stream(self.device)
+        self._decode_streams = [self.stream, torch.cuda.Stream(self.device)] if pipeline else [self.stream]
+        self._turn = 0
         self._pinned: list = [None] * max(1, n_pinned)
         self._pinned_busy: list = [None] * len(self._pinned)
         self._next = 0
@@ -212,14 +220,17 @@ class GroupDecoder:
         for t in entries:
             check_supported(t)
         d_span, host, copied = self.upload(read_span, span_start, span_len)
-        with torch.cuda.stream(self.stream):       # allocations and launches on the decode stream
+        stream = self._decode_streams[self._turn]
+        self._turn = (self._turn + 1) % len(self._decode_streams)
+        with torch.cuda.stream(stream):            # allocations and launches on this group's decode stream
             status, out, keep = self._launch_group(entries, host, d_span, copied, span_start, span_len,
-                                                   resolve_tied, dtype, xor_base or {})
+                                                   resolve_tied, dtype, xor_base or {}, stream)
             done = torch.cuda.Event()
-            done.record(self.stream)
+            done.record(stream)
         return GroupResult(out, status, done, keep)
 
-    def _launch_group(self, entries, host, d_span, copied, span_start, span_len, resolve_tied, dtype, xor_base):
+    def _launch_group(self, entries, host, d_span, copied, span_start, span_len, resolve_tied, dtype, xor_base,
+                      stream):
         import torch
         status = StatusWord(self.device)
         out: dict = {}
@@ -286,8 +297,8 @@ class GroupDecoder:
                 zst.add_frame(base + off, nb, o.data_ptr(), nbytes, xb.data_ptr() if xb is not None else 0)
             else:                                        # special/lowcard (check_supported)
                 zst.add_lowcard(base + off, host[off:off + nb], o.data_ptr(), o.numel(), o.element_size())
-        self.stream.wait_event(copied)
-        d_span.record_stream(self.stream)
+        stream.wait_event(copied)
+        d_span.record_stream(stream)
         for o, off, nb in raws:
             o.view(-1).view(torch.uint8).copy_(d_span[off:off + nb])
         if jobs:
@@ -297,18 +308,18 @@ class GroupDecoder:
                     a[:nb].copy_(d_span[off:off + nb])
             batch = ChunkBatch([j for j, _ in jobs], self.device)
             keep.append(batch)
-            batch.launch(status, self.stream)
+            batch.launch(status, stream)
         if serial_refs:
             # every large reference-format tensor of the group in one batched
             # wave-serial launch: their chains run side by side
             rb = _refstreams.RefBatch(serial_refs, self.device)
             keep.append(rb)
-            rb.launch(status.ptr, int(self.stream.cuda_stream))
+            rb.launch(status.ptr, int(stream.cuda_stream))
         for launch, o in refs:
             keep.append(launch)
-            launch.launch(o.data_ptr(), status.ptr, int(self.stream.cuda_stream))
+            launch.launch(o.data_ptr(), status.ptr, int(stream.cuda_stream))
         if zst.tasks or zst.expands:
-            zst.launch(status, self.stream)
+            zst.launch(status, stream)
             keep.append(zst.keep)
         for t in entries:
             if t["codec"] != "tied_ref":
