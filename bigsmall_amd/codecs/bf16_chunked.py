@@ -1,6 +1,6 @@
 """`bf16_chunked_v1` / `fp8_chunked_v1`: the engine's GPU-native codec.
 
-A tensor is cut into chunks of `lanes` x `steps` elements (128 x 448 by
+A tensor is cut into chunks of `lanes` x `steps` elements (128 x 432 by
 default). Each chunk is `lanes` interleaved rANS states (lanes / 64 per
 wavefront lane) over the tensor's exponent (or exact-value) symbols, sharing
 one 16-bit renormalisation word stream, plus raw sign|mantissa bytes. Full
