@@ -894,6 +894,8 @@ def main():
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--two-streams", action="store_true",
+                    help="layer workloads: also time the launches alternating between two streams")
     ap.add_argument("--rotate", type=int, default=6,
                     help="layer and c3 workloads: distinct compressed copies (and outputs) decoded in turn, so "
                          "the timed working set (6 x 725 MB for the layer) is far beyond the 256 MB Infinity Cache")
@@ -1004,25 +1006,29 @@ def main():
     ms_per = ev0.elapsed_time(ev1) / args.steps
     gbps = algo_bytes / (ms_per * 1e-3) / 1e9
 
-    # The same launches on two alternating streams, as the engine's
-    # GroupDecoder issues consecutive layers: a launch's prologue runs under the
-    # previous one's last workgroups. Reported beside the line; `value` and the
-    # roofline stay the one-stream figure, one whole launch per step.
-    alt = torch.cuda.Stream(dev)
-    p0, p1, joined = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), torch.cuda.Event()
-    for i in range(max(2, args.warmup)):              # a stream's first launches set it up: untimed
-        batches[i % R].launch(status, (stream, alt)[i % 2])
-    torch.cuda.synchronize(dev)
-    p0.record(stream)
-    alt.wait_event(p0)
-    for i in range(args.steps):
-        batches[i % R].launch(status, (stream, alt)[i % 2])
-    joined.record(alt)
-    stream.wait_event(joined)
-    p1.record(stream)
-    torch.cuda.synchronize(dev)
-    status.check("timed, two streams")
-    ms_pipe = p0.elapsed_time(p1) / args.steps
+    # With --two-streams: the same launches on two alternating streams, as the
+    # engine's GroupDecoder issues consecutive layers (a launch's prologue runs
+    # under the previous one's last workgroups). Reported beside the line;
+    # `value` and the roofline stay the one-stream figure, one whole launch per
+    # step, and the default run leaves it out so that a kernel trace of the
+    # default command times non-overlapping launches only.
+    ms_pipe = None
+    if args.two_streams:
+        alt = torch.cuda.Stream(dev)
+        p0, p1, joined = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), torch.cuda.Event()
+        for i in range(max(2, args.warmup)):          # a stream's first launches set it up: untimed
+            batches[i % R].launch(status, (stream, alt)[i % 2])
+        torch.cuda.synchronize(dev)
+        p0.record(stream)
+        alt.wait_event(p0)
+        for i in range(args.steps):
+            batches[i % R].launch(status, (stream, alt)[i % 2])
+        joined.record(alt)
+        stream.wait_event(joined)
+        p1.record(stream)
+        torch.cuda.synchronize(dev)
+        status.check("timed, two streams")
+        ms_pipe = p0.elapsed_time(p1) / args.steps
 
     # verify bit-exactness (md5 per tensor, every layer copy) after timing; a
     # copy this run never decoded (fewer launches than copies) is decoded once first
@@ -1070,9 +1076,10 @@ def main():
         },
         "ms_per_layer": round(ms_per, 5),
         "decoded_output_GBps": round(out_total / (ms_per * 1e-3) / 1e9, 2),
-        "two_streams": {"ms_per_layer": round(ms_pipe, 5), "GBps": round(algo_bytes / (ms_pipe * 1e-3) / 1e9, 2),
-                        "note": "the same launches alternating between two streams, as the engine decodes "
-                                "consecutive layers: throughput of a sequence of layers, not one launch"},
+        "two_streams": None if ms_pipe is None else {
+            "ms_per_layer": round(ms_pipe, 5), "GBps": round(algo_bytes / (ms_pipe * 1e-3) / 1e9, 2),
+            "note": "the same launches alternating between two streams, as the engine decodes consecutive "
+                    "layers: throughput of a sequence of layers, not one launch"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(workload),
                      "device_copy_GBps": round(copy_gbps, 1), "frac_of_device_copy": round(gbps / copy_gbps, 4),
