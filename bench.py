@@ -101,11 +101,14 @@ def host_cpu_info() -> dict:
     return {"cpu_model": model, "host_cpus": usable}
 
 
-def cpu_baseline(words: dict, budget_s: float = 12.0):
+def cpu_baseline(words: dict, budget_s: float = 12.0, bsck_blobs: dict | None = None):
     """Oracle port of bf16_se_single_kernel decode (bigsmall/codecs/single_kernel.py:431-580)
     on the layer's seven matrices: all of them at once, one host thread per tensor
     (the reported value), and one thread on as many tensors as fit the time
-    budget (`single_thread`). The oracle's C calls run without the GIL."""
+    budget (`single_thread`). With `bsck_blobs` (the layer's blobs in the format
+    the GPU decodes), the oracle's C decoder of that format on the same
+    matrices, one thread per tensor, is reported beside it (`same_format`). The
+    oracle's C calls run without the GIL."""
     from concurrent.futures import ThreadPoolExecutor
     import oracle
     oracle.build()
@@ -132,6 +135,20 @@ def cpu_baseline(words: dict, budget_s: float = 12.0):
         names.append(m[0].split(".")[-2])
         if t_total > budget_s:
             break
+    same = None
+    if bsck_blobs is not None:
+        def one_bsck(m):
+            out = oracle.chunk_decode(bsck_blobs[m[0]], m[1].size)
+            assert out == m[1].tobytes(), "oracle BSCK decode mismatch"
+            return m[1].nbytes + len(bsck_blobs[m[0]])
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(threads) as ex:
+            bsck_all = sum(ex.map(one_bsck, mats))
+        t_bsck = time.perf_counter() - t0
+        same = {"value": bsck_all / t_bsck / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"the oracle's C decoder of bf16_chunked_v1 (the format the GPU line decodes) on the "
+                           f"layer's {len(mats)} matrices, one host thread per tensor: "
+                           f"{bsck_all / 1e6:.0f} MB algorithmic in {t_bsck:.2f} s")}
     return {
         "value": decoded_all / t_all / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"oracle C port of the reference bf16_se_single_kernel CPU decode of the layer's "
@@ -140,6 +157,7 @@ def cpu_baseline(words: dict, budget_s: float = 12.0):
         "single_thread": {"value": decoded / t_total / 1e9, "cores": 1,
                           "sample": f"{len(names)} tensors ({', '.join(names)}): "
                                     f"{decoded / 1e6:.0f} MB algorithmic in {t_total:.2f} s"},
+        "same_format": same,
         "host": host_cpu_info(),
         "note": "one serial sign+exponent chain per tensor, so at most one thread per tensor",
     }
@@ -1051,7 +1069,7 @@ def main():
     copy_gbps = max(torch_copy_gbps, kernel_copy_gbps)
     log(f"[bench] device copy {torch_copy_gbps:.0f} GB/s (torch), {kernel_copy_gbps:.0f} GB/s (bs_copy_spans) "
         f"(read + write)")
-    cpu = None if args.no_cpu_baseline else cpu_baseline(words)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(words, bsck_blobs=blobs[0])
     result = {
         "metric": "decoded bf16 GB/s on 1 MI355X (% of HBM roofline); ms per 8B-shaped layer",
         "value": round(gbps, 2),
