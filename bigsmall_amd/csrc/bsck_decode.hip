@@ -739,31 +739,36 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
 
   // ---- which tensor does this workgroup serve. The prologue is a chain of
   // dependent global loads (task, header and symbols, chunk entry, states),
-  // each a full memory latency at launch, so it is kept short: up to 64 tasks
-  // are read one per lane in a single load and the task found by a ballot
-  // (wg_begin ascends, so the tasks starting at or before this workgroup are
-  // a prefix); more tasks take a binary search.
+  // each a full memory latency at launch, so it is kept short: tasks are read
+  // by the lanes together and found by ballots (wg_begin ascends, so the tasks
+  // starting at or before this workgroup are a prefix).
   bs_chunk_task T = single;
   if (tasks != nullptr) {
-    if (n_tasks <= (uint32_t)kWave) {
-      const uint32_t l = __lane_id();
-      const bs_chunk_task mine = l < n_tasks ? tasks[l] : bs_chunk_task{};
-      const uint64_t before = __ballot(l < n_tasks && mine.wg_begin <= blockIdx.x);
-      const uint32_t lo = before ? (uint32_t)__popcll(before) - 1u : 0u;
-      T.blob = (const uint8_t*)readlane64((uint64_t)mine.blob, lo);
-      T.blob_bytes = readlane64(mine.blob_bytes, lo);
-      T.out = (void*)readlane64((uint64_t)mine.out, lo);
-      T.n = readlane64(mine.n, lo);
-      T.wg_begin = __builtin_amdgcn_readlane(mine.wg_begin, lo);
-      T.n_chunks = __builtin_amdgcn_readlane(mine.n_chunks, lo);
-    } else {
-      uint32_t lo = 0, hi = n_tasks;
-      while (hi - lo > 1) {
-        uint32_t mid = (lo + hi) >> 1;
-        if (tasks[mid].wg_begin <= blockIdx.x) lo = mid; else hi = mid;
-      }
-      T = tasks[lo];
+    // The workgroup's task is the last one whose wg_begin is at or before it
+    // (wg_begin ascends). Each round the 64 lanes read evenly spaced wg_begin
+    // values of the range that holds it and a vote narrows the range 64-fold,
+    // so up to 4,096 tasks take two dependent loads and any count fits 64 in
+    // a few; the last round reads whole tasks, one per lane.
+    const uint32_t l = __lane_id();
+    uint32_t lo = 0, span = n_tasks;                   // the task lies in [lo, lo + span)
+    while (span > (uint32_t)kWave) {                   // wave-uniform
+      const uint32_t stride = (span + kWave - 1) / kWave;
+      const bool in = l * stride < span;
+      const uint32_t wb = in ? tasks[lo + l * stride].wg_begin : 0xFFFFFFFFu;
+      const uint64_t before = __ballot(in && wb <= blockIdx.x);
+      const uint32_t k = before ? (uint32_t)__popcll(before) - 1u : 0u;
+      lo += k * stride;
+      span = min(stride, span - k * stride);
     }
+    const bs_chunk_task mine = l < span ? tasks[lo + l] : bs_chunk_task{};
+    const uint64_t before = __ballot(l < span && mine.wg_begin <= blockIdx.x);
+    const uint32_t k = before ? (uint32_t)__popcll(before) - 1u : 0u;
+    T.blob = (const uint8_t*)readlane64((uint64_t)mine.blob, k);
+    T.blob_bytes = readlane64(mine.blob_bytes, k);
+    T.out = (void*)readlane64((uint64_t)mine.out, k);
+    T.n = readlane64(mine.n, k);
+    T.wg_begin = (uint32_t)__builtin_amdgcn_readlane((int)mine.wg_begin, (int)k);
+    T.n_chunks = (uint32_t)__builtin_amdgcn_readlane((int)mine.n_chunks, (int)k);
   }
   const uint32_t group = blockIdx.x - T.wg_begin;
   const GLB uint8_t* __restrict__ b = (const GLB uint8_t*)T.blob;

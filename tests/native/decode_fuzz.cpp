@@ -185,21 +185,29 @@ int main(int argc, char** argv) {
     }
   }
   // Batched launches of the clean BSCK blobs: once as they are (up to 64
-  // tasks, which a workgroup finds by a wavefront vote) and once five times
-  // over (more than 64, found by binary search). Some buffers sit at
-  // addresses with bit 31 of the low half set, so a lookup that widened that
-  // half with sign extension would decode from a wrong address.
+  // tasks, found by one wavefront vote), five times over (one narrowing
+  // round of the vote first) and, for the blobs of at most 256 elements,
+  // 4,200 tasks (two narrowing rounds). Some buffers sit at addresses with bit
+  // 31 of the low half set, so a lookup that widened that half with sign
+  // extension would decode from a wrong address.
   uint64_t batch_ok = 0, batch_bad = 0, high_bit = 0;
-  for (const int reps : {1, 5}) {
-    const size_t nt = clean_bsck.size() * reps;
-    if (nt == 0) break;
+  std::vector<size_t> small;
+  for (size_t i = 0; i < clean_bsck.size(); ++i)
+    if (clean_bsck[i].n <= 256) small.push_back(i);
+  std::vector<std::vector<size_t>> plans(3);
+  for (size_t i = 0; i < clean_bsck.size(); ++i) plans[0].push_back(i);
+  for (int r = 0; r < 5; ++r) plans[1].insert(plans[1].end(), plans[0].begin(), plans[0].end());
+  for (size_t t = 0; !small.empty() && t < 4200; ++t) plans[2].push_back(small[t % small.size()]);
+  for (const auto& plan : plans) {
+    const size_t nt = plan.size();
+    if (nt == 0) continue;
     Pool pool(64ull << 20);
     std::vector<uint8_t*> blobs, outs;
     std::vector<bs_chunk_task> tasks(nt);
     uint32_t groups = 0, max_mode = 0;
     const uint32_t per_group = (uint32_t)bs_chunk_chunks_per_group();
     for (size_t t = 0; t < nt; ++t) {
-      const Clean& c = clean_bsck[t % clean_bsck.size()];
+      const Clean& c = clean_bsck[plan[t]];
       blobs.push_back(pool.take(c.blob.size()));
       memcpy(blobs.back(), c.blob.data(), c.blob.size());
       outs.push_back(pool.take(c.n * c.eb));
@@ -217,7 +225,7 @@ int main(int argc, char** argv) {
     const int rc = bs_chunk_decode_batch((const bs_chunk_task*)d_tasks.p, (uint32_t)nt, groups, max_mode, &status,
                                          nullptr);
     for (size_t t = 0; t < nt; ++t) {
-      const Clean& c = clean_bsck[t % clean_bsck.size()];
+      const Clean& c = clean_bsck[plan[t]];
       if (rc == BS_OK && status == 0 && memcmp(outs[t], c.want.data(), c.n * c.eb) == 0) {
         ++batch_ok;
       } else {
