@@ -94,7 +94,12 @@ int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uin
 /* Decode many BSCK blobs (a transformer layer, a batch of KV blocks) in one
  * launch; `max_plane_mode` is the largest plane_mode among the tasks (a launch
  * without mode-2 tasks uses a kernel built without the compact-plane path;
- * both use the same LDS and occupancy). Replaces the per-tensor `_decode_blob`
+ * both use the same LDS and occupancy). Tasks are in ascending wg_begin order,
+ * task 0 at 0, each starting where the previous one's workgroups end; every
+ * blob and output is 16-byte aligned, and total_groups is the last task's end
+ * (a workgroup serves the last task whose wg_begin is at or before it, so
+ * a table out of order decodes some tensors into the wrong place but never
+ * reads or writes outside the tasks' buffers). Replaces the per-tensor `_decode_blob`
  * loop of decoder.decompress
  * (bigsmall/decoder.py:128-136) and StreamingLoader.load_layer
  * (bigsmall/streaming.py:218-227). */
