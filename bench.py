@@ -939,8 +939,8 @@ def main():
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
-              "(decode shards by tensor with no exchange; see the design notes).", file=sys.stderr)
+        print("bench.py measures one MI355X; multi-GPU runs are not part of it (a model shards by "
+              "tensor or layer for decoding, with no exchange between GPUs).", file=sys.stderr)
         sys.exit(2)
 
     import torch

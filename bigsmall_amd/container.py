@@ -56,7 +56,7 @@ def read_header(path) -> tuple[dict, int]:
             raise BigSmallVersionError(
                 required="2.4.0", installed=__version__,
                 detail=(f"file uses container format v{version}; "
-                        f"this build supports {sorted(BS_SUPPORTED_FORMAT_VERSIONS)}"))
+                        f"this engine supports {sorted(BS_SUPPORTED_FORMAT_VERSIONS)}"))
         header_len, = struct.unpack("<I", f.read(4))
         header_bytes = f.read(header_len)
         data_offset = f.tell()

@@ -8,7 +8,7 @@ the aliases go to the index's `duplicate_map`), and writes
 model's config/tokenizer files. `from_pretrained(path)` loads a .bs file or
 such a directory into one state dict, decoding every shard on the GPU.
 
-Hugging Face Hub repo IDs are not fetched: this build has no network path, so
+Hugging Face Hub repo IDs are not fetched: this engine has no network path, so
 a repo ID raises ValueError naming the missing local directory.
 """
 from __future__ import annotations
@@ -37,7 +37,7 @@ def _is_repo_id(s: str) -> bool:
 def _local_dir(source) -> Path:
     s = str(source)
     if _is_repo_id(s):
-        raise ValueError(f"{s!r} looks like a Hub repo ID; this build reads local directories only "
+        raise ValueError(f"{s!r} looks like a Hub repo ID; this engine reads local directories only "
                          f"(download the model first and pass its directory)")
     p = Path(source)
     if not p.exists():

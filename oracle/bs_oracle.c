@@ -762,9 +762,9 @@ out:
 }
 
 /* ------------------------------------------------------------------------ */
-/* BSCK — the build's GPU-native chunked rANS container format (no reference
- * counterpart). CPU restatement of the device decoder's semantics, used as a
- * checker of the product encoder. Format:
+/* BSCK — the engine's GPU-native chunked rANS container format (no reference
+ * counterpart). CPU restatement of the device decoder's semantics: the oracle
+ * for the product encoder and the GPU decoder. Format:
  *   [0]  "BSCK"  [4] u8 version=3  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
  *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2)
  *   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved

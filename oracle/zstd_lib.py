@@ -6,7 +6,7 @@ bigsmall/codecs/special.py:23-85), which is not installed here. Its algorithm
 is the published Zstandard format (RFC 8878), and this module checks against
 the system's reference implementation of that format, libzstd (1.4.8 in this
 image), called through ctypes:
-  - `decompress` is the checker for the GPU decoder;
+  - `decompress` is the oracle for the GPU decoder;
   - `compress` writes the frames the tests decode (any conforming frame must
     decode the same; frames written by another zstd version differ in bytes,
     not in meaning);

@@ -2,7 +2,7 @@
 container entries of the reference ("zstd", "special" lowcard).
 
 Bar: bit-exact. Every frame decodes on the GPU to its source bytes, which
-libzstd (the checker) also returns for it. The frames cover raw, RLE and
+libzstd (the oracle) also returns for it. The frames cover raw, RLE and
 compressed blocks; Huffman literals in one and four streams, with new and
 repeated trees; predefined, RLE, FSE-coded and repeated sequence tables;
 matches reaching across blocks; levels -5 to 22; content checksums; frames

@@ -1,6 +1,6 @@
 """CPU checks for the zstd-coded entries (no GPU needed).
 
-- the checker (libzstd through oracle.zstd_lib) against hand-built frames whose
+- the oracle (libzstd through oracle.zstd_lib) against hand-built frames whose
   meaning RFC 8878 fixes: an empty raw block, an RLE block, two raw blocks, a
   skippable frame between two frames;
 - the host-side framing readers of the product (Frame_Content_Size for every
@@ -22,7 +22,7 @@ KNOWN = zstd_lib.KNOWN_FRAMES
 
 
 @pytest.mark.parametrize("name", sorted(KNOWN))
-def test_checker_on_hand_built_frames(name):
+def test_oracle_on_hand_built_frames(name):
     frame, want = KNOWN[name]
     assert zstd_lib.decompress(frame, len(want)) == want
 
