@@ -101,7 +101,9 @@ constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 // dynamic LDS layout (bytes): decode table | per-wave ring areas | per-wave output staging
 constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
-constexpr uint32_t kLds = kTblBytes + kWaves * (kRingBytes + kStageMax);   // 75392: two workgroups per CU
+// each wave's progress in block pairs (u16 per wave), read by the others
+constexpr uint32_t kProgOff = kTblBytes + kWaves * (kRingBytes + kStageMax);
+constexpr uint32_t kLds = kProgOff + 2 * kWaves;   // 75408: two workgroups per CU
 
 template <bool HALF> struct SegVec { typedef u32x4 T; };
 template <> struct SegVec<true> { typedef u32x2 T; };
@@ -578,11 +580,16 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
 // are the younger of their CU's two: their bands end at 40/60/80 % of the
 // chunk's blocks, the others' at 20/40/60 %. Partial chunks, which have fewer
 // blocks, lower their priority sooner. A wrong guess (another kernel sharing
-// the CUs) changes only the order of issue. Llama-3-8B-shaped layer: 157.4 us
-// per launch without the priority, 154.9 with quarter bands for every wave,
-// 148.5 with the shifted bands (and the later prologue changes).
-__device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, bool younger) {
-  const uint32_t fifth = (blk * 5u) / nblk + (younger ? 0u : 1u);   // wave-uniform, 0..5
+// the CUs) changes only the order of issue. Within a band the oldest wave
+// still issues first, so the first waves of a workgroup ran ahead of the
+// others on their SIMD and ended some microseconds before them; a wave that
+// is two or more block pairs ahead of the slowest wave of its workgroup
+// (`lead`) therefore takes the next band's priority. Llama-3-8B-shaped
+// layer: 157.4 us per launch without the priority, 154.9 with quarter bands
+// for every wave, 148.5 with the shifted bands (and the later prologue
+// changes), 146.0 with the lead rule (147.8 on the same box without it).
+__device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, bool younger, uint32_t lead) {
+  const uint32_t fifth = (blk * 5u) / nblk + (younger ? 0u : 1u) + (lead >= 2u ? 1u : 0u);   // wave-uniform, 0..6
   if (fifth <= 1) __builtin_amdgcn_s_setprio(3);
   else if (fifth == 2) __builtin_amdgcn_s_setprio(2);
   else if (fifth == 3) __builtin_amdgcn_s_setprio(1);
@@ -639,8 +646,26 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   BS_KEEP2(F.w[0].x, F.w[1].x);
   if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
+  LDS uint16_t* prog = (LDS uint16_t*)((LDS uint8_t*)tbl + kProgOff);   // kWaves entries
+  const uint32_t pwave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   for (uint32_t blk = 0;;) {
-    progress_priority(blk, C.nblk, younger);
+    {
+      // publish this wave's pair count and take the workgroup's lowest (0xFFFF:
+      // no chunk, or done); a stale entry is lower than the true one, so the
+      // lead read here is never less than the true lead
+      const uint32_t pair = min(blk >> 1, 0xFFFEu);
+      if (C.lane == 0) *(volatile LDS uint16_t*)(prog + pwave) = (uint16_t)pair;
+      uint32_t m = 0xFFFFu;
+      if constexpr (kWaves == 8) {             // one 16-byte read
+        const u32x4 pv = *(volatile LDS u32x4*)prog;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = min(m, min(pv[i] & 0xFFFFu, pv[i] >> 16));
+      } else {
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) m = min(m, (uint32_t)((volatile LDS uint16_t*)prog)[i]);
+      }
+      progress_priority(blk, C.nblk, younger, rfl(pair - min(m, pair)));
+    }
     // ---- pair start: land the previous pair's loads, issue the next pair's
     const PlaneRegs<K> cur0 = F.pl[0], cur1 = F.pl[1];
     land_segments<K, MODE>(S, F, wring, pring, C.lane);
@@ -680,6 +705,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     flush_half<K, EB, PARTIAL, G::kBlock / 2>((C.nsteps - 1) / (G::kBlock / 2), C, stage);
   }
   // segments requested but never landed need no wait: nothing reads them
+  if (C.lane == 0) *(volatile LDS uint16_t*)(prog + pwave) = 0xFFFFu;   // out of the workgroup's lowest
 
   bool bad_state = false;
 #pragma unroll
@@ -915,6 +941,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
           u32x4{(uint32_t)e2[0], (uint32_t)(e2[0] >> 32), (uint32_t)e2[1], (uint32_t)(e2[1] >> 32)};
     }
   }
+  // progress entries (decode_chunk): 0 for a wave with a chunk, 0xFFFF for one without
+  if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
   lds_barrier();
 
   // ---- one chunk per wavefront
