@@ -587,7 +587,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
 // (`lead`) therefore takes the next band's priority. Llama-3-8B-shaped
 // layer: 157.4 us per launch without the priority, 154.9 with quarter bands
 // for every wave, 148.5 with the shifted bands (and the later prologue
-// changes), 146.0 with the lead rule (147.8 on the same box without it).
+// changes), 145.6 with the lead rule (147.8 without it on the same boxes).
 __device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, bool younger, uint32_t lead) {
   const uint32_t fifth = (blk * 5u) / nblk + (younger ? 0u : 1u) + (lead >= 2u ? 1u : 0u);   // wave-uniform, 0..6
   if (fifth <= 1) __builtin_amdgcn_s_setprio(3);
