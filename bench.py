@@ -12,7 +12,10 @@ Workload (one "step" = one batched decode of the whole layer):
   tensors of layer i mod 6 in ONE batched kernel launch: the timed working set
   (6 x 725 MB) is far beyond the 256 MB Infinity Cache, so no step is served
   from data an earlier step left there. Output is verified bit-exact (md5 per
-  tensor, every layer) after the timed region.
+  tensor, every layer) after the timed region. Before the W warm-up steps the
+  layers are decoded untimed for --settle-ms (default 50 ms): from idle the
+  GPU's clocks ramp over the first 15-20 ms of load, which a few warm-up steps
+  do not cover.
 
 Reported `value`: decoded GB/s counted as algorithmic bytes (compressed blob
 bytes read + bf16 bytes written) per second. `roofline` uses HIP events
@@ -22,7 +25,7 @@ stream that reads and writes HBM). `cpu_baseline`: the oracle's C port of the
 reference's fastest CPU decoder (bf16_se_single_kernel) on the same layer's
 seven matrices, one host thread per tensor, with a single-thread figure beside it.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms MS]
 """
 from __future__ import annotations
 
@@ -236,6 +239,24 @@ def _variants(base: np.ndarray, i: int) -> np.ndarray:
     return base ^ (flips * (base != 0)).astype(np.uint16)
 
 
+def settle(fn, ms: float) -> int:
+    """Run `fn` (one step of the workload) untimed for `ms` milliseconds of
+    wall time before the warm-up steps; returns the steps run. From idle the
+    GPU raises its clocks over the first 15-20 ms of sustained load: the
+    layer decode took 176 us per launch over its first 25 launches, 159 over
+    the next 25, and settled at 144 us after about 100 (per-launch HIP events,
+    one process), so a throughput figure taken over a few warm-up and 20
+    timed launches would time the ramp rather than the decode."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while ms > 0 and (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
 def _timed(fn, steps: int, stream):
     import torch
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -318,6 +339,7 @@ def run_model(args) -> dict:
         join = torch.cuda.Event()
         join.record(alt)
         stream.wait_event(join)
+    settle(run_all, args.settle_ms)
     run_all()
     torch.cuda.synchronize()
     st.check("model warmup")
@@ -433,6 +455,7 @@ def run_kv(args) -> dict:
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
     st = StatusWord(dev)
+    settle(lambda: batch.launch(st, stream), args.settle_ms)
     batch.launch(st, stream)
     torch.cuda.synchronize()
     st.check("kv warmup")
@@ -680,9 +703,10 @@ def run_c3(args) -> dict:
         st = StatusWord(dev)
         batches = [ChunkBatch([ChunkJob(d.data_ptr(), len(blob), o.data_ptr(), w.size, inf.n_chunks, inf.plane_mode)],
                               dev) for d, o in zip(d_blobs, outs)]
+        it = iter(range(1 << 62))
+        settle(lambda: batches[next(it) % R].launch(st, stream), args.settle_ms)
         for b in batches:
             b.launch(st, stream)
-        it = iter(range(1 << 62))
         ms = _timed(lambda: batches[next(it) % R].launch(st, stream), args.steps, stream)
         st.check(name)
         src = torch.from_numpy(w.view(np.uint8).copy()).to(dev)
@@ -909,6 +933,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=50.0,
+                    help="GPU workloads: run the workload untimed for this long before the warm-up steps, "
+                         "so that the timed steps run at the clocks sustained load settles at (0: off)")
     ap.add_argument("--chunk-steps", type=int, default=None)
     ap.add_argument("--lanes", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1006,6 +1033,8 @@ def main():
     status = StatusWord(dev)
     stream = torch.cuda.current_stream(dev)
 
+    rot = iter(range(1 << 62))
+    settled = settle(lambda: batches[next(rot) % R].launch(status, stream), args.settle_ms)
     for i in range(args.warmup):
         batches[i % R].launch(status, stream)
     torch.cuda.synchronize(dev)
@@ -1077,6 +1106,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"ms": args.settle_ms, "launches": settled},
         "ms_per_step": round(ms_per, 5),
         "higher_is_better": True,
         "scaling": "weak",
