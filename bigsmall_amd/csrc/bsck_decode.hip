@@ -942,6 +942,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     }
   }
   // progress entries (decode_chunk): 0 for a wave with a chunk, 0xFFFF for one without
+  // (and for one that leaves on an error below)
   if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
   lds_barrier();
 
@@ -962,6 +963,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   if (mode == 0) ok = ok && np == 0;
   if (!ok) {
     report(status, BS_DEV_ERR_BOUNDS);
+    if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = 0xFFFFu;
     return;
   }
   const GLB uint8_t* cbase = b + off;
