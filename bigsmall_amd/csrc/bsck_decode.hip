@@ -236,8 +236,9 @@ __device__ __forceinline__ PlaneRegs<K> load_plane(const GLB uint8_t* dplane, ui
     // Streaming load: a dense plane block is read once, in whole 256-byte
     // aligned lines, so it need not stay in the caches (8B-shaped layer:
     // 141.7 -> 140.7 us per launch). The renorm-word segments keep normal
-    // loads (152.9 us with streaming loads): a segment that a wave does not
-    // need is a load of its chunk's state words, which must stay cached.
+    // loads (152.9 us with streaming loads; likely because a segment that a
+    // wave does not need is issued as a load of its chunk's state words,
+    // which then stop being cache hits).
     const u32x4 v = __builtin_nontemporal_load((const GLB u32x4*)p);
     r.b[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
     r.b[PlaneRegs<K>::kWords - 1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
