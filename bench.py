@@ -381,7 +381,7 @@ def run_model(args) -> dict:
     _verify_device(outs, tensors, dev, "model end to end")
     return {"metric": "decoded bf16 GB/s, full Llama-3-8B-shaped model (decode from HBM)",
             "value": round(algo / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-            "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "u32",
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "dtype": "u32", "settle_ms": args.settle_ms,
             "data": "synthetic: seeded N(0,0.02) layer + embedding draws, per-layer sign-flipped variants",
             "config": {"workload": "bsck_decode_llama3_8b_model", "tensors": len(tensors), "elements": int(n_total),
                        "compressed_bytes": int(comp_total), "decoded_bytes": int(2 * n_total),
@@ -480,7 +480,7 @@ def run_kv(args) -> dict:
     gbps = (comp + out_bytes) / (ms * 1e-3) / 1e9
     return {"metric": "decoded bf16 GB/s, KV-cache block decompression (64 random 256-token blocks x 32 layers x K,V)",
             "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "ms_per_step": round(ms, 4),
-            "higher_is_better": True, "dtype": "u32",
+            "higher_is_better": True, "dtype": "u32", "settle_ms": args.settle_ms,
             "data": "synthetic: seeded N(0,1) x U[0.5,2] per head, per-layer sign-flipped variants",
             "config": {"workload": "bsck_kv_blocks_32x64", "blobs": len(batch.jobs), "compressed_bytes": int(comp),
                        "decoded_bytes": int(out_bytes), "ratio_pct": round(100 * cache.compression_ratio(), 3),
@@ -736,7 +736,8 @@ def run_c3(args) -> dict:
     return {"metric": "decoded GB/s, 8192x8192 stress tensors (forced rANS on this engine's format; forced tANS "
                       "on the reference's bf16_se_tans)",
             "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "ms_per_step": head["ms"], "higher_is_better": True,
-            "dtype": "u32", "data": "synthetic: Student-t df=3, half zeros, fp8 e4m3 + bf16 residual (seeded)",
+            "dtype": "u32", "settle_ms": args.settle_ms,
+            "data": "synthetic: Student-t df=3, half zeros, fp8 e4m3 + bf16 residual (seeded)",
             "host": host_cpu_info(), "config": {"workload": "c3_stress_8192sq", "elements_per_tensor": 8192 * 8192}, "tensors": res,
             "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": head["frac"]}}
