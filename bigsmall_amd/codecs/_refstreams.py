@@ -86,7 +86,7 @@ def inline_stream(blob: bytes, off: int, length: int, tail_is_byte: bool, what: 
 
     An odd trailing byte is one more word: the reference's rans.decode_stream
     shifts in zero for it (rans.py:196-203); numba_rans.decode_stream pads the
-    blob to even length, so the word is the byte itself (numba_rans.py:545-548)."""
+    blob to even length, so the word is the byte itself (numba_rans.py:209-210)."""
     if length < 4:
         raise ValueError(f"{what}: rANS stream too short for its state ({length} bytes)")
     x0 = struct.unpack_from("<I", blob, off)[0]
@@ -462,6 +462,9 @@ def encode_host(codec: str, raw, n_streams: int = 128, threads: int | None = Non
         return b""
     L = _native.lib()
     cid = ENCODER_IDS[codec]
+    # bf16_parallel.py:195 clamps N = max(1, min(n_streams, n)); the C encoder
+    # clamps the upper side, a count below 1 is clamped here (it takes a u32)
+    n_streams = min(max(1, int(n_streams)), n)
     cap = int(L.bs_refcodec_encode_bound(cid, n, n_streams))
     out = np.empty(cap, np.uint8)
     olen = ctypes.c_uint64(0)

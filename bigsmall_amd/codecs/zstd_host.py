@@ -17,8 +17,8 @@ import struct
 
 import numpy as np
 
-LOWCARD_MAX_UNIQUE = 16        # tensor_analysis.MAX_LOWCARD_UNIQUE (bigsmall/tensor_analysis.py:31)
-LOWCARD_MIN_BYTES = 256        # tensor_analysis.py:116-118
+from .. import tensor_analysis
+
 GENERIC_LEVEL = 9              # generic.encode_zstd default (generic.py:9)
 LOWCARD_LEVEL = 19             # special.encode_lowcard (special.py:55)
 
@@ -75,23 +75,10 @@ def _keys(raw, item_bytes: int) -> np.ndarray:
     return np.frombuffer(bytes(raw), dtype={1: "<u1", 2: "<u2", 4: "<u4"}[item_bytes])
 
 
-def count_unique(raw, item_bytes: int, cap: int = LOWCARD_MAX_UNIQUE + 1) -> int:
-    """Distinct element values, clamped to `cap`: the first 4096 elements
-    decide early, as tensor_analysis._count_unique_fast (tensor_analysis.py:37-51)."""
-    a = _keys(raw, item_bytes)
-    if a.size == 0:
-        return 0
-    if len(np.unique(a[:4096])) > cap:
-        return cap
-    return min(len(np.unique(a)), cap)
-
-
-def is_lowcard(raw, item_bytes: int) -> bool:
-    """The reference's lowcard test (tensor_analysis.py:111-119)."""
-    if item_bytes not in (1, 2, 4):
-        return False
-    n = count_unique(raw, item_bytes)
-    return 0 < n <= LOWCARD_MAX_UNIQUE and len(raw) >= LOWCARD_MIN_BYTES
+# the lowcard test and its distinct-value count are the routing module's
+# (tensor_analysis.py:37-51, 111-119 in the reference)
+count_unique = tensor_analysis.distinct_values
+is_lowcard = tensor_analysis.is_lowcard
 
 
 def encode_lowcard(raw, item_bytes: int) -> tuple[bytes, dict]:

@@ -842,8 +842,11 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t lanes = w5 & 0xFFFFu, nsym = w5 >> 16;
   const uint32_t nch = rfl(h1.z);
   const uint64_t per = (uint64_t)lanes * steps;
+  // an empty tensor (n = 0, no chunks) has no blob to decode: only a task
+  // table out of order can send a workgroup to one, and it stops here
   if ((lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || (steps % (2 * kBlockMax)) != 0 || nsym == 0 ||
-      nsym > 256 || (eb == 1 && mode != 0) || nch != T.n_chunks || per > kMaxChunk || nch != (n + per - 1) / per) {
+      nsym > 256 || (eb == 1 && mode != 0) || nch == 0 || nch != T.n_chunks || per > kMaxChunk ||
+      nch != (n + per - 1) / per) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
@@ -865,7 +868,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   // its latency passes under it (the build's barriers wait for LDS only)
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);   // wave-uniform: keeps chunk state scalar
   const uint32_t chunk = group * kWaves + wave;
-  // (nch >= 1 here; a wave past the last chunk reads the last entry and does not use it)
+  // (nch >= 1 here: checked above; a wave past the last chunk reads the last entry and does not use it)
   // a scalar load (the address is wave-uniform): its wait is on the scalar
   // counter, apart from the vector loads issued around it
   const u32x4 centry = *(const CST u32x4*)((const CST uint8_t*)b + ctab + 16ull * min(chunk, nch - 1u));

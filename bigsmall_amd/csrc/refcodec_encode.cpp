@@ -416,16 +416,23 @@ uint64_t bs_refcodec_encode_bound(int32_t codec, uint64_t n, uint32_t n_streams)
   // bf16_parallel_v1 its lengths, exponent list and bucket fields
   const uint64_t tables = 16 + kSeAlphabet * 6 + 4 + 256 * 2 + 256 * (1 + kMantAlphabet * 5);
   const uint64_t buckets = 4 + 256 * 2 + 256 * (16 + 1 + kMantAlphabet * 5);
-  const uint64_t streams = codec == BS_REF_PARALLEL ? (uint64_t)(n_streams + 1) * (4 + 12 + buckets) : 12 + buckets;
+  const uint64_t ns = std::max<uint64_t>(1, std::min<uint64_t>(n_streams, n));   // the encoder's clamp
+  const uint64_t streams = codec == BS_REF_PARALLEL ? (ns + 1) * (4 + 12 + buckets) : 12 + buckets;
   return 4 * n + tables + streams + 64;
 }
 
 int bs_refcodec_encode(int32_t codec, const uint16_t* h_src, uint64_t n, uint32_t n_streams, uint8_t* h_dst,
                        uint64_t cap, uint64_t* out_len, int n_threads) {
   if (!out_len || (n && !h_src) || codec < BS_REF_PARALLEL || codec > BS_REF_SINGLE_KERNEL) return BS_ERR_ARG;
-  if (n > 0xFFFFFFFFull || (codec == BS_REF_PARALLEL && (n_streams == 0 || n_streams > 0xFFFF))) return BS_ERR_ARG;
+  if (n > 0xFFFFFFFFull) return BS_ERR_ARG;
   *out_len = 0;
   if (n == 0) return BS_OK;               // an empty tensor is an empty blob in all three formats
+  // N = max(1, min(n_streams, n)) (bigsmall/codecs/bf16_parallel.py:195); the
+  // header stores N as a u16 (struct '<H'), so only a clamped N above 65535 fails
+  if (codec == BS_REF_PARALLEL) {
+    n_streams = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(n_streams, n));
+    if (n_streams > 0xFFFF) return BS_ERR_ARG;
+  }
   Out out;
   int rc = codec == BS_REF_PARALLEL ? par1_encode(h_src, n, n_streams, n_threads, out)
            : codec == BS_REF_TANS   ? tans_encode(h_src, n, n_threads, out)

@@ -34,8 +34,11 @@
 // process ends; host code reaches it only through the address
 // hipGetSymbolAddress returns on that device (the array's name is a host-side
 // stand-in, not a device address). Every call on one GPU shares it: the
-// kernel writes each literal before reading it, so nothing needs clearing, and
-// calls that overlap on one GPU race on it.
+// kernel writes each literal before reading it, so nothing needs clearing.
+// The library orders the calls on one GPU itself: each call's stream first
+// waits for an event recorded after the previous call's launch (one event per
+// device, created with the address lookup), so calls on different streams or
+// host threads run one after another instead of racing on the array.
 static __device__ __align__(256) uint8_t scratch[(uint64_t)BS_ZSTD_STATIC_MAX_TASKS * bs_zstd::kBlockMax];
 
 namespace {
@@ -98,21 +101,24 @@ __global__ __launch_bounds__(256) void lut_expand_kernel(const bs_lut_task* __re
 }
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
+std::mutex g_scratch_mu;                  // guards the tables below and orders the launches
 void* g_scratch_ptr[kMaxDevices] = {};
+hipEvent_t g_scratch_done[kMaxDevices] = {};   // recorded after each call's launch on that device
 
-// The current device's address of `scratch`, looked up once per device (with
-// that device current) and kept.
-int scratch_address(void** out) {
+// Set-up of the current device, once (with that device current): the address
+// of `scratch` and the ordering event. Called with g_scratch_mu held.
+int scratch_setup(int* dev_out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return BS_ERR_HIP;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return BS_ERR_HIP;
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return BS_ERR_HIP;
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = p;
   }
-  *out = g_scratch_ptr[dev];
+  *dev_out = dev;
   return BS_OK;
 }
 
@@ -137,12 +143,25 @@ int bs_zstd_decode_static(const bs_zstd_task* d_tasks, uint32_t n_tasks, uint64_
   if (!d_status || (n_tasks && (!d_tasks || !d_out_len))) return BS_ERR_ARG;
   if (n_tasks > BS_ZSTD_STATIC_MAX_TASKS) return BS_ERR_CAP;
   if (n_tasks == 0) return BS_OK;
-  void* work = nullptr;
-  const int rc = scratch_address(&work);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  int dev = -1;
+  const int rc = scratch_setup(&dev);
   if (rc != BS_OK) return rc;
-  hipLaunchKernelGGL(zstd_kernel, dim3(n_tasks), dim3(64), 0, (hipStream_t)stream, d_tasks, (uint8_t*)work,
-                     d_out_len, d_status);
-  return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
+  hipStream_t s = (hipStream_t)stream;
+  // Under stream capture the graph's own order applies (an event recorded
+  // outside the capture cannot be waited on inside it): the event is neither
+  // waited on nor recorded, and launches of two graphs that overlap race.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess) return BS_ERR_HIP;
+  const bool order = cap == hipStreamCaptureStatusNone;
+  // the previous call's launch (on any stream) has finished with the array;
+  // an event never recorded is complete
+  if (order && hipStreamWaitEvent(s, g_scratch_done[dev], 0) != hipSuccess) return BS_ERR_HIP;
+  hipLaunchKernelGGL(zstd_kernel, dim3(n_tasks), dim3(64), 0, s, d_tasks, (uint8_t*)g_scratch_ptr[dev], d_out_len,
+                     d_status);
+  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
+  if (order && hipEventRecord(g_scratch_done[dev], s) != hipSuccess) return BS_ERR_HIP;
+  return BS_OK;
 }
 
 int bs_lut_expand(const bs_lut_task* d_tasks, uint32_t n_tasks, uint64_t max_n, int32_t* d_status, void* stream) {

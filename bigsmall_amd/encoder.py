@@ -4,7 +4,8 @@ Mirrors the reference's `compress` (bigsmall/encoder.py:325-496): same header
 fields per tensor (name, shape, dtype, codec, special, compressed_bytes,
 offset, md5, extra) and per container (format, mode, model_type, base_model,
 tensor_count, tensors, safetensors_metadata, codec_stats), the same routing
-before codec selection:
+before codec selection (tensor_analysis.analyze_tensors, the reference's
+tensor_analysis.py:80-132, restated in bigsmall_amd/tensor_analysis.py):
   * tied: a tensor byte-identical (md5) to an earlier one of the same shape and
     item size, at least 1024 bytes, becomes `tied_ref` (tensor_analysis.py:97-110);
   * tiny: fewer than RAW_TINY_THRESHOLD bytes are stored `raw` (encoder.py:57, 386-388);
@@ -33,11 +34,11 @@ from typing import Optional
 
 import numpy as np
 
-from . import codec_registry, container, formats
+from . import codec_registry, container, formats, tensor_analysis
 from .codecs import zstd_host
 
 RAW_TINY_THRESHOLD = 512
-TIE_MIN_BYTES = 1024
+TIE_MIN_BYTES = tensor_analysis.TIE_MIN_BYTES
 
 
 def _tensor_record(name: str, t) -> dict:
@@ -99,26 +100,27 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
     reference_readable = gpu_optimised or prefer_speed
     data = container.DataSectionBuilder()
     stats = codec_registry.CodecStats()
-    seen: dict[tuple, int] = {}
     header_tensors = []
     # md5 of every tensor up front, on a few threads (hashlib releases the GIL
-    # on large buffers); the tie decisions below still run in tensor order
+    # on large buffers); the routing below uses them in tensor order
     from concurrent.futures import ThreadPoolExecutor
     with ThreadPoolExecutor(max(1, min(8, len(tensors)))) as pool:
         md5s = list(pool.map(lambda t: hashlib.md5(t["raw"]).hexdigest(), tensors))
+    decisions, _ = tensor_analysis.analyze_tensors(tensors, md5s)
     for i, t in enumerate(tensors):
         raw = t["raw"]
         md5 = md5s[i]
         special = None
-        key = (t["item_bytes"], tuple(t["shape"]), md5)
-        if len(raw) >= TIE_MIN_BYTES and key in seen:
-            blob, codec, extras, special = b"", "tied_ref", {"tied_to": tensors[seen[key]]["name"]}, "tied"
+        kind = decisions[i]["kind"]
+        if kind == "tied":
+            blob, codec, extras = b"", "tied_ref", {"tied_to": tensors[decisions[i]["tied_to"]]["name"]}
+            special = "tied"
         elif len(raw) < RAW_TINY_THRESHOLD:
             blob, codec, extras = raw, "raw", {"n_bytes": len(raw)}
         else:
-            if len(raw) >= TIE_MIN_BYTES:
-                seen[key] = i
-            lowcard = reference_readable and zstd_host.is_lowcard(raw, t["item_bytes"])
+            # wpe_delta takes the generic selection (its blosc2 coder is absent),
+            # as the reference's encoder does when that coder fails (encoder.py:162-168)
+            lowcard = reference_readable and kind == "lowcard"
             if lowcard:
                 try:
                     blob, extras = zstd_host.encode_lowcard(raw, t["item_bytes"])

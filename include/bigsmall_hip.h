@@ -9,8 +9,9 @@
  * into the caller-provided device word `d_status` (BS_DEV_* bits), which the
  * caller reads after synchronising. Host-side failures are returned as
  * negative BS_ERR_* codes. No entry point keeps global mutable state, except
- * bs_zstd_decode_static (a static device work area per GPU, below); calls on
- * different streams with disjoint buffers may run concurrently.
+ * bs_zstd_decode_static (a static device work area and an ordering event per
+ * GPU, below); calls on different streams with disjoint buffers may run
+ * concurrently.
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
  *   bs_chunk_*   — new GPU-native codec registered through the reference's
@@ -324,10 +325,14 @@ int bs_zstd_decode(const bs_zstd_task *d_tasks, uint32_t n_tasks, void *d_work, 
  * that forbid hipMalloc). No counterpart in the reference. The literal slices
  * live in a static device array of BS_ZSTD_STATIC_MAX_TASKS x 128 KiB (8 MiB)
  * that every GPU the library runs on holds until the process ends; more
- * tasks return BS_ERR_CAP. The call allocates nothing (the array's address is
- * looked up once per device, on its first call there). All calls on one GPU
- * share the array: calls that overlap on one GPU race, so serialise them
- * (one stream, or events). Otherwise as bs_zstd_decode. */
+ * tasks return BS_ERR_CAP. The call allocates no device memory (the array's
+ * address is looked up, and one ordering event created, once per device, on
+ * its first call there). All calls on one GPU share the array, and the
+ * library orders them: each call's stream waits for the previous call's
+ * launch on that GPU (whatever its stream or host thread) before its own
+ * launch. Under stream capture that ordering is left to the graph, so
+ * launches of two captured graphs that overlap on one GPU race. Otherwise as
+ * bs_zstd_decode. */
 #define BS_ZSTD_STATIC_MAX_TASKS 64
 int bs_zstd_decode_static(const bs_zstd_task *d_tasks, uint32_t n_tasks, uint64_t *d_out_len, int32_t *d_status,
                           void *stream);

@@ -71,7 +71,7 @@ static uint32_t rb_u32(rbuf *r) { const uint8_t *q = rb_take(r, 4); return q ? g
 /* Frequency quantisation                                                    */
 
 /* bigsmall/codecs/rans.py:34-92 (identical algorithm in
- * bigsmall/codecs/numba_rans.py:382-422). Floor-scale, force >=1 for nonzero,
+ * bigsmall/codecs/numba_rans.py:45-85). Floor-scale, force >=1 for nonzero,
  * then +/-1 round-robin over np.argsort(-scaled, kind="stable"). */
 int orc_quantise_ref(const int64_t *counts, int alphabet, uint32_t M, uint32_t *out) {
     if (alphabet <= 0) return ORC_ERR_ARG;
@@ -167,7 +167,7 @@ static int log2_pow2(uint32_t M) {
     int p = 0; while ((1u << p) != M) p++; return p;
 }
 
-/* bigsmall/codecs/rans.py:115-162 (byte-identical to numba_rans.py:483-501 and
+/* bigsmall/codecs/rans.py:115-162 (byte-identical to numba_rans.py:108-164 and
  * single_kernel.py:121-156 + its reversal). Output: [u32 final state][u16 words
  * in decode order]. Empty input -> the 4-byte state L. */
 int64_t orc_rans_encode(const int32_t *syms, size_t n, const uint32_t *freqs, int alphabet,
@@ -233,7 +233,7 @@ int orc_rans_decode(const uint8_t *data, size_t len, size_t n, const uint32_t *f
     return ORC_OK;
 }
 
-/* bigsmall/codecs/numba_rans.py:504-554 decode_stream/_decode_kernel: odd-length
+/* bigsmall/codecs/numba_rans.py:167-217 decode_stream/_decode_kernel: odd-length
  * data is zero-padded to a whole u16; state = u16[0] | u16[1] << 16 in uint32
  * arithmetic; renormalise while state < L and u16s remain. `start_u16` lets the
  * same loop serve single_kernel.py:159-190 (_rans_decode_one). */
@@ -264,7 +264,7 @@ static int nb_decode_bytes(const uint8_t *data, size_t len, size_t n, const uint
     for (size_t i = 0; i < len; i++) d[i / 2] |= (uint16_t)((uint32_t)data[i] << (8 * (i & 1)));
     uint32_t c = 0;
     for (int i = 0; i < alphabet; i++) { cum[i] = c; c += freqs[i]; }
-    /* numba_rans.py:432-439 slot_to_symbol_table */
+    /* numba_rans.py:95-102 slot_to_symbol_table */
     for (int s = 0; s < alphabet; s++)
         for (uint32_t k = 0; k < freqs[s] && cum[s] + k < M; k++) tbl[cum[s] + k] = (uint32_t)s;
     nb_decode_u16(d, n_u16, n, freqs, cum, tbl, prec, out);

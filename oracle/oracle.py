@@ -120,7 +120,7 @@ def rans_decode(data: bytes, n: int, freqs, M: int) -> np.ndarray:
 
 
 def rans_decode_nb(data: bytes, n: int, freqs, precision: int) -> np.ndarray:
-    """numba_rans.decode_stream (bigsmall/codecs/numba_rans.py:532-554)."""
+    """numba_rans.decode_stream (bigsmall/codecs/numba_rans.py:195-217)."""
     d = np.frombuffer(bytes(data), np.uint8).copy()
     f = np.ascontiguousarray(freqs, dtype=np.uint32)
     out = np.zeros(max(n, 1), np.uint32)

@@ -15,7 +15,14 @@ Output: tests/golden/ref_vectors.npz — data only (uint8/uint16/int64/uint32
 arrays): inputs and the reference's outputs. Nothing of the reference's source
 is stored. Sizes are kept small because the fallbacks run ~10 us/symbol.
 
-Usage:  python tests/golden/make_golden.py
+With --routing it instead writes tests/golden/routing_vectors.npz: the
+reference's own `tensor_analysis.analyze_tensors` (bigsmall/tensor_analysis.py,
+which imports only hashlib and numpy, loaded by path the same way) run over a
+list of tensors built to sit on each side of its thresholds; stored are the
+tensors (raw bytes, shape, item size, dtype string, name) and the decisions
+(kind and tied_to), as data.
+
+Usage:  python tests/golden/make_golden.py [--routing]
 """
 from __future__ import annotations
 
@@ -29,6 +36,7 @@ import numpy as np
 
 REF = Path("/root/reference/bigsmall/codecs")
 OUT = Path(__file__).resolve().parent / "ref_vectors.npz"
+ROUTING_OUT = Path(__file__).resolve().parent / "routing_vectors.npz"
 
 
 def _load_reference_codecs():
@@ -158,5 +166,70 @@ def main() -> None:
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(out)} arrays) in {time.time() - t0:.1f}s")
 
 
+def _routing_tensors() -> list[dict]:
+    """Tensors on both sides of analyze_tensors' thresholds: 16 / 17 distinct
+    values, 255 / 256 bytes, a first sample of 4096 elements with few values
+    followed by many, ties of equal bytes under another dtype, another shape
+    and below 1024 bytes, a tie whose master is lowcard, row-correlated 2-D
+    tensors with 16 and 15 rows, item sizes 1, 2, 4 and 8, an empty tensor."""
+    rng = np.random.default_rng(31)
+
+    def t(name, arr, dtype, shape=None):
+        a = np.ascontiguousarray(arr)
+        return {"name": name, "shape": list(shape if shape is not None else a.shape), "dtype": dtype,
+                "item_bytes": a.dtype.itemsize, "raw": a.tobytes()}
+
+    norm = lambda: _bf16_words(1.0 + rng.standard_normal(4096) * 0.01)       # C1 RMSNorm vectors
+    gauss = _bf16_words(rng.standard_normal(64 * 512) * 0.02).reshape(64, 512)
+    rows = np.arange(128)[:, None] / 20.0 + np.arange(128)[None, :] / 7.0
+    smooth = _bf16_words(1.0 + 0.1 * np.sin(rows))                          # position-embedding-like
+    rows15 = np.arange(15)[:, None] / 20.0 + np.arange(1024)[None, :] / 7.0
+    n0, n1 = norm(), norm()
+    late = np.concatenate([np.zeros(4096, np.uint16), rng.integers(0, 65536, 4096).astype(np.uint16)])
+    return [
+        t("model.layers.0.input_layernorm.weight", n0, "bfloat16"),
+        t("model.layers.0.post_attention_layernorm.weight", n1, "bfloat16"),
+        t("sixteen_values", rng.choice(rng.integers(0, 65536, 16).astype(np.uint16), 2048), "bfloat16"),
+        t("seventeen_values", np.resize(np.arange(17, dtype=np.uint16) * 3, 2048), "bfloat16"),
+        t("lowcard_255_bytes", rng.integers(0, 3, 255).astype(np.uint8), "uint8"),
+        t("lowcard_256_bytes", rng.integers(0, 3, 256).astype(np.uint8), "uint8"),
+        t("few_then_many", late, "bfloat16"),
+        t("embed", gauss, "bfloat16"),
+        t("embed_as_fp16", gauss, "float16"),                                 # same bytes, other dtype
+        t("embed_other_shape", gauss, "bfloat16", shape=[128, 256]),
+        t("small_a", _bf16_words(rng.standard_normal(400) * 0.02), "bfloat16"),
+        t("wpe", smooth, "bfloat16"),
+        t("wpe_15_rows", _bf16_words(1.0 + 0.1 * np.sin(rows15)), "bfloat16"),
+        t("fp32_three_values", rng.choice(np.array([0.0, 1.0, -1.0], np.float32), 1024), "float32"),
+        t("int64_counts", rng.integers(0, 5, 512).astype(np.int64), "int64"),
+        t("norm_copy", n0, "bfloat16"),                                       # tied to a lowcard master
+        t("zeros", np.zeros(4096, np.uint16), "bfloat16"),
+        t("empty", np.zeros(0, np.uint16), "bfloat16"),
+    ]
+
+
+def routing_main() -> None:
+    import json
+    spec = importlib.util.spec_from_file_location("bigsmall.tensor_analysis", REF.parent / "tensor_analysis.py")
+    ta = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(ta)
+    tensors = _routing_tensors()
+    # small_a appears twice: equal bytes below 1024, which are never tied
+    tensors.insert(11, dict(tensors[10], name="small_b"))
+    decisions, tied_map = ta.analyze_tensors(tensors)
+    out = {f"raw{i}": np.frombuffer(tt["raw"], np.uint8) for i, tt in enumerate(tensors)}
+    meta = [{k: tt[k] for k in ("name", "shape", "dtype", "item_bytes")} for tt in tensors]
+    out["meta"] = np.array(json.dumps(meta))
+    out["decisions"] = np.array(json.dumps(decisions))
+    out["tied_map"] = np.array(json.dumps({str(k): v for k, v in tied_map.items()}))
+    np.savez_compressed(ROUTING_OUT, **out)
+    for m, d in zip(meta, decisions):
+        print(f"{m['name']:48s} {d['kind']:10s} {d['tied_to']}")
+    print(f"wrote {ROUTING_OUT} ({ROUTING_OUT.stat().st_size} bytes)")
+
+
 if __name__ == "__main__":
-    main()
+    if "--routing" in sys.argv[1:]:
+        routing_main()
+    else:
+        main()

@@ -185,19 +185,23 @@ int main(int argc, char** argv) {
     }
   }
   // Batched launches of the clean BSCK blobs: once as they are (up to 64
-  // tasks, found by one wavefront vote), five times over (one narrowing
-  // round of the vote first) and, for the blobs of at most 256 elements,
-  // 4,200 tasks (two narrowing rounds). Some buffers sit at addresses with bit
-  // 31 of the low half set, so a lookup that widened that half with sign
-  // extension would decode from a wrong address.
+  // tasks: the task lookup's last round alone), five times over (one
+  // narrowing round of the wavefront vote first) and, for the blobs of at
+  // most 256 elements, 4,096, 4,097 and 4,200 tasks: 4,096 is the most that
+  // one narrowing round leaves at 64 (two dependent loads), 4,097 and more
+  // take two narrowing rounds (three loads). Some buffers sit at addresses
+  // with bit 31 of the low half set, so a lookup that widened that half with
+  // sign extension would decode from a wrong address.
   uint64_t batch_ok = 0, batch_bad = 0, high_bit = 0;
   std::vector<size_t> small;
   for (size_t i = 0; i < clean_bsck.size(); ++i)
     if (clean_bsck[i].n <= 256) small.push_back(i);
-  std::vector<std::vector<size_t>> plans(3);
+  std::vector<std::vector<size_t>> plans(5);
   for (size_t i = 0; i < clean_bsck.size(); ++i) plans[0].push_back(i);
   for (int r = 0; r < 5; ++r) plans[1].insert(plans[1].end(), plans[0].begin(), plans[0].end());
-  for (size_t t = 0; !small.empty() && t < 4200; ++t) plans[2].push_back(small[t % small.size()]);
+  const size_t big[3] = {4096, 4097, 4200};
+  for (int k = 0; k < 3; ++k)
+    for (size_t t = 0; !small.empty() && t < big[k]; ++t) plans[2 + k].push_back(small[t % small.size()]);
   for (const auto& plan : plans) {
     const size_t nt = plan.size();
     if (nt == 0) continue;
@@ -236,8 +240,42 @@ int main(int argc, char** argv) {
       }
     }
   }
-  printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu\n", (unsigned long long)batch_ok,
-         (unsigned long long)batch_bad, (unsigned long long)high_bit);
+  // A task table out of order whose lookup lands on an empty task (a blob
+  // whose header reads n = 0, no chunks): the workgroup must stop at the
+  // header check, flag it and read nothing past the blob. Tasks: a clean blob
+  // at wg_begin 0, the empty one at 5, the clean blob again at 1, so
+  // workgroup 1 counts two tasks at or before it and takes the second.
+  uint64_t empty_flagged = 0;
+  if (!clean_bsck.empty()) {
+    const Clean& c = clean_bsck[0];
+    Buf b0(c.blob.size()), b1(c.blob.size()), o0(c.n * c.eb), o1(c.n * c.eb), e(256), eo(16);
+    memcpy(b0.p, c.blob.data(), c.blob.size());
+    memcpy(b1.p, c.blob.data(), c.blob.size());
+    memset(e.p, 0, 256);
+    memcpy(e.p, "BSCK", 4);
+    e.p[4] = 3; e.p[5] = 2; e.p[6] = 1; e.p[7] = 12;    // version, bf16, dense plane, 12-bit precision
+    e.p[16] = 16; e.p[20] = 128; e.p[22] = 1;            // 16 steps, 128 lanes, one symbol; n = 0, no chunks
+    const uint32_t sym = (0x7Fu << 7) | (4096u << 16) | (1u << 31);
+    memcpy(e.p + 32, &sym, 4);
+    bs_chunk_info info;
+    if (bs_chunk_inspect(b0.p, c.blob.size(), &info) != BS_OK) return 5;
+    const uint32_t g = (info.n_chunks + (uint32_t)bs_chunk_chunks_per_group() - 1) / (uint32_t)bs_chunk_chunks_per_group();
+    bs_chunk_task tasks[3] = {{b0.p, c.blob.size(), o0.p, c.n, 0u, info.n_chunks},
+                              {e.p, 256u, eo.p, 0u, 5u, 0u},
+                              {b1.p, c.blob.size(), o1.p, c.n, 1u, info.n_chunks}};
+    Buf d_tasks(sizeof tasks);
+    memcpy(d_tasks.p, tasks, sizeof tasks);
+    int32_t status = 0;
+    const int rc = bs_chunk_decode_batch((const bs_chunk_task*)d_tasks.p, 3u, 1u + g, info.plane_mode, &status, nullptr);
+    if (rc == BS_OK && (status & BS_DEV_ERR_HEADER)) empty_flagged = 1;
+    else {
+      ++clean_bad;
+      fprintf(stderr, "out-of-order table with an empty task: rc %d status 0x%x\n", rc, status);
+    }
+  }
+  printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu, empty task flagged %llu\n",
+         (unsigned long long)batch_ok, (unsigned long long)batch_bad, (unsigned long long)high_bit,
+         (unsigned long long)empty_flagged);
   printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu\n", n_cases,
          (unsigned long long)clean_ok, (unsigned long long)clean_bad, (unsigned long long)refused_host,
          (unsigned long long)flagged, (unsigned long long)decoded);

@@ -16,8 +16,10 @@ makes from it, whenever that parser accepts it. Every access stays inside its
 buffer, or the sanitizer fails the run. The same corruption sweeps run on the
 GPU in smaller numbers (tests/test_gpu_bsck.py, tests/test_gpu_refcodecs.py).
 The clean BSCK blobs are also decoded together in batched launches of up to
-64 tasks, of 80 and of 4,200 (small ones), so that a workgroup finds its task
-by one, two and three rounds of the wavefront vote.
+64 tasks, five times that, and 4,096, 4,097 and 4,200 (small ones), so that a
+workgroup finds its task by one, two and three rounds of the wavefront vote
+(4,096 / 4,097 being the boundary between two and three); and a task table out
+of order sends a workgroup to an empty task, which must stop at its header.
 """
 from __future__ import annotations
 
@@ -171,9 +173,11 @@ def test_decode_kernels_under_sanitizers(tmp_path):
     assert "clean failed 0" in line, line
     assert counts["bsck_corrupt"] + counts["ref_corrupt"] >= 5000
     # every clean BSCK blob decoded in the batched launches (as they are, five times over,
-    # and 4,200 small ones), some from addresses with bit 31 set
-    ok, failed, high = (int(v) for v in re.findall(r"\d+", batch.replace("bit 31", "")))
-    assert ok == 6 * counts["bsck_clean"] + 4200 and failed == 0 and high > 0, batch
+    # and 4,096, 4,097 and 4,200 small ones), some from addresses with bit 31 set; the
+    # out-of-order table's empty task was flagged at its header check
+    ok, failed, high, empty = (int(v) for v in re.findall(r"\d+", batch.replace("bit 31", "")))
+    assert ok == 6 * counts["bsck_clean"] + 4096 + 4097 + 4200 and failed == 0 and high > 0, batch
+    assert empty == 1, batch
 
 
 @pytest.mark.skipif(not Path(CLANG).exists() or shutil.which("make") is None, reason="needs ROCm's clang++")

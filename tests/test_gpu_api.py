@@ -223,7 +223,7 @@ def _md5_tensor(t) -> str:
 
 @pytest.mark.parametrize("device", ["cuda", "cpu"])
 def test_reference_kv_cache_tests(device):
-    """Mirrors of the reference's KV-cache tests (tests/test_kv_cache.py:15-120):
+    """Mirrors of the reference's KV-cache tests (tests/test_kv_cache.py:15-119):
     entry round trip, CompressedKVCache set/get/has/len/memory_usage/
     compression_ratio, several layers, clear(). Decoding runs on the GPU; with
     device="cpu" the tensors come back to host memory."""

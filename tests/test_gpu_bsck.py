@@ -115,10 +115,12 @@ def test_batched_launch_matches_single(torch_gpu):
 
 @pytest.mark.parametrize("n_tasks", [64, 65])
 def test_batched_launch_at_the_task_lookup_boundary(torch_gpu, n_tasks):
-    """A workgroup finds its task by a wavefront vote over up to 64 tasks and
-    by binary search beyond: 64 and 65 blobs of one to three chunks each, the
-    outputs in separate allocations so that their addresses differ in every
-    bit range, each decoded bit-exact."""
+    """A workgroup finds its task by rounds of a 64-way wavefront vote: up to
+    64 tasks take the last round alone, 65 are the first count that needs a
+    narrowing round before it (the next boundary, 4,096 / 4,097 tasks, runs
+    in the CPU build of the kernel under AddressSanitizer). 64 and 65 blobs of
+    one to three chunks each, the outputs in separate allocations so that
+    their addresses differ in every bit range, each decoded bit-exact."""
     import torch
     from bigsmall_amd.codecs import bf16_chunked as bc
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes

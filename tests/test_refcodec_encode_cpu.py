@@ -75,12 +75,16 @@ def test_matches_oracle_and_round_trips(codec):
 
 def test_parallel_stream_counts_and_clamp():
     w = _bf16(np.random.default_rng(3).standard_normal(5_000) * 0.02)
-    for ns in (1, 2, 7, 128, 4999, 5000, 5001, 65535):
+    # N = max(1, min(n_streams, n)) (bf16_parallel.py:195): 0, negative and
+    # oversized counts write the clamped count's blob, as the reference does
+    for ns in (-3, 0, 1, 2, 7, 128, 4999, 5000, 5001, 65535, 100_000):
         blob, extras = bf16_parallel.encode(w.tobytes(), n_streams=ns)
-        assert blob == oracle.par1_encode(w, ns), ns
-        assert extras["n_streams"] == min(ns, w.size)
+        assert blob == oracle.par1_encode(w, max(1, min(ns, w.size))), ns
+        assert extras["n_streams"] == max(1, min(ns, w.size))
+    # a clamped N above 65535 does not fit the header's u16 (struct '<H' raises in the reference)
+    big = _bf16(np.random.default_rng(4).standard_normal(70_000) * 0.02)
     with pytest.raises(RuntimeError):
-        bf16_parallel.encode(w.tobytes(), n_streams=0)
+        bf16_parallel.encode(big.tobytes(), n_streams=66_000)
 
 
 def test_empty_and_odd_inputs():

@@ -1,6 +1,6 @@
 """Mirrors of the reference's own tests of the container, version-error and
 tiny-tensor behaviour that the drop-in keeps, and of the streaming model's helpers (no GPU needed):
-  tests/test_version_errors.py:12-73, tests/test_format_v2.py:55-103,
+  tests/test_version_errors.py:12-72, tests/test_format_v2.py:55-103,
   tests/test_raw_tiny.py:30-110, tests/test_streaming_inference.py:14-55.
 The decode half of the tiny-tensor round trip runs on the GPU in the reference's
 API tests; here the raw blobs are compared byte for byte."""

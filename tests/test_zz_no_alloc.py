@@ -4,8 +4,10 @@ tasks decoded by bs_zstd_decode with a caller-allocated work buffer.
 
 Bar: bit-exact. Two calls in a row, the second with fewer and smaller frames,
 so the second runs over scratch the first left behind; both must equal the
-work-buffer entry point's output and the frames' source bytes. More tasks than
-the static array holds are refused on the host, before any launch.
+work-buffer entry point's output and the frames' source bytes. Then two calls
+on two streams issued back to back, which the library orders on the shared
+array: each must decode its own frames exactly. More tasks than the static
+array holds are refused on the host, before any launch.
 """
 from __future__ import annotations
 
@@ -41,12 +43,12 @@ def _frames(seed: int, count: int, max_n: int):
     return srcs, frames
 
 
-def _run(srcs, frames, static: bool):
-    from bigsmall_amd import _native
+def _prepare(srcs, frames):
+    """Device copies of the frames, output buffers, the task table and the
+    status word, all in place (synchronised) before any decode is issued."""
     from bigsmall_amd.codecs.zstd_gpu import ZSTD_TASK_DTYPE
     from bigsmall_amd.device import StatusWord, upload_bytes
     dev = torch.device("cuda", 0)
-    L = _native.lib()
     d_src = [upload_bytes(np.frombuffer(f, np.uint8), dev) for f in frames]
     d_dst = [torch.full((len(s),), 0xA5, dtype=torch.uint8, device=dev) for s in srcs]
     t = np.zeros(len(frames), ZSTD_TASK_DTYPE)
@@ -55,18 +57,41 @@ def _run(srcs, frames, static: bool):
     d_tasks = upload_bytes(t.view(np.uint8), dev)
     out_len = torch.zeros(len(frames), dtype=torch.int64, device=dev)
     st = StatusWord(dev)
-    s = torch.cuda.current_stream(dev).cuda_stream
+    torch.cuda.synchronize(dev)
+    return d_src, d_dst, d_tasks, out_len, st
+
+
+def _issue(prep, static: bool, stream=None):
+    """Issue one decode call over prepared buffers on `stream` (the current
+    stream by default) without waiting for it; returns what _collect needs,
+    which keeps every buffer alive until then."""
+    from bigsmall_amd import _native
+    d_src, d_dst, d_tasks, out_len, st = prep
+    dev = torch.device("cuda", 0)
+    L = _native.lib()
+    frames = len(d_src)
+    s = (stream or torch.cuda.current_stream(dev)).cuda_stream
+    work = None
     if static:
-        rc = L.bs_zstd_decode_static(d_tasks.data_ptr(), len(frames), out_len.data_ptr(), st.ptr, s)
+        rc = L.bs_zstd_decode_static(d_tasks.data_ptr(), frames, out_len.data_ptr(), st.ptr, s)
         _native.check(rc, "bs_zstd_decode_static")
     else:
-        wb = int(L.bs_zstd_work_bytes(len(frames)))
+        wb = int(L.bs_zstd_work_bytes(frames))
         work = torch.empty(wb, dtype=torch.uint8, device=dev)
-        rc = L.bs_zstd_decode(d_tasks.data_ptr(), len(frames), work.data_ptr(), wb, out_len.data_ptr(), st.ptr, s)
+        rc = L.bs_zstd_decode(d_tasks.data_ptr(), frames, work.data_ptr(), wb, out_len.data_ptr(), st.ptr, s)
         _native.check(rc, "bs_zstd_decode")
-    torch.cuda.synchronize(dev)
+    return d_src, d_dst, d_tasks, out_len, st, work
+
+
+def _collect(issued):
+    _, d_dst, _, out_len, st, _ = issued
+    torch.cuda.synchronize()
     st.check("zstd")
     return [d.cpu().numpy().tobytes() for d in d_dst], out_len.cpu().tolist()
+
+
+def _run(srcs, frames, static: bool):
+    return _collect(_issue(_prepare(srcs, frames), static))
 
 
 def test_static_scratch_entry_matches_work_buffer_entry():
@@ -81,6 +106,20 @@ def test_static_scratch_entry_matches_work_buffer_entry():
         for i, (a, b, src) in enumerate(zip(got_s, got_w, srcs)):
             assert a == b == src, (call, i)
     L = _native.lib()
+    # two calls on two streams issued back to back, neither waited for before
+    # the other is issued: the library orders them on the shared array, so
+    # each decodes its own frames exactly
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    srcs1, frames1 = _frames(3, 48, 200_000)
+    srcs2, frames2 = _frames(4, 40, 150_000)
+    _say("[no-alloc] two calls on two streams")
+    p1, p2 = _prepare(srcs1, frames1), _prepare(srcs2, frames2)
+    i1 = _issue(p1, static=True, stream=a)
+    i2 = _issue(p2, static=True, stream=b)
+    for srcs, issued in ((srcs1, i1), (srcs2, i2)):
+        got, lens = _collect(issued)
+        assert lens == [len(x) for x in srcs]
+        assert got == srcs
     too_many = _native.lib().bs_zstd_decode_static(1 << 12, 65, 1 << 12, 1 << 12, None)
     assert too_many == _native.BS_ERR_CAP
     assert L.bs_zstd_decode_static(0, 0, 0, 1 << 12, None) == _native.BS_OK
