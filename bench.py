@@ -673,10 +673,12 @@ def cpu_baseline_c3(tensors) -> dict:
 
 
 def run_c3(args) -> dict:
-    """The 8192x8192 stress tensors decoded on the GPU: forced rANS = this
-    engine's bf16_chunked_v1 / fp8_chunked_v1 (one launch per tensor), forced
-    tANS = the reference's bf16_se_tans (wave-serial path), the latter beside
-    the oracle's C decoder on one host thread."""
+    """The 8192x8192 stress tensors decoded on the GPU, one launch per tensor:
+    forced rANS = this engine's bf16_chunked_v1 / fp8_chunked_v1 and forced
+    tANS = its bf16_chunked_tans_v1 / fp8_chunked_tans_v1 (fp8 as exponent
+    pairs, the automatic choice); beside them the reference's forced-tANS
+    format bf16_se_tans (wave-serial path), with the oracle's C decoder of it
+    on one host thread."""
     import torch
     from bigsmall_amd.codecs import _refstreams
     from bigsmall_amd.codecs import bf16_chunked as bc
@@ -693,32 +695,40 @@ def run_c3(args) -> dict:
     # the GPU; 128 steps fill them (4,096 chunks) at a small ratio cost
     steps = args.chunk_steps or 128
     R = max(1, args.rotate)
+    coders = [("rans_bsck", bc.CODER_RANS), ("tans_bsck", bc.CODER_TANS)]
+    if args.rans_only:
+        coders = coders[:1]
     for name, w in tensors:
-        blob = bc.encode_array(w, steps=steps, lanes=args.lanes or bc.DEFAULT_LANES)
-        inf = bc.info(blob)
-        # R copies of the blob and of the output, decoded in turn: the working
-        # set (R x up to 245 MB) is far beyond the 256 MB Infinity Cache
-        d_blobs = [upload_bytes(blob, dev) for _ in range(R)]
-        outs = [torch.empty(w.nbytes, dtype=torch.uint8, device=dev) for _ in range(R)]
-        st = StatusWord(dev)
-        batches = [ChunkBatch([ChunkJob(d.data_ptr(), len(blob), o.data_ptr(), w.size, inf.n_chunks, inf.plane_mode)],
-                              dev) for d, o in zip(d_blobs, outs)]
-        it = iter(range(1 << 62))
-        settle(lambda: batches[next(it) % R].launch(st, stream), args.settle_ms)
-        for b in batches:
-            b.launch(st, stream)
-        ms = _timed(lambda: batches[next(it) % R].launch(st, stream), args.steps, stream)
-        st.check(name)
-        src = torch.from_numpy(w.view(np.uint8).copy()).to(dev)
-        for i, o in enumerate(outs):
-            assert torch.equal(o, src), f"{name}: copy {i} differs from the source"
-        del src, outs, d_blobs, batches
-        gbps = (len(blob) + w.nbytes) / (ms * 1e-3) / 1e9
-        res[name] = {"rans_bsck": {"ms": round(ms, 4), "GBps": round(gbps, 2), "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                                   "ratio_pct": round(100 * len(blob) / w.nbytes, 3), "plane_mode": inf.plane_mode,
-                                   "elem_bytes": inf.elem_bytes, "chunk_steps": steps, "distinct_copies": R}}
-        log(f"[c3] {name}: bf16/fp8_chunked {ms:.3f} ms, {gbps:.0f} GB/s, ratio {100 * len(blob) / w.nbytes:.2f} %")
-    for name, (blob, cpu_gbps) in ({} if args.rans_only else cpu_baseline_c3(tensors)).items():
+        res[name] = {}
+        for key, coder in coders:
+            blob = bc.encode_array(w, steps=steps, lanes=args.lanes or bc.DEFAULT_LANES, coder=coder)
+            inf = bc.info(blob)
+            # R copies of the blob and of the output, decoded in turn: the working
+            # set (R x up to 245 MB) is far beyond the 256 MB Infinity Cache
+            d_blobs = [upload_bytes(blob, dev) for _ in range(R)]
+            outs = [torch.empty(w.nbytes, dtype=torch.uint8, device=dev) for _ in range(R)]
+            st = StatusWord(dev)
+            batches = [ChunkBatch([ChunkJob(d.data_ptr(), len(blob), o.data_ptr(), w.size, inf.n_chunks,
+                                            inf.plane_mode)], dev) for d, o in zip(d_blobs, outs)]
+            it = iter(range(1 << 62))
+            settle(lambda: batches[next(it) % R].launch(st, stream), args.settle_ms)
+            for b in batches:
+                b.launch(st, stream)
+            ms = _timed(lambda: batches[next(it) % R].launch(st, stream), args.steps, stream)
+            st.check(f"{name} {key}")
+            src = torch.from_numpy(w.view(np.uint8).copy()).to(dev)
+            for i, o in enumerate(outs):
+                assert torch.equal(o, src), f"{name} {key}: copy {i} differs from the source"
+            del src, outs, d_blobs, batches
+            gbps = (len(blob) + w.nbytes) / (ms * 1e-3) / 1e9
+            res[name][key] = {"codec": (bc.CODEC_BF16 if w.dtype == np.uint16 else bc.CODEC_FP8) if coder == 0 else
+                              (bc.CODEC_BF16_TANS if w.dtype == np.uint16 else bc.CODEC_FP8_TANS),
+                              "ms": round(ms, 4), "GBps": round(gbps, 2), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                              "ratio_pct": round(100 * len(blob) / w.nbytes, 3), "plane_mode": inf.plane_mode,
+                              "elem_bytes": inf.elem_bytes, "chunk_steps": steps, "distinct_copies": R}
+            log(f"[c3] {name}: {key} mode {inf.plane_mode} {ms:.4f} ms, {gbps:.0f} GB/s "
+                f"({100 * gbps / HBM_PEAK_GBPS:.1f} %), ratio {100 * len(blob) / w.nbytes:.2f} %")
+    for name, (blob, cpu_gbps) in ({} if args.rans_only or args.engine_only else cpu_baseline_c3(tensors)).items():
         w = dict(tensors)[name]
         d_blob = upload_bytes(blob, dev)
         out = torch.empty(w.size, dtype=torch.int16, device=dev)
@@ -728,13 +738,13 @@ def run_c3(args) -> dict:
         st.check(name)
         assert out.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), name
         gbps = (len(blob) + w.nbytes) / (ms * 1e-3) / 1e9
-        res[name]["tans_reference_format"] = {"ms": round(ms, 1), "GBps": round(gbps, 4),
+        res[name]["tans_reference_format"] = {"codec": "bf16_se_tans", "ms": round(ms, 1), "GBps": round(gbps, 4),
                                               "ratio_pct": round(100 * len(blob) / w.nbytes, 3),
                                               "cpu_baseline_GBps_1_thread": round(cpu_gbps, 4)}
         log(f"[c3] {name}: bf16_se_tans {ms:.0f} ms on GPU, oracle CPU {cpu_gbps:.3f} GB/s")
     head = res[next(iter(res))]["rans_bsck"]
-    return {"metric": "decoded GB/s, 8192x8192 stress tensors (forced rANS on this engine's format; forced tANS "
-                      "on the reference's bf16_se_tans)",
+    return {"metric": "decoded GB/s, 8192x8192 stress tensors (forced rANS and forced tANS on this engine's format; "
+                      "the reference's bf16_se_tans beside them)",
             "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "ms_per_step": head["ms"], "higher_is_better": True,
             "dtype": "u32", "settle_ms": args.settle_ms,
             "data": "synthetic: Student-t df=3, half zeros, fp8 e4m3 + bf16 residual (seeded)",
@@ -960,9 +970,11 @@ def main():
                     help="c3 workload: comma-separated subset of studentt,halfzero,fp8_e4m3,fp8_residual")
     ap.add_argument("--ref-codecs", default="",
                     help="reflayer workload: comma-separated subset of bf16_parallel_v1,bf16_se_tans")
+    ap.add_argument("--engine-only", action="store_true",
+                    help="c3 workload: only this engine's format, rANS and tANS (skip the reference-format "
+                         "bf16_se_tans decode and its CPU baseline)")
     ap.add_argument("--rans-only", action="store_true",
-                    help="c3 workload: only this engine's format (skip the reference-format tANS decode and its "
-                         "CPU baseline)")
+                    help="c3 workload: only this engine's format under rANS")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()

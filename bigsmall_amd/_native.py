@@ -32,7 +32,7 @@ class NativeLibraryMissing(RuntimeError):
 class BsChunkInfo(ctypes.Structure):
     _fields_ = [("n", ctypes.c_uint64), ("n_chunks", ctypes.c_uint32), ("steps", ctypes.c_uint32),
                 ("lanes", ctypes.c_uint32), ("n_syms", ctypes.c_uint32), ("elem_bytes", ctypes.c_uint32),
-                ("plane_mode", ctypes.c_uint32)]
+                ("plane_mode", ctypes.c_uint32), ("coder", ctypes.c_uint32)]
 
 
 # (restype, argtypes) of every symbol include/bigsmall_hip.h declares
@@ -46,6 +46,8 @@ SIGNATURES = {
     "bs_chunk_decode_batch": (_INT, [_P, _U32, _U32, _U32, _P, _P]),
     "bs_chunk_encode_bound": (_INT, [_U64, _U32, _U32, _U32, ctypes.POINTER(_U64)]),
     "bs_chunk_encode": (_INT, [_P, _U64, _U32, _U32, _U32, _I32, _P, _U64, ctypes.POINTER(_U64), _INT]),
+    "bs_chunk_encode_bound_ex": (_INT, [_U64, _U32, _U32, _U32, _I32, ctypes.POINTER(_U64)]),
+    "bs_chunk_encode_ex": (_INT, [_P, _U64, _U32, _U32, _U32, _I32, _I32, _P, _U64, ctypes.POINTER(_U64), _INT]),
     "bs_refcodec_decode": (_INT, [_P, _U32, _P, _P, _P, _U32, _P, _U32, _P, _U64, _P, _P, _P]),
     "bs_refcodec_serial_work_bytes": (_U64, [_U64, _U32]),
     "bs_chunk_encode_gpu_work_bytes": (_U64, [_U32, _U64, _U32]),

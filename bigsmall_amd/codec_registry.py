@@ -75,6 +75,12 @@ def _dec_raw(blob, extras, n_weights):
 
 register_codec(bf16_chunked.CODEC_BF16, _enc_bf16_chunked, bf16_chunked.decode)
 register_codec(bf16_chunked.CODEC_FP8, _enc_fp8_chunked, bf16_chunked.decode_fp8)
+# the same format with the tANS coder: forced by a CODEC_CANDIDATES override, as
+# the reference forces its codecs (tests/test_b4_auto_select.py:121-132 there)
+register_codec(bf16_chunked.CODEC_BF16_TANS, lambda raw, **ctx: bf16_chunked.encode_tans(raw, **ctx),
+               bf16_chunked.decode)
+register_codec(bf16_chunked.CODEC_FP8_TANS, lambda raw, **ctx: bf16_chunked.encode_fp8_tans(raw, **ctx),
+               bf16_chunked.decode_fp8)
 register_codec(bf16_parallel.CODEC, bf16_parallel.encode, bf16_parallel.decode)
 register_codec(bf16_tans.CODEC, bf16_tans.encode, bf16_tans.decode)
 register_codec(single_kernel.CODEC, single_kernel.encode, single_kernel.decode)

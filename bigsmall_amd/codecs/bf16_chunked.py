@@ -1,14 +1,18 @@
-"""`bf16_chunked_v1` / `fp8_chunked_v1`: the engine's GPU-native codec.
+"""`bf16_chunked_v1` / `fp8_chunked_v1` (rANS) and `bf16_chunked_tans_v1` /
+`fp8_chunked_tans_v1` (tANS): the engine's GPU-native codecs.
 
 A tensor is cut into chunks of `lanes` x `steps` elements (128 x 432 by
-default). Each chunk is `lanes` interleaved rANS states (lanes / 64 per
-wavefront lane) over the tensor's exponent (or exact-value) symbols, sharing
-one 16-bit renormalisation word stream, plus raw sign|mantissa bytes. Full
-chunks own 512-element units of the tensor interleaved across all of them
-(chunk c: units c, nf + c, 2 nf + c, ...), so the chunks a launch decodes side
-by side write neighbouring addresses; their dense planes are interleaved the
-same way in one region of the blob. The blob layout is documented in
-bigsmall_amd/csrc/bsck_decode.hip.
+default). Each chunk is `lanes` interleaved entropy-coder states (lanes / 64
+per wavefront lane) over the tensor's exponent (or exact-value) symbols,
+sharing one stream per chunk, plus raw sign|mantissa bytes. The rANS codecs
+share a 16-bit renormalisation word stream; the tANS codecs a bit stream
+that each state reads its table-given bit count from. fp8 tensors code
+pairs of exponent fields as one symbol when that is smaller (plane mode 3).
+Full chunks own 512-element units of the tensor interleaved across all of
+them (chunk c: units c, nf + c, 2 nf + c, ...), so the chunks a launch
+decodes side by side write neighbouring addresses; their dense planes are
+interleaved the same way in one region of the blob. The blob layout is
+documented in bigsmall_amd/csrc/bsck_decode.hip.
 
 Plugin shape of the reference codec API (bigsmall/codec_registry.py:39-42):
     encode(raw: bytes, **ctx) -> (blob, extras)
@@ -30,6 +34,9 @@ from ..device import (ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, re
 
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
+CODEC_BF16_TANS = "bf16_chunked_tans_v1"
+CODEC_FP8_TANS = "fp8_chunked_tans_v1"
+CODER_RANS, CODER_TANS = 0, 1
 # 432 steps x 128 states = 55,296 elements per chunk: a Llama-3-8B-shaped
 # layer is 3,948 chunks in 497 eight-wave workgroups, one dispatch round of
 # the 512 workgroup slots of 256 CUs (two per CU), with 15 CUs holding one
@@ -40,7 +47,7 @@ CODEC_FP8 = "fp8_chunked_v1"
 # state per 432 elements).
 DEFAULT_STEPS = 432
 DEFAULT_LANES = 128
-MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT = -1, 0, 1, 2
+MODE_AUTO, MODE_EXACT, MODE_DENSE, MODE_COMPACT, MODE_PAIRS = -1, 0, 1, 2, 3
 
 
 def _threads() -> int:
@@ -48,8 +55,9 @@ def _threads() -> int:
 
 
 def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO,
-                 threads: int | None = None, lanes: int = DEFAULT_LANES) -> bytes:
-    """Encode a uint16 (bf16 words) or uint8 (fp8 bytes) array."""
+                 threads: int | None = None, lanes: int = DEFAULT_LANES, coder: int = CODER_RANS) -> bytes:
+    """Encode a uint16 (bf16 words) or uint8 (fp8 bytes) array with the rANS
+    (coder 0) or tANS (coder 1) coder."""
     a = np.ascontiguousarray(arr)
     if a.dtype not in (np.uint16, np.uint8):
         raise TypeError("encode_array expects uint16 (bf16 bit patterns) or uint8 (fp8 bytes)")
@@ -59,11 +67,12 @@ def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_A
         return b""
     L = _native.lib()
     bound = ctypes.c_uint64()
-    _native.check(L.bs_chunk_encode_bound(n, eb, lanes, steps, ctypes.byref(bound)), "bs_chunk_encode_bound")
+    _native.check(L.bs_chunk_encode_bound_ex(n, eb, lanes, steps, coder, ctypes.byref(bound)),
+                  "bs_chunk_encode_bound_ex")
     out = np.empty(bound.value, np.uint8)
     olen = ctypes.c_uint64()
-    _native.check(L.bs_chunk_encode(a.ctypes.data, n, eb, lanes, steps, mode, out.ctypes.data, bound.value,
-                                    ctypes.byref(olen), threads or _threads()), "bs_chunk_encode")
+    _native.check(L.bs_chunk_encode_ex(a.ctypes.data, n, eb, lanes, steps, mode, coder, out.ctypes.data, bound.value,
+                                       ctypes.byref(olen), threads or _threads()), "bs_chunk_encode_ex")
     return out[: olen.value].tobytes()
 
 
@@ -243,8 +252,24 @@ def encode(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -
     return blob, {"steps": steps}
 
 
-def encode_fp8(raw: bytes, steps: int = DEFAULT_STEPS, **_) -> tuple[bytes, dict]:
-    blob = encode_array(np.frombuffer(raw, dtype=np.uint8), steps=steps, mode=MODE_EXACT)
+def encode_fp8(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:
+    """fp8 raw bytes -> (blob, extras): byte symbols or exponent-pair symbols,
+    whichever codes smaller."""
+    blob = encode_array(np.frombuffer(raw, dtype=np.uint8), steps=steps, mode=mode)
+    return blob, {"steps": steps}
+
+
+def encode_tans(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:
+    """bf16 raw bytes -> (blob, extras), tANS coder."""
+    if len(raw) % 2:
+        raise ValueError(f"BF16 byte length must be even, got {len(raw)}")
+    blob = encode_array(np.frombuffer(raw, dtype="<u2"), steps=steps, mode=mode, coder=CODER_TANS)
+    return blob, {"steps": steps}
+
+
+def encode_fp8_tans(raw: bytes, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO, **_) -> tuple[bytes, dict]:
+    """fp8 raw bytes -> (blob, extras), tANS coder."""
+    blob = encode_array(np.frombuffer(raw, dtype=np.uint8), steps=steps, mode=mode, coder=CODER_TANS)
     return blob, {"steps": steps}
 
 

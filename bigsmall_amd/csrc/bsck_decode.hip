@@ -1,63 +1,85 @@
-// BSCK decode: the GPU-native chunked rANS format of the BigSmall decode
-// engine, decoded on CDNA4 (gfx950).
+// BSCK decode: the GPU-native chunked entropy-coded format of the BigSmall
+// decode engine, decoded on CDNA4 (gfx950), with either of two coders.
 //
 // Format (little-endian; produced by bsck_encode.cpp):
-//   [0]  "BSCK"  [4] u8 version=3  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+//   [0]  "BSCK"  [4] u8 version (3; 2 = the earlier chunk-contiguous layout,
+//        read too)  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
 //   [7]  u8 prec_log2 = 12  [8] u64 n  [16] u32 steps  [20] u16 lanes = 64*K
-//   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
+//   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS, 1 tANS), 3 zero bytes
 //   [32] n_syms x u32 symbol entries: bits 0..15 output value (bf16 word with
-//        zero sign/mantissa for exponent symbols, or the exact word/byte),
-//        bits 16..28 quantised frequency (sum 4096), bit 31 = reads one plane byte
-//   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
-//   pad to 256; plane_mode 1 only: the dense plane region, nf*per bytes
+//        zero sign/mantissa for exponent symbols, the exact word/byte, or an
+//        exponent pair e0 | e1 << 4), bits 16..28 quantised frequency (sum
+//        4096), bit 31 = reads one plane byte
+//   pad to 16; tANS only: 4096 x u32 decode table {newX:12, nb:4, symbol:8, 0:8}
+//   n_chunks x {u64 offset, u32 n_words (rANS: renorm words; tANS: stream
+//        bits), u32 n_plane}
+//   pad to 256; plane_mode 1 and 3 only: the dense plane region, nf*per bytes
 //   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l) |
-//        n_words x u16 renorm words (pad 16) | n_plane plane bytes (pad 16),
-//        the plane bytes omitted for a full chunk in plane_mode 1
+//        the stream (rANS: n_words x u16 renorm words; tANS: whole u32 words
+//        of an LSB-first bit stream), pad 16 | n_plane plane bytes (pad 16),
+//        the plane bytes omitted for a full chunk in plane_mode 1 and 3
 //   pad to 256 (the blob length is a multiple of 256)
+// Version 2 has no plane region (every plane inline), coder 0, no plane mode
+// 3, chunks holding contiguous elements (c*per + j) and 16-byte padding.
 //
-// Chunks and elements: per = 64*K*steps elements per chunk (at most 2^24), nf = n / per full
-// chunks, and a partial chunk (c = nf) when per does not divide n. A full
-// chunk's elements are 512-element units of the tensor interleaved across the
-// full chunks: chunk element j is tensor element ((j/512)*nf + c)*512 + j%512.
-// The partial chunk holds the tail: chunk element j is element nf*per + j.
-// The chunks that run side by side therefore read and write neighbouring
-// addresses, which the memory system serves faster than one separate stream
-// per chunk. The dense planes of the full chunks are interleaved the same way,
-// per plane block (B*64*K bytes, below): block b of full chunk c is block
-// b*nf + c of the plane region.
+// Chunks and elements: per = 64*K*steps coded elements per chunk (at most
+// 2^24), nf = ne / per full chunks (ne = n, or n / 2 in plane mode 3, whose
+// coded elements are byte pairs), and a partial chunk (c = nf) when per does
+// not divide ne. A full chunk's elements are 512-element units of the tensor
+// interleaved across the full chunks: chunk element j is tensor element
+// ((j/512)*nf + c)*512 + j%512. The partial chunk holds the tail: chunk
+// element j is element nf*per + j. The chunks that run side by side therefore
+// read and write neighbouring addresses, which the memory system serves faster
+// than one separate stream per chunk. The dense planes of the full chunks are
+// interleaved the same way, per plane block (B*64*K bytes, below): block b of
+// full chunk c is block b*nf + c of the plane region.
 //
-// A chunk is decoded by one wavefront. Lane l owns K interleaved rANS states
+// A chunk is decoded by one wavefront. Lane l owns K interleaved states
 // (g = 0..K-1); at step t state (g, l) decodes element t*64K + l*K + g of the
 // chunk, so a lane's K outputs of a step are adjacent and one step of the
-// wavefront produces 64*K consecutive elements. The 64*K states share one
-// 16-bit renorm word stream, consumed per step group by group (g ascending),
-// lanes ascending among the lanes whose state fell below L = 2^16; the words
-// are placed with a wavefront ballot + mbcnt prefix.
-// Plane bytes (sign<<7 | mantissa) complete bf16 exponent symbols:
-//   plane_mode 1 (dense): every element has one, stored per block of B steps
-//                         (B = 8 for K <= 2, 4 for K = 4) with lane l's B*K
-//                         bytes contiguous, step-major (byte q*K+g); the
-//                         blocks of a full chunk in the plane region, of the
-//                         partial chunk inline;
+// wavefront produces 64*K consecutive elements.
+// Plane bytes complete the symbols that have one:
+//   plane_mode 1 (dense): every element has one (sign<<7 | mantissa of a bf16
+//                         word), stored per block of B steps (B = 8 for
+//                         K <= 2, 4 for K = 4) with lane l's B*K bytes
+//                         contiguous, step-major (byte q*K+g); the blocks of a
+//                         full chunk in the plane region, of the partial chunk
+//                         inline;
+//   plane_mode 3 (pairs): as mode 1, the plane byte of a pair of fp8 e4m3
+//                         bytes being m0 | s1 << 3 | m1 << 4 | s0 << 7;
 //   plane_mode 2 (compact): only elements whose symbol has bit 31 set have one,
-//                         in decode order (ballot + mbcnt again);
+//                         in decode order (rANS: a byte area after the words,
+//                         ballot + mbcnt placed; tANS: 8 bits in the stream
+//                         after the element's state bits);
 //   plane_mode 0: no plane (every symbol is an exact value).
 //
-// rANS state machine (the same as the reference's, bigsmall/codecs/rans.py:165-207:
+// rANS (coder 0; the reference's state machine, bigsmall/codecs/rans.py:165-207:
 // 32-bit state, L = 2^16, 16-bit renormalisation, M = 2^12):
 //   slot = x & 4095; s = sym(slot); x = f[s]*(x>>12) + slot - cf[s];
 //   if x < L: x = (x << 16) | next_word
-// A valid chunk ends with every state back at x == L and every word and plane
-// byte consumed; anything else is reported as BS_DEV_ERR_STREAM.
+// The 64*K states share one 16-bit renorm word stream, consumed per step
+// group by group (g ascending), lanes ascending among the lanes whose state
+// fell below L = 2^16; the words are placed with a wavefront ballot + mbcnt
+// prefix. A valid chunk ends with every state back at x == L and every word
+// and plane byte consumed.
+// tANS (coder 1): X in [0, 4096); e = table[X]; s = e's symbol;
+//   X = newX | next nb bits  (newX has nb zero low bits)
+// Each step every lane reads its K states' bits in order (and a compact
+// symbol's 8 plane bits after its state bits) from one stream position:
+// the wavefront's inclusive prefix sum of the lanes' bit counts (DPP). A
+// valid chunk ends with every X == 0 and every bit read.
+// Anything else is reported as BS_DEV_ERR_STREAM.
 //
-// Three decode-table layouts live in LDS (4096 slots x 8 bytes):
-//   dense bf16 (plane_mode 1): {f | exponent << 24, slot - cf}; the update is
+// Decode-table layouts in LDS (4096 slots):
+//   rANS dense bf16 (plane_mode 1): {f | exponent << 24, slot - cf}; the update is
 //     one shift and one v_mad_u32_u24 (which ignores bits 24..31 of f's word),
 //     and the exponent byte is placed with v_perm;
-//   bytes (elem_bytes 1): {f | value << 24, slot - cf}, the same update, the
-//     output byte taken from bits 24..31 with v_perm;
-//   generic (bf16 plane modes 0/2): {f, value | (slot - cf) << 16 | consume << 31};
-//     the update is one shift, one bit-field extract and one v_mad_u32_u24.
+//   rANS bytes and pairs (elem_bytes 1): {f | value << 24, slot - cf}, the same
+//     update, the output byte taken from bits 24..31 with v_perm;
+//   rANS generic (bf16 plane modes 0/2): {f, value | (slot - cf) << 16 | consume << 31};
+//     the update is one shift, one bit-field extract and one v_mad_u32_u24;
+//   tANS dense, bytes and pairs: one word {newX, nb, -, output byte};
+//   tANS generic: {newX | nb << 12 | (nb + raw) << 16 | raw << 21, value | consume << 31}.
 #include <stdint.h>
 
 #include "simt.h"
@@ -103,7 +125,10 @@ constexpr uint32_t kTblBytes = 4096 * 8;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
 // each wave's progress in block pairs (u16 per wave), read by the others
 constexpr uint32_t kProgOff = kTblBytes + kWaves * (kRingBytes + kStageMax);
-constexpr uint32_t kLds = kProgOff + 2 * kWaves;   // 75408: two workgroups per CU
+// a workgroup-wide flag set by any thread whose run of a tANS table fails its check
+constexpr uint32_t kFlagOff = kProgOff + ((2 * kWaves + 15) & ~15u);
+constexpr uint32_t kLds = kFlagOff + 16;           // 75424: two workgroups per CU
+constexpr uint32_t kTansSlots = 4096;              // tANS table positions (12-bit states)
 
 template <bool HALF> struct SegVec { typedef u32x4 T; };
 template <> struct SegVec<true> { typedef u32x2 T; };
@@ -186,6 +211,28 @@ __device__ __forceinline__ void report(int32_t* status, int32_t bits) {
 
 __device__ __forceinline__ uint32_t byte_merge(uint32_t v, uint32_t b) { return ((b * 0x101u) & 0x807Fu) | v; }
 
+// Inclusive prefix sum over the wavefront's 64 lanes: DPP adds of the value
+// 1, 2, 4 and 8 lanes below within each 16-lane row, then of lane 15's row
+// total into rows 1 and 3 and of lane 31's (rows 0-1) into rows 2 and 3.
+// Six VALU instructions; lanes without a source add 0.
+__device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);   // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);   // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);   // row_bcast:31
+  return v;
+}
+
+// 32 bits of a tANS chunk's stream from bit `pos` (LSB first), out of the
+// wave's word ring seen as 1,024 u32 words: two ring words, the second
+// covered by the ring's mirrored head when the first is the last.
+__device__ __forceinline__ uint32_t stream_bits(const LDS uint32_t* ring, uint32_t pos) {
+  const uint32_t w = (pos >> 5) & 1023u;
+  return __builtin_amdgcn_alignbit(ring[w + 1], ring[w], pos);   // shifts by pos mod 32
+}
+
 // ---- ring refills. A segment is 64 lanes x Geo::kLaneSeg bytes; segment
 // positions are multiples of the segment size.
 
@@ -257,9 +304,10 @@ __device__ __forceinline__ void consume_plane(const PlaneRegs<K>& p) {
 // Per-wavefront decode state of one chunk.
 template <int K>
 struct ChunkState {
-  uint32_t x[K];
+  uint32_t x[K];         // rANS states, or tANS states X in [0, 4096)
   uint32_t wptr, wld;    // word ring holds words [wptr, wld)
   uint32_t pptr, pld;    // plane ring (compact mode) holds bytes [pptr, pld)
+  uint32_t bpos;         // tANS: bits of the chunk's stream read so far
 };
 
 // Loads issued at a pair start (two blocks) and landed at the next one: up to
@@ -418,6 +466,73 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
   }
 }
 
+// One tANS step of the K states of every lane. Table entries: FAST (dense
+// bf16, bytes, exponent pairs) {newX:12, nb:4, -:8, output byte:8}, 4 bytes;
+// otherwise {lo: newX:12, nb:4, nb + raw:5, raw:4; hi: value | consume << 31},
+// 8 bytes, raw = 8 for a compact-mode symbol that takes a plane byte. Each
+// lane reads its states' bits in order (state bits, then raw plane bits) from
+// one stream position per lane: the wavefront prefix sum of the lanes' bit
+// counts. newX has nb low zero bits, so X = newX | bits. d as for rans_step
+// (the generic layout's value with its plane byte merged).
+template <int K, int MODE, bool FAST, bool PARTIAL>
+__device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C, const LDS void* tbl,
+                                          const LDS uint32_t* ring, uint32_t (&d)[K]) {
+  uint32_t e[K], hv[K], nb[K], nt[K];
+  bool act[K];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int g = 0; g < K; ++g) {
+    if (FAST) {
+      e[g] = ((const LDS uint32_t*)tbl)[S.x[g]];
+      hv[g] = 0;
+    } else {
+      const uint64_t v = ((const LDS uint64_t*)tbl)[S.x[g]];
+      e[g] = (uint32_t)v;
+      hv[g] = (uint32_t)(v >> 32);
+    }
+    nb[g] = __builtin_amdgcn_ubfe(e[g], 12, 4);
+    nt[g] = FAST ? nb[g] : __builtin_amdgcn_ubfe(e[g], 16, 5);
+    act[g] = true;
+    if (PARTIAL) {
+      act[g] = t * (kWave * K) + C.lane * K + g < C.nc;
+      if (!act[g]) nb[g] = nt[g] = 0;
+    }
+    tot += nt[g];
+  }
+  const uint32_t incl = wave_prefix_sum(tot);
+  uint32_t pos = S.bpos + incl - tot;                  // this lane's first bit
+  S.bpos += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+  S.wptr = (S.bpos >> 5) << 1;                          // ring words no longer needed: [.., wptr)
+  if (FAST && K <= 2) {
+    // at most 2 x 12 bits per lane: one 32-bit window
+    const uint32_t win = stream_bits(ring, pos);
+    uint32_t off = 0;
+#pragma unroll
+    for (int g = 0; g < K; ++g) {
+      const uint32_t x = (e[g] & 0xFFFu) | __builtin_amdgcn_ubfe(win, off, nb[g]);
+      off += nb[g];
+      S.x[g] = PARTIAL && !act[g] ? S.x[g] : x;
+      d[g] = e[g];
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < K; ++g) {
+      const uint32_t win = stream_bits(ring, pos);
+      pos += nt[g];
+      const uint32_t x = (e[g] & 0xFFFu) | __builtin_amdgcn_ubfe(win, 0, nb[g]);
+      S.x[g] = PARTIAL && !act[g] ? S.x[g] : x;
+      if (FAST) {
+        d[g] = e[g];
+      } else if (MODE == 2) {
+        // the plane byte follows the state bits; a symbol without one reads 0 bits
+        d[g] = byte_merge(hv[g], __builtin_amdgcn_ubfe(win, nb[g], __builtin_amdgcn_ubfe(e[g], 21, 4)));
+      } else {
+        d[g] = hv[g];
+      }
+    }
+  }
+}
+
 // Ring upkeep and prefetch, at block granularity.
 //
 // Word-ring and compact-plane segments are requested at a pair start (every
@@ -467,15 +582,20 @@ __device__ __forceinline__ void request_segments(const ChunkState<K>& S, Infligh
 }
 
 // Make sure the rings hold a block's worst-case demand. Rare: it lands the
-// in-flight segments early (waiting for them) and loads synchronously.
-template <int K, int MODE>
+// in-flight segments early (waiting for them) and loads synchronously. A
+// block needs at most one renorm word per element (rANS), or MAXB bits per
+// element (tANS: 12, or 20 with compact-mode plane bits) plus the second word
+// of the last 32-bit window, in ring words.
+template <int K, int MODE, int MAXB = 0>
 __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C,
                                        LDS uint16_t* wring, LDS uint8_t* pring) {
   typedef Geo<K, MODE> G;
   typedef typename G::Seg V;
   constexpr uint32_t kBlkElems = G::kBlkElems;
+  constexpr uint32_t kNeed = MAXB ? kBlkElems * MAXB / 16u + 8u : kBlkElems;
+  static_assert(kNeed + G::kWSeg <= G::kRing, "a block's worst case and a segment fit the ring");
   const uint32_t lane = C.lane;
-  const uint32_t need_w = min(kBlkElems, C.n_words - S.wptr);
+  const uint32_t need_w = min(kNeed, C.n_words - min(S.wptr, C.n_words));
   const uint32_t need_p = MODE == 2 ? min(kBlkElems, C.n_plane - S.pptr) : 0u;
   if (S.wld - S.wptr < need_w || (MODE == 2 && S.pld - S.pptr < need_p)) {
     land_segments<K, MODE>(S, F, wring, pring, lane);
@@ -492,19 +612,40 @@ __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, c
   }
 }
 
+// Ring geometry of a plane mode under a coder: pair mode (3) loads its dense
+// plane as mode 1 does, and tANS compact chunks keep their plane bytes in the
+// stream, so they need no plane ring (full-scale geometry, as mode 0).
+template <int MODE, int CODER>
+constexpr int ring_mode() { return MODE == 3 ? 1 : (CODER == 1 && MODE == 2 ? 0 : MODE); }
+
+// Two exponent-pair symbols into four fp8 bytes. `dup` holds their plane
+// bytes as [pA, pA, pB, pB] (p = m0 | s1 << 3 | m1 << 4 | s0 << 7), dA and dB
+// the symbols (e0 | e1 << 4) in byte 3. Bytes out: pA's s0|m0 and e0, then
+// pA's nibbles swapped (s1|m1) and e1, then the same for B. Per byte, bits 7
+// and 0-2 come from the plane and bits 3-6 from the exponent field.
+__device__ __forceinline__ uint32_t pair_merge(uint32_t dup, uint32_t dA, uint32_t dB) {
+  const uint32_t plane = ((dup << 4) & 0xFF00FF00u) | (dup & 0x00FF00FFu);   // bytes 1, 3: nibbles swapped
+  const uint32_t y = __builtin_amdgcn_perm(dB, dA, 0x07070303u);            // [bA, bA, bB, bB]
+  const uint32_t ex = ((y >> 1) & 0xFF00FF00u) | ((y << 3) & 0x00FF00FFu);  // e0, e1, e0, e1 at bits 3-6
+  return (plane & 0x87878787u) | (ex & 0x78787878u);
+}
+
 // The steps of one block, staging outputs in LDS and storing each half block
 // once it is complete (a partial chunk stores its second half at the next
-// block start, or after the last block).
-template <int K, int MODE, int EB, bool PARTIAL>
+// block start, or after the last block). Pair mode (MODE 3) runs with EB = 2:
+// a coded element is a pair of bytes.
+template <int K, int MODE, int EB, bool PARTIAL, int CODER>
 __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, ChunkState<K>& S,
                                              const ChunkParams& C, const LDS uint64_t* __restrict__ tbl,
                                              const LDS uint16_t* wring, LDS uint8_t* pring,
                                              LDS uint8_t* stage) {
+  constexpr int RM = ring_mode<MODE, CODER>();
   constexpr uint32_t kStates = kWave * K;
-  constexpr int kBlock = Geo<K, MODE>::kBlock;
+  constexpr int kBlock = Geo<K, RM>::kBlock;
   constexpr int kHalf = kBlock / 2;
   constexpr bool DENSE = MODE == 1 && EB == 2;
-  constexpr bool FAST = DENSE || EB == 1;               // mad24 table layouts
+  constexpr bool PAIR = MODE == 3;
+  constexpr bool FAST = DENSE || PAIR || EB == 1;       // one-word table layouts (output byte in bits 24..31)
   constexpr bool DIRECT = direct_stores<K, EB, PARTIAL>();
   const uint32_t lane = C.lane;
 #pragma unroll
@@ -517,8 +658,34 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     }
     const uint32_t qs = q % kHalf;                       // step within the staged half
     uint32_t d[K];
-    rans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
-    if (DENSE) {
+    if (CODER == 0) rans_step<K, RM, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
+    else tans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, (const LDS uint32_t*)wring, d);
+    if (PAIR) {
+      // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
+      const uint64_t pw = pl.b[(q * K) / 8];
+      const uint32_t o = (q * K) % 8;
+      const uint32_t phi = (uint32_t)(pw >> 32), plo = (uint32_t)pw;
+      if (K >= 2) {
+        constexpr int kPairs = K >= 2 ? K / 2 : 1;
+        uint32_t v[kPairs];
+#pragma unroll
+        for (int h = 0; h < kPairs; ++h) {
+          const uint32_t ob = o + 2 * h;
+          const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (ob + 1) * 0x01010000u | ob * 0x0101u);
+          v[h] = pair_merge(dup, d[(2 * h) % K], d[(2 * h + 1) % K]);
+        }
+        if (DIRECT) {
+          store_step<K, kBlock, EB>(C, blk, q, v[0], v[kPairs - 1]);
+        } else {
+          LDS uint8_t* dst = stage + qs * (kStates * 2) + lane * (2u * K);
+          if (K == 2) *(LDS uint32_t*)dst = v[0];
+          else *(LDS uint64_t*)dst = (uint64_t)v[0] | ((uint64_t)v[kPairs - 1] << 32);
+        }
+      } else {
+        const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
+        *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)pair_merge(dup, d[0], d[0]);
+      }
+    } else if (DENSE) {
       // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
       const uint64_t pw = pl.b[(q * K) / 8];
       const uint32_t o = (q * K) % 8;                    // byte offset in pw
@@ -603,19 +770,25 @@ __device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, b
 }
 
 // Decode one chunk with one wavefront: K interleaved states per lane, MODE =
-// plane mode, EB = element bytes, PARTIAL = chunk may be shorter than
-// 64*K*steps (the tensor's last chunk).
-template <int K, int MODE, int EB, bool PARTIAL>
+// plane mode, EB = element bytes (2 for pair mode, whose elements are byte
+// pairs), PARTIAL = chunk may be shorter than 64*K*steps (the tensor's last
+// chunk), CODER = 0 rANS, 1 tANS. n_words is the chunk table's count: renorm
+// words (rANS) or stream bits (tANS, whose stream is whole u32 words).
+template <int K, int MODE, int EB, bool PARTIAL, int CODER>
 __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* wring,
                                              LDS uint8_t* pring, LDS uint8_t* stage,
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
                                              uint32_t n_plane, const GLB uint8_t* dplane, uint64_t pstride,
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
                                              uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
-  typedef Geo<K, MODE> G;
+  constexpr int RM = ring_mode<MODE, CODER>();
+  constexpr int MAXB = CODER == 0 ? 0 : (MODE == 2 ? 20 : 12);   // tANS bits per element at most
+  typedef Geo<K, RM> G;
   constexpr uint32_t kStates = kWave * K;
   ChunkParams C;
   C.lane = __lane_id();
+  const uint32_t n_bits = n_words;                               // tANS: the stream's length in bits
+  if (CODER == 1) n_words = 2u * ((n_bits + 31u) / 32u);          // in 16-bit ring words
   const uint32_t wbytes = pad16(n_words * 2u);
   C.wsrc = cbase + 4u * kStates;
   C.psrc = cbase + 4u * kStates + wbytes;
@@ -634,23 +807,30 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   C.nblk = (nsteps + G::kBlock - 1) / G::kBlock;
 
   ChunkState<K> S;
+  bool bad_init = false;
 #pragma unroll
-  for (int g = 0; g < K; ++g) S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
-  S.wptr = S.wld = S.pptr = S.pld = 0;
+  for (int g = 0; g < K; ++g) {
+    S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
+    if (CODER == 1) {                                   // a table index: kept inside the table
+      bad_init |= S.x[g] > 4095u;
+      S.x[g] &= 4095u;
+    }
+  }
+  S.wptr = S.wld = S.pptr = S.pld = S.bpos = 0;
 
-  if (MODE == 2 && C.lane == 0) *(LDS u32x4*)(pring + G::kPZero) = u32x4{0u, 0u, 0u, 0u};
+  if (RM == 2 && C.lane == 0) *(LDS u32x4*)(pring + G::kPZero) = u32x4{0u, 0u, 0u, 0u};
 
   // First loads; land all of them before the loop so that the loop header's
   // wait-count state holds no load issued here.
-  Inflight<K, MODE> F;
+  Inflight<K, RM> F;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
-    F.pl[i] = MODE == 1 ? load_plane<K>(C.dplane, C.pstride, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
-  request_segments<K, MODE>(S, F, C);
+    F.pl[i] = RM == 1 ? load_plane<K>(C.dplane, C.pstride, min((uint32_t)i, C.nblk - 1), C.lane) : PlaneRegs<K>{};
+  request_segments<K, RM>(S, F, C);
   consume<K>(S.x);
-  if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
+  if (RM == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
   BS_KEEP2(F.w[0].x, F.w[1].x);
-  if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
+  if (RM == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
   LDS uint16_t* prog = (LDS uint16_t*)((LDS uint8_t*)tbl + kProgOff);   // kWaves entries
   const uint32_t pwave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -674,23 +854,23 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
     }
     // ---- pair start: land the previous pair's loads, issue the next pair's
     const PlaneRegs<K> cur0 = F.pl[0], cur1 = F.pl[1];
-    land_segments<K, MODE>(S, F, wring, pring, C.lane);
-    refill<K, MODE>(S, F, C, wring, pring);
+    land_segments<K, RM>(S, F, wring, pring, C.lane);
+    refill<K, RM, MAXB>(S, F, C, wring, pring);
     wave_sync();
     if (PARTIAL && blk > 0) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk - 1, C, stage);
-    request_segments<K, MODE>(S, F, C);
-    if (MODE == 1) {
+    request_segments<K, RM>(S, F, C);
+    if (RM == 1) {
       F.pl[0] = load_plane<K>(C.dplane, C.pstride, min(blk + 2, C.nblk - 1), C.lane);
       F.pl[1] = load_plane<K>(C.dplane, C.pstride, min(blk + 3, C.nblk - 1), C.lane);
     }
     wave_sync();
-    decode_block<K, MODE, EB, PARTIAL>(blk, cur0, S, C, tbl, wring, pring, stage);
+    decode_block<K, MODE, EB, PARTIAL, CODER>(blk, cur0, S, C, tbl, wring, pring, stage);
     if (PARTIAL && blk + 1 >= C.nblk) break;
     // ---- second block of the pair
-    refill<K, MODE>(S, F, C, wring, pring);
+    refill<K, RM, MAXB>(S, F, C, wring, pring);
     wave_sync();
     if (PARTIAL) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk + 1, C, stage);
-    decode_block<K, MODE, EB, PARTIAL>(blk + 1, cur1, S, C, tbl, wring, pring, stage);
+    decode_block<K, MODE, EB, PARTIAL, CODER>(blk + 1, cur1, S, C, tbl, wring, pring, stage);
     blk += 2;
     if (blk >= C.nblk) break;
     if (!PARTIAL) {
@@ -698,10 +878,10 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
       // lands the loads and leaves the stores in flight. Stating it gives the
       // compiler's wait-count tracking an exact state here; the uses below
       // keep its own waits for these registers at this point.
-      __builtin_amdgcn_s_waitcnt(wait_vm(stores_per_pair<K, MODE, EB, PARTIAL>()));
-      if (MODE == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
+      __builtin_amdgcn_s_waitcnt(wait_vm(stores_per_pair<K, RM, EB, PARTIAL>()));
+      if (RM == 1) { consume_plane(F.pl[0]); consume_plane(F.pl[1]); }
       BS_KEEP2(F.w[0].x, F.w[1].x);
-      if (MODE == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
+      if (RM == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
     }
   }
   // a partial chunk's last staged half: the second half of its last block, or
@@ -713,47 +893,66 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   // segments requested but never landed need no wait: nothing reads them
   if (C.lane == 0) *(volatile LDS uint16_t*)(prog + pwave) = 0xFFFFu;   // out of the workgroup's lowest
 
-  bool bad_state = false;
+  // a valid chunk ends in the encoder's start states (rANS x = L, tANS X = 0)
+  // with every word, bit and plane byte read
+  bool bad_state = bad_init;
 #pragma unroll
-  for (int g = 0; g < K; ++g) bad_state |= S.x[g] != kL;
-  const bool bad = __ballot(bad_state) != 0 || S.wptr != n_words || (MODE == 2 && S.pptr != n_plane);
+  for (int g = 0; g < K; ++g) bad_state |= S.x[g] != (CODER == 0 ? kL : 0u);
+  const bool bad = __ballot(bad_state) != 0 || (CODER == 0 ? S.wptr != n_words : S.bpos != n_bits) ||
+                   (RM == 2 && S.pptr != n_plane);
   if (bad) report(status, BS_DEV_ERR_STREAM);
 }
 
-template <int K, int EB, bool PARTIAL, bool COMPACT>
+template <int K, int EB, bool PARTIAL, bool COMPACT, int CODER>
 __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint64_t* tbl, LDS uint16_t* wring,
                                                   LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
                                                   uint32_t nw, uint32_t np, const GLB uint8_t* dplane,
                                                   uint64_t pstride, GLB uint8_t* out, uint64_t ubase, uint64_t ustride,
                                                   uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
-  if constexpr (EB == 1) {   // byte elements have no plane
-    decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+  if constexpr (EB == 1) {   // byte symbols (no plane); exponent pairs run as 2-byte elements
+    if (mode == 3)
+      decode_chunk<K, 3, 2, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    else
+      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   } else {
     if (mode == 0) {
-      decode_chunk<K, 0, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     } else if (mode == 1) {
-      decode_chunk<K, 1, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 1, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     } else {
       if constexpr (COMPACT)
-        decode_chunk<K, 2, EB, PARTIAL>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+        decode_chunk<K, 2, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
     }
   }
 }
 
-template <int K, bool COMPACT>
-__device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32_t mode, const LDS uint64_t* tbl,
+template <int K, bool COMPACT, int CODER>
+__device__ __forceinline__ void decode_chunk_c(uint32_t eb, bool partial, uint32_t mode, const LDS uint64_t* tbl,
                                                LDS uint16_t* wring, LDS uint8_t* pring, LDS uint8_t* stage,
                                                const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
                                                const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
                                                uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
                                                int32_t* status, bool younger) {
   if (eb == 2) {
-    if (partial) decode_chunk_mode<K, 2, true, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
-    else decode_chunk_mode<K, 2, false, COMPACT>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    if (partial) decode_chunk_mode<K, 2, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    else decode_chunk_mode<K, 2, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   } else {
-    if (partial) decode_chunk_mode<K, 1, true, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
-    else decode_chunk_mode<K, 1, false, COMPACT>(0, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    if (partial) decode_chunk_mode<K, 1, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    else decode_chunk_mode<K, 1, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
   }
+}
+
+template <int K, bool COMPACT>
+__device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32_t mode, uint32_t coder,
+                                               const LDS uint64_t* tbl, LDS uint16_t* wring, LDS uint8_t* pring,
+                                               LDS uint8_t* stage, const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
+                                               const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
+                                               uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
+                                               int32_t* status, bool younger) {
+  if (coder == 0)
+    decode_chunk_c<K, COMPACT, 0>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+  else
+    decode_chunk_c<K, COMPACT, 1>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
 }
 
 template <bool COMPACT>
@@ -829,14 +1028,17 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
 
   // ---- header checks (uniform across the workgroup)
   const uint32_t magic = rfl(h0.x), w1 = rfl(h0.y);
-  const uint32_t eb = (w1 >> 8) & 0xFFu, mode = (w1 >> 16) & 0xFFu;
+  const uint32_t ver = w1 & 0xFFu, eb = (w1 >> 8) & 0xFFu, mode = (w1 >> 16) & 0xFFu;
+  const uint32_t w7 = rfl(h1.w), coder = w7;             // byte 28: coder; bytes 29..31 zero
   if (magic != 0x4B435342u ||                                             // "BSCK"
-      (w1 & 0xFFu) != (uint32_t)kVersion || (eb != 1 && eb != 2) || mode > 2 || (w1 >> 24) != 12 ||
-      (!COMPACT && mode == 2)) {
+      (ver != 2 && ver != kVersion) || (eb != 1 && eb != 2) || mode > 3 || (w1 >> 24) != 12 || coder > 1 ||
+      (ver == 2 && (coder != 0 || mode == 3)) || (!COMPACT && mode == 2) ||
+      (eb == 1 ? (mode != 0 && mode != 3) : mode == 3)) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
   const uint64_t n = (uint64_t)rfl(h0.z) | ((uint64_t)rfl(h0.w) << 32);
+  const uint64_t ne = mode == 3 ? n / 2 : n;                 // coded elements (pair mode: byte pairs)
   const uint32_t steps = rfl(h1.x);
   const uint32_t w5 = rfl(h1.y);
   const uint32_t lanes = w5 & 0xFFFFu, nsym = w5 >> 16;
@@ -845,8 +1047,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   // an empty tensor (n = 0, no chunks) has no blob to decode: only a task
   // table out of order can send a workgroup to one, and it stops here
   if ((lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || (steps % (2 * kBlockMax)) != 0 || nsym == 0 ||
-      nsym > 256 || (eb == 1 && mode != 0) || nch == 0 || nch != T.n_chunks || per > kMaxChunk ||
-      nch != (n + per - 1) / per) {
+      nsym > 256 || (mode == 3 && (n & 1)) || nch == 0 || nch != T.n_chunks || per > kMaxChunk ||
+      nch != (ne + per - 1) / per) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
@@ -854,15 +1056,31 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_COUNT);
     return;
   }
-  const uint32_t ctab = pad16(32u + 4u * nsym);
-  const uint64_t nf = n / per;                                // full chunks
-  const uint64_t preg = ((uint64_t)ctab + 16ull * nch + 255u) & ~255ull;   // dense plane region (plane_mode 1)
+  const uint32_t stab = pad16(32u + 4u * nsym);               // tANS decode table (coder 1)
+  const uint32_t ctab = stab + (coder ? 4u * kTansSlots : 0u);
+  const uint64_t nf = ne / per;                               // full chunks
+  // layout version 3 keeps the full chunks' dense planes in one region;
+  // version 2 keeps every plane inline and lays chunks out contiguously
+  const bool region = ver == kVersion && (mode == 1 || mode == 3);
+  const uint64_t preg = ((uint64_t)ctab + 16ull * nch + 255u) & ~255ull;   // dense plane region
   if ((uint64_t)ctab + 16ull * nch > T.blob_bytes ||
-      (mode == 1 && (preg > T.blob_bytes || nf * per > T.blob_bytes - preg))) {
+      (region && (preg > T.blob_bytes || nf * per > T.blob_bytes - preg))) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_BOUNDS);
     return;
   }
-  const bool fast = eb == 2 && mode == 1;
+  const bool dense = eb == 2 && mode == 1;                    // exponent symbols of bf16 words
+  const bool fast = dense || eb == 1;                         // one-word table layouts (bytes, pairs too)
+  // tANS: this thread's run of the stored decode table (kRun entries), in
+  // flight during the symbol checks below (inside the blob: checked above)
+  constexpr uint32_t kRun = 4096u / kThreads;
+  static_assert(4096u % kThreads == 0 && kRun % 4 == 0, "slot runs");
+  u32x4 trun[kRun / 4];
+#pragma unroll
+  for (uint32_t i = 0; i < kRun / 4; ++i) trun[i] = u32x4{0u, 0u, 0u, 0u};
+  if (coder) {
+#pragma unroll
+    for (uint32_t i = 0; i < kRun / 4; ++i) trun[i] = *(const GLB u32x4*)(b + stab + 4u * (tid * kRun + 4u * i));
+  }
 
   // this wave's chunk-table entry, requested before the table build so that
   // its latency passes under it (the build's barriers wait for LDS only)
@@ -891,8 +1109,10 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
       const uint32_t e = ent4[i];
       const bool live = 4u * l + i < nsym;
       f[i] = live ? (e >> 16) & 0x1FFFu : 0u;
-      // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each
-      bad |= live && (f[i] == 0 || (fast && ((e & 0x807Fu) != 0 || (e >> 31) == 0)));
+      // dense-mode symbols are exponent classes: value e<<7 with zero sign/mantissa, one plane byte each;
+      // byte symbols are bytes, exponent-pair symbols bytes with one plane byte each
+      bad |= live && (f[i] == 0 || (dense && ((e & 0x807Fu) != 0 || (e >> 31) == 0)) ||
+                      (eb == 1 && ((e & 0xFF00u) != 0 || (e >> 31) != (mode == 3 ? 1u : 0u))));
       vals[i] = (e & 0xFFFFu) | (e & 0x80000000u);
       c += f[i];
     }
@@ -910,6 +1130,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (l == 0) {
       s_cum[0] = 0;
       *s_flag = any_bad || total != 4096u;
+      *(volatile LDS uint32_t*)(smem + kFlagOff) = 0u;   // the tANS table check's flag
     }
   }
   lds_barrier();
@@ -919,9 +1140,38 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
   }
-  constexpr uint32_t kRun = 4096u / kThreads;
-  static_assert(4096u % kThreads == 0 && kRun % 2 == 0, "slot runs");
-  {
+  if (coder) {
+    // tANS: the blob's table {newX:12, nb:4, symbol:8, 0:8}, checked (a
+    // symbol of the tensor, nb <= 12, newX + 2^nb <= 4096 with nb zero low
+    // bits, so every next state stays in the table) and laid out for the
+    // step: one word {newX, nb, output byte in bits 24..31} for dense bf16,
+    // bytes and pairs; else two, {newX, nb, nb + raw, raw} and the value with
+    // its plane flag (raw = 8 plane bits for a compact symbol that has one)
+    const uint32_t slot0 = tid * kRun;
+    bool bad = false;
+    uint32_t lo[kRun], hi[kRun];
+#pragma unroll
+    for (uint32_t k = 0; k < kRun; ++k) {
+      const uint32_t e = trun[k / 4][k % 4], sym = (e >> 16) & 0xFFu, nb = (e >> 12) & 15u, nx = e & 0xFFFu;
+      bad |= (e >> 24) != 0 || sym >= nsym || nb > 12u || nx + (1u << nb) > 4096u || (nx & ((1u << nb) - 1u)) != 0;
+      const uint32_t v = s_val[sym];
+      const uint32_t rw = mode == 2 && (v >> 31) ? 8u : 0u;
+      lo[k] = dense ? (e & 0xFFFFu) | (((v >> 7) & 0xFFu) << 24)
+              : fast ? (e & 0xFFFFu) | ((v & 0xFFu) << 24)
+                     : (e & 0xFFFFu) | ((nb + rw) << 16) | (rw << 21);
+      hi[k] = v;
+    }
+    if (fast) {
+      LDS uint32_t* t32 = (LDS uint32_t*)s_tbl + slot0;
+#pragma unroll
+      for (uint32_t k = 0; k < kRun; k += 4) *(LDS u32x4*)(t32 + k) = u32x4{lo[k], lo[k + 1], lo[k + 2], lo[k + 3]};
+    } else {
+#pragma unroll
+      for (uint32_t k = 0; k < kRun; k += 2)
+        *(LDS u32x4*)(s_tbl + slot0 + k) = u32x4{lo[k], hi[k], lo[k + 1], hi[k + 1]};
+    }
+    if (bad) *(volatile LDS uint32_t*)(smem + kFlagOff) = 1u;
+  } else {
     const uint32_t slot0 = tid * kRun;
     uint32_t lo = 0, hi = nsym;                      // cum[lo] <= slot0 < cum[hi]
     while (hi - lo > 1) {
@@ -942,9 +1192,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
           val = s_val[lo];
         }
         const uint32_t f = c1 - c0;
-        e2[h] = fast    ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
-                : eb == 1 ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
-                          : ((uint64_t)f | ((uint64_t)(val | ((slot - c0) << 16)) << 32));
+        e2[h] = dense  ? ((uint64_t)(f | ((val & 0x7F80u) << 17)) | ((uint64_t)(slot - c0) << 32))
+                : fast ? ((uint64_t)(f | ((val & 0xFFu) << 24)) | ((uint64_t)(slot - c0) << 32))
+                       : ((uint64_t)f | ((uint64_t)(val | ((slot - c0) << 16)) << 32));
       }
       *(LDS u32x4*)(s_tbl + slot0 + k) =
           u32x4{(uint32_t)e2[0], (uint32_t)(e2[0] >> 32), (uint32_t)e2[1], (uint32_t)(e2[1] >> 32)};
@@ -954,21 +1204,29 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   // (and for one that leaves on an error below)
   if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
   lds_barrier();
+  if (coder && *(volatile LDS uint32_t*)(smem + kFlagOff)) {   // the same value for every thread
+    if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
+    return;
+  }
 
   // ---- one chunk per wavefront
   if (chunk >= nch) return;
   const uint64_t cbase_idx = (uint64_t)chunk * per;     // the partial chunk's first element (nf * per)
   const bool full = chunk < nf;
-  const uint32_t nc = full ? (uint32_t)per : (uint32_t)(n - cbase_idx);
+  const uint32_t nc = full ? (uint32_t)per : (uint32_t)(ne - cbase_idx);
   const uint32_t nsteps = (nc + lanes - 1) / lanes;
   const uint32_t bsteps = lanes == 256 ? 4u : 8u;     // block_steps<K>()
   const uint32_t dense_plane = ((nsteps + bsteps - 1) / bsteps) * bsteps * lanes;
-  const bool split = mode == 1 && full;               // dense plane in the plane region
+  const bool has_plane = mode == 1 || mode == 3;      // dense plane
+  const bool split = region && full;                  // dense plane in the plane region
   const uint64_t pblk = (uint64_t)bsteps * lanes;      // plane bytes per block
-  bool ok = (off % 16) == 0 && off + 4ull * lanes + pad16(nw * 2u) + (split ? 0u : pad16(np)) <= T.blob_bytes &&
-            nw <= nsteps * lanes && T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
-  if (mode == 1) ok = ok && np == dense_plane;
-  if (mode == 2) ok = ok && np <= nc;
+  // stream: rANS nw 16-bit words; tANS nw bits (at most 12 per element, 20 with compact plane bits)
+  const uint32_t sbytes = coder ? pad16(((nw + 31u) / 32u) * 4u) : pad16(nw * 2u);
+  bool ok = (off % 16) == 0 && off + 4ull * lanes + sbytes + (split ? 0u : pad16(np)) <= T.blob_bytes &&
+            (coder ? (uint64_t)nw <= (uint64_t)nc * (mode == 2 ? 20u : 12u) : nw <= nsteps * lanes) &&
+            T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
+  if (has_plane) ok = ok && np == dense_plane;
+  if (mode == 2) ok = ok && (coder ? np == 0 : np <= nc);
   if (mode == 0) ok = ok && np == 0;
   if (!ok) {
     report(status, BS_DEV_ERR_BOUNDS);
@@ -977,24 +1235,27 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   }
   const GLB uint8_t* cbase = b + off;
   LDS uint16_t* wring = (LDS uint16_t*)(s_wring + wave * kRingBytes);
-  LDS uint8_t* pring = s_wring + wave * kRingBytes + Geo<1, 2>::kPRingOff;   // compact chunks only
+  LDS uint8_t* pring = s_wring + wave * kRingBytes + Geo<1, 2>::kPRingOff;   // rANS compact chunks only
   LDS uint8_t* stage = s_stage + wave * kStageMax;
   GLB uint8_t* out = (GLB uint8_t*)T.out;
   const bool partial = !full;
-  const GLB uint8_t* dplane = split ? b + preg + chunk * pblk : nullptr;   // nullptr: inline after the words
+  const GLB uint8_t* dplane = split ? b + preg + chunk * pblk : nullptr;   // nullptr: inline after the stream
   const uint64_t pstride = split ? nf * pblk : pblk;
-  const uint64_t ubase = full ? (uint64_t)chunk * kUnit : cbase_idx;
-  const uint64_t ustride = full ? nf * kUnit : kUnit;
+  // version 3 interleaves the full chunks' 512-element units; version 2 (and
+  // every partial chunk) holds its elements in order from chunk * per
+  const bool inter = ver == kVersion && full;
+  const uint64_t ubase = inter ? (uint64_t)chunk * kUnit : cbase_idx;
+  const uint64_t ustride = inter ? nf * kUnit : kUnit;
   const bool younger = blockIdx.x >= first_round;      // the later of its CU's two workgroups
   if (lanes == 64)
-    decode_chunk_k<1, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status, younger);
+    decode_chunk_k<1, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
+                               out, ubase, ustride, nc, nsteps, status, younger);
   else if (lanes == 128)
-    decode_chunk_k<2, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status, younger);
+    decode_chunk_k<2, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
+                               out, ubase, ustride, nc, nsteps, status, younger);
   else
-    decode_chunk_k<4, COMPACT>(eb, partial, mode, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase,
-                               ustride, nc, nsteps, status, younger);
+    decode_chunk_k<4, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
+                               out, ubase, ustride, nc, nsteps, status, younger);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
@@ -1043,7 +1304,8 @@ int bs_chunk_chunks_per_group(void) { return kWaves; }
 
 int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   if (!h || !info) return BS_ERR_ARG;
-  if (len < 32 || h[0] != 'B' || h[1] != 'S' || h[2] != 'C' || h[3] != 'K' || h[4] != kVersion) return BS_ERR_FORMAT;
+  if (len < 32 || h[0] != 'B' || h[1] != 'S' || h[2] != 'C' || h[3] != 'K' || (h[4] != 2 && h[4] != kVersion))
+    return BS_ERR_FORMAT;
   auto u32 = [&](int o) { return (uint32_t)h[o] | ((uint32_t)h[o + 1] << 8) | ((uint32_t)h[o + 2] << 16) | ((uint32_t)h[o + 3] << 24); };
   info->elem_bytes = h[5];
   info->plane_mode = h[6];
@@ -1052,19 +1314,23 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   info->lanes = (uint32_t)h[20] | ((uint32_t)h[21] << 8);
   info->n_syms = (uint32_t)h[22] | ((uint32_t)h[23] << 8);
   info->n_chunks = u32(24);
+  info->coder = u32(28);
+  const uint32_t mode = info->plane_mode, eb = info->elem_bytes;
   if (h[7] != 12 || (info->lanes != 64 && info->lanes != 128 && info->lanes != 256) || info->steps == 0 ||
-      info->steps % (2 * kBlockMax) || info->n_syms == 0 ||
-      info->n_syms > 256 || (info->elem_bytes != 1 && info->elem_bytes != 2) || info->plane_mode > 2)
+      info->steps % (2 * kBlockMax) || info->n_syms == 0 || info->n_syms > 256 || (eb != 1 && eb != 2) || mode > 3 ||
+      (eb == 1 ? (mode != 0 && mode != 3) : mode == 3) || info->coder > 1 ||
+      (h[4] == 2 && (info->coder != 0 || mode == 3)) || (mode == 3 && (info->n & 1)))
     return BS_ERR_FORMAT;
   const uint64_t per = (uint64_t)info->lanes * info->steps;
-  if (per > kMaxChunk || info->n_chunks != (info->n + per - 1) / per) return BS_ERR_FORMAT;
+  const uint64_t ne = mode == 3 ? info->n / 2 : info->n;
+  if (per > kMaxChunk || info->n_chunks != (ne + per - 1) / per) return BS_ERR_FORMAT;
   return BS_OK;
 }
 
 int bs_chunk_decode(const uint8_t* d_blob, uint64_t blob_bytes, void* d_out, uint64_t n, uint32_t n_chunks,
                     uint32_t plane_mode, int32_t* d_status, void* stream) {
   if (!d_status || (n > 0 && (!d_blob || !d_out))) return BS_ERR_ARG;
-  if (((uintptr_t)d_blob & 15u) != 0 || ((uintptr_t)d_out & 15u) != 0 || plane_mode > 2) return BS_ERR_ARG;
+  if (((uintptr_t)d_blob & 15u) != 0 || ((uintptr_t)d_out & 15u) != 0 || plane_mode > 3) return BS_ERR_ARG;
   if (n == 0 || n_chunks == 0) return BS_OK;
   bs_chunk_task t{d_blob, blob_bytes, d_out, n, 0u, n_chunks};
   return launch(nullptr, 0u, t, groups_for(n_chunks), plane_mode, d_status, stream);
@@ -1072,7 +1338,7 @@ int bs_chunk_decode(const uint8_t* d_blob, uint64_t blob_bytes, void* d_out, uin
 
 int bs_chunk_decode_batch(const bs_chunk_task* d_tasks, uint32_t n_tasks, uint32_t total_groups,
                           uint32_t max_plane_mode, int32_t* d_status, void* stream) {
-  if (!d_status || (n_tasks > 0 && !d_tasks) || max_plane_mode > 2) return BS_ERR_ARG;
+  if (!d_status || (n_tasks > 0 && !d_tasks) || max_plane_mode > 3) return BS_ERR_ARG;
   if (n_tasks == 0 || total_groups == 0) return BS_OK;
   bs_chunk_task dummy{};
   return launch(d_tasks, n_tasks, dummy, total_groups, max_plane_mode, d_status, stream);

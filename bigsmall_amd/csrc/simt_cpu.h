@@ -330,6 +330,44 @@ inline void __builtin_amdgcn_fence(int, const char*) {}
 inline void __builtin_amdgcn_fence(int, const char*, const char*) {}
 inline void __builtin_amdgcn_s_barrier() { bs_simt::ctx().blk->bar.arrive_and_wait(); }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
+// v_bfe_u32: `width` bits of src from bit `offset` (both taken mod 32; width 0 gives 0)
+inline uint32_t __builtin_amdgcn_ubfe(uint32_t src, uint32_t offset, uint32_t width) {
+  offset &= 31u;
+  width &= 31u;
+  return width ? (uint32_t)((src >> offset) & ((1ull << width) - 1ull)) : 0u;
+}
+// v_alignbit_b32: the 32 bits of {hi, lo} from bit (shift mod 32)
+inline uint32_t __builtin_amdgcn_alignbit(uint32_t hi, uint32_t lo, uint32_t shift) {
+  return (uint32_t)((((uint64_t)hi << 32) | lo) >> (shift & 31u));
+}
+// DPP data movement of a 32-bit value, for the controls the kernels use:
+// row_shr:n (0x111-0x11F: the lane n below in the same 16-lane row),
+// row_bcast:15 (0x142: lane 15 of the previous row), row_bcast:31 (0x143:
+// lane 31). A lane of a row that row_mask leaves out, or whose source lies
+// outside its row (row_shr) or before row 1 / row 2 (the broadcasts),
+// returns `old` (bound_ctrl = 0) or 0 (bound_ctrl = 1); the kernels pass 0
+// for old, so either reads as 0. bank_mask must be 0xF.
+inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+  const uint32_t l = bs_simt::ctx().lane, row = l / 16u;
+  int src_lane = -1;
+  if (ctrl >= 0x111 && ctrl <= 0x11F) {
+    const uint32_t k = (uint32_t)ctrl - 0x110u;
+    if (l % 16u >= k) src_lane = (int)(l - k);
+  } else if (ctrl == 0x142) {
+    if (row >= 1) src_lane = (int)(row * 16u - 1u);
+  } else if (ctrl == 0x143) {
+    if (row >= 2) src_lane = 31;
+  } else {
+    abort();                                     // a control this emulation does not cover
+  }
+  if (bank_mask != 0xF) abort();
+  const uint32_t v = (uint32_t)bs_simt::exchange((uint32_t)src, [src_lane](bs_simt::Wave& w) {
+    return src_lane >= 0 ? w.slot[src_lane] : 0ull;
+  });
+  if (!((row_mask >> row) & 1)) return old;
+  if (src_lane < 0) return bound_ctrl ? 0 : old;
+  return (int)v;
+}
 // v_perm_b32: byte i of the result is selected by byte i of sel from the
 // 8 bytes {a, b} (b the low dword): 0-7 that byte, 8-11 the sign of bytes
 // 1, 3, 5, 7 spread to 0x00 / 0xFF, 12 zero, 13-255 0xFF.

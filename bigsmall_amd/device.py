@@ -69,7 +69,7 @@ class StatusWord:
         if v:
             names = [n for b, n in [(_native.BS_DEV_ERR_HEADER, "bad header"), (_native.BS_DEV_ERR_COUNT, "count mismatch"),
                                     (_native.BS_DEV_ERR_BOUNDS, "section out of bounds"),
-                                    (_native.BS_DEV_ERR_STREAM, "corrupt rANS stream")] if v & b]
+                                    (_native.BS_DEV_ERR_STREAM, "corrupt entropy-coded stream")] if v & b]
             raise DecodeError(f"{what}: device integrity check failed ({', '.join(names)}; status=0x{v:x})")
 
 

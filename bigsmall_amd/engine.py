@@ -46,7 +46,8 @@ from .device import ChunkBatch, ChunkJob, StatusWord, require_gpu
 from .exceptions import BigSmallVersionError
 from .formats import torch_dtype
 
-BSCK_CODECS = {bf16_chunked.CODEC_BF16: 2, bf16_chunked.CODEC_FP8: 1}
+BSCK_CODECS = {bf16_chunked.CODEC_BF16: 2, bf16_chunked.CODEC_FP8: 1, bf16_chunked.CODEC_BF16_TANS: 2,
+               bf16_chunked.CODEC_FP8_TANS: 1}
 REF_CODECS = set(_refstreams.PARSERS)
 UNSUPPORTED = {
     "bf16_se_rans": "constriction ANS (Rust library, not available to this engine)",
@@ -99,7 +100,8 @@ def check_supported(t: dict) -> None:
     detail = f"file references codec {codec!r}"
     if codec in UNSUPPORTED:
         detail += f", whose bitstream is defined by {UNSUPPORTED[codec]}; the MI355X engine decodes " \
-                  f"bf16_chunked_v1, fp8_chunked_v1, bf16_parallel_v1, bf16_se_tans, bf16_se_single_kernel, " \
+                  f"bf16_chunked_v1, fp8_chunked_v1, bf16_chunked_tans_v1, fp8_chunked_tans_v1, bf16_parallel_v1, " \
+                  f"bf16_se_tans, bf16_se_single_kernel, " \
                   f"zstd, zstd_xor_delta, special (lowcard) and raw"
     raise BigSmallVersionError(required="newer-than-installed", installed=__version__, detail=detail)
 

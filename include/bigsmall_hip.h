@@ -54,17 +54,19 @@ extern "C" {
 int bs_version(void);
 
 /* ------------------------------------------------------------------------ */
-/* BSCK: GPU-native chunked rANS format ("bf16_chunked_v1" / "fp8_chunked_v1").
+/* BSCK: GPU-native chunked entropy-coded format, rANS ("bf16_chunked_v1" /
+ * "fp8_chunked_v1") or tANS ("bf16_chunked_tans_v1" / "fp8_chunked_tans_v1").
  * Registered through codec_registry.register_codec (bigsmall/codec_registry.py:45-47). */
 
 typedef struct {
     uint64_t n;          /* elements */
     uint32_t n_chunks;
-    uint32_t steps;      /* rANS steps per lane per full chunk */
-    uint32_t lanes;      /* interleaved rANS states per chunk (64, 128 or 256) */
+    uint32_t steps;      /* steps per lane per full chunk */
+    uint32_t lanes;      /* interleaved states per chunk (64, 128 or 256) */
     uint32_t n_syms;
     uint32_t elem_bytes; /* 2 = bf16 words, 1 = bytes (fp8) */
-    uint32_t plane_mode; /* 0 none, 1 dense, 2 compact */
+    uint32_t plane_mode; /* 0 none, 1 dense, 2 compact, 3 fp8 exponent pairs + dense plane */
+    uint32_t coder;      /* 0 rANS, 1 tANS */
 } bs_chunk_info;
 
 /* One tensor of a batched launch (device-resident array of these). */
@@ -93,9 +95,10 @@ int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uin
                     uint32_t n_chunks, uint32_t plane_mode, int32_t *d_status, void *stream);
 
 /* Decode many BSCK blobs (a transformer layer, a batch of KV blocks) in one
- * launch; `max_plane_mode` is the largest plane_mode among the tasks (a launch
- * without mode-2 tasks uses a kernel built without the compact-plane path;
- * both use the same LDS and occupancy). Tasks are in ascending wg_begin order,
+ * launch, rANS and tANS blobs alike; `max_plane_mode` is the largest
+ * plane_mode among the tasks (a launch whose tasks are all of modes 0 and 1
+ * uses a kernel built without the compact-plane path; both use the same LDS
+ * and occupancy). Tasks are in ascending wg_begin order,
  * task 0 at 0, each starting where the previous one's workgroups end; every
  * blob and output is 16-byte aligned, and total_groups is the last task's end
  * (a workgroup serves the last task whose wg_begin is at or before it, so
@@ -107,12 +110,20 @@ int bs_chunk_decode(const uint8_t *d_blob, uint64_t blob_bytes, void *d_out, uin
 int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32_t total_groups,
                           uint32_t max_plane_mode, int32_t *d_status, void *stream);
 
-/* Host encoder for BSCK. `flags`: BS_CHUNK_MODE_AUTO or a forced plane mode.
- * Replaces the encode half of the codec plugin pair (bigsmall/codec_registry.py:39-47). */
+/* Host encoder for BSCK. `mode`: BS_CHUNK_MODE_AUTO or a forced plane mode
+ * (0-2 for bf16; 0 or 3 for bytes, 3 needing an even n). `coder`: 0 rANS,
+ * 1 tANS. bs_chunk_encode is bs_chunk_encode_ex with coder 0, and
+ * bs_chunk_encode_bound its capacity (bs_chunk_encode_bound_ex for either
+ * coder). Replaces the encode half of the codec plugin pair
+ * (bigsmall/codec_registry.py:39-47). */
 #define BS_CHUNK_MODE_AUTO (-1)
 int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, uint64_t *bound);
+int bs_chunk_encode_bound_ex(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t coder,
+                             uint64_t *bound);
 int bs_chunk_encode(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                     uint8_t *h_dst, uint64_t cap, uint64_t *out_len, int n_threads);
+int bs_chunk_encode_ex(const void *h_src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps,
+                       int32_t mode, int32_t coder, uint8_t *h_dst, uint64_t cap, uint64_t *out_len, int n_threads);
 
 /* GPU encoder for BSCK, for tensors already in HBM (bf16, dense plane mode,
  * 128 states per chunk). A batch of tasks sorted by chunk_begin; task i owns

@@ -762,51 +762,111 @@ out:
 }
 
 /* ------------------------------------------------------------------------ */
-/* BSCK — the engine's GPU-native chunked rANS container format (no reference
+/* BSCK — the engine's GPU-native chunked container format (no reference
  * counterpart). CPU restatement of the device decoder's semantics: the oracle
  * for the product encoder and the GPU decoder. Format:
- *   [0]  "BSCK"  [4] u8 version=3  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
- *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2)
- *   [22] u16 n_syms  [24] u32 n_chunks  [28] u32 reserved
+ *   [0]  "BSCK"  [4] u8 version (2 or 3)  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
+ *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2,4)
+ *   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS, 1 tANS; version 3), 3 zero bytes
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
- *   pad to 16; n_chunks x {u64 offset, u32 n_words, u32 n_plane}
- *   pad to 256; plane_mode 1: the full chunks' dense planes (nf*lanes*steps bytes)
- *   chunk: lanes x u32 initial states | n_words x u16 (pad 16) | n_plane bytes (pad 16),
- *          the plane omitted for a full chunk in plane_mode 1
- *   pad to 256 (blob lengths are multiples of 256)
- * With per = lanes*steps and nf = n / per full chunks, element j of full
- * chunk c sits at ((j / 512) * nf + c) * 512 + j % 512 (512-element units
- * interleaved across the full chunks); element j of the partial chunk (c = nf)
- * at nf*per + j. With K = lanes/64, state
- * v = g*64 + l (wavefront lane l, group g) decodes element t*lanes + l*K + g at
- * step t. Decode step order: steps ascending; renorm words consumed in ascending
- * v order among states that fell below L. plane_mode 1 (dense): every element
- * consumes one byte, stored in blocks of B steps (B = 8 for K <= 2, 4 for K = 4);
- * the byte of state (g, l) for step B*b+q sits at byte l*B*K + q*K + g of the
- * chunk's plane block b (B*lanes bytes), which is block b*nf + c of the plane
- * region for a full chunk, and at b*B*lanes of the inline plane otherwise.
- * plane_mode 2 (compact): consuming elements read bytes in decode order.
- * plane byte = sign<<7 | mantissa for bf16 symbols with bit 31 set.
+ *   pad to 16; tANS only: 4096 x u32 decode table {newX:12, nb:4, symbol:8, 0:8}
+ *   n_chunks x {u64 offset, u32 n_words (rANS) or n_bits (tANS), u32 n_plane}
+ *   version 3, plane modes 1 and 3: pad to 256, the full chunks' dense planes (nf*lanes*steps bytes)
+ *   chunk: lanes x u32 initial states | rANS: n_words x u16, tANS: ceil(n_bits/32) x u32,
+ *          padded to 16 | n_plane bytes (pad 16), the plane omitted for a
+ *          full chunk of a version-3 blob in plane modes 1 and 3
+ *   version 3: pad to 256 (blob lengths are multiples of 256)
+ * Elements: bf16 words, or bytes; in plane mode 3 (fp8 exponent pairs) an
+ * element is a pair of bytes (a 16-bit word) and n counts bytes. With
+ * per = lanes*steps and nf = ne / per full chunks (ne = coded elements),
+ * element j of full chunk c sits at ((j / 512) * nf + c) * 512 + j % 512 in
+ * version 3 (512-element units interleaved across the full chunks) and at
+ * c*per + j in version 2; element j of the partial chunk (c = nf) at
+ * nf*per + j. With K = lanes/64, state v = g*64 + l (wavefront lane l,
+ * group g) decodes element t*lanes + l*K + g at step t.
+ * rANS (coder 0; bigsmall/codecs/rans.py:165-207's state machine, M = 4096,
+ * L = 2^16): slot = x & 4095; x = f[s]*(x >> 12) + slot - cum[s]; if x < L,
+ * x = x << 16 | the next word; words are consumed per step in ascending v
+ * order among states that fell below L. A chunk ends with every x == L.
+ * tANS (coder 1): X in [0, 4096); entry = table[X]; s = its symbol;
+ * X = newX + the next nb bits of the chunk's LSB-first bit stream, read in
+ * chunk element order (per step, lanes ascending, a lane's states ascending);
+ * in plane mode 2 a consuming symbol then reads its 8 plane bits. A chunk
+ * ends with every X == 0 and every bit read.
+ * Plane bytes: plane_mode 1/3 (dense): every element has one, stored in blocks
+ * of B steps (B = 8 for K <= 2, 4 for K = 4); the byte of state (g, l) for step
+ * B*b+q sits at byte l*B*K + q*K + g of the chunk's plane block b (B*lanes
+ * bytes), which is block b*nf + c of the plane region for a full chunk of a
+ * version-3 blob, and at b*B*lanes of the inline plane otherwise.
+ * plane_mode 2 (compact): consuming elements read bytes in decode order (rANS)
+ * or from the stream (tANS).
+ * bf16 value = symbol value | plane byte's bit 7 << 15 | its bits 0..6.
+ * Pair value (mode 3): symbol value k = e0 | e1 << 4, plane byte p =
+ * m0 | s1 << 3 | m1 << 4 | s0 << 7: byte 0 = s0 << 7 | e0 << 3 | m0,
+ * byte 1 = s1 << 7 | e1 << 3 | m1.
  * ------------------------------------------------------------------------ */
+
+/* LSB-first bit reader over a whole-u32-word stream */
+typedef struct { const uint8_t *p; uint64_t nbits, pos; } bitrd;
+static uint32_t br_take(bitrd *b, uint32_t k, int *err) {
+    uint32_t v = 0;
+    for (uint32_t i = 0; i < k; i++, b->pos++) {
+        if (b->pos >= b->nbits) { *err = 1; return 0; }
+        v |= (uint32_t)((b->p[b->pos >> 3] >> (b->pos & 7)) & 1u) << i;
+    }
+    return v;
+}
+
+/* The tANS decode table of quantised frequencies (sum 4096), built the
+ * long way: the slots of symbol s, [cum_s, cum_s + f_s), are placed at
+ * position slot * 2563 mod 4096; scanning positions upwards, the k-th
+ * position of s gets next = f_s + k, nb = the shift that brings next into
+ * [4096, 8192), newX = next << nb minus 4096. */
+int orc_tans_table(const uint32_t *freq, int nsym, uint32_t *out) {
+    if (nsym < 1 || nsym > 256) return ORC_ERR_ARG;
+    uint32_t cum = 0, at[4096], seen[256] = {0};
+    for (int s = 0; s < nsym; s++) {
+        if (freq[s] == 0) return ORC_ERR_ARG;
+        for (uint32_t k = 0; k < freq[s]; k++) {
+            if (cum + k >= 4096) return ORC_ERR_ARG;
+            at[((cum + k) * 2563u) % 4096u] = (uint32_t)s;
+        }
+        cum += freq[s];
+    }
+    if (cum != 4096) return ORC_ERR_ARG;
+    for (uint32_t p = 0; p < 4096; p++) {
+        uint32_t s = at[p], next = freq[s] + seen[s]++, nb = 0;
+        while ((next << nb) < 4096u) nb++;
+        out[p] = ((next << nb) - 4096u) | (nb << 12) | (s << 16);
+    }
+    return ORC_OK;
+}
+
 int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *out_v) {
     if (len < 32 || memcmp(blob, "BSCK", 4) != 0) return ORC_ERR_FORMAT;
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
-    if (ver != 3 || (eb != 1 && eb != 2) || mode > 2 || prec != 12 || (lanes != 64 && lanes != 128 && lanes != 256) ||
-        steps == 0 || steps % 16)
+    uint32_t coder = blob[28];
+    if ((ver != 2 && ver != 3) || (eb != 1 && eb != 2) || mode > 3 || prec != 12 ||
+        (lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || steps % 16 || coder > 1 ||
+        blob[29] || blob[30] || blob[31] || (ver == 2 && coder != 0) ||
+        (eb == 1 && mode != 0 && mode != 3) || (eb == 2 && mode == 3) || (mode == 3 && ver != 3))
         return ORC_ERR_FORMAT;
     if (n != n_weights) return ORC_ERR_COUNT;
+    if (mode == 3 && n % 2) return ORC_ERR_FORMAT;
     if (nsym == 0 || nsym > 256) return ORC_ERR_FORMAT;
+    uint64_t ne = mode == 3 ? n / 2 : n;                     /* coded elements */
     uint64_t per = (uint64_t)lanes * steps;
-    if (nch != (n + per - 1) / per) return ORC_ERR_FORMAT;
-    size_t tab = 32 + 4 * (size_t)nsym;
-    size_t ctab = (tab + 15) & ~(size_t)15;
+    if (nch != (ne + per - 1) / per) return ORC_ERR_FORMAT;
+    size_t stab = (32 + 4 * (size_t)nsym + 15) & ~(size_t)15;
+    size_t ctab = stab + (coder ? 4096 * 4 : 0);
     if (ctab + 16 * (size_t)nch > len) return ORC_ERR_FORMAT;
-    uint64_t nf = n / per;                                   /* full chunks */
+    uint64_t nf = ne / per;                                  /* full chunks */
+    int region = ver == 3 && (mode == 1 || mode == 3);       /* full chunks' planes in the plane region */
     size_t preg = (ctab + 16 * (size_t)nch + 255) & ~(size_t)255;
-    if (mode == 1 && preg + nf * per > len) return ORC_ERR_FORMAT;
+    if (region && preg + nf * per > len) return ORC_ERR_FORMAT;
     uint32_t val[256], fr[256], cons[256], cum[256], c = 0;
     for (uint32_t s = 0; s < nsym; s++) {
         uint32_t e = get32(blob + 32 + 4 * s);
@@ -816,54 +876,87 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
     }
     if (c != 4096) return ORC_ERR_FORMAT;
     uint8_t slot2sym[4096];
-    for (uint32_t s = 0; s < nsym; s++) for (uint32_t k = 0; k < fr[s]; k++) slot2sym[cum[s] + k] = (uint8_t)s;
+    uint32_t ttab[4096];
+    if (coder == 0) {
+        for (uint32_t s = 0; s < nsym; s++) for (uint32_t k = 0; k < fr[s]; k++) slot2sym[cum[s] + k] = (uint8_t)s;
+    } else {
+        for (uint32_t p = 0; p < 4096; p++) {
+            uint32_t e = get32(blob + stab + 4 * p), nb = (e >> 12) & 15, s = (e >> 16) & 0xFF;
+            if ((e >> 24) || s >= nsym || nb > 12 || (e & 0xFFF) + (1u << nb) > 4096) return ORC_ERR_FORMAT;
+            ttab[p] = e;
+        }
+    }
+    const uint32_t K = lanes / 64, bs = lanes == 256 ? 4 : 8;   /* states per lane, steps per plane block */
     for (uint32_t ci = 0; ci < nch; ci++) {
         const uint8_t *ce = blob + ctab + 16 * (size_t)ci;
         uint64_t off = get64(ce); uint32_t nw = get32(ce + 8), np = get32(ce + 12);
-        int split = mode == 1 && ci < nf;                   /* plane in the plane region */
-        size_t wbytes = ((size_t)nw * 2 + 15) & ~(size_t)15, pbytes = split ? 0 : ((size_t)np + 15) & ~(size_t)15;
-        if (off % 16 || off + 4 * lanes + wbytes + pbytes > len) return ORC_ERR_FORMAT;
-        const uint8_t *st = blob + off, *wd = st + 4 * lanes, *pl = wd + wbytes;
-        uint64_t nc = ci < nf ? per : n - nf * per;
+        int split = region && ci < nf;
+        size_t sbytes = coder == 0 ? ((size_t)nw * 2 + 15) & ~(size_t)15
+                                   : ((((size_t)nw + 31) / 32) * 4 + 15) & ~(size_t)15;
+        size_t pbytes = split ? 0 : ((size_t)np + 15) & ~(size_t)15;
+        if (off % 16 || off + 4 * lanes + sbytes + pbytes > len) return ORC_ERR_FORMAT;
+        const uint8_t *st = blob + off, *wd = st + 4 * lanes, *pl = wd + sbytes;
+        uint64_t nc = ci < nf ? per : ne - nf * per;
         uint64_t nsteps = (nc + lanes - 1) / lanes;
         uint32_t x[256];
         for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
+        if (coder == 1) for (uint32_t l = 0; l < lanes; l++) if (x[l] >= 4096) return ORC_ERR_FORMAT;
         uint64_t wp = 0, pp = 0;
-        const uint32_t K = lanes / 64;
+        bitrd br = {wd, nw, 0};
+        int err = 0;
         for (uint64_t t = 0; t < nsteps; t++) {
-            for (uint32_t sv = 0; sv < lanes; sv++) {
-                uint32_t g = sv / 64, wl = sv % 64;
+            for (uint32_t i = 0; i < lanes; i++) {
+                /* rANS: states in v order (group-major); tANS: chunk element order (lane-major) */
+                uint32_t g = coder == 0 ? i / 64 : i % K, wl = coder == 0 ? i % 64 : i / K, sv = g * 64 + wl;
                 uint64_t j = t * lanes + (uint64_t)wl * K + g;
                 if (j >= nc) continue;
-                uint32_t slot = x[sv] & 4095, s = slot2sym[slot];
-                x[sv] = fr[s] * (x[sv] >> 12) + slot - cum[s];
-                if (x[sv] < RANS_L) {
-                    if (wp >= nw) return ORC_ERR_FORMAT;
-                    x[sv] = (x[sv] << 16) | get16(wd + 2 * wp); wp++;
+                uint32_t s;
+                if (coder == 0) {
+                    uint32_t slot = x[sv] & 4095;
+                    s = slot2sym[slot];
+                    x[sv] = fr[s] * (x[sv] >> 12) + slot - cum[s];
+                    if (x[sv] < RANS_L) {
+                        if (wp >= nw) return ORC_ERR_FORMAT;
+                        x[sv] = (x[sv] << 16) | get16(wd + 2 * wp); wp++;
+                    }
+                } else {
+                    uint32_t e = ttab[x[sv]];
+                    s = (e >> 16) & 0xFF;
+                    x[sv] = (e & 0xFFF) + br_take(&br, (e >> 12) & 15, &err);
                 }
                 uint32_t v = val[s];
                 if (cons[s]) {
                     uint32_t b;
-                    if (mode == 1) {
-                        uint64_t bs = lanes == 256 ? 4 : 8;   /* steps per plane block */
+                    if (mode == 1 || mode == 3) {
                         uint64_t blk = t / bs, q = t % bs;
                         uint64_t in_blk = (uint64_t)wl * bs * K + q * K + g;
                         if (blk * bs * lanes + in_blk >= np) return ORC_ERR_FORMAT;
                         b = split ? blob[preg + (blk * nf + ci) * bs * lanes + in_blk] : pl[blk * bs * lanes + in_blk];
-                    } else if (mode == 2) {
+                    } else if (mode == 2 && coder == 0) {
                         if (pp >= np) return ORC_ERR_FORMAT;
                         b = pl[pp++];
+                    } else if (mode == 2) {
+                        b = br_take(&br, 8, &err);
                     } else return ORC_ERR_FORMAT;
-                    v = v | (b & 0x7F) | ((b & 0x80) << 8);
+                    if (mode == 3) {
+                        uint32_t e0 = v & 15, e1 = (v >> 4) & 15;
+                        uint32_t b0 = (b & 0x80) | (e0 << 3) | (b & 7);
+                        uint32_t b1 = (((b >> 3) & 1) << 7) | (e1 << 3) | ((b >> 4) & 7);
+                        v = b0 | (b1 << 8);
+                    } else {
+                        v = v | (b & 0x7F) | ((b & 0x80) << 8);
+                    }
                 }
-                uint64_t e = ci < nf ? ((j / 512) * nf + ci) * 512 + j % 512 : nf * per + j;
-                if (eb == 2) ((uint16_t *)out_v)[e] = (uint16_t)v;
+                if (err) return ORC_ERR_FORMAT;
+                uint64_t e = ci < nf && ver == 3 ? ((j / 512) * nf + ci) * 512 + j % 512 : (uint64_t)ci * per + j;
+                if (eb == 2 || mode == 3) ((uint16_t *)out_v)[e] = (uint16_t)v;
                 else ((uint8_t *)out_v)[e] = (uint8_t)v;
             }
         }
-        for (uint32_t l = 0; l < lanes; l++) if (x[l] != RANS_L) return ORC_ERR_FORMAT;
-        if (wp != nw) return ORC_ERR_FORMAT;
-        if (mode == 2 && pp != np) return ORC_ERR_FORMAT;
+        for (uint32_t l = 0; l < lanes; l++) if (x[l] != (coder == 0 ? RANS_L : 0)) return ORC_ERR_FORMAT;
+        if (coder == 0 && wp != nw) return ORC_ERR_FORMAT;
+        if (coder == 1 && br.pos != nw) return ORC_ERR_FORMAT;
+        if (coder == 0 && mode == 2 && pp != np) return ORC_ERR_FORMAT;
     }
     return ORC_OK;
 }

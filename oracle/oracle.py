@@ -17,7 +17,7 @@ LIB_PATH = _HERE / "_build" / "liboracle.so"
 __all__ = [
     "build", "lib", "quantise_ref", "quantise_sk", "rans_encode", "rans_decode", "rans_decode_nb",
     "par1_encode", "par1_decode", "tans_encode", "tans_decode", "sk_encode", "sk_decode",
-    "chunk_decode", "OracleError",
+    "chunk_decode", "tans_table", "OracleError",
 ]
 
 
@@ -58,6 +58,7 @@ def lib():
             "orc_sk_encode": (I64, [P, S, P, S]),
             "orc_sk_decode": (I, [P, S, S, P]),
             "orc_chunk_decode": (I, [P, S, S, P]),
+            "orc_tans_table": (I, [P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -187,5 +188,17 @@ def sk_decode(blob: bytes, n: int) -> bytes:
 
 
 def chunk_decode(blob: bytes, n: int, elem_bytes: int = 2) -> bytes:
-    """CPU decode of the build's GPU-native BSCK format (no reference counterpart)."""
+    """CPU decode of the build's GPU-native BSCK format, either coder, layout
+    versions 2 and 3 (no reference counterpart)."""
     return _decode("orc_chunk_decode", blob, n, elem_bytes)
+
+
+def tans_table(freqs) -> np.ndarray:
+    """The BSCK tANS decode table (4096 uint32 entries) of quantised
+    frequencies summing to 4096."""
+    f = np.ascontiguousarray(freqs, dtype=np.uint32)
+    out = np.zeros(4096, np.uint32)
+    rc = lib().orc_tans_table(_p(f), len(f), _p(out))
+    if rc != 0:
+        raise OracleError("orc_tans_table", rc)
+    return out

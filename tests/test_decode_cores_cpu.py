@@ -5,8 +5,8 @@ per lane, wavefront operations and barriers as switch points), driven by
 tests/native/decode_fuzz.cpp; a second build at -O2 without instrumentation
 decodes the clean blobs and a share of the corrupted ones.
 
-Cases: clean blobs of every BSCK plane mode, state width and element size,
-and of the reference's three formats on both decode paths (wave-serial and
+Cases: clean blobs of every BSCK plane mode, state width, element size and
+coder (rANS, tANS), the layout-version-2 golden blobs, and of the reference's three formats on both decode paths (wave-serial and
 lane-per-chain), each of which must decode to its source; then thousands of
 corrupted copies (single and multiple byte changes, biased to the headers,
 tables and chunk tables, and truncations). A corrupted BSCK blob goes to the
@@ -43,6 +43,12 @@ CLANG = "/opt/rocm/llvm/bin/clang++"
 def _bf16(x: np.ndarray) -> np.ndarray:
     u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _fp8(x: np.ndarray) -> np.ndarray:
+    """fp8 e4m3 bytes of x (torch's rounding)."""
+    import torch
+    return torch.from_numpy(x.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy().copy()
 
 
 def _case(kind: int, clean: bool, n: int, eb: int, blob: bytes, extra: bytes = b"", want: bytes = b"") -> bytes:
@@ -93,6 +99,26 @@ def _bsck_inputs(rng):
     hz2[rng.permutation(hz2.size)[: hz2.size // 2]] = 0
     yield hz2, dict(lanes=128, steps=64, mode=2)
     yield _bf16(rng.standard_normal(2 * 8192 + 9) * 0.02), dict(lanes=128, steps=64, mode=1)
+    # fp8 exponent pairs (plane mode 3), every state width, with a tail
+    f8 = _fp8(rng.standard_normal(2 * (3 * 2048 + 77)))
+    yield f8, dict(lanes=128, steps=16, mode=3)
+    yield f8[:2 * 700], dict(lanes=64, steps=16, mode=3)
+    yield f8, dict(lanes=256, steps=16, mode=3)
+    # tANS: every plane mode, state width and element kind, full chunks and tails
+    yield g, dict(lanes=128, steps=16, coder=1)
+    yield g[:200], dict(lanes=64, steps=16, coder=1)
+    yield _bf16(rng.standard_t(3, 9000) * 0.02), dict(lanes=256, steps=32, coder=1)
+    yield hz, dict(lanes=128, steps=16, mode=2, coder=1)
+    yield hz[:1500], dict(lanes=64, steps=32, mode=2, coder=1)
+    yield hz, dict(lanes=256, steps=16, mode=2, coder=1)
+    yield norms, dict(lanes=128, steps=16, coder=1)
+    yield rng.integers(0, 65536, 2500).astype(np.uint16), dict(lanes=128, steps=16, mode=1, coder=1)
+    yield rng.integers(0, 256, 4000).astype(np.uint8), dict(lanes=128, steps=16, coder=1)
+    yield rng.integers(0, 256, 3 * 8192 + 100).astype(np.uint8), dict(lanes=128, steps=64, coder=1)
+    yield hz2, dict(lanes=128, steps=64, mode=2, coder=1)
+    yield f8, dict(lanes=128, steps=16, mode=3, coder=1)
+    yield f8, dict(lanes=256, steps=16, mode=3, coder=1)
+    yield np.array([0x3F80], np.uint16), dict(lanes=64, steps=16, coder=1)
 
 
 def _ref_inputs(rng):
@@ -108,9 +134,11 @@ def _ref_inputs(rng):
 def _write_cases(path: Path, n_bsck: int, n_ref: int) -> dict:
     rng = np.random.default_rng(2024)
     cases, counts = [], {"bsck_clean": 0, "bsck_corrupt": 0, "ref_clean": 0, "ref_corrupt": 0, "ref_parser_refused": 0}
-    bsck = list(_bsck_inputs(rng))
-    for w, kw in bsck:
-        blob = bc.encode_array(w, **kw)
+    bsck = [(w, bc.encode_array(w, **kw)) for w, kw in _bsck_inputs(rng)]
+    # layout-version-2 blobs written by the earlier encoder (tests/golden/make_bsck_v2.py)
+    v2 = np.load(Path(__file__).resolve().parent / "golden" / "bsck_v2_vectors.npz")
+    bsck += [(v2[k], v2["blob_" + k[4:]].tobytes()) for k in v2.files if k.startswith("src_")]
+    for w, blob in bsck:
         eb = w.dtype.itemsize
         cases.append(_case(0, True, w.size, eb, blob, want=w.tobytes()))
         counts["bsck_clean"] += 1

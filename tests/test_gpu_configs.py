@@ -9,8 +9,10 @@ C2  the full Llama-3-8B-shaped model (32 layers, untied 128256x4096
     from the CPU generator.
 C3  8192x8192 stress: (a) Student-t df=3 at std 0.02, (b) half exact zeros,
     (c) fp8 e4m3 of N(0, 1) plus its bf16 residual; "forced rANS" = the
-    reference's bf16_parallel_v1 and this engine's bf16_chunked_v1, "forced tANS"
-    = the reference's bf16_se_tans (its Numba rANS codec).
+    reference's bf16_parallel_v1 and this engine's bf16_chunked_v1 /
+    fp8_chunked_v1, "forced tANS" = this engine's bf16_chunked_tans_v1 /
+    fp8_chunked_tans_v1 (table ANS) and the reference's bf16_se_tans (its Numba
+    rANS codec), forced through a CODEC_CANDIDATES override.
 C4  KV cache blocks of 256 tokens, K and V [8 heads, 32768 tokens, 128] per layer
     scaled per head by U[0.5, 2], 64 random blocks per layer decoded in one launch:
     all 32 layers encoded on the GPU from device K/V and all 4,096 decoded blocks
@@ -107,10 +109,39 @@ def test_c3_bf16_stress_forced_rans(kind):
     _check_ref("bf16_parallel_v1", oracle.par1_encode(w), w)
 
 
+def _forced(fmt: str, codec: str, words):
+    """Encode through codec_registry.auto_select_codec with CODEC_CANDIDATES
+    overridden to one codec (the reference's forcing mechanism,
+    tests/test_b4_auto_select.py:121-132 there), decode through the decoder's
+    dispatch, compare md5."""
+    from bigsmall_amd import codec_registry, decoder
+    saved = dict(codec_registry.CODEC_CANDIDATES)
+    try:
+        codec_registry.CODEC_CANDIDATES[fmt] = [codec]
+        raw = words.tobytes()
+        blob, name, extras = codec_registry.auto_select_codec(raw, fmt, "float8_e4m3fn" if fmt == "fp8" else "bfloat16")
+    finally:
+        codec_registry.CODEC_CANDIDATES.clear()
+        codec_registry.CODEC_CANDIDATES.update(saved)
+    assert name == codec
+    t = {"name": "c3", "codec": name, "extra": extras, "shape": [words.size],
+         "dtype": "float8_e4m3fn" if fmt == "fp8" else "bfloat16"}
+    got = decoder._decode_blob(t, blob)
+    assert hashlib.md5(got).hexdigest() == hashlib.md5(raw).hexdigest(), codec
+    assert got == oracle.chunk_decode(blob, words.size, words.dtype.itemsize), codec
+    return blob
+
+
 @pytest.mark.parametrize("kind", ["studentt", "halfzero"])
 def test_c3_bf16_stress_forced_tans(kind):
     w = _stress(kind)
-    _say(f"[c3] {kind} bf16_se_tans")
+    _say(f"[c3] {kind} bf16_chunked_tans_v1 (forced tANS, this engine's format)")
+    blob = _forced("bf16", "bf16_chunked_tans_v1", w)
+    assert blob[28] == 1 and blob[6] == (2 if kind == "halfzero" else 1)
+    for mode in (1, 2):
+        _say(f"[c3] {kind} bf16_chunked_tans_v1 mode={mode}")
+        _check_bsck(w, mode=mode, coder=1)
+    _say(f"[c3] {kind} bf16_se_tans (the reference's forced-tANS format)")
     _check_ref("bf16_se_tans", oracle.tans_encode(w), w)
 
 
@@ -119,13 +150,18 @@ def test_c3_fp8_and_residual():
     x = torch.randn(8192 * 8192, generator=g)
     f8 = x.to(torch.float8_e4m3fn)
     resid = (x - f8.float()).bfloat16()
-    _say("[c3] fp8 e4m3 fp8_chunked_v1")
-    _check_bsck(f8.view(torch.uint8).numpy())
+    b8 = f8.view(torch.uint8).numpy()
+    for coder, codec in ((0, "fp8_chunked_v1"), (1, "fp8_chunked_tans_v1")):
+        _say(f"[c3] fp8 e4m3 {codec} (exponent pairs, then byte symbols)")
+        blob = _forced("fp8", codec, b8)
+        assert blob[6] == 3 and blob[28] == coder
+        _check_bsck(b8, mode=0, coder=coder)
     rw = _words(resid)
-    _say("[c3] residual bf16_chunked_v1 / bf16_parallel_v1")
-    _check_bsck(rw)
+    _say("[c3] residual bf16_chunked_v1 / bf16_parallel_v1 (forced rANS)")
+    _forced("bf16", "bf16_chunked_v1", rw)
     _check_ref("bf16_parallel_v1", oracle.par1_encode(rw), rw)
-    _say("[c3] residual bf16_se_tans (forced tANS)")
+    _say("[c3] residual bf16_chunked_tans_v1 / bf16_se_tans (forced tANS)")
+    assert _forced("bf16", "bf16_chunked_tans_v1", rw)[28] == 1
     _check_ref("bf16_se_tans", oracle.tans_encode(rw), rw)
 
 

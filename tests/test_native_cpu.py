@@ -110,9 +110,10 @@ def test_planted_corruption_is_caught():
         oracle.chunk_decode(bytes(bad), w.size)
 
 
-@pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 2), ("elem_bytes", 3), ("plane_mode", 3),
-                                         ("prec", 11), ("lanes", 96), ("steps", 24), ("n_syms", 0),
-                                         ("n_chunks", 7), ("truncated", None)])
+@pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 4), ("version", 1), ("elem_bytes", 3),
+                                         ("plane_mode", 3), ("plane_mode", 4), ("prec", 11), ("lanes", 96),
+                                         ("steps", 24), ("n_syms", 0), ("n_chunks", 7), ("coder", 2),
+                                         ("truncated", None)])
 def test_malformed_header_raises_value_error(field, value):
     """bs_chunk_inspect (host code) rejects every malformed header field, and
     the codec turns that into ValueError, as the reference does for bad magic
@@ -123,7 +124,8 @@ def test_malformed_header_raises_value_error(field, value):
     head = bytearray(bc.encode_array(w)[:32])
     assert bc.info(bytes(head)).n == w.size
     offs = {"version": (4, "<B"), "elem_bytes": (5, "<B"), "plane_mode": (6, "<B"), "prec": (7, "<B"),
-            "lanes": (20, "<H"), "steps": (16, "<I"), "n_syms": (22, "<H"), "n_chunks": (24, "<I")}
+            "lanes": (20, "<H"), "steps": (16, "<I"), "n_syms": (22, "<H"), "n_chunks": (24, "<I"),
+            "coder": (28, "<I")}
     if field == "magic":
         head[0:4] = value
     elif field == "truncated":
@@ -196,7 +198,7 @@ def test_struct_layouts_match_the_header(tmp_path):
     if shutil.which("gcc") is None:
         pytest.skip("needs gcc")
     structs = {
-        "bs_chunk_info": (["n", "n_chunks", "steps", "lanes", "n_syms", "elem_bytes", "plane_mode"],
+        "bs_chunk_info": (["n", "n_chunks", "steps", "lanes", "n_syms", "elem_bytes", "plane_mode", "coder"],
                           [(f[0], getattr(_native.BsChunkInfo, f[0]).offset, ctypes.sizeof(f[1]))
                            for f in _native.BsChunkInfo._fields_]),
         "bs_chunk_task": (["blob", "blob_bytes", "out", "n", "wg_begin", "n_chunks"], TASK_DTYPE),
