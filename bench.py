@@ -87,83 +87,117 @@ def zero_layer(words: dict, fraction: float, seed: int = 1) -> dict:
 
 
 def host_cpu_info() -> dict:
-    """The host CPU model and the CPUs this process may run on."""
-    model = "unknown"
+    """The host CPU as /proc/cpuinfo names it (model name, family, model and
+    stepping numbers, logical CPUs listed) and the CPUs this process may run on."""
+    info = {}
+    fields = {"model name": "cpu_model", "cpu family": "cpu_family", "model": "cpu_model_number",
+              "stepping": "cpu_stepping", "cpu MHz": "cpu_mhz", "cache size": "cpu_cache"}
+    listed = 0
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if ":" not in line:
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                listed += k == "processor"
+                if k in fields and fields[k] not in info:     # the first CPU's values
+                    info[fields[k]] = v
     except OSError:
         pass
+    info.setdefault("cpu_model", "unknown")
     try:
         usable = len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
         usable = os.cpu_count() or 1
-    return {"cpu_model": model, "host_cpus": usable}
+    info["cpus_listed"] = listed
+    info["host_cpus"] = usable
+    return info
 
 
-def cpu_baseline(words: dict, budget_s: float = 12.0, bsck_blobs: dict | None = None):
-    """Oracle port of bf16_se_single_kernel decode (bigsmall/codecs/single_kernel.py:431-580)
-    on the layer's seven matrices: all of them at once, one host thread per tensor
-    (the reported value), and one thread on as many tensors as fit the time
-    budget (`single_thread`). With `bsck_blobs` (the layer's blobs in the format
-    the GPU decodes), the oracle's C decoder of that format on the same
-    matrices, one thread per tensor, is reported beside it (`same_format`). The
-    oracle's C calls run without the GIL."""
+def _timed_cpu(fn, items) -> tuple[float, float]:
+    """(algorithmic bytes, seconds) of fn over items, one after another."""
+    t0 = time.perf_counter()
+    done = sum(fn(it) for it in items)
+    return done, time.perf_counter() - t0
+
+
+def cpu_baseline(words: dict, budget_s: float = 6.0, bsck_blobs: dict | None = None):
+    """The reference's CPU decode of the layer's seven matrices on the host
+    cores (the oracle's C restatement, run without the GIL):
+      value          bf16_parallel_v1 (bigsmall/codecs/bf16_parallel.py:262-352),
+                     the reference's stream-parallel format: each matrix's 128
+                     streams split over every host CPU, matrix after matrix;
+      single_thread  the same on one thread, over the matrices that fit the
+                     time budget;
+      serial_chain   bf16_se_single_kernel (single_kernel.py:431-580), the
+                     reference's fastest single-chain CPU decoder: one thread
+                     per matrix (7) and one thread alone;
+      same_format    the oracle's decoder of the blobs the GPU line decodes,
+                     its chunks split over every host CPU, and on one thread."""
     from concurrent.futures import ThreadPoolExecutor
     import oracle
     oracle.build()
+    host = host_cpu_info()
+    cores = host["host_cpus"]
     mats = [(name, words[name]) for name, _ in LAYER if "norm" not in name]
-    threads = max(1, min(len(mats), os.cpu_count() or 1, 16))
-    with ThreadPoolExecutor(threads) as ex:
-        blobs = dict(zip([m[0] for m in mats], ex.map(lambda m: oracle.sk_encode(m[1]), mats)))
+    short = lambda names: ", ".join(nm.split(".")[-2] for nm in names)
+    per_tensor = max(1, min(len(mats), cores, 16))
+    with ThreadPoolExecutor(per_tensor) as ex:
+        par1 = dict(zip([m[0] for m in mats], ex.map(lambda m: oracle.par1_encode(m[1]), mats)))
+        sk = dict(zip([m[0] for m in mats], ex.map(lambda m: oracle.sk_encode(m[1]), mats)))
 
-    def one(m):
-        out = oracle.sk_decode(blobs[m[0]], m[1].size)
-        assert out == m[1].tobytes(), "oracle decode mismatch"
-        return m[1].nbytes + len(blobs[m[0]])
+    def check(out, m, blob):
+        assert out == m[1].tobytes(), f"oracle decode mismatch ({m[0]})"
+        return m[1].nbytes + len(blob)
 
-    t0 = time.perf_counter()
-    with ThreadPoolExecutor(threads) as ex:
-        decoded_all = sum(ex.map(one, mats))
-    t_all = time.perf_counter() - t0
-
-    decoded, t_total, names = 0, 0.0, []
+    # bf16_parallel_v1: every CPU on each matrix, then one thread on a budget
+    par_all, t_par_all = _timed_cpu(lambda m: check(oracle.par1_decode_threads(par1[m[0]], m[1].size, cores), m,
+                                                    par1[m[0]]), mats)
+    done, t_one, names = 0, 0.0, []
     for m in mats:
-        t0 = time.perf_counter()
-        decoded += one(m)
-        t_total += time.perf_counter() - t0
-        names.append(m[0].split(".")[-2])
-        if t_total > budget_s:
+        b, t = _timed_cpu(lambda mm: check(oracle.par1_decode(par1[mm[0]], mm[1].size), mm, par1[mm[0]]), [m])
+        done, t_one = done + b, t_one + t
+        names.append(m[0])
+        if t_one > budget_s:
             break
-    same = None
-    if bsck_blobs is not None:
-        def one_bsck(m):
-            out = oracle.chunk_decode(bsck_blobs[m[0]], m[1].size)
-            assert out == m[1].tobytes(), "oracle BSCK decode mismatch"
-            return m[1].nbytes + len(bsck_blobs[m[0]])
-        t0 = time.perf_counter()
-        with ThreadPoolExecutor(threads) as ex:
-            bsck_all = sum(ex.map(one_bsck, mats))
-        t_bsck = time.perf_counter() - t0
-        same = {"value": bsck_all / t_bsck / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": (f"the oracle's C decoder of bf16_chunked_v1 (the format the GPU line decodes) on the "
-                           f"layer's {len(mats)} matrices, one host thread per tensor: "
-                           f"{bsck_all / 1e6:.0f} MB algorithmic in {t_bsck:.2f} s")}
-    return {
-        "value": decoded_all / t_all / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"oracle C port of the reference bf16_se_single_kernel CPU decode of the layer's "
-                   f"{len(mats)} matrices, one host thread per tensor ({threads} threads): "
-                   f"{decoded_all / 1e6:.0f} MB algorithmic in {t_all:.2f} s"),
-        "single_thread": {"value": decoded / t_total / 1e9, "cores": 1,
-                          "sample": f"{len(names)} tensors ({', '.join(names)}): "
-                                    f"{decoded / 1e6:.0f} MB algorithmic in {t_total:.2f} s"},
-        "same_format": same,
-        "host": host_cpu_info(),
-        "note": "one serial sign+exponent chain per tensor, so at most one thread per tensor",
+    # bf16_se_single_kernel: one serial chain per matrix
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(per_tensor) as ex:
+        sk_all = sum(ex.map(lambda m: check(oracle.sk_decode(sk[m[0]], m[1].size), m, sk[m[0]]), mats))
+    t_sk_all = time.perf_counter() - t0
+    sk_one, t_sk_one = _timed_cpu(lambda m: check(oracle.sk_decode(sk[m[0]], m[1].size), m, sk[m[0]]), mats[:2])
+    out = {
+        "value": par_all / t_par_all / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": (f"oracle C port of the reference's bf16_parallel_v1 CPU decode (128 independent streams per "
+                   f"tensor, split over {cores} host threads) of the layer's {len(mats)} matrices: "
+                   f"{par_all / 1e6:.0f} MB algorithmic in {t_par_all:.2f} s"),
+        "single_thread": {"value": done / t_one / 1e9, "unit": "GB/s", "cores": 1,
+                          "sample": f"bf16_parallel_v1, {len(names)} tensors ({short(names)}): "
+                                    f"{done / 1e6:.0f} MB algorithmic in {t_one:.2f} s"},
+        "serial_chain": {"codec": "bf16_se_single_kernel", "value": sk_all / t_sk_all / 1e9, "unit": "GB/s",
+                         "cores": per_tensor,
+                         "sample": f"one host thread per tensor: {sk_all / 1e6:.0f} MB algorithmic in "
+                                   f"{t_sk_all:.2f} s (one serial sign+exponent chain per tensor, so at most "
+                                   f"one thread per tensor)",
+                         "single_thread": {"value": sk_one / t_sk_one / 1e9, "cores": 1,
+                                           "sample": f"{short([m[0] for m in mats[:2]])}: "
+                                                     f"{sk_one / 1e6:.0f} MB algorithmic in {t_sk_one:.2f} s"}},
+        "host": host,
     }
+    if bsck_blobs is not None:
+        bs_all, t_bs_all = _timed_cpu(lambda m: check(oracle.chunk_decode_threads(bsck_blobs[m[0]], m[1].size, cores),
+                                                      m, bsck_blobs[m[0]]), mats)
+        bs_one, t_bs_one = _timed_cpu(lambda m: check(oracle.chunk_decode(bsck_blobs[m[0]], m[1].size), m,
+                                                      bsck_blobs[m[0]]), mats[:2])
+        out["same_format"] = {
+            "value": bs_all / t_bs_all / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"the oracle's C decoder of the format the GPU line decodes on the layer's {len(mats)} "
+                       f"matrices, chunks split over {cores} host threads: {bs_all / 1e6:.0f} MB algorithmic "
+                       f"in {t_bs_all:.2f} s"),
+            "single_thread": {"value": bs_one / t_bs_one / 1e9, "cores": 1,
+                              "sample": f"{short([m[0] for m in mats[:2]])}: {bs_one / 1e6:.0f} MB algorithmic "
+                                        f"in {t_bs_one:.2f} s"}}
+    return out
 
 
 def measure_copy(dev, mib: int = 2048, reps: int = 5) -> float:
@@ -693,15 +727,19 @@ def run_c3(args) -> dict:
     # the format's default chunk (432 steps: sized for layer batches) gives one
     # 67M-element tensor 1,214 chunks, fewer than the 4,096 wavefront slots of
     # the GPU; 128 steps fill them (4,096 chunks) at a small ratio cost
-    steps = args.chunk_steps or 128
     R = max(1, args.rotate)
+    lanes = args.lanes or bc.DEFAULT_LANES
     coders = [("rans_bsck", bc.CODER_RANS), ("tans_bsck", bc.CODER_TANS)]
     if args.rans_only:
         coders = coders[:1]
     for name, w in tensors:
         res[name] = {}
+        # fp8 tensors code byte pairs (one symbol per two bytes): half the
+        # steps per chunk keep the chunk count, and so the GPU's fill, of the
+        # bf16 tensors (4,096 chunks of 128 x 128 at the default)
+        steps = args.chunk_steps or max(16, (128 * 128 // lanes) // (2 if w.dtype == np.uint8 else 1))
         for key, coder in coders:
-            blob = bc.encode_array(w, steps=steps, lanes=args.lanes or bc.DEFAULT_LANES, coder=coder)
+            blob = bc.encode_array(w, steps=steps, lanes=lanes, coder=coder)
             inf = bc.info(blob)
             # R copies of the blob and of the output, decoded in turn: the working
             # set (R x up to 245 MB) is far beyond the 256 MB Infinity Cache
@@ -970,6 +1008,8 @@ def main():
                     help="c3 workload: comma-separated subset of studentt,halfzero,fp8_e4m3,fp8_residual")
     ap.add_argument("--ref-codecs", default="",
                     help="reflayer workload: comma-separated subset of bf16_parallel_v1,bf16_se_tans")
+    ap.add_argument("--coder", choices=["rans", "tans"], default="rans",
+                    help="layer workload: the engine format's entropy coder (bf16_chunked_v1 or bf16_chunked_tans_v1)")
     ap.add_argument("--engine-only", action="store_true",
                     help="c3 workload: only this engine's format, rANS and tANS (skip the reference-format "
                          "bf16_se_tans decode and its CPU baseline)")
@@ -1011,7 +1051,11 @@ def main():
               for r in range(R)]
     log(f"[bench] {R} layer(s) generated in {time.time() - t0:.1f}s")
     t0 = time.time()
-    blobs = [{name: bc.encode_array(w, steps=steps, lanes=lanes) for name, w in words.items()} for words in layers]
+    coder = bc.CODER_TANS if args.coder == "tans" else bc.CODER_RANS
+    if coder == bc.CODER_TANS:
+        workload += "_tans"
+    blobs = [{name: bc.encode_array(w, steps=steps, lanes=lanes, coder=coder) for name, w in words.items()}
+             for words in layers]
     log(f"[bench] encoded in {time.time() - t0:.1f}s")
     words = layers[0]
     n_total = sum(w.size for w in words.values())
@@ -1132,7 +1176,8 @@ def main():
             "workload": workload,
             "tensors": len(LAYER), "elements": n_total, "decoded_bytes": out_total,
             "compressed_bytes": comp_total, "ratio_pct": round(100 * comp_total / out_total, 3),
-            "codec": bc.CODEC_BF16, "chunk_steps": steps, "chunk_lanes": lanes, "launches_per_step": 1,
+            "codec": bc.CODEC_BF16_TANS if coder == bc.CODER_TANS else bc.CODEC_BF16, "chunk_steps": steps,
+            "chunk_lanes": lanes, "launches_per_step": 1,
             "distinct_layers": R, "working_set_bytes": R * algo_bytes,
         },
         "ms_per_layer": round(ms_per, 5),

@@ -78,7 +78,9 @@
 //     update, the output byte taken from bits 24..31 with v_perm;
 //   rANS generic (bf16 plane modes 0/2): {f, value | (slot - cf) << 16 | consume << 31};
 //     the update is one shift, one bit-field extract and one v_mad_u32_u24;
-//   tANS dense, bytes and pairs: one word {newX, nb, -, output byte};
+//   tANS dense: one word {newX:12, nb:4, exponent word (e << 7):16};
+//   tANS pairs: one word {newX:12, nb:4, e0 << 3 | e1 << 11:16};
+//   tANS bytes: one word {newX:12, nb:4, -:8, byte:8};
 //   tANS generic: {newX | nb << 12 | (nb + raw) << 16 | raw << 21, value | consume << 31}.
 #include <stdint.h>
 
@@ -503,32 +505,45 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
   uint32_t pos = S.bpos + incl - tot;                  // this lane's first bit
   S.bpos += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
   S.wptr = (S.bpos >> 5) << 1;                          // ring words no longer needed: [.., wptr)
-  if (FAST && K <= 2) {
-    // at most 2 x 12 bits per lane: one 32-bit window
-    const uint32_t win = stream_bits(ring, pos);
-    uint32_t off = 0;
+  // The lane's states are read in pairs: a one-word-layout pair takes at most
+  // 2 x 12 bits (one 32-bit window), a generic pair at most 2 x 20 (a 64-bit
+  // window from three ring words, the second state's bits funnel-shifted out
+  // of it).
 #pragma unroll
-    for (int g = 0; g < K; ++g) {
-      const uint32_t x = (e[g] & 0xFFFu) | __builtin_amdgcn_ubfe(win, off, nb[g]);
-      off += nb[g];
-      S.x[g] = PARTIAL && !act[g] ? S.x[g] : x;
-      d[g] = e[g];
-    }
-  } else {
-#pragma unroll
-    for (int g = 0; g < K; ++g) {
+  for (int g = 0; g < K; g += 2) {
+    const bool two = g + 1 < K;
+    if (FAST) {
       const uint32_t win = stream_bits(ring, pos);
-      pos += nt[g];
-      const uint32_t x = (e[g] & 0xFFFu) | __builtin_amdgcn_ubfe(win, 0, nb[g]);
-      S.x[g] = PARTIAL && !act[g] ? S.x[g] : x;
-      if (FAST) {
-        d[g] = e[g];
-      } else if (MODE == 2) {
-        // the plane byte follows the state bits; a symbol without one reads 0 bits
-        d[g] = byte_merge(hv[g], __builtin_amdgcn_ubfe(win, nb[g], __builtin_amdgcn_ubfe(e[g], 21, 4)));
-      } else {
-        d[g] = hv[g];
+      const uint32_t x0 = (e[g] & 0xFFFu) | __builtin_amdgcn_ubfe(win, 0, nb[g]);
+      S.x[g] = PARTIAL && !act[g] ? S.x[g] : x0;
+      d[g] = e[g];
+      if (two) {
+        const uint32_t x1 = (e[g + 1] & 0xFFFu) | __builtin_amdgcn_ubfe(win, nb[g], nb[g + 1]);
+        S.x[g + 1] = PARTIAL && !act[g + 1] ? S.x[g + 1] : x1;
+        d[g + 1] = e[g + 1];
+        if (g + 2 < K) pos += nb[g] + nb[g + 1];
       }
+    } else {
+      const uint32_t w = (pos >> 5) & 1023u;
+      const uint32_t r0 = ring[w], r1 = ring[w + 1];
+      const uint32_t lo = __builtin_amdgcn_alignbit(r1, r0, pos);
+      uint32_t win[2] = {lo, lo};
+      if (two) {
+        // bits 32..63 from `pos` come from the third word (w + 2 <= 1025:
+        // inside the ring's mirrored head)
+        const uint32_t hi = __builtin_amdgcn_alignbit(ring[w + 2], r1, pos);
+        win[1] = __builtin_amdgcn_alignbit(hi, lo, nt[g]);   // nt <= 20: from bit nt[g] on
+      }
+#pragma unroll
+      for (int h = 0; h < (two ? 2 : 1); ++h) {
+        const int gg = g + h;
+        const uint32_t x = (e[gg] & 0xFFFu) | __builtin_amdgcn_ubfe(win[h], 0, nb[gg]);
+        S.x[gg] = PARTIAL && !act[gg] ? S.x[gg] : x;
+        // the plane byte follows the state bits; a symbol without one reads 0 bits
+        d[gg] = MODE == 2 ? byte_merge(hv[gg], __builtin_amdgcn_ubfe(win[h], nb[gg], __builtin_amdgcn_ubfe(e[gg], 21, 4)))
+                          : hv[gg];
+      }
+      if (g + 2 < K) pos += nt[g] + (two ? nt[g + 1] : 0u);
     }
   }
 }
@@ -623,10 +638,16 @@ constexpr int ring_mode() { return MODE == 3 ? 1 : (CODER == 1 && MODE == 2 ? 0 
 // the symbols (e0 | e1 << 4) in byte 3. Bytes out: pA's s0|m0 and e0, then
 // pA's nibbles swapped (s1|m1) and e1, then the same for B. Per byte, bits 7
 // and 0-2 come from the plane and bits 3-6 from the exponent field.
+template <int CODER>
 __device__ __forceinline__ uint32_t pair_merge(uint32_t dup, uint32_t dA, uint32_t dB) {
   const uint32_t plane = ((dup << 4) & 0xFF00FF00u) | (dup & 0x00FF00FFu);   // bytes 1, 3: nibbles swapped
-  const uint32_t y = __builtin_amdgcn_perm(dB, dA, 0x07070303u);            // [bA, bA, bB, bB]
-  const uint32_t ex = ((y >> 1) & 0xFF00FF00u) | ((y << 3) & 0x00FF00FFu);  // e0, e1, e0, e1 at bits 3-6
+  uint32_t ex;                                                              // e0, e1, e0, e1 at bits 3-6
+  if (CODER == 1) {
+    ex = __builtin_amdgcn_perm(dB, dA, 0x07060302u);     // tANS entries hold e0 << 3 | e1 << 11 in bits 16..31
+  } else {
+    const uint32_t y = __builtin_amdgcn_perm(dB, dA, 0x07070303u);          // [bA, bA, bB, bB]
+    ex = ((y >> 1) & 0xFF00FF00u) | ((y << 3) & 0x00FF00FFu);
+  }
   return (plane & 0x87878787u) | (ex & 0x78787878u);
 }
 
@@ -645,7 +666,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
   constexpr int kHalf = kBlock / 2;
   constexpr bool DENSE = MODE == 1 && EB == 2;
   constexpr bool PAIR = MODE == 3;
-  constexpr bool FAST = DENSE || PAIR || EB == 1;       // one-word table layouts (output byte in bits 24..31)
+  constexpr bool FAST = DENSE || PAIR || EB == 1;       // one-word table layouts (the output bits in the word)
   constexpr bool DIRECT = direct_stores<K, EB, PARTIAL>();
   const uint32_t lane = C.lane;
 #pragma unroll
@@ -672,7 +693,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         for (int h = 0; h < kPairs; ++h) {
           const uint32_t ob = o + 2 * h;
           const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (ob + 1) * 0x01010000u | ob * 0x0101u);
-          v[h] = pair_merge(dup, d[(2 * h) % K], d[(2 * h + 1) % K]);
+          v[h] = pair_merge<CODER>(dup, d[(2 * h) % K], d[(2 * h + 1) % K]);
         }
         if (DIRECT) {
           store_step<K, kBlock, EB>(C, blk, q, v[0], v[kPairs - 1]);
@@ -683,7 +704,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         }
       } else {
         const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
-        *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)pair_merge(dup, d[0], d[0]);
+        *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)pair_merge<CODER>(dup, d[0], d[0]);
       }
     } else if (DENSE) {
       // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
@@ -698,7 +719,10 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         for (int h = 0; h < kPairs; ++h) {
           const uint32_t ob = o + 2 * h;
           const uint32_t dup = __builtin_amdgcn_perm(phi, plo, (ob + 1) * 0x01010000u | ob * 0x0101u);
-          const uint32_t ex = __builtin_amdgcn_perm(d[(2 * h + 1) % K], d[(2 * h) % K], 0x070C030Cu) >> 1;
+          // the two exponent words: rANS entries hold the exponent byte in bits
+          // 24..31, tANS entries the word itself in bits 16..31
+          const uint32_t ex = CODER == 1 ? __builtin_amdgcn_perm(d[(2 * h + 1) % K], d[(2 * h) % K], 0x07060302u)
+                                         : __builtin_amdgcn_perm(d[(2 * h + 1) % K], d[(2 * h) % K], 0x070C030Cu) >> 1;
           v[h] = (dup & 0x807F807Fu) | ex;
         }
         if (DIRECT) {
@@ -710,7 +734,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         }
       } else {
         const uint32_t dup = __builtin_amdgcn_perm(phi, plo, 0x0C0C0000u | o * 0x0101u);
-        const uint32_t v = (dup & 0x807Fu) | (d[0] >> 17);
+        const uint32_t v = (dup & 0x807Fu) | (CODER == 1 ? d[0] >> 16 : d[0] >> 17);
         *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)v;
       }
     } else {
@@ -1144,9 +1168,10 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     // tANS: the blob's table {newX:12, nb:4, symbol:8, 0:8}, checked (a
     // symbol of the tensor, nb <= 12, newX + 2^nb <= 4096 with nb zero low
     // bits, so every next state stays in the table) and laid out for the
-    // step: one word {newX, nb, output byte in bits 24..31} for dense bf16,
-    // bytes and pairs; else two, {newX, nb, nb + raw, raw} and the value with
-    // its plane flag (raw = 8 plane bits for a compact symbol that has one)
+    // step: one word {newX, nb, output bits} for dense bf16, bytes and
+    // pairs (layouts in the file comment); else two, {newX, nb, nb + raw,
+    // raw} and the value with its plane flag (raw = 8 plane bits for a
+    // compact symbol that has one)
     const uint32_t slot0 = tid * kRun;
     bool bad = false;
     uint32_t lo[kRun], hi[kRun];
@@ -1156,9 +1181,13 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
       bad |= (e >> 24) != 0 || sym >= nsym || nb > 12u || nx + (1u << nb) > 4096u || (nx & ((1u << nb) - 1u)) != 0;
       const uint32_t v = s_val[sym];
       const uint32_t rw = mode == 2 && (v >> 31) ? 8u : 0u;
-      lo[k] = dense ? (e & 0xFFFFu) | (((v >> 7) & 0xFFu) << 24)
-              : fast ? (e & 0xFFFFu) | ((v & 0xFFu) << 24)
-                     : (e & 0xFFFFu) | ((nb + rw) << 16) | (rw << 21);
+      // dense: the symbol's word (exponent in place) in bits 16..31; pairs:
+      // e0 << 3 | e1 << 11 (both exponent fields in place); bytes: the byte
+      // in bits 24..31
+      lo[k] = dense       ? (e & 0xFFFFu) | ((v & 0x7F80u) << 16)
+              : mode == 3 ? (e & 0xFFFFu) | (((v & 0xFu) << 19) | ((v & 0xF0u) << 23))
+              : fast      ? (e & 0xFFFFu) | ((v & 0xFFu) << 24)
+                          : (e & 0xFFFFu) | ((nb + rw) << 16) | (rw << 21);
       hi[k] = v;
     }
     if (fast) {

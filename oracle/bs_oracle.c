@@ -439,7 +439,12 @@ static int par1_parse(const uint8_t *blob, size_t len, par1_hdr *h) {
 }
 
 /* bf16_parallel.py:262-352 decode. */
-int orc_par1_decode(const uint8_t *blob, size_t len, size_t n_weights, uint16_t *out) {
+/* Streams [k0, k1) of the blob (clamped to its N); each stream writes only
+ * its own elements k, k + N, ... of `out`, so disjoint ranges may run on
+ * separate threads (the reference decodes its streams one after another,
+ * bf16_parallel.py:298-351). */
+int orc_par1_decode_streams(const uint8_t *blob, size_t len, size_t n_weights, uint16_t *out, size_t k0,
+                            size_t k1) {
     if (n_weights == 0 || len == 0) return ORC_OK;          /* :268-269 */
     par1_hdr *h = (par1_hdr *)malloc(sizeof(par1_hdr));
     if (!h) return ORC_ERR_ARG;
@@ -455,7 +460,8 @@ int orc_par1_decode(const uint8_t *blob, size_t len, size_t n_weights, uint16_t 
     uint32_t *tmp = (uint32_t *)malloc(sizeof(uint32_t) * per);
     size_t *order = (size_t *)malloc(sizeof(size_t) * per);
     if (!se || !ms || !tmp || !order) { rc = ORC_ERR_ARG; goto out; }
-    for (size_t k = 0; k < N; k++) {
+    if (k1 > N) k1 = N;
+    for (size_t k = k0; k < k1; k++) {
         size_t nk = k < n ? (n - 1 - k) / N + 1 : 0;         /* :293-296 */
         if (nk == 0) continue;
         size_t a = get32(blob + h->header_end + 4 * k), b = get32(blob + h->header_end + 4 * (k + 1));
@@ -495,6 +501,10 @@ int orc_par1_decode(const uint8_t *blob, size_t len, size_t n_weights, uint16_t 
 out:
     free(se); free(ms); free(tmp); free(order); free(h);
     return rc;
+}
+
+int orc_par1_decode(const uint8_t *blob, size_t len, size_t n_weights, uint16_t *out) {
+    return orc_par1_decode_streams(blob, len, n_weights, out, 0, (size_t)-1);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -843,7 +853,9 @@ int orc_tans_table(const uint32_t *freq, int nsym, uint32_t *out) {
     return ORC_OK;
 }
 
-int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *out_v) {
+/* Chunks [c0, c1) (clamped to the blob's count): each writes only its own
+ * elements, so disjoint ranges may run on separate threads. */
+int orc_chunk_decode_range(const uint8_t *blob, size_t len, size_t n_weights, void *out_v, size_t c0, size_t c1) {
     if (len < 32 || memcmp(blob, "BSCK", 4) != 0) return ORC_ERR_FORMAT;
     uint32_t ver = blob[4], eb = blob[5], mode = blob[6], prec = blob[7];
     uint64_t n = get64(blob + 8);
@@ -887,7 +899,8 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
         }
     }
     const uint32_t K = lanes / 64, bs = lanes == 256 ? 4 : 8;   /* states per lane, steps per plane block */
-    for (uint32_t ci = 0; ci < nch; ci++) {
+    if (c1 > nch) c1 = nch;
+    for (size_t ci = c0; ci < c1; ci++) {
         const uint8_t *ce = blob + ctab + 16 * (size_t)ci;
         uint64_t off = get64(ce); uint32_t nw = get32(ce + 8), np = get32(ce + 12);
         int split = region && ci < nf;
@@ -959,4 +972,8 @@ int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *ou
         if (coder == 0 && mode == 2 && pp != np) return ORC_ERR_FORMAT;
     }
     return ORC_OK;
+}
+
+int orc_chunk_decode(const uint8_t *blob, size_t len, size_t n_weights, void *out_v) {
+    return orc_chunk_decode_range(blob, len, n_weights, out_v, 0, (size_t)-1);
 }

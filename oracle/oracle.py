@@ -17,7 +17,7 @@ LIB_PATH = _HERE / "_build" / "liboracle.so"
 __all__ = [
     "build", "lib", "quantise_ref", "quantise_sk", "rans_encode", "rans_decode", "rans_decode_nb",
     "par1_encode", "par1_decode", "tans_encode", "tans_decode", "sk_encode", "sk_decode",
-    "chunk_decode", "tans_table", "OracleError",
+    "chunk_decode", "tans_table", "par1_decode_threads", "chunk_decode_threads", "OracleError",
 ]
 
 
@@ -58,6 +58,8 @@ def lib():
             "orc_sk_encode": (I64, [P, S, P, S]),
             "orc_sk_decode": (I, [P, S, S, P]),
             "orc_chunk_decode": (I, [P, S, S, P]),
+            "orc_chunk_decode_range": (I, [P, S, S, P, S, S]),
+            "orc_par1_decode_streams": (I, [P, S, S, P, S, S]),
             "orc_tans_table": (I, [P, I, P]),
         }
         for name, (res, args) in sig.items():
@@ -191,6 +193,38 @@ def chunk_decode(blob: bytes, n: int, elem_bytes: int = 2) -> bytes:
     """CPU decode of the build's GPU-native BSCK format, either coder, layout
     versions 2 and 3 (no reference counterpart)."""
     return _decode("orc_chunk_decode", blob, n, elem_bytes)
+
+
+def _threaded(fn: str, blob: bytes, n: int, itemsize: int, units: int, threads: int) -> bytes:
+    """Decode with `threads` host threads, each taking a contiguous range of
+    the blob's independent units (streams or chunks) into one shared output;
+    the C calls run without the GIL."""
+    from concurrent.futures import ThreadPoolExecutor
+    b = np.frombuffer(bytes(blob), np.uint8).copy()
+    out = np.zeros(max(n, 1) * itemsize, np.uint8)
+    threads = max(1, min(threads, units))
+    cuts = [units * i // threads for i in range(threads + 1)]
+    f = getattr(lib(), fn)
+    with ThreadPoolExecutor(threads) as ex:
+        rcs = list(ex.map(lambda i: f(_p(b), len(b), n, _p(out), cuts[i], cuts[i + 1]), range(threads)))
+    for rc in rcs:
+        if rc:
+            raise OracleError(fn, rc)
+    return out[: n * itemsize].tobytes()
+
+
+def par1_decode_threads(blob: bytes, n: int, threads: int) -> bytes:
+    """bf16_parallel.decode with its N streams split over host threads (the
+    streams are independent: bigsmall/codecs/bf16_parallel.py:298-351 decodes
+    them one after another)."""
+    n_streams = int.from_bytes(bytes(blob[8:10]), "little") if len(blob) >= 10 else 1
+    return _threaded("orc_par1_decode_streams", blob, n, 2, max(1, n_streams), threads)
+
+
+def chunk_decode_threads(blob: bytes, n: int, threads: int, elem_bytes: int = 2) -> bytes:
+    """chunk_decode with the blob's chunks split over host threads."""
+    n_chunks = int.from_bytes(bytes(blob[24:28]), "little") if len(blob) >= 28 else 1
+    return _threaded("orc_chunk_decode_range", blob, n, elem_bytes, max(1, n_chunks), threads)
 
 
 def tans_table(freqs) -> np.ndarray:
