@@ -568,7 +568,8 @@ def run_refcodecs(args) -> dict:
         d_blob = upload_bytes(blob, dev)
         out = torch.empty(words.size, dtype=torch.int16, device=dev)
         st = StatusWord(dev)
-        launch = _refstreams.RefLaunch(_refstreams.PARSERS[codec](blob, words.size), d_blob.data_ptr(), dev)
+        launch = _refstreams.RefLaunch(_refstreams.PARSERS[codec](blob, words.size), d_blob.data_ptr(), dev,
+                                       out.data_ptr())
         fn = lambda: launch.launch(out.data_ptr(), st.ptr, stream.cuda_stream)
         fn()
         torch.cuda.synchronize()
@@ -634,7 +635,7 @@ def run_reflayer(args) -> dict:
         st.check(codec)
         for o, (name, w) in zip(outs, mats):
             assert o.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), (codec, name)
-        singles = [_refstreams.RefLaunch(p, d.data_ptr(), dev) for p, d in zip(plans, d_blobs)]
+        singles = [_refstreams.RefLaunch(p, d.data_ptr(), dev, o.data_ptr()) for p, d, o in zip(plans, d_blobs, outs)]
         seq = lambda: [l.launch(o.data_ptr(), st.ptr, stream.cuda_stream) for l, o in zip(singles, outs)]
         ms_seq = _timed(seq, 1, stream)
         st.check(codec)
@@ -771,7 +772,8 @@ def run_c3(args) -> dict:
         d_blob = upload_bytes(blob, dev)
         out = torch.empty(w.size, dtype=torch.int16, device=dev)
         st = StatusWord(dev)
-        launch = _refstreams.RefLaunch(_refstreams.PARSERS["bf16_se_tans"](blob, w.size), d_blob.data_ptr(), dev)
+        launch = _refstreams.RefLaunch(_refstreams.PARSERS["bf16_se_tans"](blob, w.size), d_blob.data_ptr(), dev,
+                                       out.data_ptr())
         ms = _timed(lambda: launch.launch(out.data_ptr(), st.ptr, stream.cuda_stream), 1, stream)
         st.check(name)
         assert out.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), name
@@ -1008,6 +1010,10 @@ def main():
                     help="c3 workload: comma-separated subset of studentt,halfzero,fp8_e4m3,fp8_residual")
     ap.add_argument("--ref-codecs", default="",
                     help="reflayer workload: comma-separated subset of bf16_parallel_v1,bf16_se_tans")
+    ap.add_argument("--ref-tables", choices=["auto", "lds", "scalar", "se-scalar", "mant-scalar"], default="auto",
+                    help="refcodecs/reflayer/c3 workloads: where the reference formats' chains read their decode "
+                         "tables (auto: the engine's choice; lds; scalar: SE and mantissa chains through the scalar "
+                         "cache; se-scalar / mant-scalar: only those chains)")
     ap.add_argument("--coder", choices=["rans", "tans"], default="rans",
                     help="layer workload: the engine format's entropy coder (bf16_chunked_v1 or bf16_chunked_tans_v1)")
     ap.add_argument("--engine-only", action="store_true",
@@ -1018,6 +1024,10 @@ def main():
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.ref_tables != "auto":
+        from bigsmall_amd.codecs import _refstreams
+        _refstreams.RefBatch.SE_SCALAR = args.ref_tables in ("scalar", "se-scalar")   # else False: every SE chain in LDS
+        _refstreams.RefBatch.MANT_SCALAR = args.ref_tables in ("scalar", "mant-scalar")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X; multi-GPU runs are not part of it (a model shards by "
               "tensor or layer for decoding, with no exchange between GPUs).", file=sys.stderr)

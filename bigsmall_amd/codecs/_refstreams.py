@@ -41,7 +41,9 @@ REF_TASK_DTYPE = np.dtype([("streams", "<u8"), ("se_table", "<u8"), ("bstart", "
                            ("mant_tables", "<u8"), ("out", "<u8"), ("n_out", "<u8"), ("work_offset", "<u8"),
                            ("n_streams", "<u4"), ("n_buckets", "<u4"), ("n_tables", "<u4"), ("se_group_begin", "<u4"),
                            ("tile_begin", "<u4"), ("stream_begin", "<u4"), ("mant_group_begin", "<u4"),
-                           ("reserved", "<u4")])
+                           ("flags", "<u4")])
+# bs_ref_task.flags (include/bigsmall_hip.h)
+FLAG_SE_SCALAR, FLAG_MANT_SCALAR = 1, 2
 assert SE_STREAM_DTYPE.itemsize == 40 and MANT_BUCKET_DTYPE.itemsize == 40 and REF_TASK_DTYPE.itemsize == 96
 
 
@@ -109,6 +111,26 @@ def decode_table_se(freqs: np.ndarray) -> np.ndarray:
     out[:, 0] = (freqs[sym] | ((slot - cum[sym]) << 13)).astype(np.uint32)
     out[:, 1] = sym.astype(np.uint32)
     return out
+
+
+def decode_table_se_scalar(freqs: np.ndarray):
+    """The SE table's 4-byte form for a tensor with at most 256 live symbols,
+    none of frequency 4096 (else None): 4096 x {index | f << 8 | (slot - cf)
+    << 20} and the 256 output words (sign << 15 | exponent << 7) of the
+    indexed live symbols, as one uint32 array of 4096 + 256 entries."""
+    freqs = np.asarray(freqs, dtype=np.int64)
+    live = np.flatnonzero(freqs)
+    if len(live) > 256 or freqs.max() >= M_SE:
+        return None
+    index = np.zeros(len(freqs), np.int64)
+    index[live] = np.arange(len(live))
+    sym = np.repeat(np.arange(len(freqs), dtype=np.int64), freqs)
+    cum = np.concatenate([[0], np.cumsum(freqs)[:-1]])
+    slot = np.arange(M_SE, dtype=np.int64)
+    packed = (index[sym] | (freqs[sym] << 8) | ((slot - cum[sym]) << 20)).astype(np.uint32)
+    words = np.zeros(256, np.uint32)
+    words[: len(live)] = (((live >> 8) & 1) << 15) | ((live & 0xFF) << 7)
+    return np.concatenate([packed, words])
 
 
 def decode_table_mant(freqs: np.ndarray) -> np.ndarray:
@@ -324,7 +346,11 @@ def _plan_arrays(plan: RefPlan, blob_ptr: int) -> list[np.ndarray]:
         mb[i] = (blob_ptr + s.words_off, s.x0, s.n_words, s.tail, n, pb, t, 0)
     tables = (np.stack([decode_table_mant(f) for f in plan.mant_freqs]) if plan.mant_freqs
               else np.zeros((1, M_MANT), np.uint32))
-    return [se.view(np.uint8), decode_table_se(plan.se_freqs).reshape(-1).view(np.uint8),
+    se_table = decode_table_se(plan.se_freqs).reshape(-1)
+    scalar = decode_table_se_scalar(plan.se_freqs)
+    if scalar is not None:                  # the table's 4-byte form follows its pairs (BS_REF_FLAG_SE_SCALAR)
+        se_table = np.concatenate([se_table, scalar])
+    return [se.view(np.uint8), se_table.view(np.uint8),
             np.stack(plan.bstart).reshape(-1).view(np.uint8) if plan.bstart else np.zeros(0, np.uint8),
             mb.view(np.uint8), tables.reshape(-1).view(np.uint8)]
 
@@ -362,7 +388,17 @@ class RefBatch:
     reference-format tensors) as one bs_refcodec_decode_serial_batch launch:
     all their chains run side by side, the SE chains (the longest) first. items: [(plan, blob_ptr, out_ptr)],
     every plan accepted by serial_ok. Device buffers stay alive with this
-    object until the decode launched from it has completed."""
+    object until the decode launched from it has completed. The SE chains of
+    a tensor with at most 256 live SE symbols keep their state in scalar
+    registers and read a 4-byte table through the scalar cache when no other
+    tensor's SE chains share the launch, or the tensor has one SE chain (C0 in
+    bf16_se_tans: 1.04 against 1.22 s; an 8B layer of seven bf16_parallel_v1
+    tensors: 45 against 41 ms, the 128-chain tensors' tables thrashing the
+    scalar cache); mantissa chains read LDS tables (the scalar cache measured
+    no faster for them). SE_SCALAR: "auto", True or False; MANT_SCALAR: bool."""
+
+    SE_SCALAR = "auto"
+    MANT_SCALAR = False
 
     def __init__(self, items: list, device):
         import torch
@@ -378,7 +414,14 @@ class RefBatch:
             ns, nb = len(plan.se_streams), len(plan.buckets)
             nt = max(1, len(plan.mant_freqs))
             tiles = int(L.bs_refcodec_serial_tiles(plan.n, ns))
-            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, se_g, tile, stream, mant_g, 0)
+            flags = FLAG_MANT_SCALAR if self.MANT_SCALAR else 0
+            # the SE table carries its 4-byte form: scalar-cache SE chains where
+            # they do not share CUs with other tensors' SE tables (a one-tensor
+            # batch, or one SE chain per tensor)
+            if arrays[-4].nbytes > 8 * M_SE and (self.SE_SCALAR is True or
+                                                 (self.SE_SCALAR == "auto" and (len(items) == 1 or ns == 1))):
+                flags |= FLAG_SE_SCALAR
+            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, se_g, tile, stream, mant_g, flags)
             work += (int(L.bs_refcodec_serial_work_bytes(plan.n, ns)) + 255) & ~255
             se_g, mant_g = se_g + -(-ns // per), mant_g + -(-nb // per)
             tile, stream = tile + ns * tiles, stream + ns
@@ -407,36 +450,37 @@ class RefBatch:
 
 class RefLaunch:
     """Device-side tables and descriptors of one parsed blob (kept alive until
-    the decode launched from them has completed)."""
+    the decode launched from them has completed). A tensor of
+    SERIAL_MIN_ELEMENTS or more decodes with one wavefront per chain (a
+    one-task bs_refcodec_decode_serial_batch, whose tables are built for one
+    output address: pass `out_ptr` here to build them before the first
+    launch); a smaller one with one lane per chain (bs_refcodec_decode)."""
 
-    def __init__(self, plan: RefPlan, blob_ptr: int, device):
+    def __init__(self, plan: RefPlan, blob_ptr: int, device, out_ptr: int | None = None):
         import torch
-        host = _plan_arrays(plan, blob_ptr)
-        buf, offs = _pack(host)
-        self.dev = torch.from_numpy(buf).to(device)
-        base = self.dev.data_ptr()
-        self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets, self.p_tables = (base + o for o in offs)
         self.n_streams, self.n_buckets = len(plan.se_streams), len(plan.buckets)
         self.n_tables = max(1, len(plan.mant_freqs))
         self.n = plan.n
-        # one wavefront per chain (bs_refcodec_decode_serial) unless the tensor
-        # is small, where one lane per chain (bs_refcodec_decode) is as fast
+        self.plan, self.blob_ptr, self.device = plan, blob_ptr, device
+        self._batch = None
         self.serial = serial_ok(plan)
-        se = plan.se_streams
         if self.serial:
-            nbytes = int(_native.lib().bs_refcodec_serial_work_bytes(plan.n, len(se)))
-            self.work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-        else:
-            self.perm = torch.empty(max(plan.n, 1), dtype=torch.int32, device=device)
+            if out_ptr is not None:
+                self._batch = (out_ptr, RefBatch([(plan, blob_ptr, out_ptr)], device))
+            return
+        buf, offs = _pack(_plan_arrays(plan, blob_ptr))
+        self.dev = torch.from_numpy(buf).to(device)
+        base = self.dev.data_ptr()
+        self.p_streams, self.p_se_table, self.p_bstart, self.p_buckets, self.p_tables = (base + o for o in offs)
+        self.perm = torch.empty(max(plan.n, 1), dtype=torch.int32, device=device)
 
     def launch(self, out_ptr: int, status_ptr: int, stream_ptr: int) -> None:
         L = _native.lib()
         if self.serial:
-            rc = L.bs_refcodec_decode_serial(self.p_streams, self.n_streams, self.p_se_table, self.p_bstart,
-                                             self.p_buckets,
-                                             self.n_buckets, self.p_tables, self.n_tables, out_ptr, self.n,
-                                             self.work.data_ptr(), self.work.numel(), status_ptr, stream_ptr)
-            _native.check(rc, "bs_refcodec_decode_serial")
+            # a one-task batch (its tables and flags built once per output)
+            if self._batch is None or self._batch[0] != out_ptr:
+                self._batch = (out_ptr, RefBatch([(self.plan, self.blob_ptr, out_ptr)], self.device))
+            self._batch[1].launch(status_ptr, stream_ptr)
             return
         rc = L.bs_refcodec_decode(self.p_streams, self.n_streams, self.p_se_table, self.p_bstart,
                                   self.p_buckets, self.n_buckets, self.p_tables, self.n_tables,
@@ -488,7 +532,7 @@ def decode_host(codec: str, blob: bytes, n_weights: int) -> bytes:
     d_blob = upload_bytes(blob, dev)
     out = torch.empty(n_weights, dtype=torch.int16, device=dev)
     st = StatusWord(dev)
-    launch = RefLaunch(plan, d_blob.data_ptr(), dev)
+    launch = RefLaunch(plan, d_blob.data_ptr(), dev, out.data_ptr())
     launch.launch(out.data_ptr(), st.ptr, stream_ptr(None, dev))
     torch.cuda.synchronize(dev)
     st.check(codec)
@@ -496,4 +540,4 @@ def decode_host(codec: str, blob: bytes, n_weights: int) -> bytes:
 
 
 __all__ = ["PARSERS", "RefBatch", "RefLaunch", "RefPlan", "serial_ok", "decode_host", "encode_host", "parse_parallel", "parse_tans",
-           "parse_single_kernel", "decode_table_se", "decode_table_mant"]
+           "parse_single_kernel", "decode_table_se", "decode_table_se_scalar", "decode_table_mant"]

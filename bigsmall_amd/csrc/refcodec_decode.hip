@@ -211,7 +211,7 @@ __device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint64_t max_le
 template <bool SE>
 __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
                                              uint32_t n, const LDS u32x4* __restrict__ tbl,
-                                             LDS uint8_t* ring, GLB uint8_t* __restrict__ out,
+                                             LDS uint8_t* ring, LDS uint16_t* stage, GLB uint8_t* __restrict__ out,
                                              uint32_t stride, int32_t* status) {
   constexpr uint32_t kSlotMask = SE ? 4095u : 1023u;
   constexpr uint32_t kShift = SE ? 12u : 10u;
@@ -229,7 +229,6 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   // Word window: lane l of w_lo / w_hi holds word base + l / base + 64 + l.
   // At a batch start pos - base < 64, so the batch's at most 64 words are in it.
   uint32_t base = 0, w_lo = 0, w_hi = 0;
-  uint32_t keep = 0;
   if (x0 < kL) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
     return;
@@ -256,7 +255,11 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
     }
     x = xn;
     BS_OPAQUE(x);
-    keep = lane == j ? e.z : keep;
+    // the step's output goes to slot j of the wave's 64-entry stage (every
+    // lane writes the same value), read back by lane j after the batch: a
+    // select per step (keep = lane == j ? out : keep) made the optimiser hold
+    // the batch's 64 outputs, or its 64 lane masks, in registers
+    *(volatile LDS uint16_t*)(stage + j) = (uint16_t)e.z;
   };
   for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
     // ring upkeep: the window reaches at most 128 words (256 bytes) past pos
@@ -290,12 +293,130 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
     } else {
       for (uint32_t j = 0; j < cnt; ++j) step(j);
     }
+    wave_sync();
+    const uint32_t keep = stage[lane];
     if (lane < cnt) {
       if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)keep;
       else out[i0 + lane] = (uint8_t)keep;
     }
   }
   if (__builtin_amdgcn_readfirstlane(x) != kL || pos != n_eff) {
+    if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
+  }
+}
+
+// The same chain with the state in scalar registers and the table read
+// through the scalar cache (uniform loads, read-only): one s_load_dword and
+// the update in SALU instructions; the step's output goes to the stage as in
+// serial_chain. Tables of 4-byte entries: SE, {index | f << 8 | (slot - cf)
+// << 20} (the 16 KB table of a tensor with at most 256 live sign/exponent
+// symbols, none of frequency 4096; the index selects the output word from
+// `out_words`, a 256-entry LDS map applied once per 64 outputs); mantissa,
+// the global table itself {f | (slot - cf) << 11 | symbol << 21} (4 KB per
+// bucket table). A scalar-cache hit comes back sooner than the LDS round
+// trip, and the step issues fewer instructions (C0 in bf16_se_tans: 1.04
+// against 1.22 s on one chain). With many chains of different tables on a
+// CU the scalar cache thrashes (an 8B layer in bf16_parallel_v1: 45 against
+// 41 ms), so the host sets it per task.
+__device__ __forceinline__ uint32_t uni32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ uint64_t uni64(uint64_t v) {
+  return (uint64_t)uni32((uint32_t)v) | ((uint64_t)uni32((uint32_t)(v >> 32)) << 32);
+}
+
+template <bool SE>
+__device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, uint32_t n_words, uint32_t tail,
+                                                    uint32_t x0, uint32_t n, const CST uint32_t* t4_in,
+                                                    const LDS uint32_t* out_words, LDS uint8_t* ring,
+                                                    LDS uint16_t* stage, GLB uint8_t* __restrict__ out,
+                                                    uint32_t stride, int32_t* status) {
+  // the descriptor's fields are the same in every lane: say so, so that the
+  // whole chain (state, word position, table address) stays scalar
+  n_words = uni32(n_words);
+  tail = uni32(tail);
+  n = uni32(n);
+  const CST uint32_t* __restrict__ t4 = (const CST uint32_t*)uni64((uint64_t)t4_in);
+  constexpr uint32_t kSlotMask = SE ? 4095u : 1023u;
+  constexpr uint32_t kShift = SE ? 12u : 10u;
+  const uint32_t lane = __lane_id();
+  const uint64_t wa = (uint64_t)words;
+  const GLB uint8_t* A = (const GLB uint8_t*)(wa & ~15ull);
+  const uint32_t s_off = (uint32_t)(wa & 15u);
+  const uint64_t e_off = s_off + 2ull * n_words;
+  const uint32_t n_eff = n_words + ((tail >> 16) & 1u);
+  const uint32_t tail_word = tail & 0xFFFFu;
+  uint64_t landed = 0;
+  bool inflight = false;
+  u32x4 seg = {0u, 0u, 0u, 0u};
+  uint32_t x = __builtin_amdgcn_readfirstlane(x0), pos = 0;
+  uint32_t base = 0, w_lo = 0, w_hi = 0;
+  if (x < kL) {
+    if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
+    return;
+  }
+  auto ring_word = [&](uint32_t idx) {
+    const uint32_t b = s_off + 2u * idx;
+    return (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
+  };
+  auto step = [&](uint32_t j) {
+    const uint32_t e = t4[x & kSlotMask];                  // s_load_dword: x is wave-uniform
+    const uint32_t f = SE ? (e >> 8) & 0xFFFu : e & 0x7FFu;
+    const uint32_t bias = SE ? e >> 20 : (e >> 11) & 0x3FFu;
+    uint32_t xn = f * (x >> kShift) + bias;
+    // uniform: a scalar branch, taken by about one step in five, so laid out
+    // off the straight path
+    if (__builtin_expect(xn < kL, 0)) {
+      const uint32_t d = pos - base;                       // < 128
+      const uint32_t w_a = __builtin_amdgcn_readlane(w_lo, d & 63u);
+      const uint32_t w_b = __builtin_amdgcn_readlane(w_hi, d & 63u);
+      uint32_t w = d < (uint32_t)kWave ? w_a : w_b;
+      w = pos < n_words ? w : tail_word;
+      xn = (xn << 16) | w;
+      ++pos;
+    }
+    x = xn;
+    // as in serial_chain; the SE index is the entry's low byte, stored as it is
+    *(volatile LDS uint8_t*)((LDS uint8_t*)stage + j) = (uint8_t)(SE ? e : (e >> 21) & 0x7Fu);
+  };
+  for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
+    // ring upkeep: the window reaches at most 128 words (256 bytes) past pos
+    const uint64_t consumed = s_off + 2ull * pos;
+    if (inflight) {
+      seg_land(ring, landed / kSegB, lane, seg);
+      landed += kSegB;
+      inflight = false;
+    }
+    while (landed < e_off && landed < consumed + 4u * kWave + 2u) {
+      seg_land(ring, landed / kSegB, lane, seg_block(A, landed / kSegB, lane, s_off, e_off));
+      landed += kSegB;
+    }
+    if (landed < e_off && landed + kSegB <= consumed + kRingB) {
+      seg = seg_block(A, landed / kSegB, lane, s_off, e_off);
+      inflight = true;
+    }
+    wave_sync();
+    if (i0 == 0) {
+      w_lo = ring_word(lane);
+      w_hi = ring_word(kWave + lane);
+    } else if (pos - base >= (uint32_t)kWave) {           // one move keeps pos - base < 64
+      base += kWave;
+      w_lo = w_hi;
+      w_hi = ring_word(base + kWave + lane);
+    }
+    const uint32_t cnt = min((uint32_t)kWave, n - i0);
+    if (cnt == (uint32_t)kWave) {
+#pragma unroll
+      for (uint32_t j = 0; j < (uint32_t)kWave; ++j) step(j);
+    } else {
+      for (uint32_t j = 0; j < cnt; ++j) step(j);
+    }
+    wave_sync();
+    const uint32_t keep = ((const LDS uint8_t*)stage)[lane];
+    if (lane < cnt) {
+      if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)out_words[keep];
+      else out[i0 + lane] = (uint8_t)keep;
+    }
+  }
+  if (x != kL || pos != n_eff) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
   }
 }
@@ -356,7 +477,9 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 // host lists buckets longest first, so the four buckets of a group end at
 // about the same time and the longest start first.
 constexpr uint32_t kSerWaves = 4;
-constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16;   // 73728: rings | SE table or kSerWaves mantissa tables
+constexpr uint32_t kStageB = 128;      // per chain: 64 u16 outputs of a batch
+// 74240: rings | SE table or kSerWaves mantissa tables | stages
+constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16 + kSerWaves * kStageB;
 static_assert(2 * kSerLds <= 160 * 1024 - 8192, "two chain groups per CU");
 static_assert(kSerWaves * 1024 * 16 <= 4096 * 16, "mantissa tables exceed the table area");
 
@@ -369,6 +492,7 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   LDS uint8_t* ring = (LDS uint8_t*)smem + wave * kRingB;
   LDS u32x4* tbl_area = (LDS u32x4*)(smem + kSerWaves * kRingB);
+  LDS uint16_t* stage = (LDS uint16_t*)(smem + kSerWaves * kRingB + 4096 * 16 + wave * kStageB);
   const bool se = blockIdx.x < se_groups;                 // uniform over the workgroup
   const uint32_t g = se ? blockIdx.x : blockIdx.x - se_groups;
   const bs_ref_task T = se ? pick_task<kSeGrid>(tasks, n_tasks, single, g)
@@ -384,11 +508,17 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
   const uint32_t c = local * kSerWaves + wave;            // this wave's stream or bucket (none when >= count)
   const uint64_t max_len = (uint64_t)serial_tiles(T.n_out, T.n_streams) * kTile;
   uint8_t* mant = work + T.work_offset;
+  const bool scalar_se = (T.flags & BS_REF_FLAG_SE_SCALAR) != 0;
   if (se) {
-    for (uint32_t i = tid; i < 4096; i += kSerWaves * kWave) {
-      const uint32_t lo = T.se_table[2 * i], sym = T.se_table[2 * i + 1];
-      const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
-      tbl_area[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
+    LDS uint32_t* out_words = (LDS uint32_t*)tbl_area;    // scalar-cache form: the 256 output words
+    if (scalar_se) {
+      for (uint32_t i = tid; i < 256; i += kSerWaves * kWave) out_words[i] = T.se_table[8192 + 4096 + i];
+    } else {
+      for (uint32_t i = tid; i < 4096; i += kSerWaves * kWave) {
+        const uint32_t lo = T.se_table[2 * i], sym = T.se_table[2 * i + 1];
+        const uint32_t word = (((sym >> 8) & 1u) << 15) | ((sym & 0xFFu) << 7);
+        tbl_area[i] = u32x4{lo & 0x1FFFu, lo >> 13, word, 0u};
+      }
     }
     __syncthreads();
     if (c >= count) return;
@@ -397,8 +527,13 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
-    serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl_area, ring,
-                       (GLB uint8_t*)(T.out + S.first), S.stride, status);
+    if (scalar_se)
+      serial_chain_scalar<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n,
+                                (const CST uint32_t*)(T.se_table + 8192), out_words, ring, stage,
+                                (GLB uint8_t*)(T.out + S.first), S.stride, status);
+    else
+      serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl_area, ring, stage,
+                         (GLB uint8_t*)(T.out + S.first), S.stride, status);
   } else {
     if (c >= count) return;
     const bs_mant_bucket B = T.buckets[c];
@@ -406,14 +541,19 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
-    LDS u32x4* tbl = tbl_area + wave * 1024u;
     const GLB uint32_t* t = (const GLB uint32_t*)T.mant_tables + (uint64_t)B.table * 1024u;
+    if (T.flags & BS_REF_FLAG_MANT_SCALAR) {
+      serial_chain_scalar<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, (const CST uint32_t*)t,
+                                 nullptr, ring, stage, (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
+      return;
+    }
+    LDS u32x4* tbl = tbl_area + wave * 1024u;
     for (uint32_t i = lane; i < 1024; i += kWave) {
       const uint32_t e = t[i];
       tbl[i] = u32x4{e & 0x7FFu, (e >> 11) & 0x3FFu, (e >> 21) & 0x7Fu, 0u};
     }
     wave_sync();
-    serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring,
+    serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring, stage,
                         (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
   }
 }

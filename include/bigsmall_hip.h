@@ -265,8 +265,19 @@ typedef struct {
     uint32_t tile_begin;             /* tile grid: n_streams x bs_refcodec_serial_tiles(n_out, n_streams) */
     uint32_t stream_begin;           /* stream grid: n_streams */
     uint32_t mant_group_begin;       /* chain grid, mantissa part: ceil(n_buckets / per group) workgroups */
-    uint32_t reserved;
+    uint32_t flags;                  /* BS_REF_FLAG_* */
 } bs_ref_task;
+
+/* bs_ref_task.flags. BS_REF_FLAG_SE_SCALAR: se_table continues after its 4096
+ * pairs with the table's 4-byte form, 4096 u32 {index | f << 8 | (slot - cf)
+ * << 20}, and 256 u32 output words (sign << 15 | exponent << 7 of the SE
+ * symbol with that index), which a tensor with at most 256 live SE symbols,
+ * none of frequency 4096, has; its SE chains then keep their state in scalar
+ * registers and read that table through the scalar cache. BS_REF_FLAG_MANT_SCALAR:
+ * the mantissa chains do the same with mant_tables. Either way the decoded
+ * words are the same. */
+#define BS_REF_FLAG_SE_SCALAR 1u
+#define BS_REF_FLAG_MANT_SCALAR 2u
 
 /* Wavefronts (chains) per workgroup of the wave-serial chain grid. */
 uint32_t bs_refcodec_serial_chains_per_group(void);

@@ -109,7 +109,7 @@ int main(int argc, char** argv) {
   Reader r{file.data(), file.data() + file.size()};
   if (r.get<uint32_t>() != 0x5A465342u) return 2;   // "BSFZ"
   const uint32_t n_cases = r.get<uint32_t>();
-  uint64_t clean_ok = 0, clean_bad = 0, refused_host = 0, flagged = 0, decoded = 0;
+  uint64_t clean_ok = 0, clean_bad = 0, refused_host = 0, flagged = 0, decoded = 0, scalar_mismatch = 0;
   struct Clean {
     std::vector<uint8_t> blob, want;
     uint64_t n;
@@ -135,10 +135,12 @@ int main(int argc, char** argv) {
       if (rc == BS_OK) rc = bs_chunk_decode(blob.p, blob_len, out.p, n_out, info.n_chunks, info.plane_mode, &status, nullptr);
     } else {           // reference formats: descriptors with blob-relative word arrays
       const uint32_t ns = r.get<uint32_t>(), nb = r.get<uint32_t>(), nt = r.get<uint32_t>();
+      const uint32_t se_bytes = r.get<uint32_t>();   // 4096 pairs, and the 4-byte form when the tensor has it
       std::vector<bs_se_stream> se(ns);
       memcpy(se.data(), r.take((uint64_t)ns * sizeof(bs_se_stream)), (uint64_t)ns * sizeof(bs_se_stream));
-      Buf se_table(4096 * 8);
-      memcpy(se_table.p, r.take(4096 * 8), 4096 * 8);
+      if (se_bytes != 4096 * 8 && se_bytes != 4096 * 8 + (4096 + 256) * 4) return 2;
+      Buf se_table(se_bytes);
+      memcpy(se_table.p, r.take(se_bytes), se_bytes);
       Buf bstart((uint64_t)ns * 257 * 4);
       memcpy(bstart.p, r.take((uint64_t)ns * 257 * 4), (uint64_t)ns * 257 * 4);
       std::vector<bs_mant_bucket> mb(nb);
@@ -157,6 +159,38 @@ int main(int argc, char** argv) {
                                        (const uint32_t*)bstart.p, (const bs_mant_bucket*)d_mb.p, nb,
                                        (const uint32_t*)tables.p, nt, (uint16_t*)out.p, n_out, work.p, wb, &status,
                                        nullptr);
+        // the same decode as a one-task batch whose chains read 4-byte tables
+        // through the scalar path (the SE chains only when the table has that
+        // form); its output and status must be the same
+        if (rc == BS_OK && n_out > 0 && n_out <= 0xFFFFFFFFull) {
+          Buf out2(n_out * eb), work2(wb, true);
+          memset(out2.p, 0x5A, n_out * eb);
+          const uint32_t per = bs_refcodec_serial_chains_per_group();
+          bs_ref_task t{};
+          t.streams = (const bs_se_stream*)d_se.p;
+          t.se_table = (const uint32_t*)se_table.p;
+          t.bstart = (const uint32_t*)bstart.p;
+          t.buckets = (const bs_mant_bucket*)d_mb.p;
+          t.mant_tables = (const uint32_t*)tables.p;
+          t.out = (uint16_t*)out2.p;
+          t.n_out = n_out;
+          t.n_streams = ns;
+          t.n_buckets = nb;
+          t.n_tables = nt;
+          t.flags = BS_REF_FLAG_MANT_SCALAR | (se_bytes > 4096 * 8 ? BS_REF_FLAG_SE_SCALAR : 0u);
+          const uint32_t se_g = (ns + per - 1) / per, mant_g = (nb + per - 1) / per;
+          const uint32_t tiles = bs_refcodec_serial_tiles(n_out, ns);
+          Buf d_task(sizeof t);
+          memcpy(d_task.p, &t, sizeof t);
+          int32_t status2 = 0;
+          const int rc2 = bs_refcodec_decode_serial_batch((const bs_ref_task*)d_task.p, 1, se_g, mant_g, ns * tiles, ns,
+                                                          work2.p, wb, &status2, nullptr);
+          if (rc2 != rc || status2 != status || (status == 0 && memcmp(out.p, out2.p, n_out * eb) != 0)) {
+            ++scalar_mismatch;
+            fprintf(stderr, "case %u: scalar-table batch rc %d status 0x%x, single rc %d status 0x%x\n", c, rc2,
+                    status2, rc, status);
+          }
+        }
       } else {
         Buf perm(n_out * 4);
         rc = bs_refcodec_decode((const bs_se_stream*)d_se.p, ns, (const uint32_t*)se_table.p, (const uint32_t*)bstart.p,
@@ -276,8 +310,9 @@ int main(int argc, char** argv) {
   printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu, empty task flagged %llu\n",
          (unsigned long long)batch_ok, (unsigned long long)batch_bad, (unsigned long long)high_bit,
          (unsigned long long)empty_flagged);
-  printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu\n", n_cases,
+  printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu "
+         "scalar-table mismatches %llu\n", n_cases,
          (unsigned long long)clean_ok, (unsigned long long)clean_bad, (unsigned long long)refused_host,
-         (unsigned long long)flagged, (unsigned long long)decoded);
-  return clean_bad == 0 ? 0 : 1;
+         (unsigned long long)flagged, (unsigned long long)decoded, (unsigned long long)scalar_mismatch);
+  return clean_bad == 0 && scalar_mismatch == 0 ? 0 : 1;
 }

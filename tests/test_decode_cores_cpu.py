@@ -58,7 +58,8 @@ def _case(kind: int, clean: bool, n: int, eb: int, blob: bytes, extra: bytes = b
 def _ref_extra(plan) -> bytes:
     se, tab, bst, mb, mt = _refstreams._plan_arrays(plan, 0)
     ns, nb, nt = len(plan.se_streams), len(plan.buckets), max(1, len(plan.mant_freqs))
-    return struct.pack("<III", ns, nb, nt) + se.tobytes() + tab.tobytes() + bst.tobytes() + mb.tobytes() + mt.tobytes()
+    return (struct.pack("<IIII", ns, nb, nt, tab.nbytes) + se.tobytes() + tab.tobytes() + bst.tobytes() + mb.tobytes()
+            + mt.tobytes())
 
 
 def _corrupt(rng, blob: bytes) -> bytes:

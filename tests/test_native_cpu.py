@@ -210,7 +210,7 @@ def test_struct_layouts_match_the_header(tmp_path):
                            _refstreams.MANT_BUCKET_DTYPE),
         "bs_ref_task": (["streams", "se_table", "bstart", "buckets", "mant_tables", "out", "n_out", "work_offset",
                          "n_streams", "n_buckets", "n_tables", "se_group_begin", "tile_begin", "stream_begin",
-                         "mant_group_begin", "reserved"],
+                         "mant_group_begin", "flags"],
                         _refstreams.REF_TASK_DTYPE),
         "bs_zstd_task": (["src", "src_len", "dst", "dst_len", "xor_src"], zstd_gpu.ZSTD_TASK_DTYPE),
         "bs_lut_task": (["idx", "lut", "out", "n", "n_lut", "item_bytes"], zstd_gpu.LUT_TASK_DTYPE),
