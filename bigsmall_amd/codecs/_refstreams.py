@@ -383,19 +383,67 @@ def serial_ok(plan: RefPlan) -> bool:
     return plan.n >= SERIAL_MIN_ELEMENTS and len(plan.se_streams) > 0 and max_len <= -(-plan.n // len(plan.se_streams))
 
 
+XCD_BINS = 8      # the chain kernel deals SE-group slot p to XCD p % 8 (round-robin dispatch)
+
+
+def xcd_bins(groups: list, chain_len: list, n_bins: int = XCD_BINS) -> tuple:
+    """Lay the tasks' SE groups out in n_bins equal bins of the SE part of the
+    chain grid, bin j being what XCD j decodes (bs_refcodec_decode_serial_batch
+    deals logical group (p % 8) * C + p / 8 to slot p of a grid of 8C): each
+    task's groups stay in one bin, each task goes to the emptiest bin (ties
+    to the lower bin), and C is the smallest capacity for which every task
+    fits. Up to n_bins tasks each get a bin of their own in the caller's
+    order; more are placed longest chains first, so the longest lead the
+    bins. Returns (C, order, begin, first): the tasks in grid order, each
+    task's se_group_begin, and whether it is the first (longest-chain) task
+    of its bin. One task alone spreads over every bin (C = ceil(groups /
+    n_bins)): its one table is all there is."""
+    n = len(groups)
+    if n == 1:
+        return max(1, -(-groups[0] // n_bins)), [0], {0: 0}, {0: True}
+    # sorting also reorders the mantissa groups, which follow the task array:
+    # a layer of seven one-chain tensors decoded 1.4 % slower with its longest
+    # tensors' buckets dispatched first than in the caller's order
+    idx = list(range(n)) if n <= n_bins else sorted(range(n), key=lambda i: (-chain_len[i], -groups[i], i))
+    C = max(max(groups, default=1), -(-sum(groups) // n_bins), 1)
+    while True:
+        used, bins = [0] * n_bins, [[] for _ in range(n_bins)]
+        for i in idx:
+            j = min(range(n_bins), key=lambda b: (used[b], b))
+            if used[j] + groups[i] > C:
+                break
+            bins[j].append(i)
+            used[j] += groups[i]
+        else:
+            break
+        C += 1
+    order, begin, first = [], {}, {}
+    for j, b in enumerate(bins):
+        at = j * C
+        for k, i in enumerate(b):
+            order.append(i)
+            begin[i], first[i] = at, k == 0
+            at += groups[i]
+    return C, order, begin, first
+
+
 class RefBatch:
     """The wave-serial decode of several parsed blobs (a layer's
     reference-format tensors) as one bs_refcodec_decode_serial_batch launch:
-    all their chains run side by side, the SE chains (the longest) first. items: [(plan, blob_ptr, out_ptr)],
-    every plan accepted by serial_ok. Device buffers stay alive with this
-    object until the decode launched from it has completed. The SE chains of
-    a tensor with at most 256 live SE symbols keep their state in scalar
-    registers and read a 4-byte table through the scalar cache when no other
-    tensor's SE chains share the launch, or the tensor has one SE chain (C0 in
-    bf16_se_tans: 1.04 against 1.22 s; an 8B layer of seven bf16_parallel_v1
-    tensors: 45 against 41 ms, the 128-chain tensors' tables thrashing the
-    scalar cache); mantissa chains read LDS tables (the scalar cache measured
-    no faster for them). SE_SCALAR: "auto", True or False; MANT_SCALAR: bool."""
+    all their chains run side by side, the SE chains (the longest) first.
+    items: [(plan, blob_ptr, out_ptr)], every plan accepted by serial_ok.
+    Device buffers stay alive with this object until the decode launched from
+    it has completed.
+
+    The SE groups are laid out by xcd_bins, so each XCD decodes the SE chains
+    of one tensor or a few. The first tensor of each bin, when it has at most
+    256 live SE symbols, keeps its chains' state in scalar registers and reads
+    a 4-byte table through the scalar cache (a 16 KB table: one per XCD stays
+    resident, where seven tensors' tables spread over every XCD missed, an 8B
+    layer taking 43-45 against 39-41 ms with LDS tables); the other tensors of
+    the bin, and every mantissa chain, read LDS tables (the scalar cache
+    measured no faster for mantissa chains). SE_SCALAR: "auto" (that rule),
+    True (every eligible tensor) or False; MANT_SCALAR: bool."""
 
     SE_SCALAR = "auto"
     MANT_SCALAR = False
@@ -403,28 +451,30 @@ class RefBatch:
     def __init__(self, items: list, device):
         import torch
         L = _native.lib()
-        arrays = []
-        tasks = np.zeros(len(items), REF_TASK_DTYPE)
-        per = int(L.bs_refcodec_serial_chains_per_group())
-        se_g = mant_g = tile = stream = work = 0
-        for i, (plan, blob_ptr, out_ptr) in enumerate(items):
+        for plan, _, _ in items:
             if not serial_ok(plan):
                 raise ValueError("RefBatch: a tensor the wave-serial path does not take")
+        per = int(L.bs_refcodec_serial_chains_per_group())
+        groups = [-(-len(p.se_streams) // per) for p, _, _ in items]
+        lens = [max(n for _, _, _, n in p.se_streams) for p, _, _ in items]
+        C, order, begin, first = xcd_bins(groups, lens)
+        arrays = []
+        tasks = np.zeros(len(items), REF_TASK_DTYPE)
+        mant_g = tile = stream = work = 0
+        for i, it in enumerate(order):       # task array in grid order: every *_begin ascends
+            plan, blob_ptr, out_ptr = items[it]
             arrays += _plan_arrays(plan, blob_ptr)
             ns, nb = len(plan.se_streams), len(plan.buckets)
             nt = max(1, len(plan.mant_freqs))
             tiles = int(L.bs_refcodec_serial_tiles(plan.n, ns))
             flags = FLAG_MANT_SCALAR if self.MANT_SCALAR else 0
-            # the SE table carries its 4-byte form: scalar-cache SE chains where
-            # they do not share CUs with other tensors' SE tables (a one-tensor
-            # batch, or one SE chain per tensor)
-            if arrays[-4].nbytes > 8 * M_SE and (self.SE_SCALAR is True or
-                                                 (self.SE_SCALAR == "auto" and (len(items) == 1 or ns == 1))):
-                flags |= FLAG_SE_SCALAR
-            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, se_g, tile, stream, mant_g, flags)
+            if arrays[-4].nbytes > 8 * M_SE and (self.SE_SCALAR is True or (self.SE_SCALAR == "auto" and first[it])):
+                flags |= FLAG_SE_SCALAR        # the SE table carries its 4-byte form
+            tasks[i] = (0, 0, 0, 0, 0, out_ptr, plan.n, work, ns, nb, nt, begin[it], tile, stream, mant_g, flags)
             work += (int(L.bs_refcodec_serial_work_bytes(plan.n, ns)) + 255) & ~255
-            se_g, mant_g = se_g + -(-ns // per), mant_g + -(-nb // per)
+            mant_g += -(-nb // per)
             tile, stream = tile + ns * tiles, stream + ns
+        se_g = XCD_BINS * C
         size, offs = _layout(arrays + [tasks.view(np.uint8)])
         self.dev = torch.empty(size, dtype=torch.uint8, device=device)
         base = self.dev.data_ptr()

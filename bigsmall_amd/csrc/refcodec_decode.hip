@@ -307,17 +307,19 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
 
 // The same chain with the state in scalar registers and the table read
 // through the scalar cache (uniform loads, read-only): one s_load_dword and
-// the update in SALU instructions; the step's output goes to the stage as in
-// serial_chain. Tables of 4-byte entries: SE, {index | f << 8 | (slot - cf)
+// the update in SALU instructions; the step's output goes into one lane of a
+// register. Tables of 4-byte entries: SE, {index | f << 8 | (slot - cf)
 // << 20} (the 16 KB table of a tensor with at most 256 live sign/exponent
 // symbols, none of frequency 4096; the index selects the output word from
 // `out_words`, a 256-entry LDS map applied once per 64 outputs); mantissa,
 // the global table itself {f | (slot - cf) << 11 | symbol << 21} (4 KB per
 // bucket table). A scalar-cache hit comes back sooner than the LDS round
 // trip, and the step issues fewer instructions (C0 in bf16_se_tans: 1.04
-// against 1.22 s on one chain). With many chains of different tables on a
-// CU the scalar cache thrashes (an 8B layer in bf16_parallel_v1: 45 against
-// 41 ms), so the host sets it per task.
+// against 1.22 s on one chain, before the register output). A 16 KB table
+// stays in the scalar cache only while it has the cache of its CUs to
+// itself (an 8B layer in bf16_parallel_v1, every tensor's SE groups spread
+// over every XCD: 43-45 against 39-41 ms with LDS tables), so the host sets
+// it per task and lays the SE groups out by XCD.
 __device__ __forceinline__ uint32_t uni32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ uint64_t uni64(uint64_t v) {
   return (uint64_t)uni32((uint32_t)v) | ((uint64_t)uni32((uint32_t)(v >> 32)) << 32);
@@ -327,8 +329,8 @@ template <bool SE>
 __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, uint32_t n_words, uint32_t tail,
                                                     uint32_t x0, uint32_t n, const CST uint32_t* t4_in,
                                                     const LDS uint32_t* out_words, LDS uint8_t* ring,
-                                                    LDS uint16_t* stage, GLB uint8_t* __restrict__ out,
-                                                    uint32_t stride, int32_t* status) {
+                                                    GLB uint8_t* __restrict__ out, uint32_t stride,
+                                                    int32_t* status) {
   // the descriptor's fields are the same in every lane: say so, so that the
   // whole chain (state, word position, table address) stays scalar
   n_words = uni32(n_words);
@@ -357,7 +359,8 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
     const uint32_t b = s_off + 2u * idx;
     return (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
   };
-  auto step = [&](uint32_t j) {
+  uint32_t acc = 0;            // lane j: output j of the batch
+  auto step = [&]() -> uint32_t {
     const uint32_t e = t4[x & kSlotMask];                  // s_load_dword: x is wave-uniform
     const uint32_t f = SE ? (e >> 8) & 0xFFFu : e & 0x7FFu;
     const uint32_t bias = SE ? e >> 20 : (e >> 11) & 0x3FFu;
@@ -374,8 +377,8 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
       ++pos;
     }
     x = xn;
-    // as in serial_chain; the SE index is the entry's low byte, stored as it is
-    *(volatile LDS uint8_t*)((LDS uint8_t*)stage + j) = (uint8_t)(SE ? e : (e >> 21) & 0x7Fu);
+    // the SE index is the entry's low byte, kept as it is
+    return SE ? e : (e >> 21) & 0x7Fu;
   };
   for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
     // ring upkeep: the window reaches at most 128 words (256 bytes) past pos
@@ -402,15 +405,24 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
       w_lo = w_hi;
       w_hi = ring_word(base + kWave + lane);
     }
+    // each step's output goes straight into lane j of acc (v_writelane): the
+    // LDS stage of serial_chain cost a v_mov and a ds_write per step, and its
+    // LDS count held up the wait for the next table load (a probe chain: 54.1
+    // against 50.4 ns per step)
     const uint32_t cnt = min((uint32_t)kWave, n - i0);
     if (cnt == (uint32_t)kWave) {
 #pragma unroll
-      for (uint32_t j = 0; j < (uint32_t)kWave; ++j) step(j);
+      for (uint32_t j = 0; j < (uint32_t)kWave; ++j) {
+        const uint32_t o = step();
+        BS_WRITELANE_I(acc, o, j);
+      }
     } else {
-      for (uint32_t j = 0; j < cnt; ++j) step(j);
+      for (uint32_t j = 0; j < cnt; ++j) {                 // the last, partial batch
+        const uint32_t o = step();
+        acc = lane == j ? o : acc;
+      }
     }
-    wave_sync();
-    const uint32_t keep = ((const LDS uint8_t*)stage)[lane];
+    const uint32_t keep = acc & 0xFFu;
     if (lane < cnt) {
       if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)out_words[keep];
       else out[i0 + lane] = (uint8_t)keep;
@@ -468,15 +480,28 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 }
 
 // Chain grid: workgroups of kSerWaves wavefronts, one chain each. The first
-// se_groups workgroups are SE groups (task by se_group_begin): wave w of
-// group j decodes SE stream j*kSerWaves + w (element first + i*stride for
-// symbol i) with the task's SE table, built once per workgroup and shared.
+// se_slots(se_groups) workgroups serve the SE groups (task by
+// se_group_begin; their order is below): wave w of group j decodes SE stream
+// j*kSerWaves + w (element first + i*stride for symbol i) with the task's SE
+// table, built once per workgroup and shared.
 // The rest are mantissa groups (task by mant_group_begin): wave w decodes
 // bucket j*kSerWaves + w into mant[perm_begin ...] with its own bucket table.
 // Sharing the 64 KB SE table lets a CU hold eight chains instead of two. The
 // host lists buckets longest first, so the four buckets of a group end at
 // about the same time and the longest start first.
+//
+// The SE part of the grid has se_slots(se_groups) workgroups, a multiple of
+// kXcds: workgroup p serves SE group (p % kXcds) * (slots / kXcds) + p / kXcds
+// (none past the last group). Workgroups go to the XCDs round-robin, so each
+// XCD decodes one contiguous run of groups, which covers one or two tasks: the
+// scalar-cache form of an SE table (16 KB) then meets at most two tables in an
+// XCD's scalar caches, where seven interleaved tasks' tables missed often
+// enough to make each step ~40 % slower.
 constexpr uint32_t kSerWaves = 4;
+constexpr uint32_t kXcds = 8;
+__host__ __device__ constexpr uint64_t se_slots(uint32_t se_groups) {
+  return ((uint64_t)se_groups + kXcds - 1) / kXcds * kXcds;
+}
 constexpr uint32_t kStageB = 128;      // per chain: 64 u16 outputs of a batch
 // 74240: rings | SE table or kSerWaves mantissa tables | stages
 constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16 + kSerWaves * kStageB;
@@ -493,8 +518,10 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
   LDS uint8_t* ring = (LDS uint8_t*)smem + wave * kRingB;
   LDS u32x4* tbl_area = (LDS u32x4*)(smem + kSerWaves * kRingB);
   LDS uint16_t* stage = (LDS uint16_t*)(smem + kSerWaves * kRingB + 4096 * 16 + wave * kStageB);
-  const bool se = blockIdx.x < se_groups;                 // uniform over the workgroup
-  const uint32_t g = se ? blockIdx.x : blockIdx.x - se_groups;
+  const uint32_t slots = (uint32_t)se_slots(se_groups);  // the launch checked that it fits
+  const bool se = blockIdx.x < slots;                     // uniform over the workgroup
+  const uint32_t g = se ? (blockIdx.x % kXcds) * (slots / kXcds) + blockIdx.x / kXcds : blockIdx.x - slots;
+  if (se && g >= se_groups) return;
   const bs_ref_task T = se ? pick_task<kSeGrid>(tasks, n_tasks, single, g)
                            : pick_task<kMantGrid>(tasks, n_tasks, single, g);
   const uint32_t begin = se ? T.se_group_begin : T.mant_group_begin;
@@ -529,7 +556,7 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
     }
     if (scalar_se)
       serial_chain_scalar<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n,
-                                (const CST uint32_t*)(T.se_table + 8192), out_words, ring, stage,
+                                (const CST uint32_t*)(T.se_table + 8192), out_words, ring,
                                 (GLB uint8_t*)(T.out + S.first), S.stride, status);
     else
       serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl_area, ring, stage,
@@ -544,7 +571,7 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
     const GLB uint32_t* t = (const GLB uint32_t*)T.mant_tables + (uint64_t)B.table * 1024u;
     if (T.flags & BS_REF_FLAG_MANT_SCALAR) {
       serial_chain_scalar<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, (const CST uint32_t*)t,
-                                 nullptr, ring, stage, (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
+                                 nullptr, ring, (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
       return;
     }
     LDS u32x4* tbl = tbl_area + wave * 1024u;
@@ -663,9 +690,9 @@ std::atomic<uint64_t> g_serial_lds{0};
 int launch_serial(const bs_ref_task* tasks, uint32_t n_tasks, const bs_ref_task& single, uint32_t se_groups,
                   uint32_t mant_groups, uint32_t tiles, uint32_t streams, uint8_t* work, uint64_t work_bytes,
                   int32_t* status, hipStream_t s) {
-  if ((uint64_t)se_groups + mant_groups > 0xFFFFFFFFull) return BS_ERR_ARG;
+  if (se_slots(se_groups) + mant_groups > 0xFFFFFFFFull) return BS_ERR_ARG;
   bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, g_serial_lds);
-  hipLaunchKernelGGL(serial_kernel, dim3(se_groups + mant_groups), dim3(kSerWaves * kWave), kSerLds, s, tasks,
+  hipLaunchKernelGGL(serial_kernel, dim3((uint32_t)se_slots(se_groups) + mant_groups), dim3(kSerWaves * kWave), kSerLds, s, tasks,
                      n_tasks, single, se_groups, work, work_bytes, status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
   hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes);

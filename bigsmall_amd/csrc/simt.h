@@ -16,6 +16,7 @@
 #define BS_KEEP2(a, b) ((void)(a), (void)(b))
 #define BS_KEEP4(a, b, c, d) ((void)(a), (void)(b), (void)(c), (void)(d))
 #define BS_OPAQUE(x) ((void)(x))
+#define BS_WRITELANE_I(acc, v, j) ((acc) = __lane_id() == (uint32_t)(j) ? (uint32_t)(v) : (acc))
 #else
 #include <hip/hip_runtime.h>
 #define LDS __attribute__((address_space(3)))
@@ -31,4 +32,8 @@
 #define BS_KEEP4(a, b, c, d) asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(d))
 // Hides a value's provenance from the optimiser (it stays in a vector register).
 #define BS_OPAQUE(x) asm volatile("" : "+v"(x))
+// Lane j of the 32-bit register acc takes the wave-uniform value v (one
+// v_writelane_b32; v in a scalar register); j must be a constant once the
+// caller's loop is unrolled (a compile error otherwise).
+#define BS_WRITELANE_I(acc, v, j) asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(acc) : "s"(v), "i"(j))
 #endif

@@ -248,8 +248,14 @@ uint32_t bs_refcodec_serial_tiles(uint64_t n_out, uint32_t n_streams);
  * (ceil(n_buckets / per group) each, from mant_group_begin, counted from the
  * end of the SE groups), so the longest chains start first. A task's
  * workgroups are consecutive in each grid; across the task array (device
- * memory) every *_begin ascends, each task starting where the previous one
- * ends. */
+ * memory) every *_begin ascends, and a task's range starts at or after the
+ * previous one's end (the workgroups of a gap exit at once). The SE part of
+ * the chain grid is dealt to the XCDs in bins: with total_se_groups rounded up
+ * to 8C, slot p (which the round-robin dispatch sends to XCD p % 8) decodes SE
+ * group (p % 8) * C + p / 8, so XCD j decodes groups [jC, (j+1)C). A caller
+ * that places each task's SE groups inside one bin (gaps where needed) keeps
+ * the tasks whose tables are read through the scalar cache on XCDs of their
+ * own. */
 typedef struct {
     const bs_se_stream *streams;     /* n_streams SE stream descriptors */
     const uint32_t *se_table;        /* 4096 x {f | (slot-cf) << 13, symbol} u32 pairs */

@@ -116,6 +116,13 @@ int main(int argc, char** argv) {
     uint32_t eb;
   };
   std::vector<Clean> clean_bsck;   // decoded again together, through the batched entry point
+  struct CleanRef {                 // a clean wave-serial case, as read (word arrays blob-relative)
+    std::vector<uint8_t> blob, se, se_table, bstart, mb, tables, want;
+    uint32_t ns, nb, nt;
+    uint64_t n;
+  };
+  std::vector<CleanRef> clean_ref;  // decoded again together, with gaps between the tasks' SE groups
+  CleanRef pending;
   for (uint32_t c = 0; c < n_cases; ++c) {
     const uint8_t kind = r.get<uint8_t>(), clean = r.get<uint8_t>();
     r.get<uint16_t>();
@@ -147,6 +154,15 @@ int main(int argc, char** argv) {
       memcpy(mb.data(), r.take((uint64_t)nb * sizeof(bs_mant_bucket)), (uint64_t)nb * sizeof(bs_mant_bucket));
       Buf tables((uint64_t)nt * 4096);
       memcpy(tables.p, r.take((uint64_t)nt * 4096), (uint64_t)nt * 4096);
+      if (clean && kind == 1) {
+        auto bytes = [](const void* q, uint64_t n) {
+          return std::vector<uint8_t>((const uint8_t*)q, (const uint8_t*)q + n);
+        };
+        pending = CleanRef{bytes(blob.p, blob_len), bytes(se.data(), (uint64_t)ns * sizeof(bs_se_stream)),
+                           bytes(se_table.p, se_bytes), bytes(bstart.p, (uint64_t)ns * 257 * 4),
+                           bytes(mb.data(), (uint64_t)nb * sizeof(bs_mant_bucket)), bytes(tables.p, (uint64_t)nt * 4096),
+                           {}, ns, nb, nt, n_out};
+      }
       for (auto& s : se) s.words = blob.p + (uintptr_t)s.words;
       for (auto& b : mb) b.words = blob.p + (uintptr_t)b.words;
       Buf d_se(ns * sizeof(bs_se_stream)), d_mb(nb * sizeof(bs_mant_bucket));
@@ -202,6 +218,10 @@ int main(int argc, char** argv) {
     if (clean && kind == 0)
       clean_bsck.push_back({std::vector<uint8_t>(blob_src, blob_src + blob_len),
                             std::vector<uint8_t>(want, want + n_out * eb), n_out, eb});
+    if (clean && kind == 1 && n_out > 0) {
+      pending.want.assign(want, want + n_out * eb);
+      clean_ref.push_back(std::move(pending));
+    }
     if (clean) {
       if (rc == BS_OK && status == 0 && memcmp(out.p, want, n_out * eb) == 0) {
         ++clean_ok;
@@ -307,9 +327,85 @@ int main(int argc, char** argv) {
       fprintf(stderr, "out-of-order table with an empty task: rc %d status 0x%x\n", rc, status);
     }
   }
-  printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu, empty task flagged %llu\n",
+  // The clean wave-serial cases (up to 8) in one batched launch whose SE
+  // groups have gaps: task i's groups start at i * C, C one more than the
+  // most groups of any task, in a grid of 8C SE slots (the layout that puts
+  // each task on an XCD of its own), every other task with its SE table read
+  // through the scalar path where it has that form. Each must decode to its
+  // source.
+  uint64_t ref_batch_ok = 0;
+  if (!clean_ref.empty()) {
+    const size_t nt = clean_ref.size() < 8 ? clean_ref.size() : 8;
+    const uint32_t per = bs_refcodec_serial_chains_per_group();
+    uint32_t C = 0;
+    for (size_t i = 0; i < nt; ++i) {
+      const uint32_t g = (clean_ref[i].ns + per - 1) / per;
+      if (g > C) C = g;
+    }
+    C += 1;
+    std::vector<Buf*> keep;
+    auto copy = [&](const std::vector<uint8_t>& v) {
+      keep.push_back(new Buf(v.size() ? v.size() : 1));
+      if (!v.empty()) memcpy(keep.back()->p, v.data(), v.size());
+      return keep.back()->p;
+    };
+    std::vector<bs_ref_task> tasks(nt);
+    std::vector<uint8_t*> outs(nt);
+    uint32_t mant_g = 0, tiles = 0, streams = 0;
+    uint64_t work = 0;
+    for (size_t i = 0; i < nt; ++i) {
+      CleanRef& c = clean_ref[i];
+      uint8_t* blob = copy(c.blob);
+      std::vector<bs_se_stream> se(c.ns);
+      std::vector<bs_mant_bucket> mb(c.nb);
+      memcpy(se.data(), c.se.data(), c.se.size());
+      memcpy(mb.data(), c.mb.data(), c.mb.size());
+      for (auto& q : se) q.words = blob + (uintptr_t)q.words;
+      for (auto& q : mb) q.words = blob + (uintptr_t)q.words;
+      bs_ref_task& t = tasks[i];
+      t.streams = (const bs_se_stream*)copy(std::vector<uint8_t>((uint8_t*)se.data(), (uint8_t*)se.data() + c.se.size()));
+      t.se_table = (const uint32_t*)copy(c.se_table);
+      t.bstart = (const uint32_t*)copy(c.bstart);
+      t.buckets = (const bs_mant_bucket*)copy(std::vector<uint8_t>((uint8_t*)mb.data(), (uint8_t*)mb.data() + c.mb.size()));
+      t.mant_tables = (const uint32_t*)copy(c.tables);
+      outs[i] = copy(std::vector<uint8_t>(c.n * 2, 0x5A));
+      t.out = (uint16_t*)outs[i];
+      t.n_out = c.n;
+      t.work_offset = work;
+      t.n_streams = c.ns;
+      t.n_buckets = c.nb;
+      t.n_tables = c.nt;
+      t.se_group_begin = (uint32_t)i * C;
+      t.tile_begin = tiles;
+      t.stream_begin = streams;
+      t.mant_group_begin = mant_g;
+      t.flags = (i % 2 == 0 && c.se_table.size() > 4096 * 8) ? BS_REF_FLAG_SE_SCALAR : 0u;
+      work += (bs_refcodec_serial_work_bytes(c.n, c.ns) + 255) & ~255ull;
+      mant_g += (c.nb + per - 1) / per;
+      tiles += c.ns * bs_refcodec_serial_tiles(c.n, c.ns);
+      streams += c.ns;
+    }
+    Buf d_tasks(nt * sizeof(bs_ref_task)), d_work(work, true);
+    memcpy(d_tasks.p, tasks.data(), nt * sizeof(bs_ref_task));
+    int32_t status = 0;
+    const int rc = bs_refcodec_decode_serial_batch((const bs_ref_task*)d_tasks.p, (uint32_t)nt, 8u * C, mant_g, tiles,
+                                                   streams, d_work.p, work, &status, nullptr);
+    for (size_t i = 0; i < nt; ++i) {
+      const CleanRef& c = clean_ref[i];
+      if (rc == BS_OK && status == 0 && memcmp(outs[i], c.want.data(), c.n * 2) == 0) {
+        ++ref_batch_ok;
+      } else {
+        ++clean_bad;
+        fprintf(stderr, "reference batch with gaps, task %zu (n %llu): rc %d status 0x%x\n", i,
+                (unsigned long long)c.n, rc, status);
+      }
+    }
+    for (Buf* b : keep) delete b;
+  }
+  printf("batched tasks ok %llu failed %llu, pointers with bit 31 set %llu, empty task flagged %llu, "
+         "reference batch with gaps ok %llu\n",
          (unsigned long long)batch_ok, (unsigned long long)batch_bad, (unsigned long long)high_bit,
-         (unsigned long long)empty_flagged);
+         (unsigned long long)empty_flagged, (unsigned long long)ref_batch_ok);
   printf("cases %u clean ok %llu clean failed %llu corrupted: refused %llu flagged %llu decoded %llu "
          "scalar-table mismatches %llu\n", n_cases,
          (unsigned long long)clean_ok, (unsigned long long)clean_bad, (unsigned long long)refused_host,

@@ -189,7 +189,9 @@ def test_serial_batch_rejects_inconsistent_task(gpu):
         batch = _refstreams.RefBatch(items, dev)
         off = batch.p_tasks - batch.dev.data_ptr()
         tasks = batch.dev[off:off + 2 * _refstreams.REF_TASK_DTYPE.itemsize].cpu().numpy().view(_refstreams.REF_TASK_DTYPE).copy()
-        tasks[field][1] = value
+        # the batch orders its task array by its grid layout: find the second tensor's task by its output
+        (j,) = np.flatnonzero(tasks["out"] == outs[1].data_ptr())
+        tasks[field][j] = value
         batch.dev[off:off + tasks.nbytes].copy_(torch.from_numpy(tasks.view(np.uint8)))
         st = StatusWord(dev)
         _say(f"[ref] serial batch with task 1 {field}={value}")

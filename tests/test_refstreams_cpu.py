@@ -175,3 +175,39 @@ def test_malformed_blobs_raise(golden):
     sk = golden["sk_gauss"].tobytes()
     with pytest.raises(ValueError):
         rs.parse_single_kernel(sk[:-3], n)
+
+
+@pytest.mark.parametrize("groups,lens", [
+    ([32] * 7, [131072, 32768, 32768, 131072, 458752, 458752, 458752]),   # the 8B layer in bf16_parallel_v1
+    ([1] * 7, [7, 6, 5, 4, 3, 2, 1]),                                     # the same layer in bf16_se_tans
+    ([32] * 20, list(range(20))),
+    ([3, 1, 1, 1, 1, 1, 1, 1, 1, 1], [9, 8, 7, 6, 5, 4, 3, 2, 1, 0]),
+    ([5, 40, 2, 2, 9, 33, 1, 1, 1, 17, 8], [10, 99, 3, 3, 20, 70, 1, 2, 1, 50, 9]),
+])
+def test_xcd_bins_layout(groups, lens):
+    """Each task's SE groups sit inside one of the 8 bins of C groups, no two
+    overlap, the task array ascends, the first task of each bin has the
+    longest chains in it, and the longest eight tasks lead eight bins."""
+    C, order, begin, first = rs.xcd_bins(groups, lens)
+    assert sorted(order) == list(range(len(groups)))
+    assert [begin[i] for i in order] == sorted(begin[i] for i in order)
+    used = set()
+    for i in order:
+        lo, hi = begin[i], begin[i] + groups[i]
+        assert lo // C == (hi - 1) // C and hi <= rs.XCD_BINS * C, (i, lo, hi, C)
+        span = set(range(lo, hi))
+        assert not (span & used)
+        used |= span
+    for j in range(rs.XCD_BINS):
+        members = [i for i in order if begin[i] // C == j]
+        if members:
+            assert first[members[0]] and not any(first[i] for i in members[1:])
+            assert lens[members[0]] == max(lens[i] for i in members)
+    longest = sorted(range(len(groups)), key=lambda i: (-lens[i], -groups[i], i))[:rs.XCD_BINS]
+    assert all(first[i] for i in longest)
+    assert C >= max(groups) and rs.XCD_BINS * C >= sum(groups)
+
+
+def test_xcd_bins_one_task_spreads():
+    assert rs.xcd_bins([32], [131072]) == (4, [0], {0: 0}, {0: True})
+    assert rs.xcd_bins([1], [5]) == (1, [0], {0: 0}, {0: True})
