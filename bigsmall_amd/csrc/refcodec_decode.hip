@@ -147,12 +147,13 @@ __global__ __launch_bounds__(kMantThreads) void mant_kernel(const bs_mant_bucket
 // that a renormalisation takes its word with a readlane and no branch, and
 // they stage 64 consecutive outputs (lane j keeps step j) for one coalesced
 // store. The SE chain writes sign<<15 | exp<<7 of
-// every element; the mantissa chains, which do not depend on it, run at the
-// same time in other workgroups and write their bucket's mantissas in bucket
-// order. Three parallel passes then give every element its position in its
-// (stream, exponent) bucket (a stable counting sort by exponent within each
-// stream: per-tile histograms, a scan over the stream's tiles, per-tile ranks
-// by wavefront ballots) and OR in its mantissa.
+// every element and counts the exponents of each tile of kTile symbols of its
+// stream; the mantissa chains, which do not depend on it, run at the same time
+// in other workgroups and write their bucket's mantissas in bucket order. Two
+// parallel passes then give every element its position in its (stream,
+// exponent) bucket (a stable counting sort by exponent within each stream: a
+// scan of the tile counts over the stream's tiles, then per-tile ranks by
+// wavefront ballots) and OR in its mantissa.
 
 constexpr uint32_t kRingB = 2048;     // word-stream byte ring per chain (two segments: one landed, one in flight)
 constexpr uint32_t kSegB = 1024;      // bytes per cooperative load (64 lanes x 16 B)
@@ -187,10 +188,40 @@ __device__ __forceinline__ void seg_land(LDS uint8_t* ring, uint64_t q, uint32_t
 
 // A stream descriptor every pass of the serial path may use: at most max_len
 // symbols (what the placement tiles cover) and every element index inside the
-// output. The three passes check it alike, so a bad descriptor is reported and
-// skipped, never followed.
+// output. The chain and placement kernels check it alike, so a bad
+// descriptor is reported and skipped, never followed.
 __device__ __forceinline__ bool stream_ok(const bs_se_stream& S, uint64_t max_len, uint64_t n_out) {
   return S.n <= max_len && S.stride != 0 && (S.n == 0 || S.first + (uint64_t)(S.n - 1) * S.stride < n_out);
+}
+
+// Exponent counts of an SE chain, kept in the wave's own 256 LDS bins for
+// the current tile of kTile symbols and written to ghist[tile][256] when the
+// tile ends (symbols [i0, i0 + cnt) are this batch, lane j holding output
+// word j; a stream of n symbols). Counting here, one LDS add per lane per 64
+// steps, replaced a pass that read every output word back with a stride of
+// n_streams elements (1.6 of 39 ms for an 8B layer in bf16_parallel_v1).
+__device__ __forceinline__ void tile_count(LDS uint32_t* hist, GLB uint32_t* ghist, uint32_t word, uint32_t lane,
+                                           uint32_t i0, uint32_t cnt, uint32_t n) {
+  if (lane < cnt) BS_LDS_ADD(hist + ((word >> 7) & 0xFFu), 1u);
+  const uint32_t end = i0 + cnt;
+  if (end % kTile == 0 || end == n) {
+    wave_sync();
+    GLB uint32_t* g = ghist + (uint64_t)(i0 / kTile) * 256u;
+    for (uint32_t b = lane; b < 256; b += kWave) {
+      g[b] = hist[b];
+      hist[b] = 0;
+    }
+    wave_sync();
+  }
+}
+// Before an SE chain: empty bins. After it: zero counts for the tiles its n
+// symbols do not reach (of the task's tps per stream).
+__device__ __forceinline__ void tile_count_begin(LDS uint32_t* hist, uint32_t lane) {
+  for (uint32_t b = lane; b < 256; b += kWave) hist[b] = 0;
+  wave_sync();
+}
+__device__ __forceinline__ void tile_count_end(GLB uint32_t* ghist, uint32_t lane, uint32_t n, uint32_t tps) {
+  for (uint64_t i = ((uint64_t)n + kTile - 1) / kTile * 256u + lane; i < (uint64_t)tps * 256u; i += kWave) ghist[i] = 0;
 }
 
 // Decode one chain of n symbols. The LDS table has one 16-byte entry per slot,
@@ -212,7 +243,8 @@ template <bool SE>
 __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t n_words, uint32_t tail, uint32_t x0,
                                              uint32_t n, const LDS u32x4* __restrict__ tbl,
                                              LDS uint8_t* ring, LDS uint16_t* stage, GLB uint8_t* __restrict__ out,
-                                             uint32_t stride, int32_t* status) {
+                                             uint32_t stride, LDS uint32_t* hist, GLB uint32_t* ghist, uint32_t tps,
+                                             int32_t* status) {
   constexpr uint32_t kSlotMask = SE ? 4095u : 1023u;
   constexpr uint32_t kShift = SE ? 12u : 10u;
   const uint32_t lane = __lane_id();
@@ -233,6 +265,7 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
     return;
   }
+  if (SE) tile_count_begin(hist, lane);
   auto ring_word = [&](uint32_t idx) {
     const uint32_t b = s_off + 2u * idx;
     return (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
@@ -299,7 +332,9 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
       if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)keep;
       else out[i0 + lane] = (uint8_t)keep;
     }
+    if (SE) tile_count(hist, ghist, keep, lane, i0, cnt, n);
   }
+  if (SE) tile_count_end(ghist, lane, n, tps);
   if (__builtin_amdgcn_readfirstlane(x) != kL || pos != n_eff) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
   }
@@ -330,6 +365,7 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
                                                     uint32_t x0, uint32_t n, const CST uint32_t* t4_in,
                                                     const LDS uint32_t* out_words, LDS uint8_t* ring,
                                                     GLB uint8_t* __restrict__ out, uint32_t stride,
+                                                    LDS uint32_t* hist, GLB uint32_t* ghist, uint32_t tps,
                                                     int32_t* status) {
   // the descriptor's fields are the same in every lane: say so, so that the
   // whole chain (state, word position, table address) stays scalar
@@ -355,6 +391,7 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
     return;
   }
+  if (SE) tile_count_begin(hist, lane);
   auto ring_word = [&](uint32_t idx) {
     const uint32_t b = s_off + 2u * idx;
     return (uint32_t)ring[b & (kRingB - 1u)] | ((uint32_t)ring[(b + 1u) & (kRingB - 1u)] << 8);
@@ -423,11 +460,14 @@ __device__ __forceinline__ void serial_chain_scalar(const GLB uint8_t* words, ui
       }
     }
     const uint32_t keep = acc & 0xFFu;
+    const uint32_t word = SE ? out_words[keep] : keep;
     if (lane < cnt) {
-      if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)out_words[keep];
+      if (SE) ((GLB uint16_t*)out)[(uint64_t)(i0 + lane) * stride] = (uint16_t)word;
       else out[i0 + lane] = (uint8_t)keep;
     }
+    if (SE) tile_count(hist, ghist, word, lane, i0, cnt, n);
   }
+  if (SE) tile_count_end(ghist, lane, n, tps);
   if (x != kL || pos != n_eff) {
     if (lane == 0) flag(status, BS_DEV_ERR_STREAM);
   }
@@ -480,7 +520,7 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 }
 
 // Chain grid: workgroups of kSerWaves wavefronts, one chain each. The first
-// se_slots(se_groups) workgroups serve the SE groups (task by
+// xcd_slots(se_groups) workgroups serve the SE groups (task by
 // se_group_begin; their order is below): wave w of group j decodes SE stream
 // j*kSerWaves + w (element first + i*stride for symbol i) with the task's SE
 // table, built once per workgroup and shared.
@@ -490,7 +530,7 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 // host lists buckets longest first, so the four buckets of a group end at
 // about the same time and the longest start first.
 //
-// The SE part of the grid has se_slots(se_groups) workgroups, a multiple of
+// The SE part of the grid has xcd_slots(se_groups) workgroups, a multiple of
 // kXcds: workgroup p serves SE group (p % kXcds) * (slots / kXcds) + p / kXcds
 // (none past the last group). Workgroups go to the XCDs round-robin, so each
 // XCD decodes one contiguous run of groups, which covers one or two tasks: the
@@ -499,13 +539,17 @@ __device__ __forceinline__ bs_ref_task pick_task(const bs_ref_task* __restrict__
 // enough to make each step ~40 % slower.
 constexpr uint32_t kSerWaves = 4;
 constexpr uint32_t kXcds = 8;
-__host__ __device__ constexpr uint64_t se_slots(uint32_t se_groups) {
-  return ((uint64_t)se_groups + kXcds - 1) / kXcds * kXcds;
+// A grid part of `count` workgroups dealt to the XCDs in contiguous blocks:
+// count rounded up to a multiple of kXcds.
+__host__ __device__ constexpr uint64_t xcd_slots(uint32_t count) {
+  return ((uint64_t)count + kXcds - 1) / kXcds * kXcds;
 }
 constexpr uint32_t kStageB = 128;      // per chain: 64 u16 outputs of a batch
-// 74240: rings | SE table or kSerWaves mantissa tables | stages
-constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16 + kSerWaves * kStageB;
-static_assert(2 * kSerLds <= 160 * 1024 - 8192, "two chain groups per CU");
+constexpr uint32_t kHistB = 256 * 4;   // per SE chain: the exponent counts of its current tile
+// 78336: rings | SE table or kSerWaves mantissa tables | stages | tile counts.
+// Two groups fit the 160 KB of a CU (two of 81,920 B did not).
+constexpr uint32_t kSerLds = kSerWaves * kRingB + 4096 * 16 + kSerWaves * kStageB + kSerWaves * kHistB;
+static_assert(2 * kSerLds <= 160 * 1024 - 4096, "two chain groups per CU");
 static_assert(kSerWaves * 1024 * 16 <= 4096 * 16, "mantissa tables exceed the table area");
 
 __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_task* __restrict__ tasks,
@@ -518,7 +562,8 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
   LDS uint8_t* ring = (LDS uint8_t*)smem + wave * kRingB;
   LDS u32x4* tbl_area = (LDS u32x4*)(smem + kSerWaves * kRingB);
   LDS uint16_t* stage = (LDS uint16_t*)(smem + kSerWaves * kRingB + 4096 * 16 + wave * kStageB);
-  const uint32_t slots = (uint32_t)se_slots(se_groups);  // the launch checked that it fits
+  LDS uint32_t* hist = (LDS uint32_t*)(smem + kSerWaves * kRingB + 4096 * 16 + kSerWaves * kStageB + wave * kHistB);
+  const uint32_t slots = (uint32_t)xcd_slots(se_groups);  // the launch checked that it fits
   const bool se = blockIdx.x < slots;                     // uniform over the workgroup
   const uint32_t g = se ? (blockIdx.x % kXcds) * (slots / kXcds) + blockIdx.x / kXcds : blockIdx.x - slots;
   if (se && g >= se_groups) return;
@@ -554,13 +599,16 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
       if (lane == 0) flag(status, BS_DEV_ERR_HEADER);
       return;
     }
+    // the stream's tile counts: tps x 256 after the task's mantissa area
+    const uint32_t tps = serial_tiles(T.n_out, T.n_streams);
+    GLB uint32_t* ghist = (GLB uint32_t*)(work + T.work_offset + ((T.n_out + 255) & ~255ull)) + (uint64_t)c * tps * 256u;
     if (scalar_se)
       serial_chain_scalar<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n,
                                 (const CST uint32_t*)(T.se_table + 8192), out_words, ring,
-                                (GLB uint8_t*)(T.out + S.first), S.stride, status);
+                                (GLB uint8_t*)(T.out + S.first), S.stride, hist, ghist, tps, status);
     else
       serial_chain<true>((const GLB uint8_t*)S.words, S.n_words, S.tail, S.x0, S.n, tbl_area, ring, stage,
-                         (GLB uint8_t*)(T.out + S.first), S.stride, status);
+                         (GLB uint8_t*)(T.out + S.first), S.stride, hist, ghist, tps, status);
   } else {
     if (c >= count) return;
     const bs_mant_bucket B = T.buckets[c];
@@ -571,7 +619,8 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
     const GLB uint32_t* t = (const GLB uint32_t*)T.mant_tables + (uint64_t)B.table * 1024u;
     if (T.flags & BS_REF_FLAG_MANT_SCALAR) {
       serial_chain_scalar<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, (const CST uint32_t*)t,
-                                 nullptr, ring, (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
+                                 nullptr, ring, (GLB uint8_t*)(mant + B.perm_begin), 1u, nullptr, nullptr, 0u,
+                                 status);
       return;
     }
     LDS u32x4* tbl = tbl_area + wave * 1024u;
@@ -581,32 +630,8 @@ __global__ __launch_bounds__(kSerWaves * kWave) void serial_kernel(const bs_ref_
     }
     wave_sync();
     serial_chain<false>((const GLB uint8_t*)B.words, B.n_words, B.tail, B.x0, B.n, tbl, ring, stage,
-                        (GLB uint8_t*)(mant + B.perm_begin), 1u, status);
+                        (GLB uint8_t*)(mant + B.perm_begin), 1u, nullptr, nullptr, 0u, status);
   }
-}
-
-// Tile grid, one workgroup per (stream k, tile t) of a task (t fastest):
-// exponent histogram of symbols [t*kTile, (t+1)*kTile) of stream k.
-__global__ __launch_bounds__(256) void hist_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
-                                                   bs_ref_task single, uint8_t* __restrict__ work,
-                                                   uint64_t work_bytes) {
-  __shared__ uint32_t h[256];
-  const uint32_t tid = threadIdx.x;
-  const bs_ref_task T = pick_task<kTileGrid>(tasks, n_tasks, single, blockIdx.x);
-  if (blockIdx.x < T.tile_begin || !task_ok(T, work_bytes)) return;
-  const uint32_t tps = serial_tiles(T.n_out, T.n_streams), local = blockIdx.x - T.tile_begin;
-  if (local >= T.n_streams * tps) return;
-  const uint32_t k = local / tps, t = local % tps;
-  uint32_t* hist = (uint32_t*)(work + T.work_offset + ((T.n_out + 255) & ~255ull));
-  const bs_se_stream S = T.streams[k];
-  h[tid] = 0;
-  __syncthreads();
-  const uint32_t lo = t * kTile;
-  const uint32_t hi = stream_ok(S, (uint64_t)tps * kTile, T.n_out) ? (uint32_t)min((uint64_t)S.n, (uint64_t)lo + kTile) : lo;
-  for (uint32_t i = lo + tid; i < hi; i += 256)
-    atomicAdd(&h[(T.out[S.first + (uint64_t)i * S.stride] >> 7) & 0xFFu], 1u);
-  __syncthreads();
-  hist[(uint64_t)local * 256 + tid] = h[tid];
 }
 
 // Stream grid, one workgroup per stream k of a task, thread e: turn stream
@@ -633,54 +658,84 @@ __global__ __launch_bounds__(256) void scan_kernel(const bs_ref_task* __restrict
   if (run != bs[e + 1]) flag(status, BS_DEV_ERR_COUNT);
 }
 
-// Tile grid again, one wavefront per tile: the position of each element in
-// its bucket, from the tile's first positions plus its rank among the equal
-// exponents before it (64 elements at a time: lanes with the same exponent
-// found with eight ballots); then OR the element's mantissa into it.
+// Tile grid, one wavefront per (stream k, tile t) of a task: the position of
+// each element in its bucket, from the tile's first positions plus its rank
+// among the equal exponents before it (64 elements at a time: lanes with the
+// same exponent found with eight ballots); then OR the element's mantissa
+// into it. The elements of a stream lie n_streams apart, so every word is a
+// memory round trip of its own: kPlaceU batches of 64 are loaded together,
+// ranked in order, their mantissas gathered together, then stored (one batch
+// at a time took 3.8 ms of an 8B layer in bf16_parallel_v1).
+//
+// A 128-byte line of output holds one symbol of 64 streams, so the waves of
+// one tile column (tile t of every stream of a task) share their lines. The
+// grid (a multiple of kXcds workgroups) is dealt like the SE part of the
+// chain grid: workgroup p takes tile slot (p % kXcds) * (grid / kXcds) + p /
+// kXcds of the tile grid, in which a task's tiles run streams fastest, so
+// each XCD works through whole columns one after another and a line's 64
+// writers meet in one L2. Tile order (stream, tile) spread every column
+// over all XCDs: the batched 8B layer placed in 4.5 ms against 2.2 ms for
+// its seven tensors in separate launches.
+constexpr uint32_t kPlaceU = 8;
 __global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
-                                                      bs_ref_task single, uint8_t* __restrict__ work,
+                                                      bs_ref_task single, uint32_t n_tiles, uint8_t* __restrict__ work,
                                                       uint64_t work_bytes, int32_t* __restrict__ status) {
   __shared__ uint32_t cnt[256];
   const uint32_t lane = threadIdx.x;
-  const bs_ref_task T = pick_task<kTileGrid>(tasks, n_tasks, single, blockIdx.x);
-  if (blockIdx.x < T.tile_begin || !task_ok(T, work_bytes)) return;
-  const uint32_t tps = serial_tiles(T.n_out, T.n_streams), local = blockIdx.x - T.tile_begin;
+  const uint32_t v = (blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  if (v >= n_tiles) return;
+  const bs_ref_task T = pick_task<kTileGrid>(tasks, n_tasks, single, v);
+  if (v < T.tile_begin || !task_ok(T, work_bytes)) return;
+  const uint32_t tps = serial_tiles(T.n_out, T.n_streams), local = v - T.tile_begin;
   if (local >= T.n_streams * tps) return;
-  const uint32_t k = local / tps, t = local % tps;
+  const uint32_t t = local / T.n_streams, k = local % T.n_streams;
   const uint64_t n = T.n_out;
-  const uint8_t* mant = work + T.work_offset;
+  const uint8_t* __restrict__ mant = work + T.work_offset;
   const uint32_t* first = (const uint32_t*)(mant + ((n + 255) & ~255ull));
-  uint16_t* out = T.out;
+  uint16_t* __restrict__ out = T.out;
   const bs_se_stream S = T.streams[k];
   if (!stream_ok(S, (uint64_t)tps * kTile, n)) return;     // reported by serial_kernel
-  for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[(uint64_t)local * 256 + e];
+  const uint64_t kt = (uint64_t)k * tps + t;               // the scan's (stream, tile) order
+  for (uint32_t e = lane; e < 256; e += kWave) cnt[e] = first[kt * 256 + e];
   wave_sync();
   const uint32_t lo = t * kTile, hi = (uint32_t)min((uint64_t)S.n, (uint64_t)lo + kTile);
   const uint64_t lt = (1ull << lane) - 1ull;
   bool bad = false;
-  for (uint32_t k0 = lo; k0 < hi; k0 += kWave) {
-    const uint32_t i = k0 + lane;
-    const bool valid = i < hi;
-    const uint64_t el = S.first + (uint64_t)i * S.stride;
-    const uint32_t word = valid ? out[el] : 0u;
-    const uint32_t e = (word >> 7) & 0xFFu;
-    uint64_t m = __ballot(valid);
+  for (uint32_t k0 = lo; k0 < hi; k0 += kPlaceU * kWave) {
+    uint32_t word[kPlaceU], pos[kPlaceU], mb[kPlaceU];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = (e >> b) & 1u;
-      const uint64_t bb = __ballot(bit);
-      m &= bit ? bb : ~bb;
+    for (uint32_t u = 0; u < kPlaceU; ++u) {
+      const uint32_t i = k0 + u * kWave + lane;
+      word[u] = i < hi ? out[S.first + (uint64_t)i * S.stride] : 0u;
     }
-    const uint32_t rank = (uint32_t)__popcll(m & lt), total = (uint32_t)__popcll(m);
-    const uint32_t base = cnt[e];
-    wave_sync();
-    if (valid && rank == 0) cnt[e] = base + total;
-    if (valid) {
-      const uint32_t p = base + rank;
-      if (p < n) out[el] = (uint16_t)(word | mant[p]);
-      else bad = true;
+#pragma unroll
+    for (uint32_t u = 0; u < kPlaceU; ++u) {
+      const bool valid = k0 + u * kWave + lane < hi;
+      const uint32_t e = (word[u] >> 7) & 0xFFu;
+      uint64_t m = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const bool bit = (e >> b) & 1u;
+        const uint64_t bb = __ballot(bit);
+        m &= bit ? bb : ~bb;
+      }
+      const uint32_t rank = (uint32_t)__popcll(m & lt), total = (uint32_t)__popcll(m);
+      const uint32_t base = cnt[e];
+      wave_sync();
+      if (valid && rank == 0) cnt[e] = base + total;
+      wave_sync();
+      pos[u] = valid ? base + rank : 0xFFFFFFFFu;          // none for the lanes past the tile
     }
-    wave_sync();
+#pragma unroll
+    for (uint32_t u = 0; u < kPlaceU; ++u) mb[u] = pos[u] < n ? mant[pos[u]] : 0u;
+#pragma unroll
+    for (uint32_t u = 0; u < kPlaceU; ++u) {
+      const uint32_t i = k0 + u * kWave + lane;
+      if (i < hi) {
+        if (pos[u] < n) out[S.first + (uint64_t)i * S.stride] = (uint16_t)(word[u] | mb[u]);
+        else bad = true;
+      }
+    }
   }
   if (__ballot(bad) != 0 && lane == 0) flag(status, BS_DEV_ERR_COUNT);
 }
@@ -690,16 +745,15 @@ std::atomic<uint64_t> g_serial_lds{0};
 int launch_serial(const bs_ref_task* tasks, uint32_t n_tasks, const bs_ref_task& single, uint32_t se_groups,
                   uint32_t mant_groups, uint32_t tiles, uint32_t streams, uint8_t* work, uint64_t work_bytes,
                   int32_t* status, hipStream_t s) {
-  if (se_slots(se_groups) + mant_groups > 0xFFFFFFFFull) return BS_ERR_ARG;
+  if (xcd_slots(se_groups) + mant_groups > 0xFFFFFFFFull || xcd_slots(tiles) > 0xFFFFFFFFull) return BS_ERR_ARG;
   bs_internal::ensure_lds_limit((const void*)serial_kernel, kSerLds, g_serial_lds);
-  hipLaunchKernelGGL(serial_kernel, dim3((uint32_t)se_slots(se_groups) + mant_groups), dim3(kSerWaves * kWave), kSerLds, s, tasks,
-                     n_tasks, single, se_groups, work, work_bytes, status);
-  if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(hist_kernel, dim3(tiles), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes);
+  hipLaunchKernelGGL(serial_kernel, dim3((uint32_t)xcd_slots(se_groups) + mant_groups), dim3(kSerWaves * kWave),
+                     kSerLds, s, tasks, n_tasks, single, se_groups, work, work_bytes, status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
   hipLaunchKernelGGL(scan_kernel, dim3(streams), dim3(256), 0, s, tasks, n_tasks, single, work, work_bytes, status);
   if (hipGetLastError() != hipSuccess) return BS_ERR_HIP;
-  hipLaunchKernelGGL(place_kernel, dim3(tiles), dim3(kWave), 0, s, tasks, n_tasks, single, work, work_bytes, status);
+  hipLaunchKernelGGL(place_kernel, dim3((uint32_t)xcd_slots(tiles)), dim3(kWave), 0, s, tasks, n_tasks, single, tiles,
+                     work, work_bytes, status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
 

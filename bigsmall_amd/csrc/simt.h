@@ -17,6 +17,7 @@
 #define BS_KEEP4(a, b, c, d) ((void)(a), (void)(b), (void)(c), (void)(d))
 #define BS_OPAQUE(x) ((void)(x))
 #define BS_WRITELANE_I(acc, v, j) ((acc) = __lane_id() == (uint32_t)(j) ? (uint32_t)(v) : (acc))
+#define BS_LDS_ADD(p, v) ((void)atomicAdd((p), (v)))
 #else
 #include <hip/hip_runtime.h>
 #define LDS __attribute__((address_space(3)))
@@ -36,4 +37,6 @@
 // v_writelane_b32; v in a scalar register); j must be a constant once the
 // caller's loop is unrolled (a compile error otherwise).
 #define BS_WRITELANE_I(acc, v, j) asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(acc) : "s"(v), "i"(j))
+// Atomic add to a 32-bit LDS word (ds_add_u32), ordered only within the wave.
+#define BS_LDS_ADD(p, v) ((void)__hip_atomic_fetch_add((p), (v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT))
 #endif
