@@ -662,10 +662,7 @@ __global__ __launch_bounds__(256) void scan_kernel(const bs_ref_task* __restrict
 // each element in its bucket, from the tile's first positions plus its rank
 // among the equal exponents before it (64 elements at a time: lanes with the
 // same exponent found with eight ballots); then OR the element's mantissa
-// into it. The elements of a stream lie n_streams apart, so every word is a
-// memory round trip of its own: kPlaceU batches of 64 are loaded together,
-// ranked in order, their mantissas gathered together, then stored (one batch
-// at a time took 3.8 ms of an 8B layer in bf16_parallel_v1).
+// into it.
 //
 // A 128-byte line of output holds one symbol of 64 streams, so the waves of
 // one tile column (tile t of every stream of a task) share their lines. The
@@ -674,9 +671,9 @@ __global__ __launch_bounds__(256) void scan_kernel(const bs_ref_task* __restrict
 // kXcds of the tile grid, in which a task's tiles run streams fastest, so
 // each XCD works through whole columns one after another and a line's 64
 // writers meet in one L2. Tile order (stream, tile) spread every column
-// over all XCDs: the batched 8B layer placed in 4.5 ms against 2.2 ms for
-// its seven tensors in separate launches.
-constexpr uint32_t kPlaceU = 8;
+// over all XCDs: the batched 8B layer placed in 4.5 ms against 2.4 ms in
+// column order (loading up to eight batches of 64 words at once, instead of
+// one, made no difference in column order).
 __global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restrict__ tasks, uint32_t n_tasks,
                                                       bs_ref_task single, uint32_t n_tiles, uint8_t* __restrict__ work,
                                                       uint64_t work_bytes, int32_t* __restrict__ status) {
@@ -690,9 +687,9 @@ __global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restr
   if (local >= T.n_streams * tps) return;
   const uint32_t t = local / T.n_streams, k = local % T.n_streams;
   const uint64_t n = T.n_out;
-  const uint8_t* __restrict__ mant = work + T.work_offset;
+  const uint8_t* mant = work + T.work_offset;
   const uint32_t* first = (const uint32_t*)(mant + ((n + 255) & ~255ull));
-  uint16_t* __restrict__ out = T.out;
+  uint16_t* out = T.out;
   const bs_se_stream S = T.streams[k];
   if (!stream_ok(S, (uint64_t)tps * kTile, n)) return;     // reported by serial_kernel
   const uint64_t kt = (uint64_t)k * tps + t;               // the scan's (stream, tile) order
@@ -701,41 +698,29 @@ __global__ __launch_bounds__(kWave) void place_kernel(const bs_ref_task* __restr
   const uint32_t lo = t * kTile, hi = (uint32_t)min((uint64_t)S.n, (uint64_t)lo + kTile);
   const uint64_t lt = (1ull << lane) - 1ull;
   bool bad = false;
-  for (uint32_t k0 = lo; k0 < hi; k0 += kPlaceU * kWave) {
-    uint32_t word[kPlaceU], pos[kPlaceU], mb[kPlaceU];
+  for (uint32_t k0 = lo; k0 < hi; k0 += kWave) {
+    const uint32_t i = k0 + lane;
+    const bool valid = i < hi;
+    const uint64_t el = S.first + (uint64_t)i * S.stride;
+    const uint32_t word = valid ? out[el] : 0u;
+    const uint32_t e = (word >> 7) & 0xFFu;
+    uint64_t m = __ballot(valid);
 #pragma unroll
-    for (uint32_t u = 0; u < kPlaceU; ++u) {
-      const uint32_t i = k0 + u * kWave + lane;
-      word[u] = i < hi ? out[S.first + (uint64_t)i * S.stride] : 0u;
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (e >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
     }
-#pragma unroll
-    for (uint32_t u = 0; u < kPlaceU; ++u) {
-      const bool valid = k0 + u * kWave + lane < hi;
-      const uint32_t e = (word[u] >> 7) & 0xFFu;
-      uint64_t m = __ballot(valid);
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const bool bit = (e >> b) & 1u;
-        const uint64_t bb = __ballot(bit);
-        m &= bit ? bb : ~bb;
-      }
-      const uint32_t rank = (uint32_t)__popcll(m & lt), total = (uint32_t)__popcll(m);
-      const uint32_t base = cnt[e];
-      wave_sync();
-      if (valid && rank == 0) cnt[e] = base + total;
-      wave_sync();
-      pos[u] = valid ? base + rank : 0xFFFFFFFFu;          // none for the lanes past the tile
+    const uint32_t rank = (uint32_t)__popcll(m & lt), total = (uint32_t)__popcll(m);
+    const uint32_t base = cnt[e];
+    wave_sync();
+    if (valid && rank == 0) cnt[e] = base + total;
+    if (valid) {
+      const uint32_t p = base + rank;
+      if (p < n) out[el] = (uint16_t)(word | mant[p]);
+      else bad = true;
     }
-#pragma unroll
-    for (uint32_t u = 0; u < kPlaceU; ++u) mb[u] = pos[u] < n ? mant[pos[u]] : 0u;
-#pragma unroll
-    for (uint32_t u = 0; u < kPlaceU; ++u) {
-      const uint32_t i = k0 + u * kWave + lane;
-      if (i < hi) {
-        if (pos[u] < n) out[S.first + (uint64_t)i * S.stride] = (uint16_t)(word[u] | mb[u]);
-        else bad = true;
-      }
-    }
+    wave_sync();
   }
   if (__ballot(bad) != 0 && lane == 0) flag(status, BS_DEV_ERR_COUNT);
 }
