@@ -23,7 +23,14 @@ enable_a5 / enable_fp2_residual switches.
 
 Differences, by construction of this engine: the default candidates are the
 GPU-native formats (bf16_chunked_v1 / fp8_chunked_v1), and the last resort is
-`raw` instead of zstd. The reference formats it writes (bf16_parallel_v1,
+`raw` instead of zstd. One rule of its own: bf16_chunked_tans_v1, listed after
+bf16_chunked_v1 (as in the default bf16 list), competes only against a
+bf16_chunked_v1 winner in compact plane mode (a tensor of mostly exact values,
+such as a pruned one), and wins when it is at most compact_tans_tolerance (1 %)
+larger: compact chunks decode 10-23 % faster under tANS (a half-pruned 8B
+layer: 0.151 against 0.185 ms, for 0.35 % more bytes). Elsewhere it is not
+encoded (dense tensors decode at the same speed under either coder, and rANS
+is smaller). A candidate list without it forces rANS, one with only it tANS. The reference formats it writes (bf16_parallel_v1,
 bf16_se_tans, bf16_se_single_kernel) are byte-identical to the reference
 encoder's.
 
@@ -103,7 +110,7 @@ register_codec("zstd", _enc_zstd, _dec_zstd)
 # Per-format ordered candidates. fp32/fp16 have no GPU codec here: they are
 # stored raw (the reference's constriction codecs for them are not available).
 CODEC_CANDIDATES: dict[str, list[str]] = {
-    "bf16": [bf16_chunked.CODEC_BF16],
+    "bf16": [bf16_chunked.CODEC_BF16, bf16_chunked.CODEC_BF16_TANS],
     "fp8": [bf16_chunked.CODEC_FP8],
     "fp32": ["raw"],
     "fp16": ["raw"],
@@ -128,14 +135,23 @@ def auto_select_codec(raw: bytes, fmt: str, dtype: str, tensor_name: str = "", s
                       item_bytes: int = 0, enable_a5: bool = True, enable_fp2_residual: bool = True,
                       enable_gpu_parallel: bool = False, gpu_parallel_n_streams: int = 128,
                       gpu_parallel_tolerance: float = 0.01, prefer_speed: bool = False,
-                      prefer_speed_tolerance: float = 0.0015, **_ignored) -> tuple[bytes, str, dict]:
-    """(blob, codec name, extras) chosen by the reference's rules (codec_registry.py:210-398)."""
+                      prefer_speed_tolerance: float = 0.0015, compact_tans_tolerance: float = 0.01,
+                      **_ignored) -> tuple[bytes, str, dict]:
+    """(blob, codec name, extras) chosen by the reference's rules (codec_registry.py:210-398),
+    plus this engine's compact-tANS rule (module docstring)."""
     candidates = CODEC_CANDIDATES.get(fmt, ["raw"])
     best: Optional[tuple[bytes, str, dict]] = None
     for name in candidates:
         if name == "bf16_sparsity_v1" and not enable_a5:
             continue
         if name == "fp2_residual_v1" and not enable_fp2_residual:
+            continue
+        if name == bf16_chunked.CODEC_BF16_TANS and best is not None and best[1] == bf16_chunked.CODEC_BF16:
+            # the compact-tANS rule (module docstring)
+            if bf16_chunked.info(best[0]).plane_mode == bf16_chunked.MODE_COMPACT:
+                got = _try(name, raw)
+                if got is not None and len(got[0]) <= len(best[0]) * (1.0 + compact_tans_tolerance):
+                    best = (got[0], name, got[1])
             continue
         got = _try(name, raw)
         if got is not None and (best is None or len(got[0]) < len(best[0])):

@@ -174,3 +174,49 @@ def test_compress_gpu_optimised_writes_reference_formats(tmp_path):
                "bf16_se_single_kernel": oracle.sk_decode, "bf16_chunked_v1": oracle.chunk_decode}[t["codec"]]
         want = src[t["name"]].view(torch.int16).numpy().tobytes()
         assert dec(blob, 2048 * 2048) == want
+
+
+def _sparse(n, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    y = (torch.randn(n, generator=g) * 0.02).bfloat16()
+    y[torch.randperm(n, generator=g)[: n // 2]] = 0
+    return y.view(torch.uint8).numpy().tobytes()
+
+
+def test_compact_tensors_take_the_table_ans_form(candidates):
+    """The engine's compact-tANS rule: with bf16_chunked_tans_v1 after
+    bf16_chunked_v1 in the list (the default), a compact-mode rANS winner
+    yields to the tANS blob when that is at most compact_tans_tolerance
+    larger; a dense winner is kept without encoding tANS; a list without the
+    tANS codec forces rANS, one with only it forces tANS."""
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    raw = _sparse(4_000_000)
+    rans = codec_registry.get_codec(bc.CODEC_BF16)[0](raw)[0]
+    tans = codec_registry.get_codec(bc.CODEC_BF16_TANS)[0](raw)[0]
+    assert bc.info(rans).plane_mode == bc.MODE_COMPACT and len(rans) < len(tans) <= len(rans) * 1.01
+    assert candidates["bf16"] == [bc.CODEC_BF16, bc.CODEC_BF16_TANS]
+    blob, codec, _ = codec_registry.auto_select_codec(raw, "bf16", "BF16")
+    assert codec == bc.CODEC_BF16_TANS and blob == tans
+    # the tolerance boundary: half a byte above the size difference admits it, half a byte below does not
+    d = len(tans) - len(rans)
+    assert codec_registry.auto_select_codec(raw, "bf16", "BF16",
+                                            compact_tans_tolerance=(d + 0.5) / len(rans))[1] == bc.CODEC_BF16_TANS
+    assert codec_registry.auto_select_codec(raw, "bf16", "BF16",
+                                            compact_tans_tolerance=(d - 0.5) / len(rans))[1] == bc.CODEC_BF16
+    candidates["bf16"] = [bc.CODEC_BF16]
+    assert codec_registry.auto_select_codec(raw, "bf16", "BF16")[1] == bc.CODEC_BF16
+    candidates["bf16"] = [bc.CODEC_BF16_TANS]
+    assert codec_registry.auto_select_codec(raw, "bf16", "BF16")[1] == bc.CODEC_BF16_TANS
+
+
+def test_dense_and_small_compact_tensors_keep_rans(candidates, monkeypatch):
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    calls = []
+    enc = codec_registry.get_codec(bc.CODEC_BF16_TANS)
+    monkeypatch.setitem(codec_registry._REGISTRY, bc.CODEC_BF16_TANS,
+                        (lambda raw, **ctx: calls.append(1) or enc[0](raw, **ctx), enc[1]))
+    assert codec_registry.auto_select_codec(_raw(2_000_000), "bf16", "BF16")[1] == bc.CODEC_BF16
+    assert not calls                         # a dense winner: the tANS form is not encoded
+    # a small compact tensor: the stored 16 KB decode table puts tANS more than 1 % above
+    assert codec_registry.auto_select_codec(_sparse(300_000), "bf16", "BF16")[1] == bc.CODEC_BF16
+    assert calls
