@@ -135,6 +135,41 @@ def test_mixed_reference_formats_and_misaligned_blobs(tmp_path):
                 assert t.view(torch.int16).cpu().numpy().view(np.uint16).tobytes() == src[k].tobytes()
 
 
+def test_pruned_tensors_written_as_table_ans_load_bit_exact(tmp_path):
+    """compress() gives a large half-pruned tensor the table-ANS form
+    (auto-selection's compact-tANS rule) and a dense one rANS; both come back
+    bit-exact through decoder.load (one batched launch per layer group, both
+    coders in it), decompress, verify and the streaming loader."""
+    from bigsmall_amd import decoder
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.streaming import StreamingLoader
+    from bigsmall_amd.verify import verify
+    g = torch.Generator().manual_seed(31)
+    pruned = (torch.randn(4096, 1024, generator=g) * 0.02).bfloat16()
+    pruned.view(-1)[torch.randperm(pruned.numel(), generator=g)[: pruned.numel() // 2]] = 0
+    src = {"model.layers.0.mlp.down_proj.weight": pruned,
+           "model.layers.0.self_attn.q_proj.weight": (torch.randn(1024, 1024, generator=g) * 0.02).bfloat16(),
+           "model.layers.1.mlp.down_proj.weight": pruned.flip(0).contiguous()}
+    p = tmp_path / "pruned.bs"
+    _say("[api] compress a pruned layer")
+    compress(src, p)
+    header, _ = container.read_header(p)
+    codecs = {t["name"]: t["codec"] for t in header["tensors"]}
+    assert codecs["model.layers.0.mlp.down_proj.weight"] == bc.CODEC_BF16_TANS
+    assert codecs["model.layers.1.mlp.down_proj.weight"] == bc.CODEC_BF16_TANS
+    assert codecs["model.layers.0.self_attn.q_proj.weight"] == bc.CODEC_BF16
+    _say("[api] load / decompress / verify the pruned layer")
+    dev = decoder.load(p, device="cuda")
+    assert all(_bytes(dev[k]) == _bytes(v) for k, v in src.items())
+    host = decoder.decompress(p)
+    assert all(host[k].tobytes() == _bytes(v) for k, v in src.items())
+    assert verify(p)
+    with StreamingLoader(p, device="cuda", prefetch=1) as L:
+        for li, layer in L.iter_layers():
+            for k, t in layer.items():
+                assert _bytes(t) == _bytes(src[k]), k
+
+
 @pytest.mark.parametrize("prefetch", [0, 1, 2])
 def test_streaming_loader(model_file, prefetch):
     from bigsmall_amd.streaming import StreamingLoader

@@ -169,6 +169,49 @@ def test_serial_batch_mixed_formats(gpu):
         assert _decode(c, b, w.size) == w.tobytes(), c
 
 
+def test_serial_batch_with_shared_xcd_bins(gpu):
+    """Twelve tensors in one batch: more than the eight XCD bins, so bins hold
+    several tensors and only the first of each reads its SE table through the
+    scalar cache (the others from LDS). The layout obeys the bins (every
+    task's SE groups inside one bin, the task array ascending, the grid 8C
+    groups) and every output equals its source."""
+    from bigsmall_amd.codecs import _refstreams
+    from bigsmall_amd.device import StatusWord, upload_bytes
+    torch = gpu
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(23)
+    kinds = ["bf16_parallel_v1", "bf16_se_tans", "bf16_se_single_kernel"]
+    srcs = [(kinds[i % 3], _bf16(rng.standard_normal(int(rng.integers(70_000, 260_000))) * 0.02))
+            for i in range(12)]
+    blobs = [CODECS[c][0](w) for c, w in srcs]
+    d_blobs = [upload_bytes(b, dev) for b in blobs]
+    outs = [torch.empty(w.size, dtype=torch.int16, device=dev) for _, w in srcs]
+    items = [(_refstreams.PARSERS[c](b, w.size), d.data_ptr(), o.data_ptr())
+             for (c, w), b, d, o in zip(srcs, blobs, d_blobs, outs)]
+    batch = _refstreams.RefBatch(items, dev)
+    off = batch.p_tasks - batch.dev.data_ptr()
+    n = len(items)
+    tasks = batch.dev[off:off + n * _refstreams.REF_TASK_DTYPE.itemsize].cpu().numpy().view(_refstreams.REF_TASK_DTYPE)
+    C = batch.totals[0] // _refstreams.XCD_BINS
+    per = 4
+    begins = tasks["se_group_begin"].astype(np.int64)
+    assert batch.totals[0] == _refstreams.XCD_BINS * C and np.all(np.diff(begins) > 0)
+    for t in tasks:
+        g = -(-int(t["n_streams"]) // per)
+        assert int(t["se_group_begin"]) // C == (int(t["se_group_begin"]) + g - 1) // C
+    bins = begins // C
+    scalar = (tasks["flags"] & _refstreams.FLAG_SE_SCALAR) != 0
+    assert len(set(bins.tolist())) == _refstreams.XCD_BINS      # every bin used
+    assert all(scalar[bins == b].sum() <= 1 for b in set(bins.tolist()))
+    st = StatusWord(dev)
+    _say(f"[ref] serial batch of {n} tensors in shared bins, totals {batch.totals}, scalar {int(scalar.sum())}")
+    batch.launch(st.ptr, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    st.check("serial batch, shared bins")
+    for (c, w), o in zip(srcs, outs):
+        assert o.cpu().numpy().view(np.uint16).tobytes() == w.tobytes(), (c, w.size)
+
+
 def test_serial_batch_rejects_inconsistent_task(gpu):
     """A task whose scratch lies outside the work buffer, or whose element
     count is zero, is reported (BS_DEV_ERR_HEADER) and skipped by every kernel
