@@ -81,7 +81,8 @@
 //   tANS dense: one word {newX:12, nb:4, exponent word (e << 7):16};
 //   tANS pairs: one word {newX:12, nb:4, e0 << 3 | e1 << 11:16};
 //   tANS bytes: one word {newX:12, nb:4, -:8, byte:8};
-//   tANS generic: {newX | nb << 12 | (nb + raw) << 16 | raw << 21, value | consume << 31}.
+//   tANS generic: {newX | nb << 12 | mask << 16, nt | value << 16}: nt = nb + raw bits, and
+//     mask = 0x807F for a compact-mode symbol that takes a plane byte (raw = 8), else 0.
 #include <stdint.h>
 
 #include "simt.h"
@@ -470,12 +471,17 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 
 // One tANS step of the K states of every lane. Table entries: FAST (dense
 // bf16, bytes, exponent pairs) {newX:12, nb:4, -:8, output byte:8}, 4 bytes;
-// otherwise {lo: newX:12, nb:4, nb + raw:5, raw:4; hi: value | consume << 31},
-// 8 bytes, raw = 8 for a compact-mode symbol that takes a plane byte. Each
-// lane reads its states' bits in order (state bits, then raw plane bits) from
-// one stream position per lane: the wavefront prefix sum of the lanes' bit
-// counts. newX has nb low zero bits, so X = newX | bits. d as for rans_step
-// (the generic layout's value with its plane byte merged).
+// otherwise {lo: newX:12, nb:4, mask:16; hi: nt:5, -:11, value:16}, 8 bytes,
+// nt = nb + raw with raw = 8 for a compact-mode symbol that takes a plane
+// byte, whose mask is then 0x807F (else 0). Each lane reads its states' bits
+// in order (state bits, then raw plane bits) from one stream position per
+// lane: the wavefront prefix sum of the lanes' bit counts. newX has nb low
+// zero bits, so X = newX | bits. d as for rans_step for FAST; for the generic
+// layout the output word is d's high half: (8 bits after the state bits,
+// duplicated into bytes 2 and 3) & lo | hi, which leaves the value alone when
+// the mask is 0 and merges the plane byte's sign and mantissa when it is
+// 0x807F, with no step spent on the raw count (hi's nt, in bits 0..4, is the
+// alignbit shift as it stands).
 template <int K, int MODE, bool FAST, bool PARTIAL>
 __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C, const LDS void* tbl,
                                           const LDS uint32_t* ring, uint32_t (&d)[K]) {
@@ -493,7 +499,7 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
       hv[g] = (uint32_t)(v >> 32);
     }
     nb[g] = __builtin_amdgcn_ubfe(e[g], 12, 4);
-    nt[g] = FAST ? nb[g] : __builtin_amdgcn_ubfe(e[g], 16, 5);
+    nt[g] = FAST ? nb[g] : __builtin_amdgcn_ubfe(hv[g], 0, 5);
     act[g] = true;
     if (PARTIAL) {
       act[g] = t * (kWave * K) + C.lane * K + g < C.nc;
@@ -532,16 +538,21 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
         // bits 32..63 from `pos` come from the third word (w + 2 <= 1025:
         // inside the ring's mirrored head)
         const uint32_t hi = __builtin_amdgcn_alignbit(ring[w + 2], r1, pos);
-        win[1] = __builtin_amdgcn_alignbit(hi, lo, nt[g]);   // nt <= 20: from bit nt[g] on
+        // from bit nt[g] on (nt <= 20): alignbit shifts by its operand's low 5 bits, hv's nt
+        win[1] = __builtin_amdgcn_alignbit(hi, lo, hv[g]);
       }
 #pragma unroll
       for (int h = 0; h < (two ? 2 : 1); ++h) {
         const int gg = g + h;
         const uint32_t x = (e[gg] & 0xFFFu) | __builtin_amdgcn_ubfe(win[h], 0, nb[gg]);
         S.x[gg] = PARTIAL && !act[gg] ? S.x[gg] : x;
-        // the plane byte follows the state bits; a symbol without one reads 0 bits
-        d[gg] = MODE == 2 ? byte_merge(hv[gg], __builtin_amdgcn_ubfe(win[h], nb[gg], __builtin_amdgcn_ubfe(e[gg], 21, 4)))
-                          : hv[gg];
+        // the plane byte follows the state bits; the mask drops it for a symbol without one
+        if (MODE == 2) {
+          const uint32_t b = __builtin_amdgcn_ubfe(win[h], nb[gg], 8);
+          d[gg] = (__builtin_amdgcn_perm(0u, b, 0x00000C0Cu) & e[gg]) | hv[gg];
+        } else {
+          d[gg] = hv[gg];
+        }
       }
       if (g + 2 < K) pos += nt[g] + (two ? nt[g + 1] : 0u);
     }
@@ -738,21 +749,24 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
         *(LDS uint16_t*)(stage + qs * (kStates * 2) + lane * 2u) = (uint16_t)v;
       }
     } else {
-      // the lane's K outputs of this step are adjacent: one LDS store
+      // the lane's K outputs of this step are adjacent: one LDS store. The
+      // generic tANS layout leaves each output word in d's high half
+      constexpr uint32_t kW = CODER == 1 ? 0x07060302u : 0x05040100u;
+      constexpr uint32_t kW1 = CODER == 1 ? 16u : 0u;
       LDS uint8_t* dst = stage + (qs * kStates + lane * K) * EB;
       if (DIRECT && EB == 2) {
-        store_step<K, kBlock, EB>(C, blk, q, __builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u),
-                                  __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u));
+        store_step<K, kBlock, EB>(C, blk, q, __builtin_amdgcn_perm(d[1 % K], d[0], kW),
+                                  __builtin_amdgcn_perm(d[3 % K], d[2 % K], kW));
       } else if (DIRECT) {                               // bytes: K = 2 in one half word, K = 4 in one word
         store_step<K, kBlock, EB>(C, blk, q,
                                   __builtin_amdgcn_perm(d[1 % K], d[0], 0x0C0C0703u) |
                                       (K == 4 ? __builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x0C0C0703u) << 16 : 0u),
                                   0u);
       } else if (EB == 2) {
-        if (K == 1) *(LDS uint16_t*)dst = (uint16_t)d[0];
-        else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], 0x05040100u);
-        else *(LDS uint64_t*)dst = (uint64_t)__builtin_amdgcn_perm(d[1 % K], d[0], 0x05040100u) |
-                                   ((uint64_t)__builtin_amdgcn_perm(d[3 % K], d[2 % K], 0x05040100u) << 32);
+        if (K == 1) *(LDS uint16_t*)dst = (uint16_t)(d[0] >> kW1);
+        else if (K == 2) *(LDS uint32_t*)dst = __builtin_amdgcn_perm(d[K - 1], d[0], kW);
+        else *(LDS uint64_t*)dst = (uint64_t)__builtin_amdgcn_perm(d[1 % K], d[0], kW) |
+                                   ((uint64_t)__builtin_amdgcn_perm(d[3 % K], d[2 % K], kW) << 32);
       } else {                                           // byte values in bits 24..31 of d
         if (K == 1) *dst = (uint8_t)(d[0] >> 24);
         else if (K == 2) *(LDS uint16_t*)dst = (uint16_t)__builtin_amdgcn_perm(d[K - 1], d[0], 0x0C0C0703u);
@@ -1169,8 +1183,8 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     // symbol of the tensor, nb <= 12, newX + 2^nb <= 4096 with nb zero low
     // bits, so every next state stays in the table) and laid out for the
     // step: one word {newX, nb, output bits} for dense bf16, bytes and
-    // pairs (layouts in the file comment); else two, {newX, nb, nb + raw,
-    // raw} and the value with its plane flag (raw = 8 plane bits for a
+    // pairs (layouts in the file comment); else two, {newX, nb, plane-byte
+    // mask} and {nb + raw, value} (raw = 8 plane bits, mask 0x807F, for a
     // compact symbol that has one)
     const uint32_t slot0 = tid * kRun;
     bool bad = false;
@@ -1183,12 +1197,13 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
       const uint32_t rw = mode == 2 && (v >> 31) ? 8u : 0u;
       // dense: the symbol's word (exponent in place) in bits 16..31; pairs:
       // e0 << 3 | e1 << 11 (both exponent fields in place); bytes: the byte
-      // in bits 24..31
+      // in bits 24..31; generic: the plane-byte mask in bits 16..31, and a
+      // second word of the bit count and the value
       lo[k] = dense       ? (e & 0xFFFFu) | ((v & 0x7F80u) << 16)
               : mode == 3 ? (e & 0xFFFFu) | (((v & 0xFu) << 19) | ((v & 0xF0u) << 23))
               : fast      ? (e & 0xFFFFu) | ((v & 0xFFu) << 24)
-                          : (e & 0xFFFFu) | ((nb + rw) << 16) | (rw << 21);
-      hi[k] = v;
+                          : (e & 0xFFFFu) | (rw ? 0x807F0000u : 0u);
+      hi[k] = (nb + rw) | (v << 16);
     }
     if (fast) {
       LDS uint32_t* t32 = (LDS uint32_t*)s_tbl + slot0;
