@@ -123,11 +123,17 @@ constexpr uint64_t kMaxChunk = 1ull << 24;
 // s_waitcnt immediate for gfx9: vmcnt(n), expcnt and lgkmcnt not waited on
 // (vmcnt bits 3:0 and 15:14, expcnt bits 6:4, lgkmcnt bits 11:8)
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-// dynamic LDS layout (bytes): decode table | per-wave ring areas | per-wave output staging
+// dynamic LDS layout (bytes): per-wave ring areas | decode table | per-wave
+// output staging. The rings come first, so a wave's ring starts at one
+// wave-uniform offset (wave * kRingBytes) and a ring read's address is that
+// plus the word offset, one instruction; the table's fixed offset fits the
+// immediate offset field of its reads.
 constexpr uint32_t kTblBytes = 4096 * 8;
+constexpr uint32_t kTblOff = kWaves * kRingBytes;
 constexpr uint32_t kStageMax = 1024;      // per wave: half a block of bf16 outputs (512 elements)
+static_assert(kTblOff % 16 == 0 && kTblOff <= 65535, "table offset in a ds_read immediate");
 // each wave's progress in block pairs (u16 per wave), read by the others
-constexpr uint32_t kProgOff = kTblBytes + kWaves * (kRingBytes + kStageMax);
+constexpr uint32_t kProgOff = kTblOff + kTblBytes + kWaves * kStageMax;
 // a workgroup-wide flag set by any thread whose run of a tANS table fails its check
 constexpr uint32_t kFlagOff = kProgOff + ((2 * kWaves + 15) & ~15u);
 constexpr uint32_t kLds = kFlagOff + 16;           // 75424: two workgroups per CU
@@ -232,7 +238,7 @@ __device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t v) {
 // wave's word ring seen as 1,024 u32 words: two ring words, the second
 // covered by the ring's mirrored head when the first is the last.
 __device__ __forceinline__ uint32_t stream_bits(const LDS uint32_t* ring, uint32_t pos) {
-  const uint32_t w = (pos >> 5) & 1023u;
+  const uint32_t w = __builtin_amdgcn_ubfe(pos, 5, 10);   // (pos >> 5) & 1023: the address is then one lshl_add
   return __builtin_amdgcn_alignbit(ring[w + 1], ring[w], pos);   // shifts by pos mod 32
 }
 
@@ -530,7 +536,7 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
         if (g + 2 < K) pos += nb[g] + nb[g + 1];
       }
     } else {
-      const uint32_t w = (pos >> 5) & 1023u;
+      const uint32_t w = __builtin_amdgcn_ubfe(pos, 5, 10);
       const uint32_t r0 = ring[w], r1 = ring[w + 1];
       const uint32_t lo = __builtin_amdgcn_alignbit(r1, r0, pos);
       uint32_t win[2] = {lo, lo};
@@ -870,7 +876,7 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   BS_KEEP2(F.w[0].x, F.w[1].x);
   if (RM == 2) BS_KEEP2(F.p[0].x, F.p[1].x);
 
-  LDS uint16_t* prog = (LDS uint16_t*)((LDS uint8_t*)tbl + kProgOff);   // kWaves entries
+  LDS uint16_t* prog = (LDS uint16_t*)((LDS uint8_t*)tbl + (kProgOff - kTblOff));   // kWaves entries
   const uint32_t pwave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   for (uint32_t blk = 0;;) {
     {
@@ -998,9 +1004,9 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
                                                                uint32_t n_tasks, bs_chunk_task single,
                                                                int32_t* __restrict__ status, uint32_t first_round) {
   BS_DYNAMIC_LDS(smem);
-  LDS uint64_t* s_tbl = (LDS uint64_t*)smem;
-  LDS uint8_t* s_wring = (LDS uint8_t*)(smem + kTblBytes);
-  LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblBytes + kWaves * kRingBytes);
+  LDS uint64_t* s_tbl = (LDS uint64_t*)(smem + kTblOff);
+  LDS uint8_t* s_wring = (LDS uint8_t*)smem;
+  LDS uint8_t* s_stage = (LDS uint8_t*)(smem + kTblOff + kTblBytes);
   // table-build scratch overlaps the staging area (unused until decoding starts)
   LDS uint32_t* s_cum = (LDS uint32_t*)s_stage + 3;    // 257 entries; s_cum + 1 is 16-byte aligned
   LDS uint32_t* s_val = s_cum + 257;                    // 256 entries, 16-byte aligned
@@ -1246,7 +1252,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   }
   // progress entries (decode_chunk): 0 for a wave with a chunk, 0xFFFF for one without
   // (and for one that leaves on an error below)
-  if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
+  if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)smem + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
   lds_barrier();
   if (coder && *(volatile LDS uint32_t*)(smem + kFlagOff)) {   // the same value for every thread
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
@@ -1274,7 +1280,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   if (mode == 0) ok = ok && np == 0;
   if (!ok) {
     report(status, BS_DEV_ERR_BOUNDS);
-    if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)s_tbl + kProgOff + 2 * wave) = 0xFFFFu;
+    if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)smem + kProgOff + 2 * wave) = 0xFFFFu;
     return;
   }
   const GLB uint8_t* cbase = b + off;
