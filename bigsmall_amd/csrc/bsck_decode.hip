@@ -238,7 +238,8 @@ __device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t v) {
 // wave's word ring seen as 1,024 u32 words: two ring words, the second
 // covered by the ring's mirrored head when the first is the last.
 __device__ __forceinline__ uint32_t stream_bits(const LDS uint32_t* ring, uint32_t pos) {
-  const uint32_t w = __builtin_amdgcn_ubfe(pos, 5, 10);   // (pos >> 5) & 1023: the address is then one lshl_add
+  uint32_t w;
+  BS_BFE_U32(w, pos, 5, 10);                            // (pos >> 5) & 1023: the address is then one lshl_add
   return __builtin_amdgcn_alignbit(ring[w + 1], ring[w], pos);   // shifts by pos mod 32
 }
 
@@ -505,7 +506,11 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
       hv[g] = (uint32_t)(v >> 32);
     }
     nb[g] = __builtin_amdgcn_ubfe(e[g], 12, 4);
-    nt[g] = FAST ? nb[g] : __builtin_amdgcn_ubfe(hv[g], 0, 5);
+    // generic layout: hv itself, whose low half is nt (bits 0..4) and whose
+    // high half the value: a lane's sum of at most 4 x 20 bits, and the
+    // wavefront's of at most 5,120, never carry into bit 16, so the sums' low
+    // halves are the bit counts and their high halves are ignored
+    nt[g] = FAST ? nb[g] : hv[g];
     act[g] = true;
     if (PARTIAL) {
       act[g] = t * (kWave * K) + C.lane * K + g < C.nc;
@@ -514,8 +519,11 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
     tot += nt[g];
   }
   const uint32_t incl = wave_prefix_sum(tot);
-  uint32_t pos = S.bpos + incl - tot;                  // this lane's first bit
-  S.bpos += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+  // this lane's first bit; generic layout: exact in bits 0..15, of which the
+  // step reads bits 0..14 (the ring word, 1024 words, and the shift), the
+  // high half carrying the values' sums
+  uint32_t pos = S.bpos + incl - tot;
+  S.bpos += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1) & (FAST ? 0xFFFFFFFFu : 0xFFFFu);
   S.wptr = (S.bpos >> 5) << 1;                          // ring words no longer needed: [.., wptr)
   // The lane's states are read in pairs: a one-word-layout pair takes at most
   // 2 x 12 bits (one 32-bit window), a generic pair at most 2 x 20 (a 64-bit
@@ -536,7 +544,8 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
         if (g + 2 < K) pos += nb[g] + nb[g + 1];
       }
     } else {
-      const uint32_t w = __builtin_amdgcn_ubfe(pos, 5, 10);
+      uint32_t w;
+      BS_BFE_U32(w, pos, 5, 10);
       const uint32_t r0 = ring[w], r1 = ring[w + 1];
       const uint32_t lo = __builtin_amdgcn_alignbit(r1, r0, pos);
       uint32_t win[2] = {lo, lo};

@@ -18,6 +18,7 @@
 #define BS_OPAQUE(x) ((void)(x))
 #define BS_WRITELANE_I(acc, v, j) ((acc) = __lane_id() == (uint32_t)(j) ? (uint32_t)(v) : (acc))
 #define BS_LDS_ADD(p, v) ((void)atomicAdd((p), (v)))
+#define BS_BFE_U32(dst, x, off, width) ((dst) = ((uint32_t)(x) >> (off)) & ((1u << (width)) - 1u))
 #else
 #include <hip/hip_runtime.h>
 #define LDS __attribute__((address_space(3)))
@@ -37,6 +38,11 @@
 // v_writelane_b32; v in a scalar register); j must be a constant once the
 // caller's loop is unrolled (a compile error otherwise).
 #define BS_WRITELANE_I(acc, v, j) asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(acc) : "s"(v), "i"(j))
+// dst = bits [off, off + width) of x in one v_bfe_u32 the optimiser cannot
+// rewrite (it turns a field extract followed by a scale into a shift and a
+// mask; kept whole, an LDS address from it is one v_lshl_add). off and width
+// are literal constants.
+#define BS_BFE_U32(dst, x, off, width) asm("v_bfe_u32 %0, %1, " #off ", " #width : "=v"(dst) : "v"(x))
 // Atomic add to a 32-bit LDS word (ds_add_u32), ordered only within the wave.
 #define BS_LDS_ADD(p, v) ((void)__hip_atomic_fetch_add((p), (v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT))
 #endif
