@@ -1189,6 +1189,16 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   lds_barrier();
   const uint64_t off = (uint64_t)rfl(centry.x) | ((uint64_t)rfl(centry.y) << 32);
   const uint32_t nw = rfl(centry.z), np = rfl(centry.w);
+  // Warm the chunk's first 2 KB (its initial states and first ring words) while
+  // the table is built: decode_chunk's own loads of them come after the next
+  // barrier and then hit L2 instead of waiting on HBM, which every workgroup of
+  // a launch's first round reaches at once. Only inside the blob (a uniform
+  // test); the values are dropped.
+  u32x4 warm0 = {0u, 0u, 0u, 0u}, warm1 = {0u, 0u, 0u, 0u};
+  if (chunk < nch && (off & 15u) == 0 && off + 2048u <= T.blob_bytes) {
+    warm0 = *(const GLB u32x4*)(b + off + 16u * lane);
+    warm1 = *(const GLB u32x4*)(b + off + 1024u + 16u * lane);
+  }
   if (*s_flag) {                                  // the same value for every thread
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
     return;
@@ -1262,6 +1272,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   // progress entries (decode_chunk): 0 for a wave with a chunk, 0xFFFF for one without
   // (and for one that leaves on an error below)
   if ((tid & (kWave - 1)) == 0) *(volatile LDS uint16_t*)((LDS uint8_t*)smem + kProgOff + 2 * wave) = chunk < nch ? 0u : 0xFFFFu;
+  BS_KEEP2(warm0.x, warm1.x);                           // landed long ago: the table build took longer
   lds_barrier();
   if (coder && *(volatile LDS uint32_t*)(smem + kFlagOff)) {   // the same value for every thread
     if (tid == 0) atomicOr(status, BS_DEV_ERR_HEADER);
