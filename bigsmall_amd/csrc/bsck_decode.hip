@@ -167,10 +167,6 @@ struct Geo {
   static_assert(kHalf || (kRing + kMirror) * 2 <= kRingBytes, "word ring exceeds the ring area");
 };
 
-__device__ __forceinline__ uint32_t ld_u32(const GLB uint8_t* p) {
-  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
-}
-
 // rank of this lane among the set lanes of m
 __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
