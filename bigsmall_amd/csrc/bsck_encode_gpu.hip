@@ -6,7 +6,8 @@
 //
 // A batch of tensors ("tasks") is encoded by six launches on one stream:
 //   clear     zero the per-task exponent histograms;
-//   hist      per chunk: exponent histogram (LDS), added into its task's;
+//   hist      per chunk: exponent histogram (16 interleaved copies in LDS),
+//             added into its task's;
 //   plan      per task (one wavefront): symbols = exponents present, in
 //             ascending order; frequencies by the quantiser of bsck_encode.cpp
 //             (rounding, then greedy +-1 corrections, the argmax taken across
@@ -16,13 +17,13 @@
 //             the decoder renormalises after each decode; renorm words of a
 //             (step, state group) are placed by ballot rank so the decoder
 //             reads them lane-ascending; words go to the chunk's scratch from
-//             its end backwards, final states to its head;
+//             its end backwards, final states to its head; a full chunk also
+//             stores its dense sign|mantissa plane in the plane region
+//             (interleaved per block), from the words it loads to encode;
 //   layout    per task: chunk offsets (prefix sum of chunk sizes), chunk table,
 //             blob length (or a capacity error);
 //   assemble  per chunk: states and renorm words at the chunk's offset in
-//             the blob, the dense sign|mantissa plane in the plane region
-//             (full chunks, interleaved per block) or after the words (the
-//             partial chunk).
+//             the blob; the partial chunk's plane after its words.
 // Chunk k's elements follow the layout's interleave: a full chunk (k < nf)
 // takes 512-element units k, nf + k, 2nf + k, ...; the partial chunk the tail.
 #include <hip/hip_runtime.h>
@@ -111,22 +112,45 @@ __global__ __launch_bounds__(256) void enc_clear_kernel(uint8_t* __restrict__ pl
   if (threadIdx.x == 0) { P->nsym = 0; P->ok = 0; }
 }
 
+// Per chunk (256 threads): the exponent histogram of its slice, added into
+// its task's. The slice is read with 16-byte loads (the 0-6 elements before
+// the first 16-byte boundary and the tail one at a time) and counted into 16
+// interleaved copies of the histogram in LDS (bin b, copy c at b * 16 + c;
+// thread t counts into copy t mod 16). Most lanes of a wavefront hit one of a
+// few exponents; with one histogram their LDS adds to a word serialise, here
+// at most 4 lanes of a wavefront share a copy, and the copies of a bin lie in
+// 16 different banks.
 __global__ __launch_bounds__(256) void enc_hist_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
                                                        uint32_t steps, uint8_t* __restrict__ plans) {
-  __shared__ uint32_t h[256];
+  constexpr uint32_t kCopies = 16;
+  __shared__ __attribute__((aligned(16))) uint32_t h[256 * kCopies];
   const uint32_t tid = threadIdx.x, c = blockIdx.x;
   const uint32_t ti = task_of(tasks, n_tasks, c);
   const bs_encode_task T = tasks[ti];
   const uint64_t per = (uint64_t)kLanes * steps;
   if (!task_ok(T, per) || c < T.chunk_begin || c - T.chunk_begin >= T.n_chunks) return;
-  h[tid] = 0;
+  for (uint32_t i = tid; i < 256 * kCopies; i += 256) h[i] = 0;
   __syncthreads();
   const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;   // a contiguous slice: the slices cover the tensor once
   const uint32_t nc = (uint32_t)min(per, T.n - base);
   const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
-  for (uint32_t j = tid; j < nc; j += 256) atomicAdd(&h[(src[j] >> 7) & 0xFFu], 1u);
+  const uint32_t cp = tid & (kCopies - 1);
+  auto count = [&](uint32_t w) { atomicAdd(&h[((w >> 7) & 0xFFu) * kCopies + cp], 1u); };
+  const uint32_t head = min(nc, (uint32_t)(((16u - ((uintptr_t)src & 15u)) & 15u) / 2u));   // src is 4-byte aligned
+  if (tid < head) count(src[tid]);
+  const uint32_t nv = (nc - head) / 8u;
+  const GLB u32x4* vsrc = (const GLB u32x4*)(src + head);
+  for (uint32_t v = tid; v < nv; v += 256) {
+    const u32x4 q = vsrc[v];
+    count(q.x); count(q.x >> 16); count(q.y); count(q.y >> 16);
+    count(q.z); count(q.z >> 16); count(q.w); count(q.w >> 16);
+  }
+  for (uint32_t j = head + 8u * nv + tid; j < nc; j += 256) count(src[j]);
   __syncthreads();
-  if (h[tid]) atomicAdd(&((Plan*)(plans + ti * kPlanBytes))->hist[tid], h[tid]);
+  uint32_t sum = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < kCopies; ++i) sum += h[tid * kCopies + i];
+  if (sum) atomicAdd(&((Plan*)(plans + ti * kPlanBytes))->hist[tid], sum);
 }
 
 // is candidate (c1, d1, i1) better than (c0, d0, i0)? up: larger c/d; down: smaller c/d; ties: lower index.
@@ -273,7 +297,8 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
 __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
                                                           uint32_t steps, const uint8_t* __restrict__ plans,
                                                           ChunkRec* __restrict__ recs, uint8_t* __restrict__ scratch) {
-  __shared__ uint32_t s_sym[256], s_f[256], s_c[256], s_m[256], s_s[256];
+  // per exponent: {f:13, cum:12, s1:1, s2:4} of its symbol, and the divisor's multiplier
+  __shared__ uint32_t s_fc[256], s_m[256];
   const uint32_t lane = threadIdx.x, cg = blockIdx.x;
   const uint32_t ti = task_of(tasks, n_tasks, cg);
   const bs_encode_task T = tasks[ti];
@@ -281,12 +306,26 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   const Plan* P = (const Plan*)(plans + ti * kPlanBytes);
   if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
   for (uint32_t i = lane; i < 256; i += kWave) {
-    s_sym[i] = P->sym_of_exp[i]; s_f[i] = P->freq[i]; s_c[i] = P->cum[i]; s_m[i] = P->rcp[i]; s_s[i] = P->shf[i];
+    const uint32_t sym = P->sym_of_exp[i], shf = P->shf[sym];
+    s_fc[i] = P->freq[sym] | (P->cum[sym] << 13) | ((shf & 1u) << 25) | ((shf >> 8) << 26);
+    s_m[i] = P->rcp[sym];
   }
   __syncthreads();
   const uint64_t k = cg - T.chunk_begin, nf = T.n / per;
   const uint32_t nc = (uint32_t)min(per, T.n - k * per);
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
+  // A full chunk stores its dense plane here, from the words it loads for the
+  // encode: per block of kBlock steps, lane l's 16 bytes hold (q, g) at q*2 + g
+  // for chunk element (blk*kBlock + q)*128 + 2l + g, at block blk*nf + k of
+  // the plane region (which starts after the chunk table, a place the plan
+  // fixes). The partial chunk's plane follows its words, whose count is known
+  // only after the encode: the assemble pass writes that one. A region past
+  // the capacity is not written (the layout pass reports the capacity error).
+  constexpr uint64_t kBlkBytes = (uint64_t)kBlock * kLanes;
+  const uint64_t preg = pad256(pad16(32 + 4ull * P->nsym) + 16ull * T.n_chunks);
+  const bool plane_here = k < nf && preg + nf * per <= T.cap;
+  GLB uint8_t* plane = (GLB uint8_t*)T.dst + preg + k * kBlkBytes + 16u * lane;
+  const uint64_t pstride = nf * kBlkBytes;
   const GLB uint32_t* src2 = (const GLB uint32_t*)T.src;   // two words per lane-step (even elements)
   const GLB uint16_t* src1 = (const GLB uint16_t*)T.src;
   uint8_t* chunk = scratch + (uint64_t)cg * scratch_bytes(steps);
@@ -304,7 +343,7 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   // Steps are encoded last to first in blocks of kPre; the next block's words
   // are loaded while the current block is encoded, so the loads' latency is
   // not on the encode chain.
-  constexpr uint32_t kPre = 8;
+  constexpr uint32_t kPre = kBlock;
   const uint32_t nblk = (nsteps + kPre - 1) / kPre;
   uint32_t cur[kPre];
 #pragma unroll
@@ -313,6 +352,18 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
     uint32_t nxt[kPre];
 #pragma unroll
     for (uint32_t k = 0; k < kPre; ++k) nxt[k] = b > 0 ? load_step((b - 1) * kPre + k) : 0u;
+    if (plane_here) {
+      // sign | mantissa bytes: word pair (q, g = 0, 1) -> bytes 0 and 2, then two steps per word
+      uint32_t pw[kBlock / 2];
+#pragma unroll
+      for (uint32_t i = 0; i < kBlock / 2; ++i) {
+        const uint32_t a = cur[2 * i], c2 = cur[2 * i + 1];
+        const uint32_t pa = (a & 0x007F007Fu) | ((a >> 8) & 0x00800080u);
+        const uint32_t pb = (c2 & 0x007F007Fu) | ((c2 >> 8) & 0x00800080u);
+        pw[i] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+      }
+      *(GLB u32x4*)(plane + (uint64_t)b * pstride) = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
 #pragma unroll
     for (int k = (int)kPre - 1; k >= 0; --k) {
       const uint32_t t = b * kPre + (uint32_t)k;
@@ -322,8 +373,8 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
 #pragma unroll
       for (int g = 1; g >= 0; --g) {
         const bool active = j0 + g < nc;
-        const uint32_t sym = s_sym[(wv[g] >> 7) & 0xFFu];
-        const uint32_t f = s_f[sym], cm = s_c[sym];
+        const uint32_t ex = (wv[g] >> 7) & 0xFFu;
+        const uint32_t fc = s_fc[ex], f = fc & 0x1FFFu, cm = (fc >> 13) & 0xFFFu;
         uint32_t xv = x[g];
         const bool emit = active && (uint64_t)xv >= ((uint64_t)f << 20);
         const uint64_t m = __ballot(emit);
@@ -333,7 +384,7 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
         }
         wpos -= (uint32_t)__popcll(m);
         if (active) {
-          const uint32_t q = div_by_freq(xv, s_m[sym], s_s[sym]);   // xv / f
+          const uint32_t q = div_by_freq(xv, s_m[ex], ((fc >> 25) & 1u) | ((fc >> 26) << 8));   // xv / f
           xv = (q << 12) + (xv - q * f) + cm;
         }
         x[g] = xv;
@@ -427,19 +478,41 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
   GLB uint8_t* out = (GLB uint8_t*)(T.dst + R.off);
   // states: 512 bytes
   if (lane < 32) *(GLB u32x4*)(out + 16u * lane) = *(const GLB u32x4*)(chunk + 16u * lane);
-  // words [per - nw, per) of the scratch, then zeros up to a multiple of 8 words
-  const GLB uint16_t* wsrc = (const GLB uint16_t*)(chunk + 4u * kLanes) + (per - R.nw);
-  GLB uint16_t* wdst = (GLB uint16_t*)(out + 4u * kLanes);
+  // words [per - nw, per) of the scratch, then zeros up to a multiple of 8
+  // words, in 16-byte vectors: output vector i holds words s0 + 8i .. +7, taken
+  // from the two aligned vectors around them (s0 mod 8 words into the first;
+  // indices clamped to the word area, whose words past `per` would land only
+  // in the zeroed tail)
+  const GLB u32x4* wsrc = (const GLB u32x4*)(chunk + 4u * kLanes);
+  GLB u32x4* wdst = (GLB u32x4*)(out + 4u * kLanes);
   const uint32_t nw_pad = (uint32_t)(pad16(2ull * R.nw) / 2);
-  for (uint32_t i = lane; i < nw_pad; i += kWave) wdst[i] = i < R.nw ? wsrc[i] : (uint16_t)0;
-  // dense plane: per 8-step block, lane l's 16 bytes hold (q, g) at q*2 + g for
-  // chunk element (blk*8 + q)*128 + 2l + g; block blk of a full chunk is block
-  // blk*nf + k of the plane region
+  const uint32_t s0 = (uint32_t)per - R.nw, dw = (s0 & 7u) >> 1, bsh = (s0 & 1u) * 16u;
+  const uint32_t last = (uint32_t)(per / 8) - 1u;
+  for (uint32_t i = lane; i < nw_pad / 8u; i += kWave) {
+    const uint32_t va = (s0 >> 3) + i;
+    const u32x4 a = wsrc[min(va, last)], b = wsrc[min(va + 1u, last)];
+    // dwords dw .. dw + 4 of a:b (dw is the same in every lane)
+    const uint32_t d0 = dw == 0 ? a.x : dw == 1 ? a.y : dw == 2 ? a.z : a.w;
+    const uint32_t d1 = dw == 0 ? a.y : dw == 1 ? a.z : dw == 2 ? a.w : b.x;
+    const uint32_t d2 = dw == 0 ? a.z : dw == 1 ? a.w : dw == 2 ? b.x : b.y;
+    const uint32_t d3 = dw == 0 ? a.w : dw == 1 ? b.x : dw == 2 ? b.y : b.z;
+    const uint32_t d4 = dw == 0 ? b.x : dw == 1 ? b.y : dw == 2 ? b.z : b.w;
+    uint32_t o[4] = {__builtin_amdgcn_alignbit(d1, d0, bsh), __builtin_amdgcn_alignbit(d2, d1, bsh),
+                     __builtin_amdgcn_alignbit(d3, d2, bsh), __builtin_amdgcn_alignbit(d4, d3, bsh)};
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {                   // zeros from word nw on
+      const uint32_t w = 8u * i + 2u * j;
+      o[j] = w + 1u < R.nw ? o[j] : w < R.nw ? (o[j] & 0xFFFFu) : 0u;
+    }
+    wdst[i] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+  // the partial chunk's dense plane, after its words (full chunks stored
+  // theirs in the plane region during the encode): per 8-step block, lane l's
+  // 16 bytes hold (q, g) at q*2 + g for chunk element (blk*8 + q)*128 + 2l + g
+  if (k < nf) return;
   constexpr uint64_t kBlkBytes = (uint64_t)kBlock * kLanes;
-  const bool full = k < nf;
-  GLB uint8_t* plane = full ? (GLB uint8_t*)T.dst + pad256(pad16(32 + 4ull * P->nsym) + 16ull * T.n_chunks) + k * kBlkBytes
-                            : out + 4u * kLanes + 2ull * nw_pad;
-  const uint64_t pstride = full ? nf * kBlkBytes : kBlkBytes;
+  GLB uint8_t* plane = out + 4u * kLanes + 2ull * nw_pad;
+  const uint64_t pstride = kBlkBytes;
   const uint32_t nsteps = (nc + kLanes - 1) / kLanes;
   const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
   const GLB uint16_t* src = (const GLB uint16_t*)T.src;
