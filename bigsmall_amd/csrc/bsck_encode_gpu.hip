@@ -292,6 +292,85 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
   }
 }
 
+// The steps of one chunk, last to first, in blocks of kBlock steps; the next
+// block's words are loaded while the current block is encoded, so the loads'
+// latency is not on the encode chain. FULL: a full chunk (every element
+// present, its 512-element units k, nf + k, 2nf + k, ...), which needs no
+// per-element bounds; else the partial chunk (contiguous from nf * per). Element
+// indices fit 32 bits (a task has fewer than 2^32 elements), and at each step
+// all but the lane's own offset is the same in every lane.
+template <bool FULL>
+__device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB uint16_t* src1, uint32_t lane,
+                                             uint32_t nc, uint32_t nsteps, uint32_t k, uint32_t nf, uint32_t per,
+                                             const uint32_t* s_fc, const uint32_t* s_m, GLB uint16_t* words,
+                                             uint32_t& wpos, uint32_t (&x)[2], bool plane_here, GLB uint8_t* plane,
+                                             uint64_t pstride) {
+  // this lane's two words of step t, packed (first | second << 16); 0 past the end
+  auto load_step = [&](uint32_t t) -> uint32_t {
+    if (FULL) {                                         // unit (t/4)*nf + k, quarter t mod 4
+      const uint32_t e0 = ((t >> 2) * nf + k) * kUnit + (t & 3u) * kLanes;
+      return src2[(e0 >> 1) + lane];
+    }
+    const uint32_t e0 = nf * per + t * kLanes, j0 = t * kLanes + 2 * lane;
+    if (j0 + 1 < nc) return src2[(e0 >> 1) + lane];
+    return j0 < nc ? (uint32_t)src1[e0 + 2 * lane] : 0u;
+  };
+  const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
+  uint32_t cur[kBlock];
+#pragma unroll
+  for (uint32_t q = 0; q < kBlock; ++q) cur[q] = load_step((nblk - 1) * kBlock + q);
+  for (uint32_t b = nblk; b-- > 0;) {
+    uint32_t nxt[kBlock];
+#pragma unroll
+    for (uint32_t q = 0; q < kBlock; ++q) nxt[q] = b > 0 ? load_step((b - 1) * kBlock + q) : 0u;
+    if (FULL && plane_here) {
+      // sign | mantissa bytes: word pair (q, g = 0, 1) -> bytes 0 and 2, then two steps per word
+      uint32_t pw[kBlock / 2];
+#pragma unroll
+      for (uint32_t i = 0; i < kBlock / 2; ++i) {
+        const uint32_t a = cur[2 * i], c2 = cur[2 * i + 1];
+        const uint32_t pa = (a & 0x007F007Fu) | ((a >> 8) & 0x00800080u);
+        const uint32_t pb = (c2 & 0x007F007Fu) | ((c2 >> 8) & 0x00800080u);
+        pw[i] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+      }
+      *(GLB u32x4*)(plane + (uint64_t)b * pstride) = u32x4{pw[0], pw[1], pw[2], pw[3]};
+    }
+#pragma unroll
+    for (int q = (int)kBlock - 1; q >= 0; --q) {
+      const uint32_t t = b * kBlock + (uint32_t)q;
+      if (!FULL && t >= nsteps) continue;                      // uniform: the last block may be short
+      const uint32_t j0 = t * kLanes + 2 * lane;
+      const uint32_t wv[2] = {cur[q] & 0xFFFFu, cur[q] >> 16};
+#pragma unroll
+      for (int g = 1; g >= 0; --g) {
+        const bool active = FULL || j0 + g < nc;
+        const uint32_t ex = (wv[g] >> 7) & 0xFFu;
+        const uint32_t fc = s_fc[ex], f = fc & 0x1FFFu, cm = (fc >> 13) & 0xFFFu;
+        uint32_t xv = x[g];
+        // renormalise while x >= f * 2^20 (never for f = 4096): f * 2^20 is a
+        // multiple of 2^20, so the test is x >> 20 >= f, in 32 bits
+        const bool emit = active && (xv >> 20) >= f;
+        const uint64_t m = __ballot(emit);
+        // the emitting lanes' words, lane-descending from wpos - 1: a lane's slot
+        // is the new wpos plus the emitting lanes below it
+        wpos -= (uint32_t)__popcll(m);
+        if (emit) {
+          words[wpos + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] =
+              (uint16_t)(xv & 0xFFFFu);
+          xv >>= 16;
+        }
+        if (active) {
+          const uint32_t q2 = div_by_freq(xv, s_m[ex], ((fc >> 25) & 1u) | ((fc >> 26) << 8));   // xv / f
+          xv = (q2 << 12) + (xv - q2 * f) + cm;
+        }
+        x[g] = xv;
+      }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kBlock; ++q) cur[q] = nxt[q];
+  }
+}
+
 // One wavefront per chunk: lane l owns states l (group 0) and 64 + l (group 1);
 // state (g, l) codes element t*128 + 2l + g at step t.
 __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
@@ -332,67 +411,12 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   GLB uint16_t* words = (GLB uint16_t*)(chunk + 4u * kLanes);   // capacity per; filled from the end
   uint32_t x[2] = {kL, kL};
   uint32_t wpos = (uint32_t)per;
-  const uint64_t above = ~((2ull << lane) - 1ull);               // lanes with a higher index
-  // this lane's two words of step t, packed (first | second << 16); 0 past the end
-  auto load_step = [&](uint32_t t) -> uint32_t {
-    const uint32_t j0 = t * kLanes + 2 * lane;
-    const uint64_t e = chunk_elem(k, j0, nf, per);     // j0 and j0 + 1 share a unit
-    if (j0 + 1 < nc) return src2[e / 2];
-    return j0 < nc ? (uint32_t)src1[e] : 0u;
-  };
-  // Steps are encoded last to first in blocks of kPre; the next block's words
-  // are loaded while the current block is encoded, so the loads' latency is
-  // not on the encode chain.
-  constexpr uint32_t kPre = kBlock;
-  const uint32_t nblk = (nsteps + kPre - 1) / kPre;
-  uint32_t cur[kPre];
-#pragma unroll
-  for (uint32_t k = 0; k < kPre; ++k) cur[k] = load_step((nblk - 1) * kPre + k);
-  for (uint32_t b = nblk; b-- > 0;) {
-    uint32_t nxt[kPre];
-#pragma unroll
-    for (uint32_t k = 0; k < kPre; ++k) nxt[k] = b > 0 ? load_step((b - 1) * kPre + k) : 0u;
-    if (plane_here) {
-      // sign | mantissa bytes: word pair (q, g = 0, 1) -> bytes 0 and 2, then two steps per word
-      uint32_t pw[kBlock / 2];
-#pragma unroll
-      for (uint32_t i = 0; i < kBlock / 2; ++i) {
-        const uint32_t a = cur[2 * i], c2 = cur[2 * i + 1];
-        const uint32_t pa = (a & 0x007F007Fu) | ((a >> 8) & 0x00800080u);
-        const uint32_t pb = (c2 & 0x007F007Fu) | ((c2 >> 8) & 0x00800080u);
-        pw[i] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
-      }
-      *(GLB u32x4*)(plane + (uint64_t)b * pstride) = u32x4{pw[0], pw[1], pw[2], pw[3]};
-    }
-#pragma unroll
-    for (int k = (int)kPre - 1; k >= 0; --k) {
-      const uint32_t t = b * kPre + (uint32_t)k;
-      if (t >= nsteps) continue;                                   // uniform: the last block may be short
-      const uint32_t j0 = t * kLanes + 2 * lane;
-      const uint32_t wv[2] = {cur[k] & 0xFFFFu, cur[k] >> 16};
-#pragma unroll
-      for (int g = 1; g >= 0; --g) {
-        const bool active = j0 + g < nc;
-        const uint32_t ex = (wv[g] >> 7) & 0xFFu;
-        const uint32_t fc = s_fc[ex], f = fc & 0x1FFFu, cm = (fc >> 13) & 0xFFFu;
-        uint32_t xv = x[g];
-        const bool emit = active && (uint64_t)xv >= ((uint64_t)f << 20);
-        const uint64_t m = __ballot(emit);
-        if (emit) {
-          words[wpos - 1 - (uint32_t)__popcll(m & above)] = (uint16_t)(xv & 0xFFFFu);
-          xv >>= 16;
-        }
-        wpos -= (uint32_t)__popcll(m);
-        if (active) {
-          const uint32_t q = div_by_freq(xv, s_m[ex], ((fc >> 25) & 1u) | ((fc >> 26) << 8));   // xv / f
-          xv = (q << 12) + (xv - q * f) + cm;
-        }
-        x[g] = xv;
-      }
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < kPre; ++k) cur[k] = nxt[k];
-  }
+  if (k < nf)
+    encode_steps<true>(src2, src1, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m, words,
+                       wpos, x, plane_here, plane, pstride);
+  else
+    encode_steps<false>(src2, src1, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m, words,
+                        wpos, x, false, plane, pstride);
   GLB uint32_t* st = (GLB uint32_t*)chunk;
   st[lane] = x[0];
   st[kWave + lane] = x[1];
