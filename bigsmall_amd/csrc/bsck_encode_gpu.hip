@@ -53,7 +53,7 @@ struct Plan {
   uint32_t sym_of_exp[256];   // exponent -> symbol index
   uint32_t freq[256];         // per symbol
   uint32_t cum[256];          // per symbol
-  uint32_t rcp[256];          // per symbol: multiplier for x / freq (see div_by_freq)
+  uint32_t rcp[256];          // per symbol: multiplier for x / freq (see div_constants)
   uint32_t shf[256];          // per symbol: its two shifts (s1 | s2 << 8)
   uint32_t nsym, ok, pad0, pad1;
 };
@@ -72,7 +72,7 @@ __device__ __forceinline__ uint64_t chunk_elem(uint64_t k, uint64_t j, uint64_t 
   return k < nf ? ((j / kUnit) * nf + k) * kUnit + j % kUnit : nf * per + j;
 }
 
-// x / f for a fixed divisor 1 <= f <= 4096 and any 32-bit x, without a divide
+// Constants for x / f with a fixed divisor 1 <= f <= 4096 and any 32-bit x, without a divide
 // instruction: Granlund and Montgomery, "Division by Invariant Integers using
 // Multiplication" (PLDI 1994), Figure 4.1. With l = ceil(log2 f),
 //   m = floor(2^32 * (2^l - f) / f) + 1,  s1 = min(l, 1),  s2 = max(l - 1, 0),
@@ -81,10 +81,6 @@ __device__ __forceinline__ void div_constants(uint32_t f, uint32_t& m, uint32_t&
   const uint32_t l = f > 1 ? 32u - (uint32_t)__clz(f - 1) : 0u;
   m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - f)) / f + 1);
   shf = (l ? 1u : 0u) | ((l ? l - 1 : 0u) << 8);
-}
-__device__ __forceinline__ uint32_t div_by_freq(uint32_t x, uint32_t m, uint32_t shf) {
-  const uint32_t t = __umulhi(m, x);
-  return (t + ((x - t) >> (shf & 0xFFu))) >> (shf >> 8);
 }
 __host__ __device__ inline uint64_t scratch_bytes(uint32_t steps) { return 4ull * kLanes + 2ull * kLanes * steps; }
 
@@ -345,7 +341,7 @@ __device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB
       for (int g = 1; g >= 0; --g) {
         const bool active = FULL || j0 + g < nc;
         const uint32_t ex = (wv[g] >> 7) & 0xFFu;
-        const uint32_t fc = s_fc[ex], f = fc & 0x1FFFu, cm = (fc >> 13) & 0xFFFu;
+        const uint32_t fc = s_fc[ex], f = (fc >> 5) & 0x1FFFu, cm = (fc >> 18) & 0xFFFu;
         uint32_t xv = x[g];
         // renormalise while x >= f * 2^20 (never for f = 4096): f * 2^20 is a
         // multiple of 2^20, so the test is x >> 20 >= f, in 32 bits
@@ -360,8 +356,13 @@ __device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB
           xv >>= 16;
         }
         if (active) {
-          const uint32_t q2 = div_by_freq(xv, s_m[ex], ((fc >> 25) & 1u) | ((fc >> 26) << 8));   // xv / f
-          xv = (q2 << 12) + (xv - q2 * f) + cm;
+          // q = xv / f (Granlund-Montgomery with div_constants' m, s1, s2; the
+          // second shift by fc, whose bits 0..4 are s2), then xv' = (q << 12) + xv mod f + cum
+          // = xv + cum + q * (4096 - f): q < 2^20 (xv < f * 2^20 after the
+          // renormalisation) and 4096 - f < 2^13, a 24-bit product
+          const uint32_t t = __umulhi(s_m[ex], xv);
+          const uint32_t q2 = (t + ((xv - t) >> ((fc >> 30) & 1u))) >> fc;
+          xv = xv + cm + __umul24(q2, 4096u - f);
         }
         x[g] = xv;
       }
@@ -376,7 +377,8 @@ __device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB
 __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* __restrict__ tasks, uint32_t n_tasks,
                                                           uint32_t steps, const uint8_t* __restrict__ plans,
                                                           ChunkRec* __restrict__ recs, uint8_t* __restrict__ scratch) {
-  // per exponent: {f:13, cum:12, s1:1, s2:4} of its symbol, and the divisor's multiplier
+  // per exponent: {s2:5, f:13, cum:12, s1:1} of its symbol (s2 in bits 0..4, where a
+  // shift reads its amount), and the divisor's multiplier
   __shared__ uint32_t s_fc[256], s_m[256];
   const uint32_t lane = threadIdx.x, cg = blockIdx.x;
   const uint32_t ti = task_of(tasks, n_tasks, cg);
@@ -386,7 +388,7 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   if (!task_ok(T, per) || cg < T.chunk_begin || cg - T.chunk_begin >= T.n_chunks || !P->ok) return;
   for (uint32_t i = lane; i < 256; i += kWave) {
     const uint32_t sym = P->sym_of_exp[i], shf = P->shf[sym];
-    s_fc[i] = P->freq[sym] | (P->cum[sym] << 13) | ((shf & 1u) << 25) | ((shf >> 8) << 26);
+    s_fc[i] = (shf >> 8) | (P->freq[sym] << 5) | (P->cum[sym] << 18) | ((shf & 1u) << 30);
     s_m[i] = P->rcp[sym];
   }
   __syncthreads();
