@@ -194,3 +194,46 @@ def test_kv_set_blocks_odd_block_size():
     for j, b in enumerate([1, 0]):
         assert torch.equal(kb[j].cpu().view(torch.int16), k[:, b * 257:(b + 1) * 257].view(torch.int16))
         assert torch.equal(vb[j].cpu().view(torch.int16), v[:, b * 257:(b + 1) * 257].view(torch.int16))
+
+
+@pytest.mark.parametrize("where", ["before_plane", "in_plane", "after_plane"])
+def test_capacity_too_small_reports_bounds_and_writes_nothing_past_it(where):
+    """A task whose capacity is below its blob's length: BS_DEV_ERR_BOUNDS, a
+    length of 0, and no byte at or past `cap` written. The capacity falls
+    before the dense-plane region (the plan pass refuses), inside it (the
+    chunk pass stores the full chunks' planes there and must skip them) or
+    after it but short of the blob (the layout pass refuses)."""
+    from bigsmall_amd import _native
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    from bigsmall_amd.device import StatusWord, stream_ptr, upload_bytes
+    dev = torch.device("cuda", 0)
+    steps = 16
+    per = 128 * steps
+    nf = 5
+    n = nf * per + 300                                   # five full chunks and a partial one
+    nch = nf + 1
+    w = _words(np.random.default_rng(7), "gauss", n)
+    want = bc.encode_array(w, steps=steps, mode=bc.MODE_DENSE, lanes=128)
+    nsym = int.from_bytes(want[22:24], "little")
+    ctab = (32 + 4 * nsym + 15) & ~15
+    preg = (ctab + 16 * nch + 255) & ~255
+    cap = {"before_plane": preg - 16, "in_plane": preg + nf * per // 2, "after_plane": len(want) - 16}[where]
+    assert preg + nf * per < len(want) - 16 and cap < len(want)
+    _say(f"[encode cap] {where}: n={n} blob={len(want)} plane=[{preg}, {preg + nf * per}) cap={cap}")
+    src = torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+    dst = torch.full((len(want) + 4096,), 0xAB, dtype=torch.uint8, device=dev)
+    tasks = np.zeros(1, bc.ENCODE_TASK_DTYPE)
+    tasks[0] = (src.data_ptr(), n, dst.data_ptr(), cap, 0, nch)
+    d_tasks = upload_bytes(tasks.view(np.uint8), dev)
+    L = _native.lib()
+    wb = int(L.bs_chunk_encode_gpu_work_bytes(1, nch, steps))
+    work = torch.empty(wb, dtype=torch.uint8, device=dev)
+    out_len = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    st = StatusWord(dev)
+    _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), 1, nch, steps, work.data_ptr(), wb, out_len.data_ptr(),
+                                        st.ptr, stream_ptr(None, dev)), "bs_chunk_encode_gpu")
+    torch.cuda.synchronize()
+    assert int(st.t.item()) & _native.BS_DEV_ERR_BOUNDS
+    assert int(out_len.item()) == 0
+    tail = dst[cap:].cpu().numpy()
+    assert (tail == 0xAB).all(), f"{int((tail != 0xAB).sum())} bytes written at or past the capacity"
