@@ -104,13 +104,18 @@ def _run_encode(dev, tasks: np.ndarray, total_chunks: int, steps: int, stream):
     d_tasks = upload_bytes(tasks.view(np.uint8), dev)
     wb = int(L.bs_chunk_encode_gpu_work_bytes(len(tasks), total_chunks, steps))
     work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
-    out_len = torch.zeros(len(tasks), dtype=torch.int64, device=dev)
+    # the status word (the low half of element 0) and the lengths in one
+    # buffer, so that one copy on the encode's stream brings both back
+    res = torch.zeros(1 + len(tasks), dtype=torch.int64, device=dev)
     st = StatusWord(dev)
+    st.t = res[:1].view(torch.int32)[:1]
     _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), len(tasks), total_chunks, steps, work.data_ptr(), wb,
-                                        out_len.data_ptr(), st.ptr, stream_ptr(stream, dev)), "bs_chunk_encode_gpu")
-    torch.cuda.synchronize(dev)
-    st.check("bf16_chunked GPU encode")
-    return out_len.cpu().numpy(), st
+                                        res[1:].data_ptr(), st.ptr, stream_ptr(stream, dev)), "bs_chunk_encode_gpu")
+    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+        host = res.cpu().numpy()
+    if int(host[0]) & 0xFFFFFFFF:
+        st.check("bf16_chunked GPU encode")
+    return host[1:], st
 
 
 def _pack(arena, src_offs: np.ndarray, lens: np.ndarray, dev, st: StatusWord, stream):
