@@ -360,8 +360,8 @@ __device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB
           // second shift by fc, whose bits 0..4 are s2), then xv' = (q << 12) + xv mod f + cum
           // = xv + cum + q * (4096 - f): q < 2^20 (xv < f * 2^20 after the
           // renormalisation) and 4096 - f < 2^13, a 24-bit product
-          const uint32_t t = __umulhi(s_m[ex], xv);
-          const uint32_t q2 = (t + ((xv - t) >> ((fc >> 30) & 1u))) >> fc;
+          const uint32_t mh = __umulhi(s_m[ex], xv);
+          const uint32_t q2 = (mh + ((xv - mh) >> ((fc >> 30) & 1u))) >> fc;
           xv = xv + cm + __umul24(q2, 4096u - f);
         }
         x[g] = xv;
