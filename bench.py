@@ -200,7 +200,7 @@ def cpu_baseline(words: dict, budget_s: float = 6.0, bsck_blobs: dict | None = N
     return out
 
 
-def measure_copy(dev, mib: int = 2048, reps: int = 5) -> float:
+def measure_copy(dev, mib: int = 2048, reps: int = 10) -> float:
     """Device-to-device copy rate in the same run, (read + write) bytes per
     second: the practical ceiling for a stream that reads and writes HBM. 2 GiB
     each way, far beyond the 256 MB Infinity Cache, so no pass is served from it."""
@@ -215,9 +215,34 @@ def measure_copy(dev, mib: int = 2048, reps: int = 5) -> float:
     return 2 * n / (ms * 1e-3) / 1e9
 
 
-def measure_copy_kernel(dev, mib: int = 2048, reps: int = 5) -> float:
-    """The same copy by this library's own 16-byte-per-lane copy kernel
-    (bs_copy_spans, one span), (read + write) bytes per second."""
+def hbm_probe(dev, mib: int = 2048, reps: int = 10) -> dict:
+    """HBM rates by direction over 2 GiB buffers (far beyond the Infinity
+    Cache): a read-only stream (torch's int64 sum), a write-only stream
+    (torch's fill_) and read + write copies (torch's copy_ and this library's
+    bs_copy_spans), in GB/s of bytes moved. A stream that both reads and
+    writes, as a decode does, runs below either direction alone."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    s = torch.cuda.current_stream(dev)
+    a64 = a.view(torch.int64)
+    out = {}
+    for name, fn, moved in (("read_only_sum", lambda: a64.sum(), n), ("write_only_fill", lambda: b.fill_(3), n),
+                            ("copy_torch", lambda: b.copy_(a), 2 * n)):
+        fn()
+        out[name] = round(moved / (_timed(fn, reps, s) * 1e-3) / 1e9, 1)
+    del a, b, a64
+    out["copy_bs_copy_spans"] = round(measure_copy_kernel(dev, mib, reps), 1)
+    log(f"[hbm] read-only {out['read_only_sum']:.0f} GB/s, write-only {out['write_only_fill']:.0f} GB/s, "
+        f"copy {out['copy_torch']:.0f} (torch) / {out['copy_bs_copy_spans']:.0f} (bs_copy_spans) GB/s")
+    return {"workload": "hbm_probe", "bytes_each": n, "unit": "GB/s", **out}
+
+
+def measure_copy_kernel(dev, mib: int = 2048, reps: int = 10) -> float:
+    """The same copy by this library's own copy kernel (bs_copy_spans, one
+    span: four 16-byte vectors per lane, streaming loads and stores), (read +
+    write) bytes per second."""
     import torch
     from bigsmall_amd import _native
     from bigsmall_amd.codecs.bf16_chunked import SPAN_DTYPE
@@ -1023,6 +1048,8 @@ def main():
                     help="c3 workload: only this engine's format under rANS")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--hbm-probe", action="store_true",
+                    help="only measure 2 GiB read-only, write-only and copy streams (HBM rates by direction)")
     args = ap.parse_args()
     if args.ref_tables != "auto":
         from bigsmall_amd.codecs import _refstreams
@@ -1036,6 +1063,9 @@ def main():
     import torch
     if args.copy_probe_mb:
         copy_probe(args.copy_probe_mb)
+        return
+    if args.hbm_probe:
+        print(json.dumps(hbm_probe(torch.device("cuda", 0))), flush=True)
         return
     if args.workload != "layer":
         run = {"model": run_model, "kv": run_kv, "refcodecs": run_refcodecs, "reflayer": run_reflayer, "c3": run_c3,

@@ -569,7 +569,23 @@ __global__ __launch_bounds__(256) void copy_spans_kernel(const bs_span* __restri
   const uint64_t nv = S.len / 16;
   const GLB u32x4* src = (const GLB u32x4*)S.src;
   GLB u32x4* dst = (GLB u32x4*)S.dst;
-  for (uint64_t i = (uint64_t)blockIdx.y * 256u + threadIdx.x; i < nv; i += 256ull * gridDim.y) dst[i] = src[i];
+  // four 16-byte vectors per thread in flight, loaded and then stored with
+  // streaming hints (each byte is read once and written once): a 2 GiB copy
+  // measured 5.73 TB/s this way against 5.55 TB/s one vector at a time
+  constexpr uint32_t kU = 4;
+  for (uint64_t i = (uint64_t)blockIdx.y * 256u * kU + threadIdx.x; i < nv; i += 256ull * kU * gridDim.y) {
+    u32x4 v[kU];
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u) {
+      const uint64_t j = i + 256ull * u;
+      v[u] = j < nv ? __builtin_nontemporal_load(src + j) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u) {
+      const uint64_t j = i + 256ull * u;
+      if (j < nv) __builtin_nontemporal_store(v[u], dst + j);
+    }
+  }
 }
 
 }  // namespace
@@ -610,9 +626,10 @@ int bs_chunk_encode_gpu(const bs_encode_task* d_tasks, uint32_t n_tasks, uint32_
 int bs_copy_spans(const bs_span* d_spans, uint32_t n_spans, uint64_t max_len, int32_t* d_status, void* stream) {
   if (!d_status || (n_spans && !d_spans) || n_spans > 0x7FFFFFFFu) return BS_ERR_ARG;
   if (n_spans == 0 || max_len == 0) return BS_OK;
-  // about four 16-byte vectors per thread of the longest span, at most 1024 workgroups per span
+  // one pass of four 16-byte vectors per thread over the longest span, at most
+  // 8192 workgroups per span (a 2 GiB copy ran fastest with 8192)
   const uint64_t per_block = 256ull * 16ull * 4ull;
-  const uint32_t gy = (uint32_t)std::min<uint64_t>((max_len + per_block - 1) / per_block, 1024ull);
+  const uint32_t gy = (uint32_t)std::min<uint64_t>((max_len + per_block - 1) / per_block, 8192ull);
   hipLaunchKernelGGL(copy_spans_kernel, dim3(n_spans, gy), dim3(256), 0, (hipStream_t)stream, d_spans, d_status);
   return hipGetLastError() == hipSuccess ? BS_OK : BS_ERR_HIP;
 }
