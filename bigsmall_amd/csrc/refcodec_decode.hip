@@ -277,7 +277,7 @@ __device__ __forceinline__ void serial_chain(const GLB uint8_t* words, uint32_t 
   auto step = [&](uint32_t j) {
     const u32x4 e = tbl[x & kSlotMask];
     uint32_t xn = __umul24(e.x, x >> kShift) + e.y;         // v_mad_u32_u24 (f <= 4096)
-    if (__builtin_amdgcn_readfirstlane(xn) < kL) {         // uniform: a scalar branch
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)xn) < kL) {   // uniform: a scalar branch
       const uint32_t d = pos - base;                       // < 128
       const uint32_t w_a = __builtin_amdgcn_readlane(w_lo, d & 63u);
       const uint32_t w_b = __builtin_amdgcn_readlane(w_hi, d & 63u);
