@@ -150,11 +150,8 @@ def compress(src, dst: str | Path, mode: str = "balanced", workers: Optional[int
     header = {"format": dominant, "mode": mode, "model_type": _detect_model_type([t["name"] for t in tensors]),
               "base_model": None, "tensor_count": len(tensors), "tensors": header_tensors,
               "safetensors_metadata": st_meta or None, "codec_stats": stats.as_dict()}
-    # version 2 whenever a codec needs it: the reference's v2-only codecs
-    # (bigsmall/encoder.py:482-491) and this engine's GPU formats
-    v2_codecs = {"bf16_chunked_v1", "fp8_chunked_v1", "bf16_chunked_tans_v1", "fp8_chunked_tans_v1",
-                 "bf16_parallel_v1", "bf16_sparsity_v1", "fp2_residual_v1"}
-    version = formats.BS_FORMAT_VERSION_V2 if any(h["codec"] in v2_codecs for h in header_tensors) \
+    # version 2 whenever a codec needs it (formats.V2_CODECS)
+    version = formats.BS_FORMAT_VERSION_V2 if any(h["codec"] in formats.V2_CODECS for h in header_tensors) \
         else formats.BS_FORMAT_VERSION_V1
     container.write_container(dst, header, data.getvalue(), format_version=version)
     return str(dst)

@@ -5,6 +5,10 @@ BS_FORMAT_VERSION_V1 = 1
 BS_FORMAT_VERSION_V2 = 2
 BS_FORMAT_VERSION = BS_FORMAT_VERSION_V1
 BS_SUPPORTED_FORMAT_VERSIONS = frozenset({BS_FORMAT_VERSION_V1, BS_FORMAT_VERSION_V2})
+# codecs that need a version-2 container: the reference's (encoder.py:482-491)
+# and this engine's GPU formats
+V2_CODECS = frozenset({"bf16_chunked_v1", "fp8_chunked_v1", "bf16_chunked_tans_v1", "fp8_chunked_tans_v1",
+                       "bf16_parallel_v1", "bf16_sparsity_v1", "fp2_residual_v1"})
 
 SAFETENSORS_TO_FORMAT = {"F32": "fp32", "F16": "fp16", "BF16": "bf16", "F8_E4M3": "fp8", "F8_E5M2": "fp8", "F4": "fp4"}
 
