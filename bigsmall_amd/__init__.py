@@ -13,6 +13,7 @@ kernels on the GPU:
     CompressedKVCache                       -> KV entries and blocks decoded on the GPU
     codec_registry.register_codec / get_codec / auto_select_codec
     compress_for_hub(model_dir, out_dir), from_pretrained(path) -> multi-shard .bs models + index
+    migrate.migrate(path)                   -> re-encode a container into the GPU formats where smaller
 """
 __version__ = "3.12.0+mi355x"
 
