@@ -76,10 +76,10 @@ def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_A
     return out[: olen.value].tobytes()
 
 
-# bs_encode_task (include/bigsmall_hip.h): 40 bytes
+# bs_encode_task (include/bigsmall_hip.h): 56 bytes; seg_len 0 = contiguous words
 ENCODE_TASK_DTYPE = np.dtype([("src", "<u8"), ("n", "<u8"), ("dst", "<u8"), ("cap", "<u8"),
-                              ("chunk_begin", "<u4"), ("n_chunks", "<u4")])
-assert ENCODE_TASK_DTYPE.itemsize == 40
+                              ("chunk_begin", "<u4"), ("n_chunks", "<u4"), ("seg_len", "<u8"), ("seg_stride", "<u8")])
+assert ENCODE_TASK_DTYPE.itemsize == 56
 GPU_ENCODE_LANES = 128
 
 
@@ -177,7 +177,7 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
     for k, i in enumerate(live):
         n = srcs[i].numel()
         nch = (n + per - 1) // per
-        tasks[k] = (srcs[i].data_ptr(), n, arena.data_ptr() + slots[i][0], slots[i][1], chunk, nch)
+        tasks[k] = (srcs[i].data_ptr(), n, arena.data_ptr() + slots[i][0], slots[i][1], chunk, nch, 0, 0)
         chunk += nch
     lens = np.zeros(len(srcs), np.int64)
     st = None
@@ -193,12 +193,16 @@ def encode_device(tensors, steps: int = DEFAULT_STEPS, stream=None, compact: boo
 
 
 def encode_device_rows(groups, steps: int = DEFAULT_STEPS, stream=None):
-    """encode_device for many equal-size pieces: every row of each contiguous
-    2-D bf16 device tensor in `groups` becomes one blob (e.g. the 256-token
-    blocks of a KV layer), with the task table built without a per-row Python
-    loop. Returns (arena, offsets, lengths): blobs packed back to back in one
-    device uint8 tensor, offsets and lengths as int64 numpy arrays in row order
-    over all groups."""
+    """encode_device for many equal-size pieces: every row of each bf16
+    device tensor in `groups` becomes one blob (e.g. the 256-token blocks of a
+    KV layer), with the task table built without a per-row Python loop. A
+    group is a contiguous 2-D tensor [rows, n], or a 3-D view [rows, segments,
+    seg_len] whose segments are contiguous (a block of tokens of a [heads,
+    tokens, dim] tensor: rows = blocks, segments = heads), read in place:
+    seg_len a multiple of 512, segment starts a multiple of 8 words apart.
+    Returns (arena, offsets, lengths): blobs packed back to back in one device
+    uint8 tensor, offsets and lengths as int64 numpy arrays in row order over
+    all groups."""
     import torch
     if not groups:
         return None, np.zeros(0, np.int64), np.zeros(0, np.int64)
@@ -207,26 +211,40 @@ def encode_device_rows(groups, steps: int = DEFAULT_STEPS, stream=None):
     bounds: dict[int, int] = {}
     shapes, cap_total = [], 0
     for g in groups:
-        if g.dtype != torch.bfloat16 or g.device != dev or g.dim() != 2 or not g.is_contiguous():
-            raise ValueError("encode_device_rows expects contiguous 2-D bf16 tensors on one GPU")
-        rows, n = g.shape
-        if rows and n and (g.data_ptr() % 4 or (rows > 1 and n % 2)):
+        if g.dtype != torch.bfloat16 or g.device != dev or g.dim() not in (2, 3):
+            raise ValueError("encode_device_rows expects 2-D or 3-D bf16 tensors on one GPU")
+        if g.dim() == 2:
+            if not g.is_contiguous():
+                raise ValueError("encode_device_rows expects 2-D groups to be contiguous")
+            rows, n = g.shape
+            row_stride, seg = n, (0, 0)
+        else:
+            rows, nseg, seg_len = g.shape
+            n = nseg * seg_len
+            if rows and n and (g.stride(2) != 1 or seg_len % 512 or
+                               (nseg > 1 and (g.stride(1) % 8 or g.stride(1) < seg_len or
+                                              (nseg - 1) * g.stride(1) + seg_len > 2 ** 32))):
+                raise ValueError("encode_device_rows: a 3-D group needs contiguous segments of a multiple of "
+                                 "512 words whose starts are a multiple of 8 words apart")
+            row_stride, seg = g.stride(0), ((seg_len, g.stride(1)) if nseg > 1 else (0, 0))
+        if rows and n and (g.data_ptr() % 4 or (rows > 1 and row_stride % 2)):
             raise ValueError("encode_device_rows needs 4-byte aligned rows (an even row length)")
         slot = (_encode_bound(n, steps, bounds) + 255) & ~255 if rows and n else 0
-        shapes.append((rows, n, slot, cap_total))
+        shapes.append((rows, n, slot, cap_total, row_stride, seg))
         cap_total += rows * slot
     arena = torch.empty(max(cap_total, 256), dtype=torch.uint8, device=dev)
     n_rows = sum(r for r, *_ in shapes)
     lens = np.zeros(n_rows, np.int64)
     src_offs = np.zeros(n_rows, np.int64)
     parts, chunk, r0 = [], 0, 0
-    for g, (rows, n, slot, base) in zip(groups, shapes):
+    for g, (rows, n, slot, base, row_stride, seg) in zip(groups, shapes):
         idx = np.arange(rows, dtype=np.uint64)
         src_offs[r0:r0 + rows] = base + idx.astype(np.int64) * slot
         if rows and n:
             nch = (n + per - 1) // per
             t = np.zeros(rows, ENCODE_TASK_DTYPE)
-            t["src"] = g.data_ptr() + idx * np.uint64(2 * n)
+            t["src"] = g.data_ptr() + idx * np.uint64(2 * row_stride)
+            t["seg_len"], t["seg_stride"] = seg
             t["n"] = n
             t["dst"] = arena.data_ptr() + np.uint64(base) + idx * np.uint64(slot)
             t["cap"] = _encode_bound(n, steps, bounds)

@@ -96,10 +96,43 @@ __device__ __forceinline__ uint32_t task_of(const bs_encode_task* tasks, uint32_
   return lo;
 }
 
-// Checks every kernel repeats: the task's fields agree with each other.
+// Checks every kernel repeats: the task's fields agree with each other. A
+// segmented task's segments hold whole 512-element units, start 16-byte
+// aligned relative to src, and reach no word 2^32 or more past src.
 __device__ __forceinline__ bool task_ok(const bs_encode_task& T, uint64_t per) {
   return T.n > 0 && T.n <= 0xFFFFFFFFull && ((uintptr_t)T.src & 3u) == 0 && ((uintptr_t)T.dst & 15u) == 0 &&
-         (uint64_t)T.n_chunks == (T.n + per - 1) / per;
+         (uint64_t)T.n_chunks == (T.n + per - 1) / per &&
+         (T.seg_len == 0 ||
+          (T.seg_len % kUnit == 0 && T.seg_stride >= T.seg_len && T.seg_stride % 8 == 0 &&
+           ((T.n - 1) / T.seg_len) * T.seg_stride + (T.n - 1) % T.seg_len <= 0xFFFFFFFFull));
+}
+
+// Word offset of tensor element e from the task's src: e itself, or its
+// segment's start plus its place in the segment.
+__device__ __forceinline__ uint64_t src_word(const bs_encode_task& T, uint64_t e) {
+  return T.seg_len ? (e / T.seg_len) * T.seg_stride + e % T.seg_len : e;
+}
+
+// The same for whole 512-element units, wave-uniform and without a divide:
+// us units per segment (0: contiguous), inv = floor((2^32 - 1) / us). For a
+// unit index u < 2^23, mulhi(u, inv) is u / us or one less, and one test
+// settles it.
+struct SegMap {
+  uint32_t us, inv;
+  uint64_t stride;             // words from one segment's start to the next's
+};
+__device__ __forceinline__ SegMap seg_map(const bs_encode_task& T) {
+  SegMap m;
+  m.us = (uint32_t)(T.seg_len / kUnit);
+  m.inv = m.us ? 0xFFFFFFFFu / m.us : 0u;
+  m.stride = T.seg_stride;
+  return m;
+}
+__device__ __forceinline__ uint64_t unit_word(const SegMap& m, uint32_t u) {
+  if (!m.us) return (uint64_t)u * kUnit;
+  uint32_t q = __umulhi(u, m.inv);
+  if ((q + 1u) * m.us <= u) ++q;
+  return (uint64_t)q * m.stride + (uint64_t)(u - q * m.us) * kUnit;
 }
 
 __global__ __launch_bounds__(256) void enc_clear_kernel(uint8_t* __restrict__ plans) {
@@ -127,21 +160,27 @@ __global__ __launch_bounds__(256) void enc_hist_kernel(const bs_encode_task* __r
   if (!task_ok(T, per) || c < T.chunk_begin || c - T.chunk_begin >= T.n_chunks) return;
   for (uint32_t i = tid; i < 256 * kCopies; i += 256) h[i] = 0;
   __syncthreads();
-  const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;   // a contiguous slice: the slices cover the tensor once
+  const uint64_t base = (uint64_t)(c - T.chunk_begin) * per;   // the slices cover the tensor once
   const uint32_t nc = (uint32_t)min(per, T.n - base);
-  const GLB uint16_t* src = (const GLB uint16_t*)T.src + base;
   const uint32_t cp = tid & (kCopies - 1);
   auto count = [&](uint32_t w) { atomicAdd(&h[((w >> 7) & 0xFFu) * kCopies + cp], 1u); };
-  const uint32_t head = min(nc, (uint32_t)(((16u - ((uintptr_t)src & 15u)) & 15u) / 2u));   // src is 4-byte aligned
-  if (tid < head) count(src[tid]);
-  const uint32_t nv = (nc - head) / 8u;
-  const GLB u32x4* vsrc = (const GLB u32x4*)(src + head);
-  for (uint32_t v = tid; v < nv; v += 256) {
-    const u32x4 q = vsrc[v];
-    count(q.x); count(q.x >> 16); count(q.y); count(q.y >> 16);
-    count(q.z); count(q.z >> 16); count(q.w); count(q.w >> 16);
+  // the slice in pieces that each lie inside one segment (a contiguous task: one piece)
+  for (uint64_t e = base, end = base + nc; e < end;) {
+    const uint64_t stop = T.seg_len ? min(end, (e / T.seg_len + 1) * T.seg_len) : end;
+    const uint32_t m = (uint32_t)(stop - e);
+    const GLB uint16_t* src = (const GLB uint16_t*)T.src + src_word(T, e);
+    const uint32_t head = min(m, (uint32_t)(((16u - ((uintptr_t)src & 15u)) & 15u) / 2u));   // src is 4-byte aligned
+    if (tid < head) count(src[tid]);
+    const uint32_t nv = (m - head) / 8u;
+    const GLB u32x4* vsrc = (const GLB u32x4*)(src + head);
+    for (uint32_t v = tid; v < nv; v += 256) {
+      const u32x4 q = vsrc[v];
+      count(q.x); count(q.x >> 16); count(q.y); count(q.y >> 16);
+      count(q.z); count(q.z >> 16); count(q.w); count(q.w >> 16);
+    }
+    for (uint32_t j = head + 8u * nv + tid; j < m; j += 256) count(src[j]);
+    e = stop;
   }
-  for (uint32_t j = head + 8u * nv + tid; j < nc; j += 256) count(src[j]);
   __syncthreads();
   uint32_t sum = 0;
 #pragma unroll
@@ -296,20 +335,22 @@ __global__ __launch_bounds__(kWave) void enc_plan_kernel(const bs_encode_task* _
 // indices fit 32 bits (a task has fewer than 2^32 elements), and at each step
 // all but the lane's own offset is the same in every lane.
 template <bool FULL>
-__device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB uint16_t* src1, uint32_t lane,
-                                             uint32_t nc, uint32_t nsteps, uint32_t k, uint32_t nf, uint32_t per,
-                                             const uint32_t* s_fc, const uint32_t* s_m, GLB uint16_t* words,
-                                             uint32_t& wpos, uint32_t (&x)[2], bool plane_here, GLB uint8_t* plane,
-                                             uint64_t pstride) {
-  // this lane's two words of step t, packed (first | second << 16); 0 past the end
+__device__ __forceinline__ void encode_steps(const GLB uint32_t* src2, const GLB uint16_t* src1, const SegMap& sm,
+                                             uint32_t lane, uint32_t nc, uint32_t nsteps, uint32_t k, uint32_t nf,
+                                             uint32_t per, const uint32_t* s_fc, const uint32_t* s_m,
+                                             GLB uint16_t* words, uint32_t& wpos, uint32_t (&x)[2], bool plane_here,
+                                             GLB uint8_t* plane, uint64_t pstride) {
+  // this lane's two words of step t, packed (first | second << 16); 0 past the
+  // end. A step's 128 elements lie in one unit, so their words are contiguous.
   auto load_step = [&](uint32_t t) -> uint32_t {
-    if (FULL) {                                         // unit (t/4)*nf + k, quarter t mod 4
-      const uint32_t e0 = ((t >> 2) * nf + k) * kUnit + (t & 3u) * kLanes;
-      return src2[(e0 >> 1) + lane];
-    }
-    const uint32_t e0 = nf * per + t * kLanes, j0 = t * kLanes + 2 * lane;
-    if (j0 + 1 < nc) return src2[(e0 >> 1) + lane];
-    return j0 < nc ? (uint32_t)src1[e0 + 2 * lane] : 0u;
+    // element of the step's first word: full chunks take unit (t/4)*nf + k at
+    // quarter t mod 4, the partial chunk runs on from nf * per
+    const uint32_t e0 = FULL ? ((t >> 2) * nf + k) * kUnit + (t & 3u) * kLanes : nf * per + t * kLanes;
+    const uint64_t w0 = unit_word(sm, e0 / kUnit) + e0 % kUnit;   // wave-uniform, even
+    if (FULL) return src2[(w0 >> 1) + lane];
+    const uint32_t j0 = t * kLanes + 2 * lane;
+    if (j0 + 1 < nc) return src2[(w0 >> 1) + lane];
+    return j0 < nc ? (uint32_t)src1[w0 + 2 * lane] : 0u;
   };
   const uint32_t nblk = (nsteps + kBlock - 1) / kBlock;
   uint32_t cur[kBlock];
@@ -413,12 +454,13 @@ __global__ __launch_bounds__(kWave) void enc_chunk_kernel(const bs_encode_task* 
   GLB uint16_t* words = (GLB uint16_t*)(chunk + 4u * kLanes);   // capacity per; filled from the end
   uint32_t x[2] = {kL, kL};
   uint32_t wpos = (uint32_t)per;
+  const SegMap sm = seg_map(T);
   if (k < nf)
-    encode_steps<true>(src2, src1, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m, words,
+    encode_steps<true>(src2, src1, sm, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m, words,
                        wpos, x, plane_here, plane, pstride);
   else
-    encode_steps<false>(src2, src1, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m, words,
-                        wpos, x, false, plane, pstride);
+    encode_steps<false>(src2, src1, sm, lane, nc, nsteps, (uint32_t)k, (uint32_t)nf, (uint32_t)per, s_fc, s_m,
+                        words, wpos, x, false, plane, pstride);
   GLB uint32_t* st = (GLB uint32_t*)chunk;
   st[lane] = x[0];
   st[kWave + lane] = x[1];
@@ -549,7 +591,7 @@ __global__ __launch_bounds__(kWave) void enc_assemble_kernel(const bs_encode_tas
 #pragma unroll
       for (uint32_t g = 0; g < 2; ++g) {
         const uint32_t j = (blk * kBlock + q) * kLanes + 2 * lane + g;
-        const uint32_t w = j < nc ? src[chunk_elem(k, j, nf, per)] : 0u;
+        const uint32_t w = j < nc ? src[src_word(T, chunk_elem(k, j, nf, per))] : 0u;
         const uint32_t byte = ((w >> 8) & 0x80u) | (w & 0x7Fu);
         const uint32_t k = q * 2 + g;
         b[k >> 2] |= byte << (8 * (k & 3));

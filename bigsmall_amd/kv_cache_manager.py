@@ -142,8 +142,15 @@ class CompressedKVCache:
             groups = []
             for t in (keys, values):
                 shape = list(t.shape)
-                blocked = t.detach().reshape(shape[:td] + [nb, block_tokens] + shape[td + 1:])
-                groups.append(_block_major(blocked, td).reshape(nb, block_elems))
+                pre, post = int(np.prod(shape[:td])), int(np.prod(shape[td + 1:]))
+                seg_len = block_tokens * post
+                if t.is_contiguous() and t.data_ptr() % 4 == 0 and seg_len % 512 == 0 and (T * post) % 8 == 0:
+                    # read in place: block b is `pre` segments of block_tokens * post
+                    # words, T * post words apart ([blocks, segments, seg_len])
+                    groups.append(t.detach().view(pre, nb, seg_len).permute(1, 0, 2))
+                else:
+                    blocked = t.detach().reshape(shape[:td] + [nb, block_tokens] + shape[td + 1:])
+                    groups.append(_block_major(blocked, td).reshape(nb, block_elems))
             if block_elems % 2 == 0:
                 arena, offs, lens = bf16_chunked.encode_device_rows(groups, steps=_kv_codec.KV_STEPS)
             else:       # odd blocks are not 4-byte aligned rows: one task per block view

@@ -140,6 +140,14 @@ typedef struct {
     uint64_t cap;         /* dst capacity, e.g. bs_chunk_encode_bound(n, 2, 128, steps) */
     uint32_t chunk_begin;
     uint32_t n_chunks;    /* ceil(n / (128 * steps)) */
+    /* Where the words lie: seg_len 0, contiguous (word e at src + e); else in
+     * segments of seg_len words (a multiple of 512) whose starts are
+     * seg_stride words apart (seg_stride >= seg_len, a multiple of 8): word e
+     * at src + (e / seg_len) * seg_stride + e % seg_len, every word below
+     * 2^32 from src. A block of tokens of a [heads, tokens, dim] KV tensor is
+     * such a task, read in place. */
+    uint64_t seg_len;
+    uint64_t seg_stride;
 } bs_encode_task;
 
 /* Device scratch bytes bs_chunk_encode_gpu needs. */

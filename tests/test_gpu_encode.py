@@ -223,7 +223,7 @@ def test_capacity_too_small_reports_bounds_and_writes_nothing_past_it(where):
     src = torch.from_numpy(w.view(np.int16).copy()).view(torch.bfloat16).to(dev)
     dst = torch.full((len(want) + 4096,), 0xAB, dtype=torch.uint8, device=dev)
     tasks = np.zeros(1, bc.ENCODE_TASK_DTYPE)
-    tasks[0] = (src.data_ptr(), n, dst.data_ptr(), cap, 0, nch)
+    tasks[0] = (src.data_ptr(), n, dst.data_ptr(), cap, 0, nch, 0, 0)
     d_tasks = upload_bytes(tasks.view(np.uint8), dev)
     L = _native.lib()
     wb = int(L.bs_chunk_encode_gpu_work_bytes(1, nch, steps))
@@ -237,3 +237,45 @@ def test_capacity_too_small_reports_bounds_and_writes_nothing_past_it(where):
     assert int(out_len.item()) == 0
     tail = dst[cap:].cpu().numpy()
     assert (tail == 0xAB).all(), f"{int((tail != 0xAB).sum())} bytes written at or past the capacity"
+
+
+@pytest.mark.parametrize("steps,seg_len,nseg,pad", [(16, 512, 7, 24), (16, 3072, 3, 8), (32, 1536, 5, 16),
+                                                   (256, 32768, 8, 0)])
+def test_segmented_rows_match_contiguous_encoding(steps, seg_len, nseg, pad):
+    """encode_device_rows on 3-D views [rows, segments, seg_len] (blocks of a
+    [heads, tokens, dim] tensor read in place; bs_encode_task seg_len and
+    seg_stride) writes the blobs the host encoder writes for each row copied
+    to contiguous memory. The cases put full and partial chunks across
+    segment boundaries, pad the segment stride, and start the segments 4 but
+    not 16 bytes past an alignment boundary."""
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    dev = torch.device("cuda", 0)
+    rows, stride = 3, seg_len + pad
+    g = torch.Generator().manual_seed(seg_len + nseg)
+    flat = (torch.randn(nseg * rows * stride + 2, generator=g) * 0.05).bfloat16().to(dev)[2:]
+    assert flat.data_ptr() % 16 == 4
+    view = flat.view(nseg, rows, stride)[:, :, :seg_len].permute(1, 0, 2)     # [rows, nseg, seg_len]
+    _say(f"[segmented] steps={steps} seg_len={seg_len} nseg={nseg} stride={stride} strides={view.stride()}")
+    arena, offs, lens = bc.encode_device_rows([view], steps=steps)
+    host = arena.cpu().numpy()
+    for r in range(rows):
+        words = view[r].contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        want = bc.encode_array(words, steps=steps, mode=bc.MODE_DENSE, lanes=128)
+        got = host[offs[r]:offs[r] + lens[r]].tobytes()
+        assert got == want, (r, len(got), len(want))
+    # a 2-D group in the same batch keeps its contiguous meaning
+    plain = view[0].contiguous().reshape(1, -1)
+    arena2, offs2, lens2 = bc.encode_device_rows([view, plain], steps=steps)
+    h2 = arena2.cpu().numpy()
+    assert h2[offs2[rows]:offs2[rows] + lens2[rows]].tobytes() == host[offs[0]:offs[0] + lens[0]].tobytes()
+
+
+def test_segmented_rows_reject_bad_views():
+    from bigsmall_amd.codecs import bf16_chunked as bc
+    dev = torch.device("cuda", 0)
+    x = torch.zeros(4, 3, 1024, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):                     # segments not a multiple of 512 words
+        bc.encode_device_rows([x[:, :, :1000].permute(1, 0, 2)])
+    with pytest.raises(ValueError):                     # segment starts not 8 words apart in multiples
+        bc.encode_device_rows([torch.zeros(4 * 3 * 1028, dtype=torch.bfloat16, device=dev)
+                               .view(4, 3, 1028)[:, :, :512].permute(1, 0, 2)])

@@ -202,7 +202,8 @@ def test_struct_layouts_match_the_header(tmp_path):
                           [(f[0], getattr(_native.BsChunkInfo, f[0]).offset, ctypes.sizeof(f[1]))
                            for f in _native.BsChunkInfo._fields_]),
         "bs_chunk_task": (["blob", "blob_bytes", "out", "n", "wg_begin", "n_chunks"], TASK_DTYPE),
-        "bs_encode_task": (["src", "n", "dst", "cap", "chunk_begin", "n_chunks"], bf16_chunked.ENCODE_TASK_DTYPE),
+        "bs_encode_task": (["src", "n", "dst", "cap", "chunk_begin", "n_chunks", "seg_len", "seg_stride"],
+                           bf16_chunked.ENCODE_TASK_DTYPE),
         "bs_span": (["src", "dst", "len"], bf16_chunked.SPAN_DTYPE),
         "bs_se_stream": (["words", "x0", "n_words", "tail", "n", "first", "stride", "reserved"],
                          _refstreams.SE_STREAM_DTYPE),
