@@ -30,7 +30,7 @@ import numpy as np
 
 from .. import _native
 from ..device import (ChunkBatch, ChunkJob, StatusWord, inspect_chunk_header, require_gpu, stream_ptr,
-                      upload_bytes)
+                      upload_bytes, upload_bytes_async)
 
 CODEC_BF16 = "bf16_chunked_v1"
 CODEC_FP8 = "fp8_chunked_v1"
@@ -101,14 +101,20 @@ def _run_encode(dev, tasks: np.ndarray, total_chunks: int, steps: int, stream):
     checked status word)."""
     import torch
     L = _native.lib()
-    d_tasks = upload_bytes(tasks.view(np.uint8), dev)
+    # one upload: a zeroed result area (the status word, the low half of
+    # element 0, then the lengths) and the task table after it; one copy on
+    # the encode's stream brings the results back
+    nres = 8 * (1 + len(tasks))
+    toff = (nres + 255) & ~255                          # the task table stays 256-byte aligned
+    buf = np.zeros(toff + tasks.nbytes, np.uint8)
+    buf[toff:] = tasks.view(np.uint8)
+    d_buf = upload_bytes_async(buf, dev, stream)
+    res = d_buf[:nres].view(torch.int64)
+    d_tasks = d_buf[toff:]
     wb = int(L.bs_chunk_encode_gpu_work_bytes(len(tasks), total_chunks, steps))
-    work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
-    # the status word (the low half of element 0) and the lengths in one
-    # buffer, so that one copy on the encode's stream brings both back
-    res = torch.zeros(1 + len(tasks), dtype=torch.int64, device=dev)
-    st = StatusWord(dev)
-    st.t = res[:1].view(torch.int32)[:1]
+    with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+        work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
+    st = StatusWord(view=res[:1].view(torch.int32)[:1])
     _native.check(L.bs_chunk_encode_gpu(d_tasks.data_ptr(), len(tasks), total_chunks, steps, work.data_ptr(), wb,
                                         res[1:].data_ptr(), st.ptr, stream_ptr(stream, dev)), "bs_chunk_encode_gpu")
     with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
@@ -135,7 +141,7 @@ def _pack(arena, src_offs: np.ndarray, lens: np.ndarray, dev, st: StatusWord, st
         spans["src"] = arena.data_ptr() + src_offs[live].astype(np.uint64)
         spans["dst"] = tight.data_ptr() + offs[live].astype(np.uint64)
         spans["len"] = lens[live]
-        d_spans = upload_bytes(spans.view(np.uint8), dev)
+        d_spans = upload_bytes_async(spans.view(np.uint8), dev, stream)
         _native.check(_native.lib().bs_copy_spans(d_spans.data_ptr(), len(spans), int(lens.max()), st.ptr,
                                                   stream_ptr(stream, dev)), "bs_copy_spans")
         if stream is not None:        # the launch's inputs stay allocated until it has run

@@ -4,6 +4,8 @@ happens in the HIP kernels of libbigsmall_hip.so.
 """
 from __future__ import annotations
 
+import contextlib
+
 import ctypes
 from dataclasses import dataclass
 
@@ -50,12 +52,33 @@ def upload_bytes(data, device, align: int = 256):
     return out
 
 
+def upload_bytes_async(data, device, stream=None):
+    """upload_bytes through pinned staging with a non-blocking copy on
+    `stream` (the current stream if None): the host does not wait for the
+    copy, or for the work queued before it; later work on that stream sees the
+    bytes. The staging block comes from torch's pinned caching allocator,
+    which keeps it from reuse until the copy has run."""
+    import torch
+    arr = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data.view(np.uint8).reshape(-1)
+    out = torch.empty(len(arr), dtype=torch.uint8, device=device)
+    if len(arr):
+        host = torch.empty(len(arr), dtype=torch.uint8, pin_memory=True)
+        host.numpy()[:] = arr
+        with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+            out.copy_(host, non_blocking=True)
+        if stream is not None:
+            out.record_stream(stream)
+    return out
+
+
 class StatusWord:
     """Device int32 that kernels OR their BS_DEV_* bits into."""
 
-    def __init__(self, device):
+    def __init__(self, device=None, view=None):
+        """A new zeroed word on `device`, or `view`: an int32 element of
+        another device buffer that is already zero."""
         import torch
-        self.t = torch.zeros(1, dtype=torch.int32, device=device)
+        self.t = view if view is not None else torch.zeros(1, dtype=torch.int32, device=device)
 
     @property
     def ptr(self) -> int:
