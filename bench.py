@@ -876,7 +876,7 @@ def run_streaming(args) -> dict:
         h2d = measure_h2d(dev)
         ids = torch.randint(0, 128256, (1, 128), generator=torch.Generator().manual_seed(1)).cuda()
         res = {}
-        for prefetch in (0, 1):
+        for prefetch in (0, 1, 2):
             m = BigSmallStreamingModel.from_pretrained(path, device="cuda", prefetch=prefetch)
             m.forward(ids)
             torch.cuda.synchronize()
@@ -914,6 +914,7 @@ def run_streaming(args) -> dict:
             "config": {"workload": "streaming_llama3_8b_shape", "layers": n_layers,
                        "compressed_bytes_per_layer": per_layer, "prefetch": 1},
             "prefetch0_ms_per_layer": round(res[0] * 1e3 / n_layers, 3),
+            "prefetch2_ms_per_layer": round(res[2] * 1e3 / n_layers, 3),
             "decoder_load": {"file_bytes": file_bytes, "seconds": round(load_s, 4),
                              "file_GBps": round(file_bytes / load_s / 1e9, 2),
                              "frac_of_h2d": round(file_bytes / load_s / h2d, 4)},
