@@ -754,17 +754,18 @@ def run_c3(args) -> dict:
     # 67M-element tensor 1,214 chunks, fewer than the 4,096 wavefront slots of
     # the GPU; 128 steps fill them (4,096 chunks) at a small ratio cost
     R = max(1, args.rotate)
-    lanes = args.lanes or bc.DEFAULT_LANES
     coders = [("rans_bsck", bc.CODER_RANS), ("tans_bsck", bc.CODER_TANS)]
     if args.rans_only:
         coders = coders[:1]
     for name, w in tensors:
         res[name] = {}
-        # fp8 tensors code byte pairs (one symbol per two bytes): half the
-        # steps per chunk keep the chunk count, and so the GPU's fill, of the
-        # bf16 tensors (4,096 chunks of 128 x 128 at the default)
-        steps = args.chunk_steps or max(16, (128 * 128 // lanes) // (2 if w.dtype == np.uint8 else 1))
         for key, coder in coders:
+            # the codecs' state counts (tANS: four states per wavefront lane);
+            # fp8 tensors code byte pairs (one symbol per two bytes): half the
+            # steps per chunk keep the chunk count, and so the GPU's fill, of
+            # the bf16 tensors (4,096 chunks of 16,384 elements)
+            lanes = args.lanes or (bc.TANS_LANES if coder == bc.CODER_TANS else bc.DEFAULT_LANES)
+            steps = args.chunk_steps or max(16, (128 * 128 // lanes) // (2 if w.dtype == np.uint8 else 1))
             blob = bc.encode_array(w, steps=steps, lanes=lanes, coder=coder)
             inf = bc.info(blob)
             # R copies of the blob and of the output, decoded in turn: the working
@@ -789,7 +790,8 @@ def run_c3(args) -> dict:
                               (bc.CODEC_BF16_TANS if w.dtype == np.uint16 else bc.CODEC_FP8_TANS),
                               "ms": round(ms, 4), "GBps": round(gbps, 2), "frac": round(gbps / HBM_PEAK_GBPS, 4),
                               "ratio_pct": round(100 * len(blob) / w.nbytes, 3), "plane_mode": inf.plane_mode,
-                              "elem_bytes": inf.elem_bytes, "chunk_steps": steps, "distinct_copies": R}
+                              "elem_bytes": inf.elem_bytes, "chunk_steps": steps, "lanes": lanes,
+                              "distinct_copies": R}
             log(f"[c3] {name}: {key} mode {inf.plane_mode} {ms:.4f} ms, {gbps:.0f} GB/s "
                 f"({100 * gbps / HBM_PEAK_GBPS:.1f} %), ratio {100 * len(blob) / w.nbytes:.2f} %")
     for name, (blob, cpu_gbps) in ({} if args.rans_only or args.engine_only else cpu_baseline_c3(tensors)).items():
@@ -1076,8 +1078,10 @@ def main():
     from bigsmall_amd.codecs import bf16_chunked as bc
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
 
-    steps = args.chunk_steps or bc.DEFAULT_STEPS
-    lanes = args.lanes or bc.DEFAULT_LANES
+    tans = args.coder == "tans"
+    # the tANS codec's geometry: four states per wavefront lane over half the steps
+    steps = args.chunk_steps or (bc.tans_steps(bc.DEFAULT_STEPS) if tans else bc.DEFAULT_STEPS)
+    lanes = args.lanes or (bc.TANS_LANES if tans else bc.DEFAULT_LANES)
     R = max(1, args.rotate)
     t0 = time.time()
     base_words = make_layer(0)

@@ -5,7 +5,8 @@
 //   [0]  "BSCK"  [4] u8 version (3; 2 = the earlier chunk-contiguous layout,
 //        read too)  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
 //   [7]  u8 prec_log2 = 12  [8] u64 n  [16] u32 steps  [20] u16 lanes = 64*K
-//   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS, 1 tANS), 3 zero bytes
+//   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS; tANS: 1 with a
+//        state array, 2 with the states at the stream head), 3 zero bytes
 //   [32] n_syms x u32 symbol entries: bits 0..15 output value (bf16 word with
 //        zero sign/mantissa for exponent symbols, the exact word/byte, or an
 //        exponent pair e0 | e1 << 4), bits 16..28 quantised frequency (sum
@@ -14,11 +15,15 @@
 //   n_chunks x {u64 offset, u32 n_words (rANS: renorm words; tANS: stream
 //        bits), u32 n_plane}
 //   pad to 256; plane_mode 1 and 3 only: the dense plane region, nf*per bytes
-//   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l) |
-//        the stream (rANS: n_words x u16 renorm words; tANS: whole u32 words
-//        of an LSB-first bit stream), pad 16 | n_plane plane bytes (pad 16),
-//        the plane bytes omitted for a full chunk in plane_mode 1 and 3
-//   pad to 256 (the blob length is a multiple of 256)
+//   chunk (16-aligned): 64*K x u32 initial states (state v = g*64 + l; not
+//        in coder 2) | the stream (rANS: n_words x u16 renorm words; tANS:
+//        whole u32 words of an LSB-first bit stream, in coder 2 starting with
+//        the 12-bit initial states, lane l's state g at bit 12*(l*K + g)),
+//        pad 16 | n_plane plane bytes (pad 16), the plane bytes omitted for a
+//        full chunk in plane_mode 1 and 3
+//   pad to 256 (the blob length is a multiple of 256; coder 2: and at least
+//        the last chunk's offset + 256, so 256 bytes from any chunk's start
+//        are inside the blob)
 // Version 2 has no plane region (every plane inline), coder 0, no plane mode
 // 3, chunks holding contiguous elements (c*per + j) and 16-byte padding.
 //
@@ -62,7 +67,7 @@
 // fell below L = 2^16; the words are placed with a wavefront ballot + mbcnt
 // prefix. A valid chunk ends with every state back at x == L and every word
 // and plane byte consumed.
-// tANS (coder 1): X in [0, 4096); e = table[X]; s = e's symbol;
+// tANS (coders 1 and 2): X in [0, 4096); e = table[X]; s = e's symbol;
 //   X = newX | next nb bits  (newX has nb zero low bits)
 // Each step every lane reads its K states' bits in order (and a compact
 // symbol's 8 plane bits after its state bits) from one stream position:
@@ -634,9 +639,11 @@ __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, c
   const uint32_t lane = C.lane;
   const uint32_t need_w = min(kNeed, C.n_words - min(S.wptr, C.n_words));
   const uint32_t need_p = MODE == 2 ? min(kBlkElems, C.n_plane - S.pptr) : 0u;
-  if (S.wld - S.wptr < need_w || (MODE == 2 && S.pld - S.pptr < need_p)) {
+  // wld < wptr + need, not wld - wptr < need: a coder-2 chunk starts with
+  // wptr past the ring words of its states, before any word has landed
+  if (S.wld < S.wptr + need_w || (MODE == 2 && S.pld - S.pptr < need_p)) {
     land_segments<K, MODE>(S, F, wring, pring, lane);
-    while (S.wld - S.wptr < need_w) {
+    while (S.wld < S.wptr + need_w) {
       store_wseg<G>(wring, S.wld, load_seg<V>(C.wsrc, S.wld / (G::kLaneSeg / 2u), C.wvalid, lane, C.safe), lane);
       S.wld += G::kWSeg;
     }
@@ -822,14 +829,16 @@ __device__ __forceinline__ void progress_priority(uint32_t blk, uint32_t nblk, b
 // plane mode, EB = element bytes (2 for pair mode, whose elements are byte
 // pairs), PARTIAL = chunk may be shorter than 64*K*steps (the tensor's last
 // chunk), CODER = 0 rANS, 1 tANS. n_words is the chunk table's count: renorm
-// words (rANS) or stream bits (tANS, whose stream is whole u32 words).
+// words (rANS) or stream bits (tANS, whose stream is whole u32 words). fl:
+// bit 0 = the later of its CU's two workgroups, bit 1 = tANS states at the
+// stream head (coder 2; the stream then holds at least their 12 * 64K bits).
 template <int K, int MODE, int EB, bool PARTIAL, int CODER>
 __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tbl, LDS uint16_t* wring,
                                              LDS uint8_t* pring, LDS uint8_t* stage,
                                              const GLB uint8_t* __restrict__ cbase, uint32_t n_words,
                                              uint32_t n_plane, const GLB uint8_t* dplane, uint64_t pstride,
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
-                                             uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
+                                             uint32_t nc, uint32_t nsteps, int32_t* status, uint32_t fl) {
   constexpr int RM = ring_mode<MODE, CODER>();
   constexpr int MAXB = CODER == 0 ? 0 : (MODE == 2 ? 20 : 12);   // tANS bits per element at most
   typedef Geo<K, RM> G;
@@ -839,8 +848,11 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
   const uint32_t n_bits = n_words;                               // tANS: the stream's length in bits
   if (CODER == 1) n_words = 2u * ((n_bits + 31u) / 32u);          // in 16-bit ring words
   const uint32_t wbytes = pad16(n_words * 2u);
-  C.wsrc = cbase + 4u * kStates;
-  C.psrc = cbase + 4u * kStates + wbytes;
+  const bool younger = fl & 1u;
+  const bool head = CODER == 1 && (fl & 2u);
+  const uint32_t sarr = head ? 0u : 4u * kStates;                // bytes of the u32 state array
+  C.wsrc = cbase + sarr;
+  C.psrc = cbase + sarr + wbytes;
   C.dplane = dplane ? dplane : C.psrc;
   C.pstride = pstride;
   C.safe = cbase;
@@ -857,15 +869,32 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
 
   ChunkState<K> S;
   bool bad_init = false;
+  S.wptr = S.wld = S.pptr = S.pld = S.bpos = 0;
+  if (head) {
+    // the lane's K 12-bit states at bit 12K * lane of the stream: at most 48
+    // bits from a shift below 32, so inside three words; words past the
+    // stream's last are not read (the last is read again in their place, and
+    // its bits beyond the states are not used)
+    const uint32_t b0 = 12u * K * C.lane, w0 = b0 >> 5, last = (n_bits + 31u) / 32u - 1u;
+    const GLB uint32_t* s32 = (const GLB uint32_t*)cbase;
+    const uint32_t r0 = s32[w0], r1 = s32[min(w0 + 1u, last)];
+    const uint32_t lo = __builtin_amdgcn_alignbit(r1, r0, b0);
+    const uint32_t hi = K == 4 ? __builtin_amdgcn_alignbit(s32[min(w0 + 2u, last)], r1, b0) : 0u;
+    const uint64_t win = (uint64_t)lo | ((uint64_t)hi << 32);
 #pragma unroll
-  for (int g = 0; g < K; ++g) {
-    S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
-    if (CODER == 1) {                                   // a table index: kept inside the table
-      bad_init |= S.x[g] > 4095u;
-      S.x[g] &= 4095u;
+    for (int g = 0; g < K; ++g) S.x[g] = (uint32_t)(win >> (12 * g)) & 4095u;
+    S.bpos = 12u * kStates;
+    S.wptr = (S.bpos >> 5) << 1;                        // ring words before the first element's bits
+  } else {
+#pragma unroll
+    for (int g = 0; g < K; ++g) {
+      S.x[g] = ((const GLB uint32_t*)cbase)[g * kWave + C.lane];
+      if (CODER == 1) {                                 // a table index: kept inside the table
+        bad_init |= S.x[g] > 4095u;
+        S.x[g] &= 4095u;
+      }
     }
   }
-  S.wptr = S.wld = S.pptr = S.pld = S.bpos = 0;
 
   if (RM == 2 && C.lane == 0) *(LDS u32x4*)(pring + G::kPZero) = u32x4{0u, 0u, 0u, 0u};
 
@@ -957,20 +986,20 @@ __device__ __forceinline__ void decode_chunk_mode(uint32_t mode, const LDS uint6
                                                   LDS uint8_t* pring, LDS uint8_t* stage, const GLB uint8_t* cbase,
                                                   uint32_t nw, uint32_t np, const GLB uint8_t* dplane,
                                                   uint64_t pstride, GLB uint8_t* out, uint64_t ubase, uint64_t ustride,
-                                                  uint32_t nc, uint32_t nsteps, int32_t* status, bool younger) {
+                                                  uint32_t nc, uint32_t nsteps, int32_t* status, uint32_t fl) {
   if constexpr (EB == 1) {   // byte symbols (no plane); exponent pairs run as 2-byte elements
     if (mode == 3)
-      decode_chunk<K, 3, 2, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 3, 2, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
     else
-      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
   } else {
     if (mode == 0) {
-      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 0, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
     } else if (mode == 1) {
-      decode_chunk<K, 1, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+      decode_chunk<K, 1, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
     } else {
       if constexpr (COMPACT)
-        decode_chunk<K, 2, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+        decode_chunk<K, 2, EB, PARTIAL, CODER>(tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
     }
   }
 }
@@ -981,13 +1010,13 @@ __device__ __forceinline__ void decode_chunk_c(uint32_t eb, bool partial, uint32
                                                const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
                                                const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
                                                uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
-                                               int32_t* status, bool younger) {
+                                               int32_t* status, uint32_t fl) {
   if (eb == 2) {
-    if (partial) decode_chunk_mode<K, 2, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
-    else decode_chunk_mode<K, 2, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    if (partial) decode_chunk_mode<K, 2, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
+    else decode_chunk_mode<K, 2, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
   } else {
-    if (partial) decode_chunk_mode<K, 1, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
-    else decode_chunk_mode<K, 1, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    if (partial) decode_chunk_mode<K, 1, true, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
+    else decode_chunk_mode<K, 1, false, COMPACT, CODER>(mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
   }
 }
 
@@ -997,11 +1026,11 @@ __device__ __forceinline__ void decode_chunk_k(uint32_t eb, bool partial, uint32
                                                LDS uint8_t* stage, const GLB uint8_t* cbase, uint32_t nw, uint32_t np,
                                                const GLB uint8_t* dplane, uint64_t pstride, GLB uint8_t* out,
                                                uint64_t ubase, uint64_t ustride, uint32_t nc, uint32_t nsteps,
-                                               int32_t* status, bool younger) {
+                                               int32_t* status, uint32_t fl) {
   if (coder == 0)
-    decode_chunk_c<K, COMPACT, 0>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    decode_chunk_c<K, COMPACT, 0>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
   else
-    decode_chunk_c<K, COMPACT, 1>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, younger);
+    decode_chunk_c<K, COMPACT, 1>(eb, partial, mode, tbl, wring, pring, stage, cbase, nw, np, dplane, pstride, out, ubase, ustride, nc, nsteps, status, fl);
 }
 
 template <bool COMPACT>
@@ -1080,7 +1109,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const uint32_t ver = w1 & 0xFFu, eb = (w1 >> 8) & 0xFFu, mode = (w1 >> 16) & 0xFFu;
   const uint32_t w7 = rfl(h1.w), coder = w7;             // byte 28: coder; bytes 29..31 zero
   if (magic != 0x4B435342u ||                                             // "BSCK"
-      (ver != 2 && ver != kVersion) || (eb != 1 && eb != 2) || mode > 3 || (w1 >> 24) != 12 || coder > 1 ||
+      (ver != 2 && ver != kVersion) || (eb != 1 && eb != 2) || mode > 3 || (w1 >> 24) != 12 || coder > 2 ||
       (ver == 2 && (coder != 0 || mode == 3)) || (!COMPACT && mode == 2) ||
       (eb == 1 ? (mode != 0 && mode != 3) : mode == 3)) {
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_HEADER);
@@ -1105,7 +1134,7 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
     if (threadIdx.x == 0) atomicOr(status, BS_DEV_ERR_COUNT);
     return;
   }
-  const uint32_t stab = pad16(32u + 4u * nsym);               // tANS decode table (coder 1)
+  const uint32_t stab = pad16(32u + 4u * nsym);               // tANS decode table (coders 1 and 2)
   const uint32_t ctab = stab + (coder ? 4u * kTansSlots : 0u);
   const uint64_t nf = ne / per;                               // full chunks
   // layout version 3 keeps the full chunks' dense planes in one region;
@@ -1286,10 +1315,14 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const bool has_plane = mode == 1 || mode == 3;      // dense plane
   const bool split = region && full;                  // dense plane in the plane region
   const uint64_t pblk = (uint64_t)bsteps * lanes;      // plane bytes per block
-  // stream: rANS nw 16-bit words; tANS nw bits (at most 12 per element, 20 with compact plane bits)
+  // stream: rANS nw 16-bit words; tANS nw bits (at most 12 per element, 20 with compact plane
+  // bits; coder 2: the 12-bit states first). Coder 2 has no state array, and 256 bytes from the
+  // chunk's start lie inside the blob (ring loads of lanes past a stream's end read there).
   const uint32_t sbytes = coder ? pad16(((nw + 31u) / 32u) * 4u) : pad16(nw * 2u);
-  bool ok = (off % 16) == 0 && off + 4ull * lanes + sbytes + (split ? 0u : pad16(np)) <= T.blob_bytes &&
-            (coder ? (uint64_t)nw <= (uint64_t)nc * (mode == 2 ? 20u : 12u) : nw <= nsteps * lanes) &&
+  const uint64_t sarr = coder == 2 ? 0u : 4ull * lanes, hbits = coder == 2 ? 12ull * lanes : 0u;
+  bool ok = (off % 16) == 0 && off + sarr + sbytes + (split ? 0u : pad16(np)) <= T.blob_bytes &&
+            (coder != 2 || (off + 256u <= T.blob_bytes && nw >= hbits)) &&
+            (coder ? (uint64_t)nw <= (uint64_t)nc * (mode == 2 ? 20u : 12u) + hbits : nw <= nsteps * lanes) &&
             T.out != nullptr && ((uintptr_t)T.out & 15u) == 0;
   if (has_plane) ok = ok && np == dense_plane;
   if (mode == 2) ok = ok && (coder ? np == 0 : np <= nc);
@@ -1312,16 +1345,17 @@ __global__ __launch_bounds__(kThreads) void bsck_decode_kernel(const bs_chunk_ta
   const bool inter = ver == kVersion && full;
   const uint64_t ubase = inter ? (uint64_t)chunk * kUnit : cbase_idx;
   const uint64_t ustride = inter ? nf * kUnit : kUnit;
-  const bool younger = blockIdx.x >= first_round;      // the later of its CU's two workgroups
+  // bit 0: the later of its CU's two workgroups; bit 1: tANS states at the stream head
+  const uint32_t fl = (blockIdx.x >= first_round ? 1u : 0u) | (coder == 2 ? 2u : 0u);
   if (lanes == 64)
     decode_chunk_k<1, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
-                               out, ubase, ustride, nc, nsteps, status, younger);
+                               out, ubase, ustride, nc, nsteps, status, fl);
   else if (lanes == 128)
     decode_chunk_k<2, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
-                               out, ubase, ustride, nc, nsteps, status, younger);
+                               out, ubase, ustride, nc, nsteps, status, fl);
   else
     decode_chunk_k<4, COMPACT>(eb, partial, mode, coder, s_tbl, wring, pring, stage, cbase, nw, np, dplane, pstride,
-                               out, ubase, ustride, nc, nsteps, status, younger);
+                               out, ubase, ustride, nc, nsteps, status, fl);
 }
 
 inline uint32_t groups_for(uint32_t n_chunks) { return (n_chunks + kWaves - 1) / kWaves; }
@@ -1384,7 +1418,7 @@ int bs_chunk_inspect(const uint8_t* h, uint64_t len, bs_chunk_info* info) {
   const uint32_t mode = info->plane_mode, eb = info->elem_bytes;
   if (h[7] != 12 || (info->lanes != 64 && info->lanes != 128 && info->lanes != 256) || info->steps == 0 ||
       info->steps % (2 * kBlockMax) || info->n_syms == 0 || info->n_syms > 256 || (eb != 1 && eb != 2) || mode > 3 ||
-      (eb == 1 ? (mode != 0 && mode != 3) : mode == 3) || info->coder > 1 ||
+      (eb == 1 ? (mode != 0 && mode != 3) : mode == 3) || info->coder > 2 ||
       (h[4] == 2 && (info->coder != 0 || mode == 3)) || (mode == 3 && (info->n & 1)))
     return BS_ERR_FORMAT;
   const uint64_t per = (uint64_t)info->lanes * info->steps;

@@ -16,7 +16,8 @@
 //                                 Needs an even element count.
 // The encoder picks the smallest by estimated entropy unless a mode is forced.
 //
-// Two entropy coders share the layout (header byte 28):
+// Two entropy coders share the layout (header byte 28, which also says where a
+// tANS chunk keeps its initial states):
 //   coder 0, rANS: 64*K interleaved 32-bit states per chunk (K = lanes / 64 per
 //     wavefront lane; L = 2^16, M = 2^12, 16-bit renormalisation: the
 //     reference's state machine, bigsmall/codecs/rans.py:115-162). State
@@ -34,6 +35,12 @@
 //     bits, then in compact mode its 8 raw plane bits) are appended to one
 //     LSB-first bit stream per chunk in chunk element order, which is the
 //     decoder's order (steps ascending, then lanes, then the lane's states).
+//     Coder 1 stores the chunk's initial states X as 64*K u32 words before
+//     the stream (state v = g*64 + l); coder 2 stores them as 12-bit fields
+//     at the head of the stream itself, in the same reading order (lane l's
+//     state g at bit 12*(l*K + g)), which saves 2.5 bytes per state. A
+//     coder-2 blob also extends to at least 256 bytes past its last chunk's
+//     offset, so that every chunk has 256 readable bytes from its start.
 //
 // Chunk c holds elements of the tensor in 512-element units: a full chunk
 // (c < nf = n / (lanes*steps)) holds units c, nf + c, 2nf + c, ..., so the
@@ -79,7 +86,7 @@ constexpr uint32_t kTabSlots = 4096;      // tANS table positions (= kM)
 
 struct Plan {
   int mode = 1;
-  int coder = 0;                // 0 rANS, 1 tANS
+  int coder = 0;                // 0 rANS, 1 tANS (u32 state array), 2 tANS (states at the stream head)
   uint32_t eb = 2;
   uint32_t nsym = 0;
   uint32_t value[256];
@@ -314,7 +321,7 @@ bool make_plan(const std::vector<uint64_t>& hist, const std::vector<uint64_t>* p
   uint32_t c = 0;
   for (uint32_t s = 0; s < P.nsym; ++s) { P.cum[s] = c; c += P.freq[s]; }
   if (c != kM || P.nsym < 1 || P.nsym > 256) return false;
-  if (coder == 1) build_tans(P);
+  if (coder != 0) build_tans(P);
   return true;
 }
 
@@ -399,12 +406,14 @@ void encode_chunk_rans(const Plan& P, const std::vector<uint8_t>& sym, const std
   else if (n_plane) memcpy(out.data() + 4 * lanes + wb, plane.data(), n_plane);
 }
 
-// tANS: states (u32 X each) | bit stream (whole u32 words, 16-padded) |
-// plane (modes 1 and 3; 16-padded, or to *plane_out). n_bits = the stream's
-// length in bits; compact mode keeps its plane bytes in the stream.
+// tANS: [coder 1: states, u32 X each] | bit stream (whole u32 words,
+// 16-padded; coder 2: the states' 12-bit fields first) | plane (modes 1 and
+// 3; 16-padded, or to *plane_out). n_bits = the stream's length in bits;
+// compact mode keeps its plane bytes in the stream.
 void encode_chunk_tans(const Plan& P, const std::vector<uint8_t>& sym, const std::vector<uint8_t>& pb, uint32_t nc,
                        uint32_t lanes, uint32_t& n_bits, uint32_t& n_plane, std::vector<uint8_t>& out,
                        std::vector<uint8_t>* plane_out) {
+  const bool head = P.coder == 2;
   const uint32_t nsteps = (nc + lanes - 1) / lanes;
   std::vector<uint32_t> field(nc);       // element j's bits, LSB first
   std::vector<uint8_t> width(nc);
@@ -423,7 +432,7 @@ void encode_chunk_tans(const Plan& P, const std::vector<uint8_t>& sym, const std
       width[j] = (uint8_t)w;
     }
   }
-  uint64_t total = 0;
+  uint64_t total = head ? 12ull * lanes : 0;
   for (uint32_t j = 0; j < nc; ++j) total += width[j];
   n_bits = (uint32_t)total;
   const uint64_t sbytes = pad16(((total + 31) / 32) * 4);
@@ -431,11 +440,20 @@ void encode_chunk_tans(const Plan& P, const std::vector<uint8_t>& sym, const std
   if (P.mode == 1 || P.mode == 3) plane = dense_plane(pb, nc, lanes);
   n_plane = (uint32_t)plane.size();
   const uint64_t pbytes = plane_out ? 0 : pad16(n_plane);
-  out.assign(4 * lanes + sbytes + pbytes, 0);
-  for (uint32_t l = 0; l < lanes; ++l) put32(out.data() + 4 * l, x[l] - kTabSlots);
-  uint8_t* bs = out.data() + 4 * lanes;
+  const uint32_t sarr = head ? 0u : 4 * lanes;   // bytes of the u32 state array
+  out.assign(sarr + sbytes + pbytes, 0);
+  if (!head)
+    for (uint32_t l = 0; l < lanes; ++l) put32(out.data() + 4 * l, x[l] - kTabSlots);
+  uint8_t* bs = out.data() + sarr;
   uint64_t acc = 0;                       // pending bits, LSB first
   uint32_t pending = 0;
+  if (head) {
+    for (uint32_t i = 0; i < lanes; ++i) {  // reading order i = l*K + g: state v = g*64 + l
+      acc |= (uint64_t)(x[(i % K) * kWave + i / K] - kTabSlots) << pending;
+      pending += 12;
+      if (pending >= 32) { put32(bs, (uint32_t)acc); bs += 4; acc >>= 32; pending -= 32; }
+    }
+  }
   for (uint32_t j = 0; j < nc; ++j) {     // chunk element order is the decoder's reading order
     acc |= (uint64_t)field[j] << pending; // < 2^52: pending < 32, fields of at most 20 bits
     pending += width[j];
@@ -443,7 +461,7 @@ void encode_chunk_tans(const Plan& P, const std::vector<uint8_t>& sym, const std
   }
   if (pending) put32(bs, (uint32_t)acc);
   if (plane_out) plane_out->swap(plane);
-  else if (n_plane) memcpy(out.data() + 4 * lanes + sbytes, plane.data(), n_plane);
+  else if (n_plane) memcpy(out.data() + sarr + sbytes, plane.data(), n_plane);
 }
 
 }  // namespace
@@ -458,14 +476,16 @@ static bool chunk_ok(uint32_t lanes, uint32_t steps) { return (uint64_t)lanes * 
 int bs_chunk_encode_bound_ex(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t coder,
                              uint64_t* bound) {
   if (!bound || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes) ||
-      !chunk_ok(lanes, steps) || (coder != 0 && coder != 1))
+      !chunk_ok(lanes, steps) || coder < 0 || coder > 2)
     return BS_ERR_ARG;
   const uint64_t per = (uint64_t)lanes * steps;
   const uint64_t nch = (n + per - 1) / per;
-  // per element at most one 16-bit word (rANS) or 20 bits (tANS), and one plane byte
-  const uint64_t stream = coder == 0 ? pad16(2 * per) : pad16(((per * 20 + 31) / 32) * 4);
-  *bound = pad16(32 + 4 * 256) + (coder == 1 ? 4 * kTabSlots : 0) + 16 * nch +
-           nch * (4 * lanes + stream + pad16(per) + 32) + 512;
+  // per element at most one 16-bit word (rANS) or 20 bits (tANS), and one
+  // plane byte; per state 4 bytes (rANS, tANS coder 1) or 12 bits (coder 2);
+  // and the coder-2 tail of up to 256 bytes after the last chunk
+  const uint64_t stream = coder == 0 ? pad16(2 * per) : pad16(((per * 20 + 12ull * lanes + 31) / 32) * 4);
+  *bound = pad16(32 + 4 * 256) + (coder != 0 ? 4 * kTabSlots : 0) + 16 * nch +
+           nch * (4 * lanes + stream + pad16(per) + 32) + 512 + 256;
   return BS_OK;
 }
 
@@ -476,7 +496,7 @@ int bs_chunk_encode_bound(uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint3
 int bs_chunk_encode_ex(const void* src, uint64_t n, uint32_t elem_bytes, uint32_t lanes, uint32_t steps, int32_t mode,
                        int32_t coder, uint8_t* dst, uint64_t cap, uint64_t* out_len, int n_threads) {
   if (!out_len || (elem_bytes != 1 && elem_bytes != 2) || steps == 0 || steps % kStepAlign || !lanes_ok(lanes) ||
-      !chunk_ok(lanes, steps) || (coder != 0 && coder != 1))
+      !chunk_ok(lanes, steps) || coder < 0 || coder > 2)
     return BS_ERR_ARG;
   if (n == 0) { *out_len = 0; return BS_OK; }
   if (!src || !dst) return BS_ERR_ARG;
@@ -498,7 +518,7 @@ int bs_chunk_encode_ex(const void* src, uint64_t n, uint32_t elem_bytes, uint32_
   const uint64_t nf = ne / per;                       // full chunks
   const bool split_plane = P.mode == 1 || P.mode == 3;   // full chunks' dense planes go to the plane region
   const uint64_t stab = pad16(32 + 4ull * P.nsym);
-  const uint64_t ctab = stab + (coder == 1 ? 4ull * kTabSlots : 0);   // tANS: the decode table first
+  const uint64_t ctab = stab + (coder != 0 ? 4ull * kTabSlots : 0);   // tANS: the decode table first
   const uint64_t preg = pad256(ctab + 16ull * nch);  // plane region: nf*per bytes in modes 1 and 3
   const uint64_t pblk = (uint64_t)block_steps(lanes) * lanes;   // plane bytes per block
   std::vector<std::vector<uint8_t>> chunks(nch);
@@ -524,7 +544,8 @@ int bs_chunk_encode_ex(const void* src, uint64_t n, uint32_t elem_bytes, uint32_
   std::vector<uint64_t> offs(nch);
   for (uint32_t c = 0; c < nch; ++c) { offs[c] = total; total += chunks[c].size(); }
   const uint64_t end = total;
-  total = pad256(total);                             // blob lengths are multiples of 256
+  // blob lengths are multiples of 256; coder 2: 256 bytes at least from the last chunk's start
+  total = pad256(coder == 2 ? std::max(total, offs[nch - 1] + 256) : total);
   if (total > cap) return BS_ERR_CAP;
   memset(dst, 0, preg);
   memcpy(dst, "BSCK", 4);
@@ -533,7 +554,7 @@ int bs_chunk_encode_ex(const void* src, uint64_t n, uint32_t elem_bytes, uint32_
   put32(dst + 24, nch); put32(dst + 28, (uint32_t)coder);
   for (uint32_t s = 0; s < P.nsym; ++s)
     put32(dst + 32 + 4 * s, (P.value[s] & 0xFFFF) | (P.freq[s] << 16) | (P.consume[s] << 31));
-  if (coder == 1)
+  if (coder != 0)
     for (uint32_t p = 0; p < kTabSlots; ++p) put32(dst + stab + 4 * p, P.dtab[p]);
   for (uint32_t c = 0; c < nch; ++c) {
     put64(dst + ctab + 16ull * c, offs[c]);

@@ -66,7 +66,7 @@ typedef struct {
     uint32_t n_syms;
     uint32_t elem_bytes; /* 2 = bf16 words, 1 = bytes (fp8) */
     uint32_t plane_mode; /* 0 none, 1 dense, 2 compact, 3 fp8 exponent pairs + dense plane */
-    uint32_t coder;      /* 0 rANS, 1 tANS */
+    uint32_t coder;      /* 0 rANS; tANS: 1 (u32 state array), 2 (12-bit states at the stream head) */
 } bs_chunk_info;
 
 /* One tensor of a batched launch (device-resident array of these). */
@@ -112,7 +112,9 @@ int bs_chunk_decode_batch(const bs_chunk_task *d_tasks, uint32_t n_tasks, uint32
 
 /* Host encoder for BSCK. `mode`: BS_CHUNK_MODE_AUTO or a forced plane mode
  * (0-2 for bf16; 0 or 3 for bytes, 3 needing an even n). `coder`: 0 rANS,
- * 1 tANS. bs_chunk_encode is bs_chunk_encode_ex with coder 0, and
+ * 1 or 2 tANS (2, the smaller, keeps a chunk's 12-bit initial states at the
+ * head of its bit stream; 1 stores them as u32 words, the layout of earlier
+ * blobs, which still decode). bs_chunk_encode is bs_chunk_encode_ex with coder 0, and
  * bs_chunk_encode_bound its capacity (bs_chunk_encode_bound_ex for either
  * coder). Replaces the encode half of the codec plugin pair
  * (bigsmall/codec_registry.py:39-47). */

@@ -777,16 +777,19 @@ out:
  * for the product encoder and the GPU decoder. Format:
  *   [0]  "BSCK"  [4] u8 version (2 or 3)  [5] u8 elem_bytes (1|2)  [6] u8 plane_mode
  *   [7]  u8 prec_log2 (12)  [8] u64 n  [16] u32 steps  [20] u16 lanes (64*K, K in 1,2,4)
- *   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS, 1 tANS; version 3), 3 zero bytes
+ *   [22] u16 n_syms  [24] u32 n_chunks  [28] u8 coder (0 rANS; version 3: 1 tANS with a
+ *        state array, 2 tANS with the states at the stream head), 3 zero bytes
  *   [32] n_syms x u32 symbol entries: bits 0..15 value, bits 16..28 freq,
  *        bit 31 = consumes one plane byte
  *   pad to 16; tANS only: 4096 x u32 decode table {newX:12, nb:4, symbol:8, 0:8}
  *   n_chunks x {u64 offset, u32 n_words (rANS) or n_bits (tANS), u32 n_plane}
  *   version 3, plane modes 1 and 3: pad to 256, the full chunks' dense planes (nf*lanes*steps bytes)
- *   chunk: lanes x u32 initial states | rANS: n_words x u16, tANS: ceil(n_bits/32) x u32,
- *          padded to 16 | n_plane bytes (pad 16), the plane omitted for a
- *          full chunk of a version-3 blob in plane modes 1 and 3
- *   version 3: pad to 256 (blob lengths are multiples of 256)
+ *   chunk: lanes x u32 initial states (not in coder 2) | rANS: n_words x u16,
+ *          tANS: ceil(n_bits/32) x u32, padded to 16 | n_plane bytes (pad 16),
+ *          the plane omitted for a full chunk of a version-3 blob in plane
+ *          modes 1 and 3
+ *   version 3: pad to 256 (blob lengths are multiples of 256); coder 2: the
+ *   blob holds 256 bytes from every chunk's offset
  * Elements: bf16 words, or bytes; in plane mode 3 (fp8 exponent pairs) an
  * element is a pair of bytes (a 16-bit word) and n counts bytes. With
  * per = lanes*steps and nf = ne / per full chunks (ne = coded elements),
@@ -799,11 +802,13 @@ out:
  * L = 2^16): slot = x & 4095; x = f[s]*(x >> 12) + slot - cum[s]; if x < L,
  * x = x << 16 | the next word; words are consumed per step in ascending v
  * order among states that fell below L. A chunk ends with every x == L.
- * tANS (coder 1): X in [0, 4096); entry = table[X]; s = its symbol;
+ * tANS (coders 1 and 2): X in [0, 4096); entry = table[X]; s = its symbol;
  * X = newX + the next nb bits of the chunk's LSB-first bit stream, read in
  * chunk element order (per step, lanes ascending, a lane's states ascending);
  * in plane mode 2 a consuming symbol then reads its 8 plane bits. A chunk
- * ends with every X == 0 and every bit read.
+ * ends with every X == 0 and every bit read. Coder 2's stream starts with the
+ * initial states, 12 bits each, in the same reading order (lane l's state g at
+ * bit 12*(l*K + g)); coder 1 keeps them in the u32 array.
  * Plane bytes: plane_mode 1/3 (dense): every element has one, stored in blocks
  * of B steps (B = 8 for K <= 2, 4 for K = 4); the byte of state (g, l) for step
  * B*b+q sits at byte l*B*K + q*K + g of the chunk's plane block b (B*lanes
@@ -862,7 +867,7 @@ int orc_chunk_decode_range(const uint8_t *blob, size_t len, size_t n_weights, vo
     uint32_t steps = get32(blob + 16), lanes = get16(blob + 20), nsym = get16(blob + 22), nch = get32(blob + 24);
     uint32_t coder = blob[28];
     if ((ver != 2 && ver != 3) || (eb != 1 && eb != 2) || mode > 3 || prec != 12 ||
-        (lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || steps % 16 || coder > 1 ||
+        (lanes != 64 && lanes != 128 && lanes != 256) || steps == 0 || steps % 16 || coder > 2 ||
         blob[29] || blob[30] || blob[31] || (ver == 2 && coder != 0) ||
         (eb == 1 && mode != 0 && mode != 3) || (eb == 2 && mode == 3) || (mode == 3 && ver != 3))
         return ORC_ERR_FORMAT;
@@ -907,16 +912,22 @@ int orc_chunk_decode_range(const uint8_t *blob, size_t len, size_t n_weights, vo
         size_t sbytes = coder == 0 ? ((size_t)nw * 2 + 15) & ~(size_t)15
                                    : ((((size_t)nw + 31) / 32) * 4 + 15) & ~(size_t)15;
         size_t pbytes = split ? 0 : ((size_t)np + 15) & ~(size_t)15;
-        if (off % 16 || off + 4 * lanes + sbytes + pbytes > len) return ORC_ERR_FORMAT;
-        const uint8_t *st = blob + off, *wd = st + 4 * lanes, *pl = wd + sbytes;
+        size_t sarr = coder == 2 ? 0 : 4 * (size_t)lanes;          /* the u32 state array */
+        if (off % 16 || off + sarr + sbytes + pbytes > len || (coder == 2 && off + 256 > len)) return ORC_ERR_FORMAT;
+        const uint8_t *st = blob + off, *wd = st + sarr, *pl = wd + sbytes;
         uint64_t nc = ci < nf ? per : ne - nf * per;
         uint64_t nsteps = (nc + lanes - 1) / lanes;
         uint32_t x[256];
-        for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
-        if (coder == 1) for (uint32_t l = 0; l < lanes; l++) if (x[l] >= 4096) return ORC_ERR_FORMAT;
         uint64_t wp = 0, pp = 0;
         bitrd br = {wd, nw, 0};
         int err = 0;
+        if (coder == 2) {
+            for (uint32_t i = 0; i < lanes; i++) x[(i % K) * 64 + i / K] = br_take(&br, 12, &err);
+            if (err) return ORC_ERR_FORMAT;
+        } else {
+            for (uint32_t l = 0; l < lanes; l++) x[l] = get32(st + 4 * l);
+        }
+        if (coder == 1) for (uint32_t l = 0; l < lanes; l++) if (x[l] >= 4096) return ORC_ERR_FORMAT;
         for (uint64_t t = 0; t < nsteps; t++) {
             for (uint32_t i = 0; i < lanes; i++) {
                 /* rANS: states in v order (group-major); tANS: chunk element order (lane-major) */
@@ -968,7 +979,7 @@ int orc_chunk_decode_range(const uint8_t *blob, size_t len, size_t n_weights, vo
         }
         for (uint32_t l = 0; l < lanes; l++) if (x[l] != (coder == 0 ? RANS_L : 0)) return ORC_ERR_FORMAT;
         if (coder == 0 && wp != nw) return ORC_ERR_FORMAT;
-        if (coder == 1 && br.pos != nw) return ORC_ERR_FORMAT;
+        if (coder != 0 && br.pos != nw) return ORC_ERR_FORMAT;
         if (coder == 0 && mode == 2 && pp != np) return ORC_ERR_FORMAT;
     }
     return ORC_OK;

@@ -9,7 +9,10 @@ pinned on the CPU (oracle/bs_oracle.c's decoder is the checker).
   128 states (two per lane) every step reads one bit per state in chunk
   element order, so the expected words follow from the states and bits
   directly; reading MSB first, group-major instead of lane-major, or from the
-  wrong end breaks it.
+  wrong end breaks it. The same blob in coder 2 carries X0 as 12-bit fields
+  at the head of the stream, lane-major (state g of lane l at bit
+  12 * (l * 2 + g)), and its planted mistakes are group-major or MSB-first
+  fields.
 * Round trips of the product encoder through the oracle for both coders and
   every plane mode, with the tANS table the blob stores equal to the oracle's
   own construction from the quantised frequencies.
@@ -35,16 +38,25 @@ def _bf16(x: np.ndarray) -> np.ndarray:
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
-def hand_built_tans(seed: int = 0):
+def _fields12(vals, msb_first: bool = False) -> np.ndarray:
+    """12-bit fields as stream bits, LSB first (or each field reversed)."""
+    bits = (np.asarray(vals, np.int64)[:, None] >> np.arange(12)) & 1
+    return (bits[:, ::-1] if msb_first else bits).reshape(-1)
+
+
+def hand_built_tans(seed: int = 0, coder: int = 1, head_order: str = "lane", msb_first: bool = False):
     """(blob, expected words) of the hand-built tANS blob described above:
-    bf16 exact-value symbols 1.0 and 2.0, 128 states, 2 steps (256 elements)."""
+    bf16 exact-value symbols 1.0 and 2.0, 128 states, 2 steps (256 elements).
+    Coder 2 puts the states at the stream head in `head_order` ("lane": the
+    format's; "group": a planted mistake), fields LSB first unless
+    `msb_first`."""
     rng = np.random.default_rng(seed)
     lanes, steps, n = 128, 16, 256
     A, B = 0x3F80, 0x4000
     sym = rng.integers(0, 2, n)                        # element j's symbol index
     x0 = sym[:128]                                     # step 0: element l*2+g is state v = g*64 + l
     bits = np.concatenate([sym[128:], np.zeros(128, np.int64)])   # stream: step 1's symbols, then zeros
-    head = b"BSCK" + bytes([3, 2, 0, 12]) + struct.pack("<QIHHI", n, steps, lanes, 2, 1) + bytes([1, 0, 0, 0])
+    head = b"BSCK" + bytes([3, 2, 0, 12]) + struct.pack("<QIHHI", n, steps, lanes, 2, 1) + bytes([coder, 0, 0, 0])
     syms = struct.pack("<II", A | (2048 << 16), B | (2048 << 16))
     stab = 48
     table = np.array([(p & ~1) | (1 << 12) | ((p & 1) << 16) for p in range(4096)], np.uint32).tobytes()
@@ -54,17 +66,44 @@ def hand_built_tans(seed: int = 0):
     for j in range(128):
         l, g = j // 2, j % 2
         states[g * 64 + l] = x0[j]
-    stream = np.packbits(bits.astype(np.uint8), bitorder="little").tobytes()
-    blob = head + syms + b"\0" * (stab - 40) + table + struct.pack("<QII", off, n, 0) + states.tobytes() + stream
-    blob += b"\0" * ((-len(blob)) % 256)
+    if coder == 2:
+        order = x0 if head_order == "lane" else states       # states[v] is group-major
+        bits = np.concatenate([_fields12(order, msb_first), bits])
+        body = np.packbits(bits.astype(np.uint8), bitorder="little").tobytes()
+    else:
+        body = states.tobytes() + np.packbits(bits.astype(np.uint8), bitorder="little").tobytes()
+    blob = head + syms + b"\0" * (stab - 40) + table + struct.pack("<QII", off, bits.size, 0) + body
+    blob += b"\0" * (max(off + 256 - len(blob), 0) + (-max(len(blob), off + 256)) % 256)
     want = np.where(sym == 0, A, B).astype(np.uint16)
     return blob, want
 
 
 def test_hand_built_tans_blob():
     oracle.build()
-    blob, want = hand_built_tans()
-    assert oracle.chunk_decode(blob, want.size) == want.tobytes()
+    for coder in (1, 2):
+        blob, want = hand_built_tans(coder=coder)
+        assert len(blob) % 256 == 0 and blob[28] == coder
+        assert oracle.chunk_decode(blob, want.size) == want.tobytes(), coder
+
+
+def test_hand_built_tans_head_states_planted_mistakes():
+    """Coder 2 with the head states group-major or MSB first changes the
+    decode (or fails it); so does the blob cut to less than 256 bytes past
+    its chunk's offset."""
+    oracle.build()
+    blob, want = hand_built_tans(2, coder=2)
+    for kw in (dict(head_order="group"), dict(msb_first=True)):
+        bad, _ = hand_built_tans(2, coder=2, **kw)
+        assert bad != blob
+        try:
+            got = oracle.chunk_decode(bad, want.size)
+        except oracle.OracleError:
+            continue
+        assert got != want.tobytes(), kw
+    off = 48 + 4 * 4096 + 16
+    assert len(blob) >= off + 256
+    with pytest.raises(oracle.OracleError):
+        oracle.chunk_decode(blob[:off + 240], want.size)
 
 
 def test_hand_built_tans_planted_mistakes():
@@ -105,7 +144,7 @@ def _inputs(rng):
     yield "one", np.array([0x3F80], np.uint16), [-1, 1]
 
 
-@pytest.mark.parametrize("coder", [0, 1])
+@pytest.mark.parametrize("coder", [0, 1, 2])
 @pytest.mark.parametrize("lanes", [64, 128, 256])
 def test_round_trips_through_the_oracle(coder, lanes):
     oracle.build()
@@ -115,7 +154,7 @@ def test_round_trips_through_the_oracle(coder, lanes):
             blob = bc.encode_array(w, steps=32, mode=mode, lanes=lanes, coder=coder)
             assert blob[28] == coder and (mode < 0 or blob[6] == mode), (name, mode)
             assert oracle.chunk_decode(blob, w.size, w.dtype.itemsize) == w.tobytes(), (name, mode)
-            if coder == 1:
+            if coder != 0:
                 nsym = struct.unpack_from("<H", blob, 22)[0]
                 freqs = [(struct.unpack_from("<I", blob, 32 + 4 * s)[0] >> 16) & 0x1FFF for s in range(nsym)]
                 stab = (32 + 4 * nsym + 15) & ~15

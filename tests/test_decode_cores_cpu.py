@@ -6,7 +6,8 @@ tests/native/decode_fuzz.cpp; a second build at -O2 without instrumentation
 decodes the clean blobs and a share of the corrupted ones.
 
 Cases: clean blobs of every BSCK plane mode, state width, element size and
-coder (rANS, tANS), the layout-version-2 golden blobs, and of the reference's three formats on both decode paths (wave-serial and
+coder (rANS; tANS with its states at the stream head or in a u32 array), the
+layout-version-2 golden blobs, and of the reference's three formats on both decode paths (wave-serial and
 lane-per-chain), each of which must decode to its source; then thousands of
 corrupted copies (single and multiple byte changes, biased to the headers,
 tables and chunk tables, and truncations). A corrupted BSCK blob goes to the
@@ -105,21 +106,23 @@ def _bsck_inputs(rng):
     yield f8, dict(lanes=128, steps=16, mode=3)
     yield f8[:2 * 700], dict(lanes=64, steps=16, mode=3)
     yield f8, dict(lanes=256, steps=16, mode=3)
-    # tANS: every plane mode, state width and element kind, full chunks and tails
-    yield g, dict(lanes=128, steps=16, coder=1)
-    yield g[:200], dict(lanes=64, steps=16, coder=1)
-    yield _bf16(rng.standard_t(3, 9000) * 0.02), dict(lanes=256, steps=32, coder=1)
-    yield hz, dict(lanes=128, steps=16, mode=2, coder=1)
-    yield hz[:1500], dict(lanes=64, steps=32, mode=2, coder=1)
-    yield hz, dict(lanes=256, steps=16, mode=2, coder=1)
-    yield norms, dict(lanes=128, steps=16, coder=1)
-    yield rng.integers(0, 65536, 2500).astype(np.uint16), dict(lanes=128, steps=16, mode=1, coder=1)
-    yield rng.integers(0, 256, 4000).astype(np.uint8), dict(lanes=128, steps=16, coder=1)
-    yield rng.integers(0, 256, 3 * 8192 + 100).astype(np.uint8), dict(lanes=128, steps=64, coder=1)
-    yield hz2, dict(lanes=128, steps=64, mode=2, coder=1)
-    yield f8, dict(lanes=128, steps=16, mode=3, coder=1)
-    yield f8, dict(lanes=256, steps=16, mode=3, coder=1)
-    yield np.array([0x3F80], np.uint16), dict(lanes=64, steps=16, coder=1)
+    # tANS: every plane mode, state width and element kind, full chunks and tails, with the
+    # initial states at the stream head (coder 2) and in the u32 array of earlier blobs (coder 1)
+    tans = [(g, dict(lanes=128, steps=16)), (g[:200], dict(lanes=64, steps=16)),
+            (_bf16(rng.standard_t(3, 9000) * 0.02), dict(lanes=256, steps=32)),
+            (hz, dict(lanes=128, steps=16, mode=2)), (hz[:1500], dict(lanes=64, steps=32, mode=2)),
+            (hz, dict(lanes=256, steps=16, mode=2)), (norms, dict(lanes=128, steps=16)),
+            (rng.integers(0, 65536, 2500).astype(np.uint16), dict(lanes=128, steps=16, mode=1)),
+            (rng.integers(0, 256, 4000).astype(np.uint8), dict(lanes=128, steps=16)),
+            (rng.integers(0, 256, 3 * 8192 + 100).astype(np.uint8), dict(lanes=128, steps=64)),
+            (hz2, dict(lanes=128, steps=64, mode=2)), (f8, dict(lanes=128, steps=16, mode=3)),
+            (f8, dict(lanes=256, steps=16, mode=3)), (np.array([0x3F80], np.uint16), dict(lanes=64, steps=16)),
+            # one symbol: no element bits, so a coder-2 stream is its head states alone
+            (np.full(700, 0x3F80, np.uint16), dict(lanes=256, steps=16)),
+            (np.full(300, 0x3F80, np.uint16), dict(lanes=64, steps=16))]
+    for coder in (2, 1):
+        for w, kw in tans:
+            yield w, dict(kw, coder=coder)
 
 
 def _ref_inputs(rng):

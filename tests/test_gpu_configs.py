@@ -21,6 +21,7 @@ C4  KV cache blocks of 256 tokens, K and V [8 heads, 32768 tokens, 128] per laye
 from __future__ import annotations
 
 import hashlib
+import struct
 import sys
 
 import numpy as np
@@ -137,10 +138,11 @@ def test_c3_bf16_stress_forced_tans(kind):
     w = _stress(kind)
     _say(f"[c3] {kind} bf16_chunked_tans_v1 (forced tANS, this engine's format)")
     blob = _forced("bf16", "bf16_chunked_tans_v1", w)
-    assert blob[28] == 1 and blob[6] == (2 if kind == "halfzero" else 1)
+    assert blob[28] == 2 and blob[6] == (2 if kind == "halfzero" else 1)
+    assert struct.unpack_from("<IH", blob, 16) == (224, 256)     # the tANS codec's chunk geometry
     for mode in (1, 2):
         _say(f"[c3] {kind} bf16_chunked_tans_v1 mode={mode}")
-        _check_bsck(w, mode=mode, coder=1)
+        _check_bsck(w, mode=mode, coder=2, lanes=256, steps=64)
     _say(f"[c3] {kind} bf16_se_tans (the reference's forced-tANS format)")
     _check_ref("bf16_se_tans", oracle.tans_encode(w), w)
 
@@ -151,7 +153,7 @@ def test_c3_fp8_and_residual():
     f8 = x.to(torch.float8_e4m3fn)
     resid = (x - f8.float()).bfloat16()
     b8 = f8.view(torch.uint8).numpy()
-    for coder, codec in ((0, "fp8_chunked_v1"), (1, "fp8_chunked_tans_v1")):
+    for coder, codec in ((0, "fp8_chunked_v1"), (2, "fp8_chunked_tans_v1")):
         _say(f"[c3] fp8 e4m3 {codec} (exponent pairs, then byte symbols)")
         blob = _forced("fp8", codec, b8)
         assert blob[6] == 3 and blob[28] == coder
@@ -161,7 +163,7 @@ def test_c3_fp8_and_residual():
     _forced("bf16", "bf16_chunked_v1", rw)
     _check_ref("bf16_parallel_v1", oracle.par1_encode(rw), rw)
     _say("[c3] residual bf16_chunked_tans_v1 / bf16_se_tans (forced tANS)")
-    assert _forced("bf16", "bf16_chunked_tans_v1", rw)[28] == 1
+    assert _forced("bf16", "bf16_chunked_tans_v1", rw)[28] == 2
     _check_ref("bf16_se_tans", oracle.tans_encode(rw), rw)
 
 

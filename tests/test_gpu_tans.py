@@ -7,7 +7,9 @@ and == the oracle's CPU decode of the same blob. Also: the hand-built tANS
 blob whose decode follows from its table (tests/test_bsck_formats_cpu.py),
 one batched launch mixing both coders and every plane mode, corrupted tANS
 blobs (each decodes to something or raises, never faults), and the v2
-golden blobs.
+golden blobs. tANS runs with its initial states at the stream head (coder
+2, what the encoder writes by default) and in the u32 state array of
+earlier blobs (coder 1).
 """
 from __future__ import annotations
 
@@ -58,11 +60,13 @@ def _check(words, label, **kw):
     return blob
 
 
+@pytest.mark.parametrize("coder", [2, 1])
 @pytest.mark.parametrize("lanes", [64, 128, 256])
 @pytest.mark.parametrize("n", [1, 63, 64, 65, 129, 4097, 65536 * 3 + 1000, 1 << 20])
-def test_tans_gaussian_sizes(torch_gpu, n, lanes):
+def test_tans_gaussian_sizes(torch_gpu, n, lanes, coder):
     rng = np.random.default_rng(n + lanes)
-    _check(_bf16(rng.standard_normal(n) * 0.02), f"gauss{n}", steps=64, lanes=lanes, coder=1)
+    blob = _check(_bf16(rng.standard_normal(n) * 0.02), f"gauss{n}", steps=64, lanes=lanes, coder=coder)
+    assert blob[28] == coder
 
 
 @pytest.mark.parametrize("lanes", [64, 128, 256])
@@ -73,11 +77,11 @@ def test_tans_modes_and_steps(torch_gpu, mode, steps, lanes):
     w = _bf16(rng.standard_normal(300_007) * 0.02)
     if mode == 2:
         w[rng.permutation(w.size)[: w.size // 2]] = 0
-    blob = _check(w, f"mode{mode}", steps=steps, mode=mode, lanes=lanes, coder=1)
-    assert blob[28] == 1
+    blob = _check(w, f"mode{mode}", steps=steps, mode=mode, lanes=lanes, coder=2)
+    assert blob[28] == 2
 
 
-@pytest.mark.parametrize("coder", [0, 1])
+@pytest.mark.parametrize("coder", [0, 1, 2])
 @pytest.mark.parametrize("lanes", [64, 128, 256])
 def test_symbol_models(torch_gpu, coder, lanes):
     """Heavy tails, every word value, norms (exact values), one symbol,
@@ -101,9 +105,10 @@ def test_hand_built_tans_blob(torch_gpu):
     from bigsmall_amd.codecs import bf16_chunked as bc
     from test_bsck_formats_cpu import hand_built_tans
     for seed in range(4):
-        blob, want = hand_built_tans(seed)
-        _say(f"[tans] hand-built blob {seed}")
-        assert bc.decode(blob, {}, want.size) == want.tobytes()
+        for coder in (1, 2):
+            blob, want = hand_built_tans(seed, coder=coder)
+            _say(f"[tans] hand-built blob {seed}, coder {coder}")
+            assert bc.decode(blob, {}, want.size) == want.tobytes()
 
 
 def test_layout_version_2_golden_blobs(torch_gpu):
@@ -125,7 +130,7 @@ def test_batch_mixing_coders_and_modes(torch_gpu):
     from bigsmall_amd.device import ChunkBatch, ChunkJob, StatusWord, upload_bytes
     rng = np.random.default_rng(5)
     items = []
-    for coder in (0, 1):
+    for coder in (0, 1, 2):
         g = _bf16(rng.standard_normal(80_001) * 0.02)
         hz = g.copy()
         hz[rng.permutation(hz.size)[: hz.size // 2]] = 0
@@ -149,21 +154,22 @@ def test_batch_mixing_coders_and_modes(torch_gpu):
         assert o.cpu().numpy().tobytes() == w.tobytes(), i
 
 
+@pytest.mark.parametrize("coder", [2, 1])
 @pytest.mark.parametrize("mode", [1, 2, 3])
-def test_corrupted_tans_blobs_never_fault(torch_gpu, mode):
+def test_corrupted_tans_blobs_never_fault(torch_gpu, mode, coder):
     """Single-byte corruptions biased to the header, tables and chunk table:
     each decodes (to anything) or raises ValueError / DecodeError."""
     from bigsmall_amd.codecs import bf16_chunked as bc
     from bigsmall_amd.exceptions import DecodeError
-    rng = np.random.default_rng(40 + mode)
+    rng = np.random.default_rng(40 + mode + 10 * coder)
     if mode == 3:
         w = _fp8(rng.standard_normal(2 * 20_000))
     else:
         w = _bf16(rng.standard_normal(40_000) * 0.02)
         if mode == 2:
             w[rng.permutation(w.size)[:20_000]] = 0
-    blob = bc.encode_array(w, steps=16, mode=mode, coder=1)
-    _say(f"[tans] corruption sweep mode {mode}, blob {len(blob)} bytes")
+    blob = bc.encode_array(w, steps=16, mode=mode, coder=coder)
+    _say(f"[tans] corruption sweep mode {mode}, coder {coder}, blob {len(blob)} bytes")
     raised = decoded = 0
     for _ in range(120):
         b = bytearray(blob)

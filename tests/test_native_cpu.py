@@ -112,7 +112,7 @@ def test_planted_corruption_is_caught():
 
 @pytest.mark.parametrize("field,value", [("magic", b"BSCX"), ("version", 4), ("version", 1), ("elem_bytes", 3),
                                          ("plane_mode", 3), ("plane_mode", 4), ("prec", 11), ("lanes", 96),
-                                         ("steps", 24), ("n_syms", 0), ("n_chunks", 7), ("coder", 2),
+                                         ("steps", 24), ("n_syms", 0), ("n_chunks", 7), ("coder", 3),
                                          ("truncated", None)])
 def test_malformed_header_raises_value_error(field, value):
     """bs_chunk_inspect (host code) rejects every malformed header field, and
