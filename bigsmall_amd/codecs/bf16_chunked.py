@@ -74,7 +74,8 @@ def _threads() -> int:
 def encode_array(arr: np.ndarray, steps: int = DEFAULT_STEPS, mode: int = MODE_AUTO,
                  threads: int | None = None, lanes: int = DEFAULT_LANES, coder: int = CODER_RANS) -> bytes:
     """Encode a uint16 (bf16 words) or uint8 (fp8 bytes) array with the rANS
-    (coder 0) or tANS (coder 1) coder."""
+    coder (CODER_RANS) or the tANS coder (CODER_TANS; CODER_TANS_STATE_ARRAY
+    writes the earlier layout of its initial states)."""
     a = np.ascontiguousarray(arr)
     if a.dtype not in (np.uint16, np.uint8):
         raise TypeError("encode_array expects uint16 (bf16 bit patterns) or uint8 (fp8 bytes)")
