@@ -1,7 +1,9 @@
 """Property-based checks on the CPU (hypothesis), after the reference's
 tests/test_property_based.py: for any array the host encoder accepts, the
 oracle's BSCK decoder gives it back byte for byte, in every plane mode, state
-width and chunk length; auto-selection only names registered codecs and its
+width, chunk length and coder (rANS; tANS with its states at the stream head or
+in a u32 array), and a tANS blob with head states is at most its 256-byte
+tail larger than the same chunks with the state array; auto-selection only names registered codecs and its
 blob decodes (oracle) to the input; the binary multi-shard index round-trips
 arbitrary names, offsets and codecs.
 """
@@ -43,17 +45,21 @@ def _words(kind: str, n: int, seed: int) -> np.ndarray:
 
 @given(kind=st.sampled_from(["gauss", "few", "sparse", "uniform"]), n=st.integers(1, 20_000),
        seed=st.integers(0, 2**31), lanes=st.sampled_from([64, 128, 256]), steps=st.sampled_from([16, 32, 80]),
-       mode=st.sampled_from([-1, 0, 1, 2]))
+       mode=st.sampled_from([-1, 0, 1, 2]), coder=st.sampled_from([0, 1, 2]))
 @settings(**SETTINGS)
-def test_bsck_encode_then_oracle_decode_is_identity(kind, n, seed, lanes, steps, mode):
+def test_bsck_encode_then_oracle_decode_is_identity(kind, n, seed, lanes, steps, mode, coder):
     w = _words(kind, n, seed)
     if mode == 0 and np.unique(w).size > 256:
         mode = -1
-    blob = bc.encode_array(w, steps=steps, mode=mode, lanes=lanes)
+    blob = bc.encode_array(w, steps=steps, mode=mode, lanes=lanes, coder=coder)
     inf = bc.info(blob)
-    assert inf.n == n and inf.lanes == lanes and inf.steps == steps
+    assert inf.n == n and inf.lanes == lanes and inf.steps == steps and inf.coder == coder
     assert mode < 0 or inf.plane_mode == mode
     assert oracle.chunk_decode(blob, n) == w.tobytes()
+    if coder == 2:
+        # 2.5 bytes saved per state; the 256-byte tail after the last chunk can take some back
+        legacy = bc.encode_array(w, steps=steps, mode=inf.plane_mode, lanes=lanes, coder=1)
+        assert len(blob) <= len(legacy) + 256
 
 
 @given(n=st.integers(1, 50_000), seed=st.integers(0, 2**31))
