@@ -1,7 +1,7 @@
 """GPU backend of the decode engine (mirrors bigsmall/kernels/__init__.py:36-111).
 
     use_gpu() -> bool
-    backend_name() -> "hip" | "none"
+    backend_name() -> "hip" | "cpu"
     decode_bf16_parallel(blob, extras, n_weights) -> bytes
 
 One backend: the HIP kernels of libbigsmall_hip.so on a ROCm GPU (gfx950).
@@ -48,8 +48,12 @@ def use_gpu() -> bool:
 
 
 def backend_name() -> str:
+    """The backend's name: "hip", or "cpu" when no GPU backend is usable, the reference's names
+    for the two cases (kernels/__init__.py:84-86), so callers that branch on
+    them take the same branch. Here "cpu" means only that: there is no CPU
+    decoder, and decode_bf16_parallel raises RuntimeError."""
     _probe_backend()
-    return _GPU_BACKEND or "none"
+    return _GPU_BACKEND or "cpu"
 
 
 def decode_bf16_parallel(blob: bytes, extras: dict, n_weights: int) -> bytes:

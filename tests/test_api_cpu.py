@@ -177,7 +177,7 @@ def test_no_cpu_fallback(container_file):
     from bigsmall_amd import decoder
     p, _ = container_file
     kernels._GPU_BACKEND = None
-    assert not kernels.use_gpu() and kernels.backend_name() == "none"
+    assert not kernels.use_gpu() and kernels.backend_name() == "cpu"
     with pytest.raises(RuntimeError):
         kernels.decode_bf16_parallel(b"PAR1xxxx", {}, 10)
     with pytest.raises(RuntimeError):

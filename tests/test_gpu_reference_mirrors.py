@@ -98,7 +98,7 @@ def test_force_cpu_env_disables_gpu():
     kernels._GPU_BACKEND = None
     os.environ["BIGSMALL_FORCE_CPU"] = "1"
     try:
-        assert kernels.use_gpu() is False and kernels.backend_name() == "none"
+        assert kernels.use_gpu() is False and kernels.backend_name() == "cpu"
         blob = oracle.par1_encode(np.frombuffer(_gauss_raw(0, 1024), np.uint16))
         with pytest.raises(RuntimeError):
             kernels.decode_bf16_parallel(blob, {}, 1024)
