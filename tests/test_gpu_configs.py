@@ -143,6 +143,9 @@ def test_c3_bf16_stress_forced_tans(kind):
     for mode in (1, 2):
         _say(f"[c3] {kind} bf16_chunked_tans_v1 mode={mode}")
         _check_bsck(w, mode=mode, coder=2, lanes=256, steps=64)
+    # the earlier tANS layout (u32 initial states, 128 lanes) still decodes at full size
+    _say(f"[c3] {kind} tANS coder 1 (u32 state array)")
+    _check_bsck(w, coder=1, lanes=128, steps=128)
     _say(f"[c3] {kind} bf16_se_tans (the reference's forced-tANS format)")
     _check_ref("bf16_se_tans", oracle.tans_encode(w), w)
 
