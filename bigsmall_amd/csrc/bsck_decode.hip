@@ -490,9 +490,14 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 // the mask is 0 and merges the plane byte's sign and mantissa when it is
 // 0x807F, with no step spent on the raw count (hi's nt, in bits 0..4, is the
 // alignbit shift as it stands).
-template <int K, int MODE, bool FAST, bool PARTIAL>
+//
+// Compact chunks (MODE 2) pass `ensure`, called with the ring words this
+// step reads once their count is known: the block-level refill checks only
+// 12 bits per element there (a compact symbol takes up to 20), and ensure
+// lands the rest in the rare step that needs it.
+template <int K, int MODE, bool FAST, bool PARTIAL, class Ensure>
 __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C, const LDS void* tbl,
-                                          const LDS uint32_t* ring, uint32_t (&d)[K]) {
+                                          const LDS uint32_t* ring, uint32_t (&d)[K], Ensure&& ensure) {
   uint32_t e[K], hv[K], nb[K], nt[K];
   bool act[K];
   uint32_t tot = 0;
@@ -526,6 +531,7 @@ __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const Ch
   uint32_t pos = S.bpos + incl - tot;
   S.bpos += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1) & (FAST ? 0xFFFFFFFFu : 0xFFFFu);
   S.wptr = (S.bpos >> 5) << 1;                          // ring words no longer needed: [.., wptr)
+  if constexpr (MODE == 2) ensure(((S.bpos + 31u) >> 5) << 1);   // the ring words up to the step's last bit
   // The lane's states are read in pairs: a one-word-layout pair takes at most
   // 2 x 12 bits (one 32-bit window), a generic pair at most 2 x 20 (a 64-bit
   // window from three ring words, the second state's bits funnel-shifted out
@@ -625,9 +631,10 @@ __device__ __forceinline__ void request_segments(const ChunkState<K>& S, Infligh
 
 // Make sure the rings hold a block's worst-case demand. Rare: it lands the
 // in-flight segments early (waiting for them) and loads synchronously. A
-// block needs at most one renorm word per element (rANS), or MAXB bits per
-// element (tANS: 12, or 20 with compact-mode plane bits) plus the second word
-// of the last 32-bit window, in ring words.
+// block needs at most one renorm word per element (rANS), or MAXB = 12 bits
+// per element (tANS) plus the second word of the last 32-bit window, in ring
+// words; a compact tANS step that takes more (plane bits: up to 20 per
+// element) lands the rest itself.
 template <int K, int MODE, int MAXB = 0>
 __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C,
                                        LDS uint16_t* wring, LDS uint8_t* pring) {
@@ -686,9 +693,9 @@ __device__ __forceinline__ uint32_t pair_merge(uint32_t dup, uint32_t dA, uint32
 // a coded element is a pair of bytes.
 template <int K, int MODE, int EB, bool PARTIAL, int CODER>
 __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& pl, ChunkState<K>& S,
-                                             const ChunkParams& C, const LDS uint64_t* __restrict__ tbl,
-                                             const LDS uint16_t* wring, LDS uint8_t* pring,
-                                             LDS uint8_t* stage) {
+                                             Inflight<K, ring_mode<MODE, CODER>()>& F, const ChunkParams& C,
+                                             const LDS uint64_t* __restrict__ tbl, LDS uint16_t* wring,
+                                             LDS uint8_t* pring, LDS uint8_t* stage) {
   constexpr int RM = ring_mode<MODE, CODER>();
   constexpr uint32_t kStates = kWave * K;
   constexpr int kBlock = Geo<K, RM>::kBlock;
@@ -708,8 +715,25 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
     }
     const uint32_t qs = q % kHalf;                       // step within the staged half
     uint32_t d[K];
-    if (CODER == 0) rans_step<K, RM, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
-    else tans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, (const LDS uint32_t*)wring, d);
+    if (CODER == 0) {
+      rans_step<K, RM, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
+    } else {
+      // compact tANS: lands ring words up to `need` (16-bit words, at most the stream's) when a
+      // step takes more than the block-level refill provided; rare, and uniform across the wave
+      tans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, (const LDS uint32_t*)wring, d, [&](uint32_t need) {
+        typedef Geo<K, RM> G;
+        need = min(need, C.n_words);
+        if (S.wld < need) {
+          land_segments<K, RM>(S, F, wring, pring, lane);
+          while (S.wld < need) {
+            store_wseg<G>(wring, S.wld, load_seg<typename G::Seg>(C.wsrc, S.wld / (G::kLaneSeg / 2u), C.wvalid,
+                                                                  lane, C.safe), lane);
+            S.wld += G::kWSeg;
+          }
+          wave_sync();
+        }
+      });
+    }
     if (PAIR) {
       // plane bytes of this step: bytes q*K .. q*K+K-1 of the lane's 8K bytes
       const uint64_t pw = pl.b[(q * K) / 8];
@@ -840,7 +864,10 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
                                              uint32_t nc, uint32_t nsteps, int32_t* status, uint32_t fl) {
   constexpr int RM = ring_mode<MODE, CODER>();
-  constexpr int MAXB = CODER == 0 ? 0 : (MODE == 2 ? 20 : 12);   // tANS bits per element at most
+  // tANS: bits per element the block-level refill provides; at most 12 take
+  // the state bits, and a compact symbol's 8 plane bits beyond them are
+  // landed by the step that needs them (tans_step's ensure)
+  constexpr int MAXB = CODER == 0 ? 0 : 12;
   typedef Geo<K, RM> G;
   constexpr uint32_t kStates = kWave * K;
   ChunkParams C;
@@ -942,13 +969,13 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
       F.pl[1] = load_plane<K>(C.dplane, C.pstride, min(blk + 3, C.nblk - 1), C.lane);
     }
     wave_sync();
-    decode_block<K, MODE, EB, PARTIAL, CODER>(blk, cur0, S, C, tbl, wring, pring, stage);
+    decode_block<K, MODE, EB, PARTIAL, CODER>(blk, cur0, S, F, C, tbl, wring, pring, stage);
     if (PARTIAL && blk + 1 >= C.nblk) break;
     // ---- second block of the pair
     refill<K, RM, MAXB>(S, F, C, wring, pring);
     wave_sync();
     if (PARTIAL) flush_half<K, EB, PARTIAL, G::kBlock / 2>(2 * blk + 1, C, stage);
-    decode_block<K, MODE, EB, PARTIAL, CODER>(blk + 1, cur1, S, C, tbl, wring, pring, stage);
+    decode_block<K, MODE, EB, PARTIAL, CODER>(blk + 1, cur1, S, F, C, tbl, wring, pring, stage);
     blk += 2;
     if (blk >= C.nblk) break;
     if (!PARTIAL) {

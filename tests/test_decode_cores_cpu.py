@@ -117,6 +117,10 @@ def _bsck_inputs(rng):
             (rng.integers(0, 256, 3 * 8192 + 100).astype(np.uint8), dict(lanes=128, steps=64)),
             (hz2, dict(lanes=128, steps=64, mode=2)), (f8, dict(lanes=128, steps=16, mode=3)),
             (f8, dict(lanes=256, steps=16, mode=3)), (np.array([0x3F80], np.uint16), dict(lanes=64, steps=16)),
+            # compact mode at ~20 bits per element (uniform words: 8-bit exponent classes plus
+            # 8 plane bits), beyond the 12 per element the block-level ring refill provides
+            (rng.integers(0, 65536, 3 * 8192 + 5).astype(np.uint16), dict(lanes=256, steps=32, mode=2)),
+            (rng.integers(0, 65536, 2 * 8192 + 3).astype(np.uint16), dict(lanes=128, steps=64, mode=2)),
             # one symbol: no element bits, so a coder-2 stream is its head states alone
             (np.full(700, 0x3F80, np.uint16), dict(lanes=256, steps=16)),
             (np.full(300, 0x3F80, np.uint16), dict(lanes=64, steps=16))]

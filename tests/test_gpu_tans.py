@@ -101,6 +101,25 @@ def test_symbol_models(torch_gpu, coder, lanes):
            lanes=lanes, coder=coder)
 
 
+@pytest.mark.parametrize("coder", [2, 1])
+@pytest.mark.parametrize("lanes", [64, 128, 256])
+def test_compact_tans_beyond_the_refill_bound(torch_gpu, lanes, coder):
+    """Compact chunks that take ~20 bits per element (uniform words: 8-bit
+    exponent classes plus 8 plane bits), beyond the 12 per element the
+    block-level ring refill provides: the steps land the rest themselves.
+    Short and long chunks, with a partial chunk, and a tensor mixing such
+    stretches with half-zero ones."""
+    rng = np.random.default_rng(700 + lanes + coder)
+    w = rng.integers(0, 65536, 400_003).astype(np.uint16)
+    for steps in (16, 432):
+        blob = _check(w, f"uniform compact steps={steps}", steps=steps, mode=2, lanes=lanes, coder=coder)
+        assert blob[6] == 2 and blob[28] == coder
+    mixed = _bf16(rng.standard_normal(600_000) * 0.02)
+    mixed[rng.permutation(mixed.size)[:300_000]] = 0
+    mixed[200_000:260_000] = rng.integers(0, 65536, 60_000).astype(np.uint16)
+    _check(mixed, "mixed compact", steps=64, mode=2, lanes=lanes, coder=coder)
+
+
 def test_hand_built_tans_blob(torch_gpu):
     from bigsmall_amd.codecs import bf16_chunked as bc
     from test_bsck_formats_cpu import hand_built_tans
