@@ -493,8 +493,8 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 //
 // Compact chunks (MODE 2) pass `ensure`, called with the ring words this
 // step reads once their count is known: the block-level refill checks only
-// 12 bits per element there (a compact symbol takes up to 20), and ensure
-// lands the rest in the rare step that needs it.
+// 6 bits per element there (a compact symbol takes up to 20), and ensure
+// lands the rest in the step that needs it.
 template <int K, int MODE, bool FAST, bool PARTIAL, class Ensure>
 __device__ __forceinline__ void tans_step(uint32_t t, ChunkState<K>& S, const ChunkParams& C, const LDS void* tbl,
                                           const LDS uint32_t* ring, uint32_t (&d)[K], Ensure&& ensure) {
@@ -631,10 +631,11 @@ __device__ __forceinline__ void request_segments(const ChunkState<K>& S, Infligh
 
 // Make sure the rings hold a block's worst-case demand. Rare: it lands the
 // in-flight segments early (waiting for them) and loads synchronously. A
-// block needs at most one renorm word per element (rANS), or MAXB = 12 bits
-// per element (tANS) plus the second word of the last 32-bit window, in ring
-// words; a compact tANS step that takes more (plane bits: up to 20 per
-// element) lands the rest itself.
+// block needs at most one renorm word per element (rANS), or MAXB bits per
+// element (tANS: 12, a state's worst case) plus the second word of the last
+// 32-bit window, in ring words; compact tANS blocks ask for 6 bits per
+// element, and a step that takes more (plane bits: up to 20 per element)
+// lands the rest itself.
 template <int K, int MODE, int MAXB = 0>
 __device__ __forceinline__ void refill(ChunkState<K>& S, Inflight<K, MODE>& F, const ChunkParams& C,
                                        LDS uint16_t* wring, LDS uint8_t* pring) {
@@ -864,10 +865,13 @@ __device__ __forceinline__ void decode_chunk(const LDS uint64_t* __restrict__ tb
                                              GLB uint8_t* __restrict__ out8, uint64_t ubase, uint64_t ustride,
                                              uint32_t nc, uint32_t nsteps, int32_t* status, uint32_t fl) {
   constexpr int RM = ring_mode<MODE, CODER>();
-  // tANS: bits per element the block-level refill provides; at most 12 take
-  // the state bits, and a compact symbol's 8 plane bits beyond them are
-  // landed by the step that needs them (tans_step's ensure)
-  constexpr int MAXB = CODER == 0 ? 0 : 12;
+  // tANS: bits per element the block-level refill provides. The one-word
+  // layouts take at most 12 (a state's worst case). Compact steps land what
+  // they need beyond it themselves (tans_step's ensure), so their blocks ask
+  // for 6, about what a compact element takes on average: a larger reserve
+  // made blocks wait for segments more often (12 bits: 0.3-1 % slower on the
+  // half-zeros tensor and the pruned layer).
+  constexpr int MAXB = CODER == 0 ? 0 : (MODE == 2 ? 6 : 12);
   typedef Geo<K, RM> G;
   constexpr uint32_t kStates = kWave * K;
   ChunkParams C;
