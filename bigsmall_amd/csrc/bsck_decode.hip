@@ -491,8 +491,8 @@ __device__ __forceinline__ void rans_step(uint32_t t, ChunkState<K>& S, const Ch
 // 0x807F, with no step spent on the raw count (hi's nt, in bits 0..4, is the
 // alignbit shift as it stands).
 //
-// Compact chunks (MODE 2) pass `ensure`, called with the ring words this
-// step reads once their count is known: the block-level refill checks only
+// In compact chunks (MODE 2) the step calls `ensure` with the ring words it
+// reads once their count is known: the block-level refill checks only
 // 6 bits per element there (a compact symbol takes up to 20), and ensure
 // lands the rest in the step that needs it.
 template <int K, int MODE, bool FAST, bool PARTIAL, class Ensure>
@@ -720,7 +720,7 @@ __device__ __forceinline__ void decode_block(uint32_t blk, const PlaneRegs<K>& p
       rans_step<K, RM, FAST, PARTIAL>(t, S, C, tbl, wring, pring, d);
     } else {
       // compact tANS: lands ring words up to `need` (16-bit words, at most the stream's) when a
-      // step takes more than the block-level refill provided; rare, and uniform across the wave
+      // step takes more than the block-level refill provided (a wave-uniform branch)
       tans_step<K, MODE, FAST, PARTIAL>(t, S, C, tbl, (const LDS uint32_t*)wring, d, [&](uint32_t need) {
         typedef Geo<K, RM> G;
         need = min(need, C.n_words);
