@@ -27,8 +27,8 @@ GPU-native formats (bf16_chunked_v1 / fp8_chunked_v1), and the last resort is
 bf16_chunked_v1 (as in the default bf16 list), competes only against a
 bf16_chunked_v1 winner in compact plane mode (a tensor of mostly exact values,
 such as a pruned one), and wins when it is at most compact_tans_tolerance (1 %)
-larger: compact chunks decode 10-23 % faster under tANS (a half-pruned 8B
-layer: 0.151 against 0.185 ms, for 0.35 % more bytes). Elsewhere it is not
+larger: compact chunks decode in 17-29 % less time under tANS (a half-pruned
+8B layer: 0.131 against 0.185 ms, for 0.01 % more bytes). Elsewhere it is not
 encoded (dense tensors decode at the same speed under either coder, and rANS
 is smaller). A candidate list without it forces rANS, one with only it tANS. The reference formats it writes (bf16_parallel_v1,
 bf16_se_tans, bf16_se_single_kernel) are byte-identical to the reference
